@@ -1,0 +1,6 @@
+"""MI355X (gfx950) implementation of Alelyon Compute Kit's vq4/v1 path.
+
+``alelyon_compute_kit.vq`` keeps the reference's import path and API;
+``alelyon_compute_kit.ack`` is the device/buffer binding of libackvq.so.
+"""
+__all__ = ["ack", "vq"]

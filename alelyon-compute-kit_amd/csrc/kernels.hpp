@@ -1,0 +1,70 @@
+// Launch interface between the C ABI (abi.cpp) and the gfx950 kernels.
+//
+// Every launcher enqueues on the caller's stream and returns the launch
+// status; none allocates or synchronises. Pointers are device addresses of
+// the first instance; `stride` gives the byte distance between consecutive
+// batch instances of each slot (ack_vq_batch), zero for a single instance.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace ackvq {
+
+struct Operands {
+  const void* in[4] = {nullptr, nullptr, nullptr, nullptr};
+  void* out = nullptr;
+  uint32_t* status = nullptr;
+  uint64_t stride[5] = {0, 0, 0, 0, 0};  // slots 0..3, then out
+  uint32_t count = 1;
+};
+
+// Which implementation serves an op-2 product.
+enum class MatmulPath : int {
+  General = 0,    // tiled, sequential FP32 per output: bit-identical to vq4.comp
+  GemvBins = 1,   // B groups along n: codebook-factorised bins, small m
+  GemvTable = 2,  // B groups along k (B stored (n,k)): dot-product table, small m
+  Mfma = 3,       // large m: decode to LDS tiles, FP32 MFMA
+};
+
+const char* matmul_path_name(MatmulPath p);
+
+// Chooses the path for a product; `policy` 1 forces General.
+MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                              uint32_t policy);
+
+// Bytes of device workspace a path needs (split-k partials, counters).
+size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
+                              uint32_t flags, uint32_t count);
+
+hipError_t launch_encode(hipStream_t s, const Operands& o, uint32_t m, uint32_t group);
+hipError_t launch_decode(hipStream_t s, const Operands& o, uint32_t m, uint32_t group);
+hipError_t launch_adamw(hipStream_t s, const Operands& o, uint32_t m, uint32_t group);
+hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                         uint32_t group, uint32_t flags, MatmulPath path, void* workspace,
+                         size_t workspace_bytes);
+
+// Fused VQAdamW passes (ack_vq_adamw_step). codes4/books4/coeffs are the
+// op-3 inputs.
+struct AdamwInputs {
+  const uint32_t* codes4;
+  const float* books4;
+  const float* coeffs;
+  uint32_t m;
+  uint32_t group;
+};
+
+// AdamW at whole vectors `vectors[0..count)`: out = [3][count][group].
+hipError_t launch_adamw_gather(hipStream_t s, const AdamwInputs& in, const uint32_t* vectors,
+                               uint32_t count, float* out, uint32_t* status);
+// Entries of `book` selected by complete vectors of state `state` under the
+// float64 rule; OR-ed into *mask.
+hipError_t launch_adamw_used(hipStream_t s, const AdamwInputs& in, const float* book,
+                             uint32_t state, uint32_t* mask, uint32_t* status);
+// Recompute and encode all three states against books3; count changed W.
+hipError_t launch_adamw_encode(hipStream_t s, const AdamwInputs& in, const float* books3,
+                               uint32_t* out_codes, uint32_t* changed, uint32_t* status);
+
+}  // namespace ackvq

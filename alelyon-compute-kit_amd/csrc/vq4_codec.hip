@@ -1,0 +1,475 @@
+// vq4/v1 codec kernels for gfx950: encode (op 0), decode (op 1), AdamW from
+// four packed states (op 3), and the passes of the fused VQAdamW step.
+//
+// Numerics follow src/alelyon_compute_kit/_kit/kernels/vq4.comp exactly. The
+// library is compiled with -ffp-contract=off, so every `a * b + c` below is a
+// rounded multiply followed by a rounded add, as GLSL `precise` demands; FP32
+// division and square root are IEEE correctly rounded.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "kernels.hpp"
+
+namespace ackvq {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr uint32_t kMaxGridX = 16384;
+
+__device__ __forceinline__ bool finite_f32(float x) { return fabsf(x) <= FLT_MAX; }
+
+__device__ __forceinline__ uint32_t nibble(const uint32_t* codes, uint32_t vector) {
+  return (codes[vector >> 3] >> ((vector & 7u) * 4u)) & 15u;
+}
+
+__device__ __forceinline__ uint32_t words_for(uint32_t values, uint32_t group) {
+  uint32_t vectors = values / group + (values % group != 0);
+  return vectors / 8 + (vectors % 8 != 0);
+}
+
+template <typename T>
+__device__ __forceinline__ const T* item_ptr(const void* base, uint64_t stride, uint32_t item) {
+  return reinterpret_cast<const T*>(static_cast<const char*>(base) + stride * item);
+}
+template <typename T>
+__device__ __forceinline__ T* item_ptr_mut(void* base, uint64_t stride, uint32_t item) {
+  return reinterpret_cast<T*>(static_cast<char*>(base) + stride * item);
+}
+
+// Status sweep over a codebook (vq4.comp:153-158): any nonfinite value sets
+// bit 1. Run by one block per instance.
+__device__ void sweep_book(const float* book, uint32_t values, uint32_t* status) {
+  bool bad = false;
+  for (uint32_t i = threadIdx.x; i < values; i += blockDim.x) bad |= !finite_f32(book[i]);
+  if (__any(bad) && (threadIdx.x % warpSize) == 0) atomicOr(status, 1u);
+}
+
+// Argmin of vq4.comp:118-144 for one vector: for each code ascending, the
+// FP32 distance accumulated as d = d + (x_j - c_j)^2 with every operation
+// rounded, j ascending over the valid components; strict `<` keeps the
+// lowest index; best starts at +inf, selected at 0. `bad` reports a
+// nonfinite final distance (a nonfinite partial distance stays nonfinite
+// when values and book are finite, so this equals the shader's per-step
+// test; nonfinite values and books are reported by their own checks).
+template <int G, bool Full>
+__device__ __forceinline__ uint32_t argmin32(const float (&x)[G], uint32_t valid,
+                                             const float* sbook, bool& bad) {
+  float best = __int_as_float(0x7f800000);
+  uint32_t selected = 0;
+#pragma unroll 2
+  for (uint32_t code = 0; code < 16; ++code) {
+    const float* c = sbook + code * G;
+    float d = 0.0f;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (Full || uint32_t(j) < valid) {
+        const float delta = x[j] - c[j];
+        const float sq = delta * delta;
+        d = d + sq;
+      }
+    }
+    bad |= !finite_f32(d);
+    if (d < best) {
+      best = d;
+      selected = code;
+    }
+  }
+  return selected;
+}
+
+// OR the nibbles of 8 consecutive lanes into lane (v % 8 == 0)'s word.
+__device__ __forceinline__ uint32_t gather_word(uint32_t part) {
+  part |= __shfl_xor(part, 1);
+  part |= __shfl_xor(part, 2);
+  part |= __shfl_xor(part, 4);
+  return part;
+}
+
+// ---- op 0: encode -------------------------------------------------------
+template <int G>
+__global__ __launch_bounds__(kThreads) void k_encode(Operands o, uint32_t m) {
+  const uint32_t item = blockIdx.y;
+  const float* x = item_ptr<float>(o.in[0], o.stride[0], item);
+  const float* book = item_ptr<float>(o.in[1], o.stride[1], item);
+  uint32_t* out = item_ptr_mut<uint32_t>(o.out, o.stride[4], item);
+  __shared__ float sbook[16 * G];
+  for (uint32_t i = threadIdx.x; i < 16 * G; i += kThreads) sbook[i] = book[i];
+  if (blockIdx.x == 0) sweep_book(book, 16 * G, o.status);
+  __syncthreads();
+
+  const uint32_t vectors = m / G + (m % G != 0);
+  const uint32_t words = vectors / 8 + (vectors % 8 != 0);
+  const bool aligned = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0);
+  bool bad = false;
+  for (uint32_t base = blockIdx.x * kThreads; base < words * 8; base += gridDim.x * kThreads) {
+    const uint32_t v = base + threadIdx.x;
+    uint32_t code = 0;
+    if (v < vectors) {
+      const uint32_t start = v * G;
+      const uint32_t valid = (m - start) < G ? (m - start) : G;
+      float xv[G];
+      if (valid == G) {
+        if (aligned) {
+#pragma unroll
+          for (int j = 0; j < G; j += 4) {
+            const float4 q = *reinterpret_cast<const float4*>(x + start + j);
+            xv[j] = q.x; xv[j + 1] = q.y; xv[j + 2] = q.z; xv[j + 3] = q.w;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < G; ++j) xv[j] = x[start + j];
+        }
+#pragma unroll
+        for (int j = 0; j < G; ++j) bad |= !finite_f32(xv[j]);
+        code = argmin32<G, true>(xv, G, sbook, bad);
+      } else {
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          xv[j] = uint32_t(j) < valid ? x[start + j] : 0.0f;
+          bad |= uint32_t(j) < valid && !finite_f32(xv[j]);
+        }
+        code = argmin32<G, false>(xv, valid, sbook, bad);
+      }
+    }
+    const uint32_t word = gather_word(code << (4u * (v & 7u)));
+    if ((v & 7u) == 0 && (v >> 3) < words) out[v >> 3] = word;
+  }
+  if (__any(bad) && (threadIdx.x % warpSize) == 0) atomicOr(o.status, 1u);
+}
+
+// ---- op 1: decode -------------------------------------------------------
+// out[i] = book[code(i / G)][i % G], a bit copy. Each lane writes one
+// 16-byte quad (G is a multiple of 4, so a quad never straddles vectors).
+template <int G>
+__global__ __launch_bounds__(kThreads) void k_decode(Operands o, uint32_t m) {
+  const uint32_t item = blockIdx.y;
+  const uint32_t* codes = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
+  const uint32_t* book = item_ptr<uint32_t>(o.in[1], o.stride[1], item);
+  uint32_t* out = item_ptr_mut<uint32_t>(o.out, o.stride[4], item);
+  __shared__ __align__(16) uint32_t sbook[16 * G];
+  for (uint32_t i = threadIdx.x; i < 16 * G; i += kThreads) sbook[i] = book[i];
+  if (blockIdx.x == 0) sweep_book(reinterpret_cast<const float*>(book), 16 * G, o.status);
+  __syncthreads();
+  const uint32_t quads = m / 4;
+  if ((reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
+    for (uint32_t q = blockIdx.x * kThreads + threadIdx.x; q < quads; q += gridDim.x * kThreads) {
+      const uint32_t e = q * 4;
+      const uint32_t code = nibble(codes, e / G);
+      *reinterpret_cast<uint4*>(out + e) = *reinterpret_cast<const uint4*>(sbook + code * G + e % G);
+    }
+  } else {
+    for (uint32_t e = blockIdx.x * kThreads + threadIdx.x; e < quads * 4; e += gridDim.x * kThreads)
+      out[e] = sbook[nibble(codes, e / G) * G + e % G];
+  }
+  if (blockIdx.x == 0 && threadIdx.x < m % 4) {
+    const uint32_t e = quads * 4 + threadIdx.x;
+    out[e] = sbook[nibble(codes, e / G) * G + e % G];
+  }
+}
+
+// ---- op 3: AdamW ---------------------------------------------------------
+struct Coeffs {
+  float lr, beta1, beta2, eps, decay, c1, c2;
+  uint32_t fail;  // 0 ok, 1 nonfinite coefficient, 4 outside its domain
+};
+
+// vq4.comp:81-91: every coefficient finite, then the domains.
+__device__ __forceinline__ Coeffs load_coeffs(const float* b2) {
+  Coeffs c;
+  c.lr = b2[0]; c.beta1 = b2[1]; c.beta2 = b2[2]; c.eps = b2[3];
+  c.decay = b2[4]; c.c1 = b2[5]; c.c2 = b2[6];
+  c.fail = 0;
+  for (int j = 0; j < 7; ++j)
+    if (!finite_f32(b2[j])) c.fail = 1;
+  if (c.fail == 0 &&
+      (c.lr < 0.0f || c.beta1 < 0.0f || c.beta1 >= 1.0f || c.beta2 < 0.0f || c.beta2 >= 1.0f ||
+       c.eps <= 0.0f || c.decay < 0.0f || c.c1 <= 0.0f || c.c1 > 1.0f || c.c2 <= 0.0f ||
+       c.c2 > 1.0f))
+    c.fail = 4;
+  return c;
+}
+
+struct AdamwOut {
+  float w, m, v;
+  uint32_t flags;  // status bits this element raises
+  bool write;      // the shader writes the element (vq4.comp:92-115)
+};
+
+// unpack_state (vq4.comp:74-78) and adamw_value (:80-116) for element i.
+template <int G>
+__device__ __forceinline__ AdamwOut adamw_element(const uint32_t* codes4, const float* books4,
+                                                  uint32_t words, uint32_t i, const Coeffs& c) {
+  AdamwOut r;
+  r.flags = 0;
+  r.write = false;
+  r.w = r.m = r.v = 0.0f;
+  const uint32_t vector = i / G;
+  const uint32_t t = i % G;
+  float s[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+    s[st] = books4[st * 16 * G + nibble(codes4 + st * words, vector) * G + t];
+  const float weight = s[0], moment = s[1], variance = s[2], gradient = s[3];
+  if (!finite_f32(weight) || !finite_f32(moment) || !finite_f32(variance) || !finite_f32(gradient)) {
+    r.flags = 1;
+    return r;
+  }
+  if (variance < 0.0f) {
+    r.flags = 4;
+    return r;
+  }
+  const float next_m = c.beta1 * moment + (1.0f - c.beta1) * gradient;
+  const float next_v = c.beta2 * variance + (1.0f - c.beta2) * (gradient * gradient);
+  const float corrected_m = next_m / c.c1;
+  const float corrected_v = next_v / c.c2;
+  const float denominator = sqrtf(corrected_v) + c.eps;
+  const float decayed = weight * (1.0f - c.lr * c.decay);
+  const float next_w = decayed - c.lr * corrected_m / denominator;
+  if (!finite_f32(next_m) || !finite_f32(next_v) || !finite_f32(corrected_m) ||
+      !finite_f32(corrected_v) || !finite_f32(denominator) || !finite_f32(decayed) ||
+      !finite_f32(next_w))
+    r.flags = 1;
+  r.w = next_w;
+  r.m = next_m;
+  r.v = next_v;
+  r.write = true;
+  return r;
+}
+
+template <int G>
+__global__ __launch_bounds__(kThreads) void k_adamw(Operands o, uint32_t m) {
+  const uint32_t item = blockIdx.y;
+  const uint32_t* codes4 = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
+  const float* books4 = item_ptr<float>(o.in[1], o.stride[1], item);
+  const float* coeff = item_ptr<float>(o.in[2], o.stride[2], item);
+  float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
+  if (blockIdx.x == 0) sweep_book(books4, 64 * G, o.status);
+  const Coeffs c = load_coeffs(coeff);
+  if (c.fail) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(o.status, c.fail);
+    return;
+  }
+  const uint32_t words = words_for(m, G);
+  uint32_t flags = 0;
+  for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < m; i += gridDim.x * kThreads) {
+    const AdamwOut r = adamw_element<G>(codes4, books4, words, i, c);
+    flags |= r.flags;
+    if (r.write) {
+      out[i] = r.w;
+      out[m + i] = r.m;
+      out[2 * m + i] = r.v;
+    }
+  }
+  // Wave-reduce the bits before touching the status word.
+  for (int off = 1; off < warpSize; off <<= 1) flags |= __shfl_xor(flags, off);
+  if (flags && (threadIdx.x % warpSize) == 0) atomicOr(o.status, flags);
+}
+
+// ---- fused VQAdamW passes -------------------------------------------------
+template <int G>
+__global__ __launch_bounds__(kThreads) void k_adamw_gather(AdamwInputs in, const uint32_t* vectors,
+                                                           uint32_t count, float* out,
+                                                           uint32_t* status) {
+  const Coeffs c = load_coeffs(in.coeffs);
+  if (c.fail) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(status, c.fail);
+    return;
+  }
+  const uint32_t words = words_for(in.m, G);
+  const uint32_t total = count * G;
+  uint32_t flags = 0;
+  for (uint32_t e = blockIdx.x * kThreads + threadIdx.x; e < total; e += gridDim.x * kThreads) {
+    const uint32_t i = vectors[e / G] * G + e % G;
+    const AdamwOut r = adamw_element<G>(in.codes4, in.books4, words, i, c);
+    flags |= r.flags;
+    out[e] = r.w;
+    out[total + e] = r.m;
+    out[2 * total + e] = r.v;
+  }
+  for (int off = 1; off < warpSize; off <<= 1) flags |= __shfl_xor(flags, off);
+  if (flags && (threadIdx.x % warpSize) == 0) atomicOr(status, flags);
+}
+
+// The float64 CPU encode (vq.py:166-174): d = d + (x - c)^2 in float64 with
+// every operation rounded, j ascending; argmin keeps the first minimum.
+template <int G>
+__global__ __launch_bounds__(kThreads) void k_adamw_used(AdamwInputs in, const float* book,
+                                                         uint32_t state, uint32_t* mask,
+                                                         uint32_t* status) {
+  __shared__ double sbook[16 * G];
+  for (uint32_t i = threadIdx.x; i < 16 * G; i += kThreads) sbook[i] = double(book[i]);
+  __syncthreads();
+  const Coeffs c = load_coeffs(in.coeffs);
+  if (c.fail) return;  // the encode pass reports coefficient failures
+  const uint32_t words = words_for(in.m, G);
+  const uint32_t complete = in.m / G;
+  uint32_t used = 0;
+  for (uint32_t v = blockIdx.x * kThreads + threadIdx.x; v < complete; v += gridDim.x * kThreads) {
+    double x[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const AdamwOut r = adamw_element<G>(in.codes4, in.books4, words, v * G + j, c);
+      x[j] = double(state == 0 ? r.w : state == 1 ? r.m : r.v);
+    }
+    double best = 0.0;
+    uint32_t sel = 0;
+    for (uint32_t code = 0; code < 16; ++code) {
+      double d = 0.0;
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        const double delta = x[j] - sbook[code * G + j];
+        const double sq = delta * delta;
+        d = d + sq;
+      }
+      if (code == 0 || d < best) {
+        best = d;
+        sel = code;
+      }
+    }
+    used |= 1u << sel;
+  }
+  for (int off = 1; off < warpSize; off <<= 1) used |= __shfl_xor(used, off);
+  if (used && (threadIdx.x % warpSize) == 0) atomicOr(mask, used);
+  (void)status;
+}
+
+// Recompute W', M', V' per vector and encode each against its new book with
+// op 0's FP32 rule; count W values whose decoded value moved.
+template <int G>
+__global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const float* books3,
+                                                           uint32_t* out_codes, uint32_t* changed,
+                                                           uint32_t* status) {
+  __shared__ float sbook[3 * 16 * G];
+  __shared__ float soldw[16 * G];
+  for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) sbook[i] = books3[i];
+  for (uint32_t i = threadIdx.x; i < 16 * G; i += kThreads) soldw[i] = in.books4[i];
+  if (blockIdx.x == 0) sweep_book(books3, 3 * 16 * G, status);
+  __syncthreads();
+  const Coeffs c = load_coeffs(in.coeffs);
+  if (c.fail) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(status, c.fail);
+    return;
+  }
+  const uint32_t m = in.m;
+  const uint32_t words = words_for(m, G);
+  const uint32_t vectors = m / G + (m % G != 0);
+  uint32_t flags = 0;
+  uint32_t moved = 0;
+  bool bad = false;
+  for (uint32_t base = blockIdx.x * kThreads; base < words * 8; base += gridDim.x * kThreads) {
+    const uint32_t v = base + threadIdx.x;
+    uint32_t code[3] = {0, 0, 0};
+    if (v < vectors) {
+      const uint32_t start = v * G;
+      const uint32_t valid = (m - start) < G ? (m - start) : G;
+      float xs[3][G];
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        if (uint32_t(j) < valid) {
+          const AdamwOut r = adamw_element<G>(in.codes4, in.books4, words, start + j, c);
+          flags |= r.flags;
+          xs[0][j] = r.w; xs[1][j] = r.m; xs[2][j] = r.v;
+          bad |= !finite_f32(r.w) || !finite_f32(r.m) || !finite_f32(r.v);
+        } else {
+          xs[0][j] = xs[1][j] = xs[2][j] = 0.0f;
+        }
+      }
+#pragma unroll
+      for (int st = 0; st < 3; ++st) {
+        code[st] = valid == G ? argmin32<G, true>(xs[st], G, sbook + st * 16 * G, bad)
+                              : argmin32<G, false>(xs[st], valid, sbook + st * 16 * G, bad);
+      }
+      const uint32_t old_code = nibble(in.codes4, v);
+      for (uint32_t j = 0; j < valid; ++j)
+        moved += sbook[code[0] * G + j] != soldw[old_code * G + j];
+    }
+#pragma unroll
+    for (int st = 0; st < 3; ++st) {
+      const uint32_t word = gather_word(code[st] << (4u * (v & 7u)));
+      if ((v & 7u) == 0 && (v >> 3) < words) out_codes[st * words + (v >> 3)] = word;
+    }
+  }
+  if (bad) flags |= 1;
+  for (int off = 1; off < warpSize; off <<= 1) {
+    flags |= __shfl_xor(flags, off);
+    moved += __shfl_xor(moved, off);
+  }
+  if ((threadIdx.x % warpSize) == 0) {
+    if (flags) atomicOr(status, flags);
+    if (moved) atomicAdd(changed, moved);
+  }
+}
+
+uint32_t grid_for(uint64_t items, uint32_t per_block) {
+  uint64_t blocks = (items + per_block - 1) / per_block;
+  if (blocks == 0) blocks = 1;
+  return blocks > kMaxGridX ? kMaxGridX : uint32_t(blocks);
+}
+
+}  // namespace
+
+#define ACKVQ_DISPATCH_GROUP(group, KERNEL, ...)                         \
+  do {                                                                  \
+    if ((group) == 8) { KERNEL<8><<<__VA_ARGS__>>>; }                   \
+    else if ((group) == 16) { KERNEL<16><<<__VA_ARGS__>>>; }            \
+    else { KERNEL<32><<<__VA_ARGS__>>>; }                               \
+  } while (0)
+
+hipError_t launch_encode(hipStream_t s, const Operands& o, uint32_t m, uint32_t group) {
+  const uint32_t vectors = m / group + (m % group != 0);
+  const uint32_t words = vectors / 8 + (vectors % 8 != 0);
+  dim3 grid(grid_for(uint64_t(words) * 8, kThreads), o.count);
+  if (group == 8) k_encode<8><<<grid, kThreads, 0, s>>>(o, m);
+  else if (group == 16) k_encode<16><<<grid, kThreads, 0, s>>>(o, m);
+  else k_encode<32><<<grid, kThreads, 0, s>>>(o, m);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode(hipStream_t s, const Operands& o, uint32_t m, uint32_t group) {
+  dim3 grid(grid_for((m + 3) / 4, kThreads), o.count);
+  if (group == 8) k_decode<8><<<grid, kThreads, 0, s>>>(o, m);
+  else if (group == 16) k_decode<16><<<grid, kThreads, 0, s>>>(o, m);
+  else k_decode<32><<<grid, kThreads, 0, s>>>(o, m);
+  return hipGetLastError();
+}
+
+hipError_t launch_adamw(hipStream_t s, const Operands& o, uint32_t m, uint32_t group) {
+  dim3 grid(grid_for(m, kThreads), o.count);
+  if (group == 8) k_adamw<8><<<grid, kThreads, 0, s>>>(o, m);
+  else if (group == 16) k_adamw<16><<<grid, kThreads, 0, s>>>(o, m);
+  else k_adamw<32><<<grid, kThreads, 0, s>>>(o, m);
+  return hipGetLastError();
+}
+
+hipError_t launch_adamw_gather(hipStream_t s, const AdamwInputs& in, const uint32_t* vectors,
+                               uint32_t count, float* out, uint32_t* status) {
+  dim3 grid(grid_for(uint64_t(count) * in.group, kThreads));
+  if (in.group == 8) k_adamw_gather<8><<<grid, kThreads, 0, s>>>(in, vectors, count, out, status);
+  else if (in.group == 16) k_adamw_gather<16><<<grid, kThreads, 0, s>>>(in, vectors, count, out, status);
+  else k_adamw_gather<32><<<grid, kThreads, 0, s>>>(in, vectors, count, out, status);
+  return hipGetLastError();
+}
+
+hipError_t launch_adamw_used(hipStream_t s, const AdamwInputs& in, const float* book,
+                             uint32_t state, uint32_t* mask, uint32_t* status) {
+  dim3 grid(grid_for(in.m / in.group, kThreads));
+  if (in.group == 8) k_adamw_used<8><<<grid, kThreads, 0, s>>>(in, book, state, mask, status);
+  else if (in.group == 16) k_adamw_used<16><<<grid, kThreads, 0, s>>>(in, book, state, mask, status);
+  else k_adamw_used<32><<<grid, kThreads, 0, s>>>(in, book, state, mask, status);
+  return hipGetLastError();
+}
+
+hipError_t launch_adamw_encode(hipStream_t s, const AdamwInputs& in, const float* books3,
+                               uint32_t* out_codes, uint32_t* changed, uint32_t* status) {
+  const uint32_t vectors = in.m / in.group + (in.m % in.group != 0);
+  const uint32_t words = vectors / 8 + (vectors % 8 != 0);
+  dim3 grid(grid_for(uint64_t(words) * 8, kThreads));
+  if (in.group == 8) k_adamw_encode<8><<<grid, kThreads, 0, s>>>(in, books3, out_codes, changed, status);
+  else if (in.group == 16) k_adamw_encode<16><<<grid, kThreads, 0, s>>>(in, books3, out_codes, changed, status);
+  else k_adamw_encode<32><<<grid, kThreads, 0, s>>>(in, books3, out_codes, changed, status);
+  return hipGetLastError();
+}
+
+}  // namespace ackvq

@@ -1,0 +1,411 @@
+// vq4/v1 packed-pair products C = op(A) . op(B) for gfx950 (op 2 of
+// src/alelyon_compute_kit/_kit/kernels/vq4.comp:165-176).
+//
+// Two implementations live here:
+//
+// * General: 64x64 output tiles, both operands decoded per element into LDS
+//   through the flat storage index (groups may straddle rows), each output
+//   accumulated as total = total + a*b with k ascending and every operation
+//   rounded -- the shader's order, so its results are bit-identical to
+//   vq4.comp. Serves every shape and layout.
+//
+// * GemvBins (small m, B stored (k,n) with each row a whole number of
+//   words): per output group j and code e the kernel accumulates
+//   S[r][j][e] = sum over rows k with code(k,j) = e of x[r][k] with one LDS
+//   atomic add per nibble, then y[r][j*G+t] = sum_e C_B[e][t] * S[r][j][e].
+//   That is G times fewer additions than decoding the weight, which is what
+//   lets a product that reads only half a byte per G weights run at the
+//   packed-weight bandwidth instead of the FP32 FMA rate. The summation
+//   order differs from the shader's; results agree within FP32 rounding.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "kernels.hpp"
+
+namespace ackvq {
+namespace {
+
+__device__ __forceinline__ bool finite_f32(float x) { return fabsf(x) <= FLT_MAX; }
+
+__device__ __forceinline__ uint32_t nibble(const uint32_t* codes, uint32_t vector) {
+  return (codes[vector >> 3] >> ((vector & 7u) * 4u)) & 15u;
+}
+
+template <typename T>
+__device__ __forceinline__ const T* item_ptr(const void* base, uint64_t stride, uint32_t item) {
+  return reinterpret_cast<const T*>(static_cast<const char*>(base) + stride * item);
+}
+template <typename T>
+__device__ __forceinline__ T* item_ptr_mut(void* base, uint64_t stride, uint32_t item) {
+  return reinterpret_cast<T*>(static_cast<char*>(base) + stride * item);
+}
+
+__device__ void sweep_books(const float* a, const float* b, uint32_t values, uint32_t* status) {
+  bool bad = false;
+  for (uint32_t i = threadIdx.x; i < values; i += blockDim.x)
+    bad |= !finite_f32(a[i]) || !finite_f32(b[i]);
+  if (__any(bad) && (threadIdx.x % warpSize) == 0) atomicOr(status, 1u);
+}
+
+// ---- General -------------------------------------------------------------
+constexpr int kGT = 64;   // output tile edge
+constexpr int kGK = 16;   // inner step
+constexpr int kGThreads = 256;
+
+template <int G>
+__global__ __launch_bounds__(kGThreads) void k_matmul_general(Operands o, uint32_t m, uint32_t n,
+                                                              uint32_t k, uint32_t flags) {
+  __shared__ float sa_book[16 * G];
+  __shared__ float sb_book[16 * G];
+  __shared__ float as[kGK][kGT + 4];
+  __shared__ float bs[kGK][kGT + 4];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t tx = tid % 16, ty = tid / 16;
+  const uint32_t n0 = blockIdx.x * kGT, m0 = blockIdx.y * kGT;
+  for (uint32_t item = blockIdx.z; item < o.count; item += gridDim.z) {
+    const uint32_t* a_codes = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
+    const float* a_book = item_ptr<float>(o.in[1], o.stride[1], item);
+    const uint32_t* b_codes = item_ptr<uint32_t>(o.in[2], o.stride[2], item);
+    const float* b_book = item_ptr<float>(o.in[3], o.stride[3], item);
+    float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
+    __syncthreads();
+    for (uint32_t i = tid; i < 16 * G; i += kGThreads) {
+      sa_book[i] = a_book[i];
+      sb_book[i] = b_book[i];
+    }
+    if (blockIdx.x == 0 && blockIdx.y == 0) sweep_books(a_book, b_book, 16 * G, o.status);
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    for (uint32_t k0 = 0; k0 < k; k0 += kGK) {
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < (kGK * kGT) / kGThreads; ++t) {
+        const uint32_t e = tid + t * kGThreads;
+        const uint32_t r = e % kGT, kk = e / kGT;
+        const uint32_t inner = k0 + kk;
+        float av = 0.0f, bv = 0.0f;
+        if (inner < k) {
+          const uint32_t row = m0 + r;
+          if (row < m) {
+            const uint32_t flat = (flags & 1u) ? inner * m + row : row * k + inner;
+            av = sa_book[nibble(a_codes, flat / G) * G + flat % G];
+          }
+          const uint32_t col = n0 + r;
+          if (col < n) {
+            const uint32_t flat = (flags & 2u) ? col * k + inner : inner * n + col;
+            bv = sb_book[nibble(b_codes, flat / G) * G + flat % G];
+          }
+        }
+        as[kk][r] = av;
+        bs[kk][r] = bv;
+      }
+      __syncthreads();
+      const uint32_t steps = (k - k0) < kGK ? (k - k0) : kGK;
+      for (uint32_t kk = 0; kk < steps; ++kk) {
+        float a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = as[kk][ty + 16 * i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = bs[kk][tx + 16 * j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float product = a[i] * b[j];
+            acc[i][j] = acc[i][j] + product;
+          }
+      }
+    }
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t row = m0 + ty + 16 * i;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t col = n0 + tx + 16 * j;
+        if (row < m && col < n) {
+          out[uint64_t(row) * n + col] = acc[i][j];
+          bad |= !finite_f32(acc[i][j]);
+        }
+      }
+    }
+    if (__any(bad) && (tid % warpSize) == 0) atomicOr(o.status, 1u);
+  }
+}
+
+// ---- GemvBins ------------------------------------------------------------
+// Tile: kTileWords words of each B row (8 * kTileWords output groups), all m
+// rows of A, a slice of k. Lane (q = lane % 32, half = lane / 32) reads word
+// q of row 2*wave_row + half, so a wave reads two whole 128-byte tile rows.
+// Bins are laid out [r][nibble][e][q]: the 32 lanes of a half-wave hit 32
+// distinct banks for any codes.
+constexpr int kTileWords = 32;
+constexpr int kTileGroups = kTileWords * 8;
+constexpr int kBinThreads = 256;
+constexpr int kBinRowsPerPass = kBinThreads / 32;  // 8 rows per pass
+constexpr int kBinUnroll = 8;
+constexpr uint32_t kGemvMaxM = 8;
+constexpr uint32_t kChunk = 256;  // x rows staged in LDS at a time
+
+__device__ __forceinline__ uint32_t bin_index(uint32_t r, uint32_t nib, uint32_t e, uint32_t q) {
+  return ((r * 8 + nib) * 16 + e) * kTileWords + q;
+}
+
+// x[r][kk] for rows r < m and inner rows [k0, kend), decoded from A by flat
+// index into sx[r * kChunk + kk].
+template <int G, int M>
+__device__ void decode_a_chunk(const uint32_t* a_codes, const float* sa_book, uint32_t k,
+                               uint32_t flags, uint32_t k0, uint32_t kend, float* sx) {
+  for (uint32_t e = threadIdx.x; e < M * kChunk; e += blockDim.x) {
+    const uint32_t r = e / kChunk, kk = e % kChunk;
+    const uint32_t inner = k0 + kk;
+    float v = 0.0f;
+    if (inner < kend) {
+      const uint32_t flat = (flags & 1u) ? inner * M + r : r * k + inner;
+      v = sa_book[nibble(a_codes, flat / G) * G + flat % G];
+    }
+    sx[e] = v;
+  }
+}
+
+// grid: (n tiles, k splits, instances). Dynamic shared memory: the bins
+// (M * 16 * kTileGroups floats) then one x chunk (M * kChunk floats).
+template <int G, int M>
+__global__ __launch_bounds__(kBinThreads) void k_gemv_bins(Operands o, uint32_t n, uint32_t k,
+                                                           uint32_t flags, uint32_t ks,
+                                                           float* partial) {
+  extern __shared__ float smem[];
+  float* bins = smem;
+  float* sx = smem + M * 16 * kTileGroups;
+  __shared__ float sa_book[16 * G];
+  __shared__ float sb_book[16 * G];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t tile = blockIdx.x, split = blockIdx.y;
+  const uint32_t row_words = n / (8 * G);
+  const uint32_t k0 = split * ks;
+  const uint32_t kend = (k0 + ks) < k ? (k0 + ks) : k;
+  const uint32_t lane = tid % 64, wave = tid / 64;
+  const uint32_t q = lane % 32, half = lane / 32;
+  const uint32_t word_col = tile * kTileWords + q;
+  const bool live = word_col < row_words;
+  for (uint32_t item = blockIdx.z; item < o.count; item += gridDim.z) {
+    const uint32_t* a_codes = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
+    const float* a_book = item_ptr<float>(o.in[1], o.stride[1], item);
+    const uint32_t* b_codes = item_ptr<uint32_t>(o.in[2], o.stride[2], item);
+    const float* b_book = item_ptr<float>(o.in[3], o.stride[3], item);
+    __syncthreads();
+    for (uint32_t i = tid; i < 16 * G; i += kBinThreads) {
+      sa_book[i] = a_book[i];
+      sb_book[i] = b_book[i];
+    }
+    for (uint32_t i = tid; i < M * 16 * kTileGroups; i += kBinThreads) bins[i] = 0.0f;
+    if (tile == 0 && split == 0) sweep_books(a_book, b_book, 16 * G, o.status);
+    const uint32_t* col_codes = b_codes + word_col;
+    for (uint32_t kc = k0; kc < kend; kc += kChunk) {
+      const uint32_t kce = (kc + kChunk) < kend ? (kc + kChunk) : kend;
+      __syncthreads();
+      decode_a_chunk<G, M>(a_codes, sa_book, k, flags, kc, kce, sx);
+      __syncthreads();
+      for (uint32_t kb = kc; kb < kce; kb += kBinRowsPerPass * kBinUnroll) {
+        uint32_t w[kBinUnroll];
+#pragma unroll
+        for (int u = 0; u < kBinUnroll; ++u) {
+          const uint32_t row = kb + u * kBinRowsPerPass + wave * 2 + half;
+          w[u] = (live && row < kce) ? col_codes[uint64_t(row) * row_words] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kBinUnroll; ++u) {
+          const uint32_t row = kb + u * kBinRowsPerPass + wave * 2 + half;
+          if (!live || row >= kce) continue;
+          float xr[M];
+#pragma unroll
+          for (int r = 0; r < M; ++r) xr[r] = sx[r * kChunk + (row - kc)];
+#pragma unroll
+          for (uint32_t nib = 0; nib < 8; ++nib) {
+            const uint32_t e = (w[u] >> (4 * nib)) & 15u;
+#pragma unroll
+            for (int r = 0; r < M; ++r) atomicAdd(&bins[bin_index(r, nib, e, q)], xr[r]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+    // Finalise this tile: y[r][j*G+t] = sum_e C_B[e][t] * S[r][j][e].
+    const uint32_t groups = (row_words - tile * kTileWords) < kTileWords
+                                ? (row_words - tile * kTileWords) * 8
+                                : kTileGroups;
+    if (gridDim.y == 1) {
+      float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
+      bool bad = false;
+      for (uint32_t e = tid; e < M * groups * G; e += kBinThreads) {
+        const uint32_t r = e / (groups * G);
+        const uint32_t jt = e % (groups * G);
+        const uint32_t j = jt / G, t = jt % G;
+        float acc = 0.0f;
+#pragma unroll
+        for (uint32_t c = 0; c < 16; ++c)
+          acc = fmaf(sb_book[c * G + t], bins[bin_index(r, j % 8, c, j / 8)], acc);
+        out[uint64_t(r) * n + tile * kTileGroups * G + jt] = acc;
+        bad |= !finite_f32(acc);
+      }
+      if (__any(bad) && (tid % warpSize) == 0) atomicOr(o.status, 1u);
+    } else {
+      // partial[item][split][tile][r][j][e]
+      float* p = partial + ((uint64_t(item) * gridDim.y + split) * gridDim.x + tile) *
+                               (M * 16 * kTileGroups);
+      for (uint32_t e = tid; e < M * 16 * kTileGroups; e += kBinThreads) {
+        const uint32_t r = e / (16 * kTileGroups);
+        const uint32_t je = e % (16 * kTileGroups);
+        const uint32_t j = je / 16, c = je % 16;
+        p[e] = bins[bin_index(r, j % 8, c, j / 8)];
+      }
+    }
+  }
+}
+
+// Sum the split-k bins in split order, then apply the B codebook.
+template <int G, int M>
+__global__ __launch_bounds__(256) void k_gemv_bins_finish(Operands o, uint32_t n, uint32_t splits,
+                                                          uint32_t tiles, const float* partial) {
+  __shared__ float sb_book[16 * G];
+  const uint32_t tile = blockIdx.x;
+  const uint32_t row_words = n / (8 * G);
+  const uint32_t groups = (row_words - tile * kTileWords) < kTileWords
+                              ? (row_words - tile * kTileWords) * 8
+                              : kTileGroups;
+  for (uint32_t item = blockIdx.z; item < o.count; item += gridDim.z) {
+    const float* b_book = item_ptr<float>(o.in[3], o.stride[3], item);
+    float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < 16 * G; i += blockDim.x) sb_book[i] = b_book[i];
+    __syncthreads();
+    bool bad = false;
+    for (uint32_t e = blockIdx.y * blockDim.x + threadIdx.x; e < M * groups * G;
+         e += gridDim.y * blockDim.x) {
+      const uint32_t r = e / (groups * G);
+      const uint32_t jt = e % (groups * G);
+      const uint32_t j = jt / G, t = jt % G;
+      float s[16];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) s[c] = 0.0f;
+      for (uint32_t sp = 0; sp < splits; ++sp) {
+        const float* p = partial + ((uint64_t(item) * splits + sp) * tiles + tile) *
+                                       (M * 16 * kTileGroups) +
+                         (r * kTileGroups + j) * 16;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) s[c] += p[c];
+      }
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) acc = fmaf(sb_book[c * G + t], s[c], acc);
+      out[uint64_t(r) * n + tile * kTileGroups * G + jt] = acc;
+      bad |= !finite_f32(acc);
+    }
+    if (__any(bad) && (threadIdx.x % warpSize) == 0) atomicOr(o.status, 1u);
+  }
+}
+
+uint32_t gemv_splits(uint32_t n, uint32_t k, uint32_t group, uint32_t count) {
+  const uint32_t tiles = (n / (8 * group) + kTileWords - 1) / kTileWords;
+  const uint64_t blocks = uint64_t(tiles) * count;
+  // Enough blocks for 256 compute units; never slices shorter than 128 rows.
+  uint32_t splits = 1;
+  while (blocks * splits < 256 && k / (splits * 2) >= 128) splits *= 2;
+  return splits;
+}
+
+size_t bins_shmem(uint32_t m) { return (size_t(m) * 16 * kTileGroups + size_t(m) * kChunk) * 4; }
+
+template <int G, int M>
+hipError_t launch_bins_m(hipStream_t s, const Operands& o, uint32_t n, uint32_t k, uint32_t flags,
+                         void* workspace) {
+  const uint32_t tiles = (n / (8 * G) + kTileWords - 1) / kTileWords;
+  const uint32_t splits = gemv_splits(n, k, G, o.count);
+  const uint32_t ks = (k + splits - 1) / splits;
+  const uint32_t zc = o.count < 65535 ? o.count : 65535;
+  const size_t shmem = bins_shmem(M);
+  if (shmem > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_bins<G, M>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
+    if (e != hipSuccess) return e;
+  }
+  dim3 grid(tiles, splits, zc);
+  k_gemv_bins<G, M><<<grid, kBinThreads, shmem, s>>>(o, n, k, flags, ks,
+                                                     static_cast<float*>(workspace));
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || splits == 1) return err;
+  dim3 fgrid(tiles, 4, zc);
+  k_gemv_bins_finish<G, M><<<fgrid, 256, 0, s>>>(o, n, splits, tiles,
+                                                 static_cast<const float*>(workspace));
+  return hipGetLastError();
+}
+
+template <int G>
+hipError_t launch_bins(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                       uint32_t flags, void* workspace) {
+  switch (m) {
+    case 1: return launch_bins_m<G, 1>(s, o, n, k, flags, workspace);
+    case 2: return launch_bins_m<G, 2>(s, o, n, k, flags, workspace);
+    case 3: return launch_bins_m<G, 3>(s, o, n, k, flags, workspace);
+    case 4: return launch_bins_m<G, 4>(s, o, n, k, flags, workspace);
+    case 5: return launch_bins_m<G, 5>(s, o, n, k, flags, workspace);
+    case 6: return launch_bins_m<G, 6>(s, o, n, k, flags, workspace);
+    case 7: return launch_bins_m<G, 7>(s, o, n, k, flags, workspace);
+    default: return launch_bins_m<G, 8>(s, o, n, k, flags, workspace);
+  }
+}
+
+}  // namespace
+
+const char* matmul_path_name(MatmulPath p) {
+  switch (p) {
+    case MatmulPath::General: return "general";
+    case MatmulPath::GemvBins: return "gemv-bins";
+    case MatmulPath::GemvTable: return "gemv-table";
+    case MatmulPath::Mfma: return "mfma";
+  }
+  return "unknown";
+}
+
+MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                              uint32_t policy) {
+  (void)k;
+  if (policy == 1) return MatmulPath::General;
+  if (m <= kGemvMaxM && (flags & 2u) == 0 && n % (8 * group) == 0) return MatmulPath::GemvBins;
+  return MatmulPath::General;
+}
+
+size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
+                              uint32_t flags, uint32_t count) {
+  (void)flags;
+  if (p != MatmulPath::GemvBins) return 0;
+  const uint32_t splits = gemv_splits(n, k, group, count);
+  if (splits == 1) return 0;
+  const uint32_t tiles = (n / (8 * group) + kTileWords - 1) / kTileWords;
+  return size_t(count) * splits * tiles * m * 16 * kTileGroups * sizeof(float);
+}
+
+hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                         uint32_t group, uint32_t flags, MatmulPath path, void* workspace,
+                         size_t workspace_bytes) {
+  (void)workspace_bytes;
+  if (path == MatmulPath::GemvBins) {
+    if (group == 8) return launch_bins<8>(s, o, m, n, k, flags, workspace);
+    if (group == 16) return launch_bins<16>(s, o, m, n, k, flags, workspace);
+    return launch_bins<32>(s, o, m, n, k, flags, workspace);
+  }
+  const uint32_t zc = o.count < 65535 ? o.count : 65535;
+  dim3 grid((n + kGT - 1) / kGT, (m + kGT - 1) / kGT, zc);
+  if (group == 8) k_matmul_general<8><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
+  else if (group == 16) k_matmul_general<16><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
+  else k_matmul_general<32><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
+  return hipGetLastError();
+}
+
+}  // namespace ackvq

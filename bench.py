@@ -1,0 +1,271 @@
+"""Benchmark of the vq4 packed matmul on one MI355X.
+
+Metric: packed-weight GB/s (and % of HBM peak) at M=1, and
+TFLOP/s at M=2048.
+
+Headline line (`value`): BASELINE config 3, the decode-shaped GEMV -- a
+4096x4096 weight ~N(0, 0.02^2) at group 16 times one activation row
+~N(0,1), both vq4-encoded -- measured cache-cold: one step is one batched
+launch (ack_vq_batch) over R distinct packed weights whose total exceeds
+twice the 256 MiB Infinity Cache, so every packed byte comes from HBM.
+`value` = R * 525,312 B / (kernel time per launch), timed with HIP events on
+the library's stream, inputs resident in HBM. The R weights are one
+genuinely encoded weight with a different relabelling of its 16 entries
+each (codes permuted, book rows permuted back): every item decodes to the
+same matrix, so all R outputs must agree, while no two items share bytes.
+
+Secondary (`extra.prefill`): BASELINE config 4, X 2048x4096 times W
+4096x14336 at group 32 and dY 2048x14336 times W^T, TFLOP/s = 2*M*N*K / time.
+
+`cpu_baseline`: the oracle's numpy CPU path for config 3 (decode the weight
+with a gather, then numpy matmul) on a bounded sample of matrices, timed on
+this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--items R]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT / "alelyon-compute-kit_amd"), str(ROOT)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+W_BYTES = 524288 + 1024           # packed codes + codebook of one 4096x4096 g16 weight
+
+
+def log(*parts):
+    print("[bench]", *parts, file=sys.stderr, flush=True)
+
+
+def relabelled_items(codes: np.ndarray, book: np.ndarray, count: int, seed: int):
+    """`count` byte-distinct images of one tensor: item i maps code c to
+    perm_i[c] and stores book row c at perm_i[c]."""
+    rng = np.random.default_rng(seed)
+    raw = codes.view(np.uint8)
+    out_codes = np.empty((count, codes.size), np.uint32)
+    out_books = np.empty((count, 16, book.shape[1]), np.float32)
+    for i in range(count):
+        perm = np.arange(16) if i == 0 else rng.permutation(16)
+        lut = (perm[np.arange(256) & 15] | (perm[np.arange(256) >> 4] << 4)).astype(np.uint8)
+        out_codes[i] = lut[raw].view(np.uint32)
+        out_books[i, perm] = book
+    return out_codes, out_books
+
+
+def timed(device, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    device.synchronize()
+    device.timer_start()
+    for _ in range(steps):
+        fn()
+    ms = device.timer_stop()
+    return ms / steps
+
+
+def bench_gemv(device, dev, items, steps, warmup):
+    from alelyon_compute_kit import vq
+    from oracle.vq4_numpy import ShaderOracle, max_rel
+    rng = np.random.default_rng(3)
+    log("encoding the 4096x4096 weight")
+    w = (rng.standard_normal((4096, 4096)) * 0.02).astype(np.float32)
+    w_img = dev.encode(w, vq.fit_codebook(w, group=16), group=16)
+    x = rng.standard_normal((1, 4096)).astype(np.float32)
+    x_img = dev.encode(x, vq.fit_codebook(x, group=16), group=16)
+    log(f"building {items} relabelled weights")
+    codes, books = relabelled_items(w_img.codes, w_img.codebook, items, 4)
+    xa = np.tile(x_img.codes, items)
+    xb = np.tile(x_img.codebook.reshape(-1), items)
+    bufs = [device.buffer(a.nbytes) for a in (xa, xb, codes, books)]
+    for b, a in zip(bufs, (xa, xb, codes, books)):
+        b.upload(a)
+    out = device.buffer(items * 4096 * 4)
+    status = device.buffer(4)
+    status.upload(np.zeros(1, np.uint32))
+    words = (2, 1, 4096, 4096, 16, 16, 0, 0)
+    path = dev.path_name(words)
+    try:
+        def launch():
+            dev.run(words, bufs, out, status, count=items)
+        log(f"timing {steps} launches of {items} items, path {path}")
+        ms = timed(device, launch, steps, warmup)
+        flags = int(status.download(np.uint32)[0])
+        y = out.download(np.float32).reshape(items, 4096)
+        # single-matrix latency (resident, cache-warm): one ack_vq of item 0
+        s_bufs = [device.buffer(a.nbytes) for a in (x_img.codes, x_img.codebook, w_img.codes,
+                                                    w_img.codebook)]
+        for b, a in zip(s_bufs, (x_img.codes, x_img.codebook, w_img.codes, w_img.codebook)):
+            b.upload(a)
+        s_out = device.buffer(4096 * 4)
+        single_ms = timed(device, lambda: dev.run(words, s_bufs, s_out, status), 50, 5)
+        for b in s_bufs + [s_out]:
+            b.free()
+    finally:
+        for b in bufs + [out, status]:
+            b.free()
+    if flags:
+        raise SystemExit(f"status word {flags} after the timed GEMV launches")
+    oracle = ShaderOracle()
+    ref, _ = oracle.matmul(x_img.codes, x_img.codebook, w_img.codes, w_img.codebook,
+                           1, 4096, 4096, 16, 0)
+    err = max(max_rel(y[0], ref[0]), float(np.max(np.abs(y - y[0]))) / float(np.max(np.abs(ref))))
+    return {"ms": ms, "single_ms": single_ms, "path": path, "max_rel": err,
+            "x_img": x_img, "w_img": w_img}
+
+
+def bench_prefill(device, dev, steps, warmup):
+    from alelyon_compute_kit import vq
+    rng = np.random.default_rng(4)
+    m, k, n = 2048, 4096, 14336
+    log("encoding the config-4 operands")
+    w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+    w_img = dev.encode(w, vq.fit_codebook(w, group=32), group=32)
+    del w
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x_img = dev.encode(x, vq.fit_codebook(x, group=32), group=32)
+    dy = (rng.standard_normal((m, n)) * 0.1).astype(np.float32)
+    dy_img = dev.encode(dy, vq.fit_codebook(dy, group=32), group=32)
+    del x, dy
+    results = {}
+    for name, a, flags, nn in (("forward", x_img, 0, n), ("backward", dy_img, 2, k)):
+        kk = k if flags == 0 else n
+        arrays = (a.codes, a.codebook, w_img.codes, w_img.codebook)
+        bufs = [device.buffer(arr.nbytes) for arr in arrays]
+        for b, arr in zip(bufs, arrays):
+            b.upload(arr)
+        out = device.buffer(m * nn * 4)
+        status = device.buffer(4)
+        status.upload(np.zeros(1, np.uint32))
+        words = (2, m, nn, kk, 32, 16, flags, 0)
+        try:
+            log(f"timing {name}: {m}x{nn}x{kk}, path {dev.path_name(words)}")
+            ms = timed(device, lambda: dev.run(words, bufs, out, status), steps, warmup)
+            flags_out = int(status.download(np.uint32)[0])
+            sample = out.download(np.float32).reshape(m, nn)[:8]
+        finally:
+            for b in bufs + [out, status]:
+                b.free()
+        if flags_out:
+            raise SystemExit(f"status word {flags_out} after the {name} launches")
+        a_dense = a.decode()[:8].astype(np.float64)
+        wd = w_img.decode().astype(np.float64)
+        ref = a_dense @ (wd if flags == 0 else wd.T)
+        err = float(np.max(np.abs(sample - ref)) / np.max(np.abs(ref)))
+        flop = 2.0 * m * nn * kk
+        results[name] = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "path": dev.path_name(words),
+                         "max_rel_first_rows": err}
+    return results
+
+
+def cpu_baseline(x_img, w_img, budget_s=10.0):
+    """The oracle's numpy CPU path for config 3: decode + matmul per matrix."""
+    from oracle import vq4_numpy as o
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()
+                       if i.get("user_api") == "blas"), default=1)
+    except Exception:  # pragma: no cover - threadpoolctl is optional
+        threads = os.cpu_count() or 1
+    x = o.decode(x_img.codes, x_img.codebook, 4096, 16).reshape(1, 4096)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        wd = o.decode(w_img.codes, w_img.codebook, 4096 * 4096, 16).reshape(4096, 4096)
+        _ = x @ wd
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 1000:
+            break
+    per = float(np.median(times))
+    return {"value": W_BYTES / per / 1e9, "unit": "GB/s", "cores": int(threads), "kind": "port",
+            "sample": f"{len(times)} matrices of config 3 (numpy gather decode of the 4096x4096 "
+                      f"g16 weight + numpy matmul with a 1x4096 row), median {per * 1e3:.1f} ms "
+                      f"per matrix; BLAS threads {threads}, os.cpu_count {os.cpu_count()}"}
+
+
+def load_traffic():
+    path = ROOT / "profiles" / "gemv_bins_config3_traffic.json"
+    if path.is_file():
+        try:
+            return json.loads(path.read_text()).get("traffic_bytes_per_launch")
+        except ValueError:
+            return None
+    return None
+
+
+def main(argv=None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--items", type=int, default=1024)
+    parser.add_argument("--no-prefill", action="store_true")
+    parser.add_argument("--no-cpu", action="store_true")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
+              "(the vq4 path is single-device; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        return 2
+    from alelyon_compute_kit import ack, vq
+    with ack.Device() as device:
+        dev = vq.VQDevice(device)
+        log("device", device.name)
+        gemv = bench_gemv(device, dev, args.items, args.steps, args.warmup)
+        prefill = None if args.no_prefill else bench_prefill(device, dev, max(3, args.steps // 4),
+                                                              1)
+    gbs = args.items * W_BYTES / (gemv["ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "vq4 packed matmul: packed-weight GB/s (% HBM peak) at M=1; TFLOP/s at M=2048",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gemv["ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 (u4 codes)",
+        "data": "synthetic: seeded N(0,0.02^2) weight and N(0,1) activation, vq4-encoded on the "
+                "GPU; R byte-distinct relabellings of the weight",
+        "config": {"workload": "config 3: decode-shaped GEMV, W 4096x4096 g16, M=1, cache-cold "
+                               f"batch of {args.items} packed weights per launch",
+                   "items": args.items, "m": 1, "n": 4096, "k": 4096, "group": 16,
+                   "path": gemv["path"], "hbm_fraction": round(gbs / HBM_PEAK_GBS, 4),
+                   "single_matrix_us": round(gemv["single_ms"] * 1e3, 3),
+                   "max_rel_vs_oracle": gemv["max_rel"]},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic()},
+    }
+    if prefill:
+        line["extra"] = {"prefill": {
+            "workload": "config 4: X 2048x4096 . W 4096x14336 g32 (forward), dY 2048x14336 . W^T "
+                        "(backward)",
+            **{f"{k}_{f}": (round(v[f], 4) if isinstance(v[f], float) else v[f])
+               for k, v in prefill.items() for f in v},
+            "roofline": {"bound": "mfma", "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "achieved": round(min(v["tflops"] for v in prefill.values()), 3),
+                         "frac": round(min(v["tflops"] for v in prefill.values())
+                                       / FP32_MFMA_PEAK_TFLOPS, 4)}}}
+    if not args.no_cpu:
+        log("timing the CPU baseline")
+        line["cpu_baseline"] = cpu_baseline(gemv["x_img"], gemv["w_img"])
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,182 @@
+/*
+ * ack_vq.h -- C ABI of the MI355X (gfx950) vq4/v1 library, libackvq.so.
+ *
+ * vq4/v1 stores one 4-bit index per group of 8, 16 or 32 FP32 values, eight
+ * indices per little-endian u32 word (vector v in word v/8, bits 4*(v%8)),
+ * with one 16-entry FP32 codebook (16 x group values) per tensor.
+ *
+ * The first block of entry points is the drop-in surface: each one replaces
+ * the reference entry of the same name in
+ * src/alelyon_compute_kit/_kit/src/ffi.rs and keeps its argument meaning,
+ * check order, return codes and refusal messages. Handles are registry ids,
+ * never dereferenced: a device handle is a process-wide counter value, a
+ * buffer handle is (device id << 32) | sequence (ffi.rs:10-24).
+ *
+ * ACK_OK from ack_vq means the work was enqueued on the device's stream, not
+ * that it finished (ffi.rs:46-60). ack_download is a synchronisation point:
+ * download the status word before trusting any output.
+ *
+ * The second block holds extensions with no reference counterpart; each says
+ * who it is for.
+ */
+#ifndef ACK_VQ_H
+#define ACK_VQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct AckDevice AckDevice; /* opaque; the pointer value is an id */
+typedef struct AckBuffer AckBuffer; /* opaque; the pointer value is an id */
+
+/* Return codes, values as ffi.rs:726-760. ACK_ERR_DEVICE is the reference's
+ * ACK_ERR_VULKAN: a failure reported by the device runtime (HIP here). */
+#define ACK_OK 0
+#define ACK_ERR_NULL (-1)
+#define ACK_ERR_DEVICE (-2)
+#define ACK_ERR_SHAPE (-3)
+#define ACK_ERR_SIZE (-4)
+#define ACK_ERR_LIVE_BUFFERS (-5)
+#define ACK_ERR_CLOSED (-6)
+#define ACK_ERR_FOREIGN (-7)
+#define ACK_ERR_FREED (-8)
+#define ACK_ERR_ABI (-9)
+#define ACK_ERR_POISONED (-10)
+#define ACK_ERR_UNSUPPORTED_OP (-11)
+
+/* Status-word bits written by every vq kernel (vq4.comp:4-7). */
+#define ACK_VQ_STATUS_NONFINITE 1u
+#define ACK_VQ_STATUS_LAYOUT 2u
+#define ACK_VQ_STATUS_OPTIMIZER 4u
+
+#define ACK_VQ_PLAN_BYTES 32
+
+/* ---- drop-in surface ---------------------------------------------------- */
+
+/* Replaces ack_vq_schema (ffi.rs:6004-6009). Returns 1. */
+uint32_t ack_vq_schema(void);
+
+/* Replaces ack_vq (ffi.rs:6037-6151). plan = 8 LE u32
+ * [op, m, n, k, group, 16, flags, 0]; op 0 encode, 1 decode, 2 packed-pair
+ * matmul (flags bit0: A stored (k,m); bit1: B stored (n,k)), 3 AdamW from
+ * four packed states into dense [W'|M'|V'] scratch. Check order: null plan
+ * (-1), plan length (-4), plan words (-3/-4), device (-1/-6), poisoned
+ * (-10), six handles (-1/-7/-8), capacities/aliases/grid (-4/-3), launch. */
+int32_t ack_vq(const AckDevice* dev, const AckBuffer* b0, const AckBuffer* b1,
+               const AckBuffer* b2, const AckBuffer* b3, const AckBuffer* out,
+               const AckBuffer* status, const uint8_t* plan, size_t plan_len);
+
+/* Replaces ack_open (ffi.rs:2037). Opens the HIP device ACK_DEVICE names
+ * ("gpu:<n>", default gpu:0). Null with ack_last_error set on failure. */
+AckDevice* ack_open(void);
+
+/* Replaces ack_close (ffi.rs:2365-2401). ACK_ERR_LIVE_BUFFERS while buffers
+ * are allocated on the device. */
+int32_t ack_close(AckDevice* dev);
+
+/* Replaces ack_device_name (ffi.rs:3296-3318). */
+int32_t ack_device_name(const AckDevice* dev, char* out, size_t len);
+
+/* Replaces ack_last_error (ffi.rs:3325-3339): this thread's last message. */
+int32_t ack_last_error(char* out, size_t len);
+
+/* Replaces ack_buffer_alloc (ffi.rs:3345-3375): device memory of `bytes`
+ * (> 0); null with ack_last_error set on failure. */
+AckBuffer* ack_buffer_alloc(const AckDevice* dev, uint64_t bytes);
+
+/* Replaces ack_buffer_free (ffi.rs:3413-3441). */
+int32_t ack_buffer_free(const AckDevice* dev, AckBuffer* buf);
+
+/* Replaces ack_upload (ffi.rs:3477-3511): len must equal the buffer size. */
+int32_t ack_upload(const AckDevice* dev, const AckBuffer* buf, const uint8_t* data, size_t len);
+
+/* Replaces ack_download (ffi.rs:3525-3569): len must equal the buffer size;
+ * waits for every operation enqueued on the device before copying. */
+int32_t ack_download(const AckDevice* dev, const AckBuffer* buf, uint8_t* data, size_t len);
+
+/* ---- extensions (no counterpart in the reference) ----------------------- */
+
+/* Host-only admission query for bindings and tests, which cannot reach the
+ * reference's Rust VqPlan: fills the six required byte counts, the work-item
+ * count and the reference grid for `plan`. bounds 0 = this library's
+ * multiply-add bound (2^38), 1 = the reference's scalar-shader bound (2^28).
+ * Returns ack_vq's code for a refused plan, with the same message. Any
+ * output pointer may be null. */
+int32_t ack_vq_plan_query(const uint8_t* plan, size_t plan_len, uint32_t bounds,
+                          uint64_t* required_bytes6, uint32_t* work_items,
+                          uint32_t* dispatch3);
+
+/* Host-only buffer admission, for the same callers: the reference's
+ * validate_buffers on caller-supplied capacities and ids. */
+int32_t ack_vq_plan_check_buffers(const uint8_t* plan, size_t plan_len,
+                                  const uint64_t* capacities6, const uint64_t* ids6);
+
+/* Batched ack_vq for callers that hold many equally shaped tensors (an
+ * expert bank): `count` independent instances of `plan` in one launch. Slot
+ * i holds `count` back-to-back images, each of the plan's required_bytes[i];
+ * `out` likewise; one status word collects every instance's bits. Same check
+ * order and codes as ack_vq, capacities scaled by `count` (count >= 1). */
+int32_t ack_vq_batch(const AckDevice* dev, const AckBuffer* b0, const AckBuffer* b1,
+                     const AckBuffer* b2, const AckBuffer* b3, const AckBuffer* out,
+                     const AckBuffer* status, const uint8_t* plan, size_t plan_len,
+                     uint32_t count);
+
+/* One fused VQAdamW step for VQAdamW.step on this library (vq.py:388-410):
+ * the op-3 inputs (b0 = codes of W, M, V, G back to back; b1 = their four
+ * books; b2 = seven FP32 coefficients; plan = the op-3 plan) are decoded and
+ * updated per element exactly as op 3 computes them, but no dense scratch is
+ * written. Instead: AdamW is evaluated at fit_codebook's strided sample of
+ * whole vectors, each of W', M', V' gets a codebook from the host fit warm-
+ * started from its current book (vq.py:182-229, `iterations` and
+ * `sample_vectors` as there; the whole-tensor keep pass runs on the device),
+ * and a second device pass recomputes every element and encodes it against
+ * its new book (op 0's FP32 rule) straight into `out_codes` (3 x words(m)
+ * u32: W', M', V'). `out_books` receives the three books (3 x 16 x group
+ * FP32), `changed` (one u32) the number of W values whose decoded value
+ * differs from the old W's. Synchronous: returns after the device finished.
+ * Status bits as op 3 and op 0; a nonzero status means the outputs must be
+ * discarded. Both write slots and the status word must be distinct buffers
+ * that alias no input. */
+int32_t ack_vq_adamw_step(const AckDevice* dev, const AckBuffer* b0, const AckBuffer* b1,
+                          const AckBuffer* b2, const AckBuffer* out_codes,
+                          const AckBuffer* out_books, const AckBuffer* changed,
+                          const AckBuffer* status, const uint8_t* plan, size_t plan_len,
+                          uint32_t iterations, uint32_t sample_vectors);
+
+/* Stream timer for benchmarks: phase 0 records a start event on the device
+ * stream, phase 1 records a stop event, waits for it and writes the elapsed
+ * milliseconds to *ms_out. */
+int32_t ack_stream_timer(const AckDevice* dev, uint32_t phase, float* ms_out);
+
+/* Wait for every operation enqueued on the device. */
+int32_t ack_sync(const AckDevice* dev);
+
+/* Name of the kernel path ack_vq would take for `plan` on this library
+ * (for tests that must know a fast path ran). */
+int32_t ack_vq_path_name(const uint8_t* plan, size_t plan_len, char* out, size_t len);
+
+/* Path policy for one device: 0 = automatic, 1 = the general tiled kernel
+ * for every matmul (a second implementation to cross-check fast paths). */
+int32_t ack_vq_set_policy(const AckDevice* dev, uint32_t policy);
+
+/* CPU reference encode (vq.py:154-179): nearest entry by float64 squared
+ * distance, lowest index on ties, the final partial vector compared on its
+ * valid values only. codes_out receives words(m) u32. */
+int32_t ack_vq_host_encode(const float* values, uint64_t m, const float* book, uint32_t group,
+                           uint32_t* codes_out);
+
+/* Codebook calibration (vq.py:182-257): bounded Lloyd on a strided sample
+ * with farthest-point reseed and the warm-start keep rule. init may be null.
+ * book_out receives 16 x group FP32. */
+int32_t ack_vq_host_fit_codebook(const float* values, uint64_t m, uint32_t group,
+                                 uint32_t iterations, uint32_t sample_vectors,
+                                 const float* init, float* book_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ACK_VQ_H */

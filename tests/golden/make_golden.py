@@ -1,0 +1,207 @@
+"""Write the golden vectors in this directory from the reference's own Python.
+
+Run in the build container only, where the reference is mounted:
+
+    PYTHONPATH=/root/reference/src python tests/golden/make_golden.py
+
+It imports the reference's CPU functions -- ``encode``, ``fit_codebook``,
+``VQArray``, ``VQAdamW`` (src/alelyon_compute_kit/_kit/python/vq.py) and
+``ExpertBank.initialize_expert`` (_kit/python/expert_bank.py:357-390) -- the
+functions no closed form or known-answer test pins bit for bit, and records
+their inputs and outputs as .npz fixtures (no pickles). Nothing under
+/root/reference is needed, read or copied at test time.
+"""
+from __future__ import annotations
+
+import math
+import sys
+import tempfile
+from pathlib import Path
+
+import numpy as np
+
+OUT = Path(__file__).resolve().parent
+
+try:
+    from alelyon_compute_kit._kit.python import expert_bank as ref_bank
+    from alelyon_compute_kit._kit.python import vq as ref_vq
+except ImportError as exc:  # pragma: no cover - build container only
+    sys.exit(f"the reference is not importable ({exc}); set PYTHONPATH=/root/reference/src")
+
+if not str(Path(ref_vq.__file__)).startswith("/root/reference/"):
+    sys.exit(f"refusing to record fixtures from {ref_vq.__file__}: not the reference")
+
+
+def encode_cases() -> dict:
+    rng = np.random.default_rng(20261201)
+    out = {}
+    n = 0
+    for group in (8, 16, 32):
+        for m in (1, group - 1, group, 8 * group + 3, 1000, 4096 + 5):
+            x = rng.standard_normal(m).astype(np.float32)
+            book = rng.standard_normal((16, group)).astype(np.float32)
+            img = ref_vq.encode(x, book, group=group)
+            out[f"c{n}_x"], out[f"c{n}_book"] = x, book
+            out[f"c{n}_group"] = np.array(group)
+            out[f"c{n}_codes"] = img.codes
+            n += 1
+        # exact ties: every value equals the midpoint of entries 3 and 9
+        book = rng.standard_normal((16, group)).astype(np.float32)
+        book[9] = book[3] + np.float32(2.0)
+        x = np.tile(book[3] + np.float32(1.0), 40).astype(np.float32)
+        img = ref_vq.encode(x, book, group=group)
+        out[f"c{n}_x"], out[f"c{n}_book"] = x, book
+        out[f"c{n}_group"] = np.array(group)
+        out[f"c{n}_codes"] = img.codes
+        n += 1
+    out["count"] = np.array(n)
+    return out
+
+
+def review_shape(group, rare_at=-1):
+    """The reference test's 65,536-value construction
+    (tests/test_fit_codebook_keeps_every_entry.py:245-250)."""
+    vectors = 65536 // group
+    atoms = np.random.default_rng(1).standard_normal((16, group)).astype(np.float32)
+    index = np.insert(np.arange(vectors - 1) % 15, rare_at % vectors, 15)
+    return atoms, index
+
+
+def fit_cases() -> dict:
+    rng = np.random.default_rng(7)
+    cases = []
+    for group in (8, 16, 32):
+        x = rng.standard_normal(1200 * group + 5).astype(np.float32)
+        cases.append(dict(values=x, group=group, iterations=4, sample_vectors=4096, init=None))
+        cases.append(dict(values=x, group=group, iterations=2, sample_vectors=64, init=None))
+        init = rng.standard_normal((16, group)).astype(np.float32)
+        cases.append(dict(values=x, group=group, iterations=4, sample_vectors=256, init=init))
+    # occupancy patterns with exact duplicates (tests/test_fit_codebook_keeps_every_entry.py:43-48)
+    atoms = np.random.default_rng(1).standard_normal((16, 16))
+    for counts in ([64] * 16, [120] * 8 + [8] * 8,
+                   [max(1, int(512 * 0.55 ** i)) for i in range(16)], [900] + [4] * 15):
+        sample = np.repeat(atoms, counts, axis=0).astype(np.float32)
+        cases.append(dict(values=sample.reshape(-1), group=16, iterations=4,
+                          sample_vectors=4096, init=None))
+    cases.append(dict(values=np.ones(512 * 16, dtype=np.float32), group=16, iterations=4,
+                      sample_vectors=4096, init=None))
+    # warm start whose whole-tensor pass keeps an entry the sample misses
+    atoms8, index = review_shape(8, rare_at=1)
+    cases.append(dict(values=atoms8[index].reshape(-1), group=8, iterations=4,
+                      sample_vectors=4096, init=atoms8))
+    # warm start from a zero book (a fresh optimizer's moments)
+    cases.append(dict(values=(rng.standard_normal(5000 * 8) * 1e-3).astype(np.float32),
+                      group=8, iterations=4, sample_vectors=4096,
+                      init=np.zeros((16, 8), dtype=np.float32)))
+    out = {}
+    stored = []
+    for i, c in enumerate(cases):
+        book = ref_vq.fit_codebook(c["values"], group=c["group"], iterations=c["iterations"],
+                                   sample_vectors=c["sample_vectors"], init=c["init"])
+        # inputs shared between cases are stored once; c{i}_values_ref names the copy
+        same = [j for j, v in stored if v is c["values"]]
+        if same:
+            out[f"c{i}_values_ref"] = np.array(same[0])
+        else:
+            out[f"c{i}_values"] = c["values"]
+            stored.append((i, c["values"]))
+        out[f"c{i}_group"] = np.array(c["group"])
+        out[f"c{i}_iterations"] = np.array(c["iterations"])
+        out[f"c{i}_sample_vectors"] = np.array(c["sample_vectors"])
+        out[f"c{i}_init"] = (np.zeros((0,), np.float32) if c["init"] is None
+                             else np.asarray(c["init"], np.float32))
+        out[f"c{i}_book"] = book
+    out["count"] = np.array(len(cases))
+    return out
+
+
+def config1() -> dict:
+    """256x256 N(0,1) seed 0, group 16, fit -> encode; x
+    1x256 N(0,1) seed 1 fitted and encoded."""
+    w = np.random.default_rng(0).standard_normal((256, 256)).astype(np.float32)
+    book = ref_vq.fit_codebook(w, group=16)
+    img = ref_vq.encode(w, book, group=16)
+    x = np.random.default_rng(1).standard_normal((1, 256)).astype(np.float32)
+    x_img = ref_vq.encode(x, ref_vq.fit_codebook(x, group=16), group=16)
+    return {"w": w, "w_image": np.frombuffer(img.to_bytes(), dtype=np.uint8),
+            "x": x, "x_image": np.frombuffer(x_img.to_bytes(), dtype=np.uint8),
+            "w_decoded": img.decode(), "x_decoded": x_img.decode()}
+
+
+def expert_payloads() -> dict:
+    out = {}
+    with tempfile.TemporaryDirectory() as tmp:
+        bank = ref_bank.ExpertBank.create(
+            Path(tmp) / "c2", ref_bank.BankConfig(1, 1, ((128, 128),) * 3, 16))
+        bank.initialize_expert(0, 0, seed=7)
+        for i, t in enumerate(bank.read_expert_state(0, 0).tensors):
+            out[f"c2_{i}_codes"], out[f"c2_{i}_book"] = t.codes, t.codebook
+        bank = ref_bank.ExpertBank.create(
+            Path(tmp) / "h", ref_bank.BankConfig(1, 1, ((4, 3), (4, 3), (4, 3)), 8))
+        bank.initialize_expert(0, 0, seed=4, zero_optimizer_state=True)
+        for i, t in enumerate(bank.read_expert_state(0, 0).tensors):
+            out[f"h_{i}_codes"], out[f"h_{i}_book"] = t.codes, t.codebook
+    return out
+
+
+class _Float32Backend:
+    """A host backend whose AdamW is vq4.comp's arithmetic in numpy float32
+    (every operation rounded, in the shader's order) and whose encode is the
+    reference's CPU encode. Used to record VQAdamW.step end to end."""
+
+    def encode(self, values, codebook, *, group):
+        return ref_vq.encode(values, codebook, group=group)
+
+    def decode(self, value):
+        return value.decode()
+
+    def adamw(self, weight, momentum, variance, gradient, *, lr, beta1, beta2, eps,
+              weight_decay, step):
+        f = np.float32
+        c = np.array([lr, beta1, beta2, eps, weight_decay, 1 - beta1 ** step,
+                      1 - beta2 ** step], dtype=np.float32)
+        w, m, v, g = (s.decode() for s in (weight, momentum, variance, gradient))
+        nm = c[1] * m + (f(1) - c[1]) * g
+        nv = c[2] * v + (f(1) - c[2]) * (g * g)
+        cm, cv = nm / c[5], nv / c[6]
+        den = np.sqrt(cv) + c[3]
+        nw = w * (f(1) - c[0] * c[4]) - c[0] * cm / den
+        return nw.astype(np.float32), nm.astype(np.float32), nv.astype(np.float32)
+
+
+def vqadamw_steps() -> dict:
+    rng = np.random.default_rng(11)
+    out = {}
+    for i, (shape, group) in enumerate((((64, 48), 16), ((40, 40), 8), ((3000, 32), 32))):
+        w = (rng.standard_normal(shape) * 0.05).astype(np.float32)
+        weight = ref_vq.encode(w, ref_vq.fit_codebook(w, group=group), group=group)
+        opt = ref_vq.VQAdamW(_Float32Backend(), weight, lr=1e-3, betas=(0.9, 0.999),
+                             eps=1e-8, weight_decay=0.01)
+        out[f"s{i}_group"] = np.array(group)
+        out[f"s{i}_shape"] = np.array(shape)
+        out[f"s{i}_w0_codes"], out[f"s{i}_w0_book"] = weight.codes, weight.codebook
+        for step in range(2):
+            g = (rng.standard_normal(shape) * 1e-2).astype(np.float32)
+            g_img = ref_vq.encode(g, ref_vq.fit_codebook(g, group=group), group=group)
+            out[f"s{i}_g{step}_codes"], out[f"s{i}_g{step}_book"] = g_img.codes, g_img.codebook
+            report = opt.step(g_img)
+            out[f"s{i}_changed{step}"] = np.array(report["changed_weight_values"])
+            for name, state in (("w", opt.weight), ("m", opt.momentum), ("v", opt.variance)):
+                out[f"s{i}_{name}{step + 1}_codes"] = state.codes
+                out[f"s{i}_{name}{step + 1}_book"] = state.codebook
+    return out
+
+
+def main() -> int:
+    np.savez_compressed(OUT / "encode_cpu.npz", **encode_cases())
+    np.savez_compressed(OUT / "fit_codebook.npz", **fit_cases())
+    np.savez_compressed(OUT / "config1.npz", **config1())
+    np.savez_compressed(OUT / "expert_payloads.npz", **expert_payloads())
+    np.savez_compressed(OUT / "vqadamw_steps.npz", **vqadamw_steps())
+    for p in sorted(OUT.glob("*.npz")):
+        print(p.name, p.stat().st_size)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

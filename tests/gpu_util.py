@@ -1,0 +1,54 @@
+"""Helpers for GPU tests: run one plan on resident buffers and return both
+the output and the status word (VQDevice raises on a nonzero status before
+downloading the output)."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+
+
+def say(*parts) -> None:
+    print("[gpu case]", *parts, flush=True)
+    sys.stdout.flush()
+
+
+def run_plan(vqdev, words, arrays, out_bytes, out_dtype, *, count=1, fill=0):
+    """Upload `arrays`, run `words` (ack_vq, or ack_vq_batch when count > 1),
+    download (output, status). The output buffer starts filled with `fill`
+    bytes so unwritten elements are recognisable."""
+    from alelyon_compute_kit import ack
+    device = vqdev.device
+    bufs = []
+    try:
+        for a in arrays:
+            b = device.buffer(a.nbytes)
+            bufs.append(b)
+            b.upload(a)
+        out = device.buffer(out_bytes)
+        bufs.append(out)
+        out.upload(np.full(out_bytes, fill, dtype=np.uint8))
+        status = device.buffer(4)
+        bufs.append(status)
+        status.upload(np.zeros(1, np.uint32))
+        vqdev.run(words, bufs[:len(arrays)], out, status, count=count)
+        flags = int(status.download(np.uint32)[0])
+        return out.download(out_dtype), flags
+    finally:
+        for b in bufs:
+            try:
+                b.free()
+            except ack.AckError:
+                pass
+
+
+def image(rng, m, group, scale=1.0):
+    """Random codes (tail nibbles zero) and a normal codebook."""
+    vectors = -(-m // group)
+    idx = rng.integers(0, 16, vectors).astype(np.uint32)
+    words = np.zeros(-(-vectors // 8), np.uint32)
+    for lane in range(8):
+        part = idx[lane::8]
+        words[:part.size] |= part << np.uint32(4 * lane)
+    book = (rng.standard_normal((16, group)) * scale).astype(np.float32)
+    return words, book

@@ -1,0 +1,87 @@
+"""The fused VQAdamW step on the GPU (ack_vq_adamw_step) against the same
+step composed from op 3, the native fit and the GPU encode -- the sequence
+the reference's VQAdamW.step runs (vq.py:388-410). Both must reach identical
+images and the same changed-weight count."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+
+class Unfused:
+    """VQDevice's adamw and encode, without the fused entry: VQAdamW then
+    takes the reference's unfused sequence."""
+
+    def __init__(self, vqdev):
+        self.vqdev = vqdev
+
+    def adamw(self, *args, **kwargs):
+        return self.vqdev.adamw(*args, **kwargs)
+
+    def encode(self, values, codebook, *, group):
+        return self.vqdev.encode(values, codebook, group=group)
+
+    def decode(self, value):
+        return self.vqdev.decode(value)
+
+
+def _weight(rng, shape, group, scale=0.05):
+    from alelyon_compute_kit import vq
+    w = (rng.standard_normal(shape) * scale).astype(np.float32)
+    return vq.encode(w, vq.fit_codebook(w, group=group), group=group)
+
+
+@pytest.mark.parametrize("shape,group", [((64, 48), 16), ((40, 40), 8), ((3000, 32), 32),
+                                         ((512, 512), 8), ((1000, 77), 16)])
+def test_fused_step_equals_the_unfused_sequence(vqdev, shape, group):
+    from alelyon_compute_kit import vq
+    rng = np.random.default_rng(group + shape[0])
+    weight = _weight(rng, shape, group)
+    fused = vq.VQAdamW(vqdev, weight, lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01)
+    plain = vq.VQAdamW(Unfused(vqdev), weight, lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01)
+    for step in range(3):
+        g = (rng.standard_normal(shape) * 1e-2).astype(np.float32)
+        grad = vq.encode(g, vq.fit_codebook(g, group=group), group=group)
+        say("adamw step", shape, group, step)
+        r1 = fused.step(grad)
+        r2 = plain.step(grad)
+        assert r1["changed_weight_values"] == r2["changed_weight_values"]
+        for a, b in ((fused.weight, plain.weight), (fused.momentum, plain.momentum),
+                     (fused.variance, plain.variance)):
+            np.testing.assert_array_equal(a.codebook, b.codebook)
+            np.testing.assert_array_equal(a.codes, b.codes)
+
+
+@pytest.mark.parametrize("group,rare_at", [(8, -1), (16, -1), (32, -1), (8, 1)])
+def test_zero_gradient_moves_no_weight_on_the_gpu(vqdev, group, rare_at):
+    from alelyon_compute_kit import vq
+    vectors = 65536 // group
+    atoms = np.random.default_rng(1).standard_normal((16, group)).astype(np.float32)
+    index = np.insert(np.arange(vectors - 1) % 15, rare_at % vectors, 15)
+    values = atoms[index].reshape(-1)
+    weight = vq.encode(values, atoms, group=group)
+    zero = vq.VQArray(weight.shape, group, np.zeros_like(weight.codes),
+                      np.zeros((16, group), np.float32))
+    opt = vq.VQAdamW(vqdev, weight, lr=1e-3, weight_decay=0.0)
+    say("zero gradient", group, rare_at)
+    report = opt.step(zero)
+    assert report["changed_weight_values"] == 0
+    assert np.array_equal(opt.weight.decode(), values)
+    assert len(np.unique(opt.weight.codebook.round(6), axis=0)) == 16
+
+
+def test_fused_step_refuses_bad_coefficients_and_keeps_state(vqdev):
+    from alelyon_compute_kit import ack, vq
+    rng = np.random.default_rng(3)
+    weight = _weight(rng, (64, 64), 16)
+    variance = vq.VQArray(weight.shape, 16, weight.codes, -np.abs(weight.codebook) - 1)
+    opt = vq.VQAdamW(vqdev, weight)
+    opt.variance = variance
+    say("adamw step negative variance")
+    with pytest.raises(ack.AckError, match="status=4"):
+        opt.step(weight)
+    assert opt.steps == 0 and opt.weight is weight

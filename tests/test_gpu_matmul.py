@@ -1,0 +1,166 @@
+"""GPU parity of the packed-pair product (op 2).
+
+The general kernel keeps the shader's per-output order and must equal the
+oracle bit for bit; the codebook-factorised paths reorder the sum and must
+lie within the north star's FP32 tolerance: max|y - y_ref| / max|y_ref| <=
+1e-5, against both the oracle and a float64 product of the decoded operands.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gpu_util import image, run_plan, say
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _operands(rng, m, n, k, group, a_scale=1.0, b_scale=1.0):
+    a_codes, a_book = image(rng, m * k, group, a_scale)
+    b_codes, b_book = image(rng, k * n, group, b_scale)
+    return a_codes, a_book, b_codes, b_book
+
+
+def _dense(codes, book, count, shape, group):
+    from oracle import vq4_numpy as o
+    return o.decode(codes, book, count, group).reshape(shape)
+
+
+def _ref64(ops, m, n, k, group, flags):
+    from oracle import vq4_numpy as o
+    a_codes, a_book, b_codes, b_book = ops
+    a = _dense(a_codes, a_book, m * k, (k, m) if flags & 1 else (m, k), group)
+    b = _dense(b_codes, b_book, k * n, (n, k) if flags & 2 else (k, n), group)
+    return o.matmul64(a, b, bool(flags & 1), bool(flags & 2))
+
+
+def _gpu(vqdev, ops, m, n, k, group, flags, count=1):
+    out, status = run_plan(vqdev, (2, m, n, k, group, 16, flags, 0), ops, 4 * m * n * count,
+                           np.float32, count=count)
+    return out.reshape(count, m, n) if count > 1 else out.reshape(m, n), status
+
+
+@pytest.fixture
+def general(device):
+    device.set_policy(1)
+    yield
+    device.set_policy(0)
+
+
+GENERAL_SHAPES = [(3, 5, 7, 8), (37, 53, 96, 16), (64, 64, 64, 32), (1, 256, 256, 16),
+                  (130, 70, 33, 8)]
+
+
+@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+def test_general_kernel_is_bit_identical_to_the_shader(vqdev, oracle, general, flags):
+    rng = np.random.default_rng(flags)
+    for m, n, k, group in GENERAL_SHAPES:
+        say("general", m, n, k, group, flags)
+        ops = _operands(rng, m, n, k, group)
+        out, status = _gpu(vqdev, ops, m, n, k, group, flags)
+        ref, ref_status = oracle.matmul(*ops, m, n, k, group, flags)
+        np.testing.assert_array_equal(out.view(np.uint32), ref.view(np.uint32))
+        assert status == ref_status == 0
+
+
+def test_general_kernel_status_on_overflow(vqdev, oracle, general):
+    from oracle import vq4_numpy as o
+    codes = o.pack_indices(np.zeros(4, np.int64))
+    book = np.full((16, 8), 3e19, np.float32)
+    say("general overflow")
+    _, status = _gpu(vqdev, (codes, book, codes, book), 4, 4, 8, 8, 0)
+    assert status == oracle.matmul(codes, book, codes, book, 4, 4, 8, 8, 0)[1] == 1
+
+
+GEMV_SHAPES = [(256, 256, 16), (4096, 4096, 16), (512, 1024, 8), (1024, 768, 32),
+               (100, 512, 16), (3000, 2048, 8)]
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
+def test_gemv_bins_within_tolerance(vqdev, oracle, m):
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(50 + m)
+    for k, n, group in GEMV_SHAPES:
+        words = (2, m, n, k, group, 16, 0, 0)
+        assert vqdev.path_name(words) == "gemv-bins"
+        say("gemv-bins", m, k, n, group)
+        ops = _operands(rng, m, n, k, group, 1.0, 0.02)
+        out, status = _gpu(vqdev, ops, m, n, k, group, 0)
+        assert status == 0
+        if m * n * k <= 1 << 24:
+            ref, _ = oracle.matmul(*ops, m, n, k, group, 0)
+            assert o.max_rel(out, ref) <= TOL
+        assert o.max_rel(out, _ref64(ops, m, n, k, group, 0)) <= TOL
+
+
+def test_gemv_bins_transposed_a(vqdev, oracle):
+    """A stored (k, m): the activation decode follows the flat index."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(77)
+    for m, k, n, group in ((1, 256, 256, 16), (4, 200, 512, 8), (3, 96, 1024, 32)):
+        say("gemv-bins a^T", m, k, n, group)
+        ops = _operands(rng, m, n, k, group)
+        out, status = _gpu(vqdev, ops, m, n, k, group, 1)
+        ref, _ = oracle.matmul(*ops, m, n, k, group, 1)
+        assert status == 0 and o.max_rel(out, ref) <= TOL
+
+
+def test_gemv_bins_batched(vqdev, oracle):
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(88)
+    m, k, n, group, count = 1, 512, 512, 16, 6
+    items = [_operands(rng, m, n, k, group) for _ in range(count)]
+    ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
+    say("gemv-bins batch", count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    for i, it in enumerate(items):
+        ref, _ = oracle.matmul(*it, m, n, k, group, 0)
+        assert o.max_rel(out[i], ref) <= TOL
+
+
+def test_config1_matmul(vqdev, oracle):
+    """x (1x256) times W (256x256), group 16, both images
+    recorded from the reference."""
+    from alelyon_compute_kit import vq
+    from conftest import golden
+    from oracle import vq4_numpy as o
+    g = golden("config1.npz")
+    w = vq.VQArray.from_bytes(g["w_image"].tobytes())
+    x = vq.VQArray.from_bytes(g["x_image"].tobytes())
+    say("config1 matmul")
+    y = vqdev.matmul(x, w)
+    ref, _ = oracle.matmul(x.codes, x.codebook, w.codes, w.codebook, 1, 256, 256, 16, 0)
+    assert o.max_rel(y, ref) <= TOL
+    assert o.max_rel(y, g["x_decoded"].astype(np.float64) @ g["w_decoded"]) <= TOL
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_config3_decode_shaped_gemv(vqdev, m):
+    """BASELINE config 3 at full size: W 4096x4096 ~N(0, 0.02^2) fitted at
+    group 16, X m x 4096 ~N(0,1) fitted and encoded; forward only."""
+    from alelyon_compute_kit import vq
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((4096, 4096)) * 0.02).astype(np.float32)
+    w_img = vq.encode(w, vq.fit_codebook(w, group=16), group=16)
+    x = rng.standard_normal((m, 4096)).astype(np.float32)
+    x_img = vq.encode(x, vq.fit_codebook(x, group=16), group=16)
+    say("config3", m)
+    y = vqdev.matmul(x_img, w_img)
+    ref = x_img.decode().astype(np.float64) @ w_img.decode().astype(np.float64)
+    assert o.max_rel(y, ref) <= TOL
+
+
+def test_transposed_products_agree_with_float64(vqdev):
+    """dY . W^T and A^T . B at moderate size through the automatic path."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(99)
+    for m, n, k, group, flags in ((64, 96, 128, 32, 2), (33, 40, 64, 8, 1), (100, 64, 256, 16, 3)):
+        say("auto", m, n, k, group, flags)
+        ops = _operands(rng, m, n, k, group)
+        out, status = _gpu(vqdev, ops, m, n, k, group, flags)
+        assert status == 0
+        assert o.max_rel(out, _ref64(ops, m, n, k, group, flags)) <= TOL
