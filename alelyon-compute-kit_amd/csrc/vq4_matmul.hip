@@ -142,48 +142,84 @@ __global__ __launch_bounds__(kGThreads) void k_matmul_general(Operands o, uint32
 // Tile: kTileWords words of each B row (8 * kTileWords output groups), all m
 // rows of A, a slice of k. Lane (q = lane % 32, half = lane / 32) reads word
 // q of row 2*wave_row + half, so a wave reads two whole 128-byte tile rows.
+//
+// The bins are 32-bit fixed point: x is scaled by 2^s (s from the A
+// codebook's largest magnitude) and rounded to an integer once, when its
+// chunk is staged in LDS, and the bins are summed with integer LDS atomics
+// -- exact, and on gfx950 some thirty times the rate of FP32 LDS atomics.
+// Every kWindow rows the integer bins are flushed into FP32 accumulators
+// held in registers, which bounds |bin| < 2^30 (no overflow) while keeping
+// the rounding of x to 2^-s at most 2^-23 of the largest |x|.
 // Bins are laid out [r][nibble][e][q]: the 32 lanes of a half-wave hit 32
 // distinct banks for any codes.
 constexpr int kTileWords = 32;
 constexpr int kTileGroups = kTileWords * 8;
 constexpr int kBinThreads = 256;
 constexpr int kBinRowsPerPass = kBinThreads / 32;  // 8 rows per pass
-constexpr int kBinUnroll = 8;
+constexpr int kBinUnroll = 16;
 constexpr uint32_t kGemvMaxM = 8;
-constexpr uint32_t kChunk = 256;  // x rows staged in LDS at a time
+constexpr uint32_t kChunk = kBinRowsPerPass * kBinUnroll * 2;  // 256 x rows staged at a time
+constexpr uint32_t kWindow = 512;                               // rows per integer window
+constexpr int kBinsPerThread = 16 * kTileGroups / kBinThreads;  // 16 bins per M row
+
+// Byte offset of bin (nib, e, q) inside one M row's bins: e*128 + q*4 +
+// nib*2048, with the nibble taken straight from the word.
+template <int NIB>
+__device__ __forceinline__ uint32_t bin_byte(uint32_t w, uint32_t q4) {
+  constexpr int sh = 4 * NIB - 7;
+  const uint32_t e128 = (sh >= 0 ? (w >> (sh >= 0 ? sh : 0)) : (w << (sh < 0 ? -sh : 0))) & 0x780u;
+  return (e128 | q4) + NIB * 2048;
+}
 
 __device__ __forceinline__ uint32_t bin_index(uint32_t r, uint32_t nib, uint32_t e, uint32_t q) {
   return ((r * 8 + nib) * 16 + e) * kTileWords + q;
 }
 
 // x[r][kk] for rows r < m and inner rows [k0, kend), decoded from A by flat
-// index into sx[r * kChunk + kk].
+// index, scaled by 2^shift and rounded to int32 into sxq[r * kChunk + kk].
 template <int G, int M>
-__device__ void decode_a_chunk(const uint32_t* a_codes, const float* sa_book, uint32_t k,
-                               uint32_t flags, uint32_t k0, uint32_t kend, float* sx) {
+__device__ void stage_x_chunk(const uint32_t* a_codes, const float* sa_book, uint32_t k,
+                              uint32_t flags, uint32_t k0, uint32_t kend, int shift,
+                              int32_t* sxq) {
   for (uint32_t e = threadIdx.x; e < M * kChunk; e += blockDim.x) {
     const uint32_t r = e / kChunk, kk = e % kChunk;
     const uint32_t inner = k0 + kk;
-    float v = 0.0f;
+    int32_t v = 0;
     if (inner < kend) {
       const uint32_t flat = (flags & 1u) ? inner * M + r : r * k + inner;
-      v = sa_book[nibble(a_codes, flat / G) * G + flat % G];
+      v = int32_t(rintf(ldexpf(sa_book[nibble(a_codes, flat / G) * G + flat % G], shift)));
     }
-    sx[e] = v;
+    sxq[e] = v;
   }
 }
 
-// grid: (n tiles, k splits, instances). Dynamic shared memory: the bins
-// (M * 16 * kTileGroups floats) then one x chunk (M * kChunk floats).
+// Largest |value| of a 16 x G book, reduced over the block.
+template <int G>
+__device__ float book_absmax(const float* sbook, float* sred) {
+  float v = 0.0f;
+  for (uint32_t i = threadIdx.x; i < 16 * G; i += blockDim.x) v = fmaxf(v, fabsf(sbook[i]));
+  for (int off = 1; off < warpSize; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
+  if (threadIdx.x % warpSize == 0) sred[threadIdx.x / warpSize] = v;
+  __syncthreads();
+  float m = 0.0f;
+  for (uint32_t i = 0; i < blockDim.x / warpSize; ++i) m = fmaxf(m, sred[i]);
+  __syncthreads();
+  return m;
+}
+
+// grid: (n tiles, k splits, instances). Dynamic shared memory: the integer
+// bins (M * 16 * kTileGroups) then one x chunk (M * kChunk int32).
 template <int G, int M>
 __global__ __launch_bounds__(kBinThreads) void k_gemv_bins(Operands o, uint32_t n, uint32_t k,
                                                            uint32_t flags, uint32_t ks,
                                                            float* partial) {
-  extern __shared__ float smem[];
-  float* bins = smem;
-  float* sx = smem + M * 16 * kTileGroups;
+  extern __shared__ int32_t smem[];
+  int32_t* bins = smem;
+  int32_t* sxq = smem + M * 16 * kTileGroups;
+  float* fbins = reinterpret_cast<float*>(smem);
   __shared__ float sa_book[16 * G];
   __shared__ float sb_book[16 * G];
+  __shared__ float sred[kBinThreads / 64];
   const uint32_t tid = threadIdx.x;
   const uint32_t tile = blockIdx.x, split = blockIdx.y;
   const uint32_t row_words = n / (8 * G);
@@ -191,8 +227,10 @@ __global__ __launch_bounds__(kBinThreads) void k_gemv_bins(Operands o, uint32_t 
   const uint32_t kend = (k0 + ks) < k ? (k0 + ks) : k;
   const uint32_t lane = tid % 64, wave = tid / 64;
   const uint32_t q = lane % 32, half = lane / 32;
+  const uint32_t q4 = q * 4;
   const uint32_t word_col = tile * kTileWords + q;
   const bool live = word_col < row_words;
+  char* bin_bytes = reinterpret_cast<char*>(bins);
   for (uint32_t item = blockIdx.z; item < o.count; item += gridDim.z) {
     const uint32_t* a_codes = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
     const float* a_book = item_ptr<float>(o.in[1], o.stride[1], item);
@@ -203,37 +241,77 @@ __global__ __launch_bounds__(kBinThreads) void k_gemv_bins(Operands o, uint32_t 
       sa_book[i] = a_book[i];
       sb_book[i] = b_book[i];
     }
-    for (uint32_t i = tid; i < M * 16 * kTileGroups; i += kBinThreads) bins[i] = 0.0f;
+    for (uint32_t i = tid; i < M * 16 * kTileGroups; i += kBinThreads) bins[i] = 0;
     if (tile == 0 && split == 0) sweep_books(a_book, b_book, 16 * G, o.status);
+    __syncthreads();
+    // 2^shift * max|x| * kWindow < 2^30: no window sum can overflow int32.
+    const float xmax = book_absmax<G>(sa_book, sred);
+    int shift = 0;
+    if (xmax > 0.0f) {
+      int ex;
+      frexpf(xmax, &ex);  // xmax < 2^ex, so xmax * kWindow < 2^(ex + 9)
+      shift = 30 - (ex + 9);
+      shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
+    }
+    const float unscale = ldexpf(1.0f, -shift);
+    float acc[M][kBinsPerThread];
+#pragma unroll
+    for (int r = 0; r < M; ++r)
+#pragma unroll
+      for (int i = 0; i < kBinsPerThread; ++i) acc[r][i] = 0.0f;
     const uint32_t* col_codes = b_codes + word_col;
-    for (uint32_t kc = k0; kc < kend; kc += kChunk) {
-      const uint32_t kce = (kc + kChunk) < kend ? (kc + kChunk) : kend;
-      __syncthreads();
-      decode_a_chunk<G, M>(a_codes, sa_book, k, flags, kc, kce, sx);
-      __syncthreads();
-      for (uint32_t kb = kc; kb < kce; kb += kBinRowsPerPass * kBinUnroll) {
-        uint32_t w[kBinUnroll];
+    for (uint32_t kw = k0; kw < kend; kw += kWindow) {
+      const uint32_t kwe = (kw + kWindow) < kend ? (kw + kWindow) : kend;
+      for (uint32_t kc = kw; kc < kwe; kc += kChunk) {
+        const uint32_t kce = (kc + kChunk) < kwe ? (kc + kChunk) : kwe;
+        __syncthreads();
+        stage_x_chunk<G, M>(a_codes, sa_book, k, flags, kc, kce, shift, sxq);
+        __syncthreads();
+        for (uint32_t kb = kc; kb < kce; kb += kBinRowsPerPass * kBinUnroll) {
+          uint32_t w[kBinUnroll];
 #pragma unroll
-        for (int u = 0; u < kBinUnroll; ++u) {
-          const uint32_t row = kb + u * kBinRowsPerPass + wave * 2 + half;
-          w[u] = (live && row < kce) ? col_codes[uint64_t(row) * row_words] : 0u;
-        }
+          for (int u = 0; u < kBinUnroll; ++u) {
+            const uint32_t row = kb + u * kBinRowsPerPass + wave * 2 + half;
+            w[u] = (live && row < kce) ? col_codes[uint64_t(row) * row_words] : 0u;
+          }
 #pragma unroll
-        for (int u = 0; u < kBinUnroll; ++u) {
-          const uint32_t row = kb + u * kBinRowsPerPass + wave * 2 + half;
-          if (!live || row >= kce) continue;
-          float xr[M];
+          for (int u = 0; u < kBinUnroll; ++u) {
+            const uint32_t row = kb + u * kBinRowsPerPass + wave * 2 + half;
+            if (!live || row >= kce) continue;
 #pragma unroll
-          for (int r = 0; r < M; ++r) xr[r] = sx[r * kChunk + (row - kc)];
-#pragma unroll
-          for (uint32_t nib = 0; nib < 8; ++nib) {
-            const uint32_t e = (w[u] >> (4 * nib)) & 15u;
-#pragma unroll
-            for (int r = 0; r < M; ++r) atomicAdd(&bins[bin_index(r, nib, e, q)], xr[r]);
+            for (int r = 0; r < M; ++r) {
+              const int32_t xr = sxq[r * kChunk + (row - kc)];
+              char* base = bin_bytes + r * (16 * kTileGroups * 4);
+              const uint32_t ww = w[u];
+              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<0>(ww, q4)), xr);
+              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<1>(ww, q4)), xr);
+              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<2>(ww, q4)), xr);
+              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<3>(ww, q4)), xr);
+              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<4>(ww, q4)), xr);
+              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<5>(ww, q4)), xr);
+              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<6>(ww, q4)), xr);
+              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<7>(ww, q4)), xr);
+            }
           }
         }
       }
+      // flush the window: integer bins -> FP32 accumulators, bins reset
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < M; ++r)
+#pragma unroll
+        for (int i = 0; i < kBinsPerThread; ++i) {
+          const uint32_t b = r * 16 * kTileGroups + tid + i * kBinThreads;
+          acc[r][i] += float(bins[b]);
+          bins[b] = 0;
+        }
     }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < M; ++r)
+#pragma unroll
+      for (int i = 0; i < kBinsPerThread; ++i)
+        fbins[r * 16 * kTileGroups + tid + i * kBinThreads] = acc[r][i] * unscale;
     __syncthreads();
 
     // Finalise this tile: y[r][j*G+t] = sum_e C_B[e][t] * S[r][j][e].
@@ -247,65 +325,70 @@ __global__ __launch_bounds__(kBinThreads) void k_gemv_bins(Operands o, uint32_t 
         const uint32_t r = e / (groups * G);
         const uint32_t jt = e % (groups * G);
         const uint32_t j = jt / G, t = jt % G;
-        float acc = 0.0f;
+        float y = 0.0f;
 #pragma unroll
         for (uint32_t c = 0; c < 16; ++c)
-          acc = fmaf(sb_book[c * G + t], bins[bin_index(r, j % 8, c, j / 8)], acc);
-        out[uint64_t(r) * n + tile * kTileGroups * G + jt] = acc;
-        bad |= !finite_f32(acc);
+          y = fmaf(sb_book[c * G + t], fbins[bin_index(r, j % 8, c, j / 8)], y);
+        out[uint64_t(r) * n + tile * kTileGroups * G + jt] = y;
+        bad |= !finite_f32(y);
       }
       if (__any(bad) && (tid % warpSize) == 0) atomicOr(o.status, 1u);
     } else {
-      // partial[item][split][tile][r][j][e]
-      float* p = partial + ((uint64_t(item) * gridDim.y + split) * gridDim.x + tile) *
+      // partial[item][tile][split][r][j][e]
+      float* p = partial + ((uint64_t(item) * gridDim.x + tile) * gridDim.y + split) *
                                (M * 16 * kTileGroups);
       for (uint32_t e = tid; e < M * 16 * kTileGroups; e += kBinThreads) {
         const uint32_t r = e / (16 * kTileGroups);
         const uint32_t je = e % (16 * kTileGroups);
         const uint32_t j = je / 16, c = je % 16;
-        p[e] = bins[bin_index(r, j % 8, c, j / 8)];
+        p[e] = fbins[bin_index(r, j % 8, c, j / 8)];
       }
     }
   }
 }
 
-// Sum the split-k bins in split order, then apply the B codebook.
+// Sum the split-k bins in split order (one thread per bin), then apply the B
+// codebook. grid: (n tiles * kFinishParts, 1, instances); each block owns
+// kTileGroups / kFinishParts groups of one tile.
+constexpr uint32_t kFinishParts = 16;
+constexpr uint32_t kFinishGroups = kTileGroups / kFinishParts;  // 16 groups, 256 bins
+
 template <int G, int M>
 __global__ __launch_bounds__(256) void k_gemv_bins_finish(Operands o, uint32_t n, uint32_t splits,
                                                           uint32_t tiles, const float* partial) {
   __shared__ float sb_book[16 * G];
-  const uint32_t tile = blockIdx.x;
+  __shared__ float ssum[M][kFinishGroups * 16];
+  const uint32_t tile = blockIdx.x / kFinishParts, part = blockIdx.x % kFinishParts;
   const uint32_t row_words = n / (8 * G);
   const uint32_t groups = (row_words - tile * kTileWords) < kTileWords
                               ? (row_words - tile * kTileWords) * 8
                               : kTileGroups;
+  const uint32_t j0 = part * kFinishGroups;
+  if (j0 >= groups) return;
+  const uint32_t jn = (groups - j0) < kFinishGroups ? (groups - j0) : kFinishGroups;
   for (uint32_t item = blockIdx.z; item < o.count; item += gridDim.z) {
     const float* b_book = item_ptr<float>(o.in[3], o.stride[3], item);
     float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < 16 * G; i += blockDim.x) sb_book[i] = b_book[i];
+    const float* base = partial + (uint64_t(item) * tiles + tile) * splits * (M * 16 * kTileGroups);
+    for (uint32_t e = threadIdx.x; e < M * jn * 16; e += blockDim.x) {
+      const uint32_t r = e / (jn * 16), je = e % (jn * 16);
+      const float* p = base + r * 16 * kTileGroups + j0 * 16 + je;
+      float s = 0.0f;
+      for (uint32_t sp = 0; sp < splits; ++sp) s += p[uint64_t(sp) * (M * 16 * kTileGroups)];
+      ssum[r][je] = s;
+    }
     __syncthreads();
     bool bad = false;
-    for (uint32_t e = blockIdx.y * blockDim.x + threadIdx.x; e < M * groups * G;
-         e += gridDim.y * blockDim.x) {
-      const uint32_t r = e / (groups * G);
-      const uint32_t jt = e % (groups * G);
+    for (uint32_t e = threadIdx.x; e < M * jn * G; e += blockDim.x) {
+      const uint32_t r = e / (jn * G), jt = e % (jn * G);
       const uint32_t j = jt / G, t = jt % G;
-      float s[16];
+      float y = 0.0f;
 #pragma unroll
-      for (int c = 0; c < 16; ++c) s[c] = 0.0f;
-      for (uint32_t sp = 0; sp < splits; ++sp) {
-        const float* p = partial + ((uint64_t(item) * splits + sp) * tiles + tile) *
-                                       (M * 16 * kTileGroups) +
-                         (r * kTileGroups + j) * 16;
-#pragma unroll
-        for (int c = 0; c < 16; ++c) s[c] += p[c];
-      }
-      float acc = 0.0f;
-#pragma unroll
-      for (int c = 0; c < 16; ++c) acc = fmaf(sb_book[c * G + t], s[c], acc);
-      out[uint64_t(r) * n + tile * kTileGroups * G + jt] = acc;
-      bad |= !finite_f32(acc);
+      for (int c = 0; c < 16; ++c) y = fmaf(sb_book[c * G + t], ssum[r][j * 16 + c], y);
+      out[uint64_t(r) * n + (tile * kTileGroups + j0) * G + jt] = y;
+      bad |= !finite_f32(y);
     }
     if (__any(bad) && (threadIdx.x % warpSize) == 0) atomicOr(o.status, 1u);
   }
@@ -314,9 +397,9 @@ __global__ __launch_bounds__(256) void k_gemv_bins_finish(Operands o, uint32_t n
 uint32_t gemv_splits(uint32_t n, uint32_t k, uint32_t group, uint32_t count) {
   const uint32_t tiles = (n / (8 * group) + kTileWords - 1) / kTileWords;
   const uint64_t blocks = uint64_t(tiles) * count;
-  // Enough blocks for 256 compute units; never slices shorter than 128 rows.
+  // Enough blocks for 256 compute units; never slices shorter than 256 rows.
   uint32_t splits = 1;
-  while (blocks * splits < 256 && k / (splits * 2) >= 128) splits *= 2;
+  while (blocks * splits < 256 && k / (splits * 2) >= 256) splits *= 2;
   return splits;
 }
 
@@ -340,7 +423,7 @@ hipError_t launch_bins_m(hipStream_t s, const Operands& o, uint32_t n, uint32_t 
                                                      static_cast<float*>(workspace));
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || splits == 1) return err;
-  dim3 fgrid(tiles, 4, zc);
+  dim3 fgrid(tiles * kFinishParts, 1, zc);
   k_gemv_bins_finish<G, M><<<fgrid, 256, 0, s>>>(o, n, splits, tiles,
                                                  static_cast<const float*>(workspace));
   return hipGetLastError();
