@@ -319,14 +319,14 @@ AckDevice* ack_open(void) {
     set_error(std::string("device open: ") + hipGetErrorString(e));
     return nullptr;
   }
+  char name[256] = {0};
   hipDeviceProp_t prop;
-  if (hipGetDeviceProperties(&prop, index) == hipSuccess) {
-    dev->name = prop.name;
-    if (dev->name.empty()) dev->name = prop.gcnArchName;
-    dev->name += std::string(" (") + prop.gcnArchName + ")";
-  } else {
+  const bool have_prop = hipGetDeviceProperties(&prop, index) == hipSuccess;
+  if (hipDeviceGetName(name, sizeof name, index) == hipSuccess && name[0] != '\0')
+    dev->name = name;
+  else
     dev->name = "HIP device " + std::to_string(index);
-  }
+  if (have_prop) dev->name += std::string(" (") + prop.gcnArchName + ")";
   dev->id = g_next_device.fetch_add(1);
   Registry& r = registry();
   std::lock_guard<std::mutex> lock(r.mu);

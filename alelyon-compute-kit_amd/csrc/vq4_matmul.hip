@@ -140,35 +140,51 @@ __global__ __launch_bounds__(kGThreads) void k_matmul_general(Operands o, uint32
 
 // ---- GemvBins ------------------------------------------------------------
 // Tile: kTileWords words of each B row (8 * kTileWords output groups), all m
-// rows of A, a slice of k. Lane (q = lane % 32, half = lane / 32) reads word
-// q of row 2*wave_row + half, so a wave reads two whole 128-byte tile rows.
+// rows of A, a slice of k. In one batch each wave covers 32 rows: lane
+// (q = lane % 32, half = lane / 32) reads word q of rows base + half*16 + u,
+// u < 16, so every load instruction of a wave reads two whole 128-byte tile
+// rows and a lane's 16 activations are contiguous in LDS. The next batch's
+// words are loaded while the current batch is binned.
 //
 // The bins are 32-bit fixed point: x is scaled by 2^s (s from the A
-// codebook's largest magnitude) and rounded to an integer once, when its
-// chunk is staged in LDS, and the bins are summed with integer LDS atomics
-// -- exact, and on gfx950 some thirty times the rate of FP32 LDS atomics.
-// Every kWindow rows the integer bins are flushed into FP32 accumulators
-// held in registers, which bounds |bin| < 2^30 (no overflow) while keeping
-// the rounding of x to 2^-s at most 2^-23 of the largest |x|.
+// codebook's largest magnitude) and rounded to an integer once, when it is
+// staged in LDS, and the bins are summed with integer LDS atomics -- exact,
+// and on gfx950 some thirty times the rate of FP32 LDS atomics. Every
+// kWindow rows the integer bins are flushed into FP32 accumulators held in
+// registers, which bounds |bin| < 2^30 (no overflow) while keeping the
+// rounding of x to 2^-s at most 2^-23 of the largest |x|.
 // Bins are laid out [r][nibble][e][q]: the 32 lanes of a half-wave hit 32
 // distinct banks for any codes.
 constexpr int kTileWords = 32;
 constexpr int kTileGroups = kTileWords * 8;
 constexpr int kBinThreads = 256;
-constexpr int kBinRowsPerPass = kBinThreads / 32;  // 8 rows per pass
-constexpr int kBinUnroll = 16;
+constexpr int kBinWaves = kBinThreads / 64;
+constexpr int kRowsPerLane = 16;
+constexpr uint32_t kBatchRows = kBinWaves * 2 * kRowsPerLane;   // 128 rows per batch
 constexpr uint32_t kGemvMaxM = 8;
-constexpr uint32_t kChunk = kBinRowsPerPass * kBinUnroll * 2;  // 256 x rows staged at a time
-constexpr uint32_t kWindow = 512;                               // rows per integer window
+constexpr uint32_t kWindow = 1024;                              // rows per integer window
+constexpr uint32_t kXBytes = 16384;                             // LDS for staged x
 constexpr int kBinsPerThread = 16 * kTileGroups / kBinThreads;  // 16 bins per M row
 
-// Byte offset of bin (nib, e, q) inside one M row's bins: e*128 + q*4 +
-// nib*2048, with the nibble taken straight from the word.
+template <int M>
+__host__ __device__ constexpr uint32_t x_chunk_rows() {
+  return (kXBytes / (4 * M)) / kWindow * kWindow;               // whole windows
+}
+
+// Byte offset of bin (e, q) for nibble NIB of w inside one M row's bins.
 template <int NIB>
 __device__ __forceinline__ uint32_t bin_byte(uint32_t w, uint32_t q4) {
-  constexpr int sh = 4 * NIB - 7;
-  const uint32_t e128 = (sh >= 0 ? (w >> (sh >= 0 ? sh : 0)) : (w << (sh < 0 ? -sh : 0))) & 0x780u;
-  return (e128 | q4) + NIB * 2048;
+  return (__builtin_amdgcn_ubfe(w, 4 * NIB, 4) << 7) | q4;
+}
+
+typedef __attribute__((address_space(3))) int32_t lds_i32;
+
+// Integer add into LDS at an absolute byte address. The bins sit at LDS
+// address 0 (the kernel has no static LDS), so a bin's address is known to
+// the compiler bit for bit and needs no base addition.
+__device__ __forceinline__ void lds_add(uint32_t byte_addr, int32_t v) {
+  __hip_atomic_fetch_add(reinterpret_cast<lds_i32*>(static_cast<size_t>(byte_addr)), v,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 __device__ __forceinline__ uint32_t bin_index(uint32_t r, uint32_t nib, uint32_t e, uint32_t q) {
@@ -176,13 +192,12 @@ __device__ __forceinline__ uint32_t bin_index(uint32_t r, uint32_t nib, uint32_t
 }
 
 // x[r][kk] for rows r < m and inner rows [k0, kend), decoded from A by flat
-// index, scaled by 2^shift and rounded to int32 into sxq[r * kChunk + kk].
+// index, scaled by 2^shift and rounded to int32 into sxq[r * rows + kk].
 template <int G, int M>
-__device__ void stage_x_chunk(const uint32_t* a_codes, const float* sa_book, uint32_t k,
-                              uint32_t flags, uint32_t k0, uint32_t kend, int shift,
-                              int32_t* sxq) {
-  for (uint32_t e = threadIdx.x; e < M * kChunk; e += blockDim.x) {
-    const uint32_t r = e / kChunk, kk = e % kChunk;
+__device__ void stage_x(const uint32_t* a_codes, const float* sa_book, uint32_t k, uint32_t flags,
+                        uint32_t k0, uint32_t kend, uint32_t rows, int shift, int32_t* sxq) {
+  for (uint32_t e = threadIdx.x; e < M * rows; e += blockDim.x) {
+    const uint32_t r = e / rows, kk = e % rows;
     const uint32_t inner = k0 + kk;
     int32_t v = 0;
     if (inner < kend) {
@@ -207,19 +222,33 @@ __device__ float book_absmax(const float* sbook, float* sred) {
   return m;
 }
 
+// Load this lane's 16 words of a batch (zero past kend or off the tile).
+__device__ __forceinline__ void load_batch(const uint32_t* col_codes, uint32_t row_words,
+                                           uint32_t first, uint32_t kend, bool live,
+                                           uint32_t (&w)[kRowsPerLane]) {
+#pragma unroll
+  for (int u = 0; u < kRowsPerLane; ++u) {
+    const uint32_t row = first + u;
+    w[u] = (live && row < kend) ? col_codes[uint64_t(row) * row_words] : 0u;
+  }
+}
+
 // grid: (n tiles, k splits, instances). Dynamic shared memory: the integer
-// bins (M * 16 * kTileGroups) then one x chunk (M * kChunk int32).
+// bins (M * 16 * kTileGroups) then the staged x (M * x_chunk_rows int32).
 template <int G, int M>
 __global__ __launch_bounds__(kBinThreads) void k_gemv_bins(Operands o, uint32_t n, uint32_t k,
                                                            uint32_t flags, uint32_t ks,
                                                            float* partial) {
+  constexpr uint32_t kXRows = x_chunk_rows<M>();
+  // All LDS is dynamic so the bins start at address 0: a bin address is then
+  // (e << 7) | q4 with disjoint bits, one AND-OR per nibble.
   extern __shared__ int32_t smem[];
   int32_t* bins = smem;
   int32_t* sxq = smem + M * 16 * kTileGroups;
   float* fbins = reinterpret_cast<float*>(smem);
-  __shared__ float sa_book[16 * G];
-  __shared__ float sb_book[16 * G];
-  __shared__ float sred[kBinThreads / 64];
+  float* sa_book = reinterpret_cast<float*>(sxq + kXBytes / 4);
+  float* sb_book = sa_book + 16 * G;
+  float* sred = sb_book + 16 * G;
   const uint32_t tid = threadIdx.x;
   const uint32_t tile = blockIdx.x, split = blockIdx.y;
   const uint32_t row_words = n / (8 * G);
@@ -228,14 +257,23 @@ __global__ __launch_bounds__(kBinThreads) void k_gemv_bins(Operands o, uint32_t 
   const uint32_t lane = tid % 64, wave = tid / 64;
   const uint32_t q = lane % 32, half = lane / 32;
   const uint32_t q4 = q * 4;
+  const uint32_t lane_row = wave * 32 + half * kRowsPerLane;  // first row of this lane in a batch
   const uint32_t word_col = tile * kTileWords + q;
   const bool live = word_col < row_words;
-  char* bin_bytes = reinterpret_cast<char*>(bins);
+  // Defensive: absolute bin addresses assume the bins start at LDS 0.
+  if (static_cast<uint32_t>(reinterpret_cast<size_t>((lds_i32*)bins)) != 0) {
+    if (tid == 0) atomicOr(o.status, 2u);
+    return;
+  }
   for (uint32_t item = blockIdx.z; item < o.count; item += gridDim.z) {
     const uint32_t* a_codes = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
     const float* a_book = item_ptr<float>(o.in[1], o.stride[1], item);
     const uint32_t* b_codes = item_ptr<uint32_t>(o.in[2], o.stride[2], item);
     const float* b_book = item_ptr<float>(o.in[3], o.stride[3], item);
+    const uint32_t* col_codes = b_codes + word_col;
+    // the first batch's words are in flight while the block sets up
+    uint32_t wn[kRowsPerLane];
+    load_batch(col_codes, row_words, k0 + lane_row, kend, live, wn);
     __syncthreads();
     for (uint32_t i = tid; i < 16 * G; i += kBinThreads) {
       sa_book[i] = a_book[i];
@@ -249,8 +287,8 @@ __global__ __launch_bounds__(kBinThreads) void k_gemv_bins(Operands o, uint32_t 
     int shift = 0;
     if (xmax > 0.0f) {
       int ex;
-      frexpf(xmax, &ex);  // xmax < 2^ex, so xmax * kWindow < 2^(ex + 9)
-      shift = 30 - (ex + 9);
+      frexpf(xmax, &ex);  // xmax < 2^ex, so xmax * kWindow < 2^(ex + 10)
+      shift = 30 - (ex + 10);
       shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
     }
     const float unscale = ldexpf(1.0f, -shift);
@@ -259,54 +297,64 @@ __global__ __launch_bounds__(kBinThreads) void k_gemv_bins(Operands o, uint32_t 
     for (int r = 0; r < M; ++r)
 #pragma unroll
       for (int i = 0; i < kBinsPerThread; ++i) acc[r][i] = 0.0f;
-    const uint32_t* col_codes = b_codes + word_col;
-    for (uint32_t kw = k0; kw < kend; kw += kWindow) {
-      const uint32_t kwe = (kw + kWindow) < kend ? (kw + kWindow) : kend;
-      for (uint32_t kc = kw; kc < kwe; kc += kChunk) {
-        const uint32_t kce = (kc + kChunk) < kwe ? (kc + kChunk) : kwe;
-        __syncthreads();
-        stage_x_chunk<G, M>(a_codes, sa_book, k, flags, kc, kce, shift, sxq);
-        __syncthreads();
-        for (uint32_t kb = kc; kb < kce; kb += kBinRowsPerPass * kBinUnroll) {
-          uint32_t w[kBinUnroll];
+
+    uint32_t xbase = k0;  // first row of the staged x chunk
+    stage_x<G, M>(a_codes, sa_book, k, flags, xbase, kend, kXRows, shift, sxq);
+    __syncthreads();
+    for (uint32_t kb = k0; kb < kend; kb += kBatchRows) {
+      uint32_t w[kRowsPerLane];
 #pragma unroll
-          for (int u = 0; u < kBinUnroll; ++u) {
-            const uint32_t row = kb + u * kBinRowsPerPass + wave * 2 + half;
-            w[u] = (live && row < kce) ? col_codes[uint64_t(row) * row_words] : 0u;
+      for (int u = 0; u < kRowsPerLane; ++u) w[u] = wn[u];
+      if (kb + kBatchRows < kend)
+        load_batch(col_codes, row_words, kb + kBatchRows + lane_row, kend, live, wn);
+      if (live) {
+        const uint32_t first = kb + lane_row;
+#pragma unroll
+        for (int r = 0; r < M; ++r) {
+          const uint32_t base = r * (16 * kTileGroups * 4);
+          // the lane's 16 activations, 16-byte aligned; rows past kend are
+          // staged as zero (and carry w = 0), so their adds are no-ops
+          const int4* xr = reinterpret_cast<const int4*>(sxq + r * kXRows + (first - xbase));
+          int32_t xs[kRowsPerLane];
+#pragma unroll
+          for (int i = 0; i < kRowsPerLane / 4; ++i) {
+            const int4 v = xr[i];
+            xs[4 * i] = v.x; xs[4 * i + 1] = v.y; xs[4 * i + 2] = v.z; xs[4 * i + 3] = v.w;
           }
 #pragma unroll
-          for (int u = 0; u < kBinUnroll; ++u) {
-            const uint32_t row = kb + u * kBinRowsPerPass + wave * 2 + half;
-            if (!live || row >= kce) continue;
-#pragma unroll
-            for (int r = 0; r < M; ++r) {
-              const int32_t xr = sxq[r * kChunk + (row - kc)];
-              char* base = bin_bytes + r * (16 * kTileGroups * 4);
-              const uint32_t ww = w[u];
-              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<0>(ww, q4)), xr);
-              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<1>(ww, q4)), xr);
-              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<2>(ww, q4)), xr);
-              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<3>(ww, q4)), xr);
-              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<4>(ww, q4)), xr);
-              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<5>(ww, q4)), xr);
-              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<6>(ww, q4)), xr);
-              atomicAdd(reinterpret_cast<int32_t*>(base + bin_byte<7>(ww, q4)), xr);
-            }
+          for (int u = 0; u < kRowsPerLane; ++u) {
+            const int32_t xv = xs[u];
+            const uint32_t ww = w[u];
+            lds_add(base + 0 * 2048 + bin_byte<0>(ww, q4), xv);
+            lds_add(base + 1 * 2048 + bin_byte<1>(ww, q4), xv);
+            lds_add(base + 2 * 2048 + bin_byte<2>(ww, q4), xv);
+            lds_add(base + 3 * 2048 + bin_byte<3>(ww, q4), xv);
+            lds_add(base + 4 * 2048 + bin_byte<4>(ww, q4), xv);
+            lds_add(base + 5 * 2048 + bin_byte<5>(ww, q4), xv);
+            lds_add(base + 6 * 2048 + bin_byte<6>(ww, q4), xv);
+            lds_add(base + 7 * 2048 + bin_byte<7>(ww, q4), xv);
           }
         }
       }
-      // flush the window: integer bins -> FP32 accumulators, bins reset
-      __syncthreads();
+      const uint32_t done = kb + kBatchRows;
+      if (done >= kend || (done - k0) % kWindow == 0) {
+        // flush the window: integer bins -> FP32 accumulators, bins reset
+        __syncthreads();
 #pragma unroll
-      for (int r = 0; r < M; ++r)
+        for (int r = 0; r < M; ++r)
 #pragma unroll
-        for (int i = 0; i < kBinsPerThread; ++i) {
-          const uint32_t b = r * 16 * kTileGroups + tid + i * kBinThreads;
-          acc[r][i] += float(bins[b]);
-          bins[b] = 0;
+          for (int i = 0; i < kBinsPerThread; ++i) {
+            const uint32_t b = r * 16 * kTileGroups + tid + i * kBinThreads;
+            acc[r][i] += float(bins[b]);
+            bins[b] = 0;
+          }
+        if (done < kend && done - xbase >= kXRows) {
+          xbase = done;
+          stage_x<G, M>(a_codes, sa_book, k, flags, xbase, kend, kXRows, shift, sxq);
         }
+        __syncthreads();
+      }
     }
-    __syncthreads();
 #pragma unroll
     for (int r = 0; r < M; ++r)
 #pragma unroll
@@ -403,7 +451,9 @@ uint32_t gemv_splits(uint32_t n, uint32_t k, uint32_t group, uint32_t count) {
   return splits;
 }
 
-size_t bins_shmem(uint32_t m) { return (size_t(m) * 16 * kTileGroups + size_t(m) * kChunk) * 4; }
+size_t bins_shmem(uint32_t m, uint32_t g) {
+  return size_t(m) * 16 * kTileGroups * 4 + kXBytes + 2 * 16 * g * 4 + kBinWaves * 4;
+}
 
 template <int G, int M>
 hipError_t launch_bins_m(hipStream_t s, const Operands& o, uint32_t n, uint32_t k, uint32_t flags,
@@ -412,7 +462,7 @@ hipError_t launch_bins_m(hipStream_t s, const Operands& o, uint32_t n, uint32_t 
   const uint32_t splits = gemv_splits(n, k, G, o.count);
   const uint32_t ks = (k + splits - 1) / splits;
   const uint32_t zc = o.count < 65535 ? o.count : 65535;
-  const size_t shmem = bins_shmem(M);
+  const size_t shmem = bins_shmem(M, G);
   if (shmem > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_bins<G, M>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));

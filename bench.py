@@ -212,12 +212,24 @@ def main(argv=None) -> int:
     parser.add_argument("--items", type=int, default=1024)
     parser.add_argument("--no-prefill", action="store_true")
     parser.add_argument("--no-cpu", action="store_true")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run a 512 MiB device-to-device copy (the reference for "
+                             "scaling FETCH_SIZE/WRITE_SIZE counters) and exit")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
               "(the vq4 path is single-device; see DESIGN.md for how it would shard)",
               file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        import torch
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel(), "launches": 3}))
+        return 0
     from alelyon_compute_kit import ack, vq
     with ack.Device() as device:
         dev = vq.VQDevice(device)
