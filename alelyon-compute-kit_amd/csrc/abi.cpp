@@ -232,7 +232,7 @@ int32_t run_vq(const AckDevice* handle, const AckBuffer* const slots[6], const u
     case ackvq::Op::AdamW: he = ackvq::launch_adamw(dev->stream, o, m, g); break;
     case ackvq::Op::Matmul: {
       const ackvq::MatmulPath path =
-          ackvq::choose_matmul_path(m, n, k, g, plan.flags(), dev->policy);
+          ackvq::choose_matmul_path(m, n, k, g, plan.flags(), count, dev->policy);
       const size_t ws = ackvq::matmul_workspace_bytes(path, m, n, k, g, plan.flags(), count);
       if (int32_t rc = ensure_workspace(*dev, ws)) return rc;
       he = ackvq::launch_matmul(dev->stream, o, m, n, k, g, plan.flags(), path, dev->workspace,
@@ -555,7 +555,7 @@ int32_t ack_vq_path_name(const uint8_t* plan, size_t plan_len, char* out, size_t
   if (p.op == ackvq::Op::AdamW) name = "adamw";
   if (p.op == ackvq::Op::Matmul)
     name = ackvq::matmul_path_name(
-        ackvq::choose_matmul_path(p.m(), p.n(), p.k(), p.group(), p.flags(), 0));
+        ackvq::choose_matmul_path(p.m(), p.n(), p.k(), p.group(), p.flags(), 1, 0));
   const size_t n = std::strlen(name) < len - 1 ? std::strlen(name) : len - 1;
   std::memcpy(out, name, n);
   out[n] = '\0';

@@ -26,14 +26,20 @@ enum class MatmulPath : int {
   General = 0,    // tiled, sequential FP32 per output: bit-identical to vq4.comp
   GemvBins = 1,   // B groups along n: codebook-factorised bins, small m
   GemvTable = 2,  // B groups along k (B stored (n,k)): dot-product table, small m
-  Mfma = 3,       // large m: decode to LDS tiles, FP32 MFMA
+  Mfma = 3,       // reserved
+  RowBins = 4,    // large m, B groups along n: wave-uniform codes, bins in VGPRs
 };
 
 const char* matmul_path_name(MatmulPath p);
 
 // Chooses the path for a product; `policy` 1 forces General.
 MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
-                              uint32_t policy);
+                              uint32_t count, uint32_t policy);
+
+bool rowbins_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
+size_t rowbins_workspace_bytes(uint32_t n, uint32_t k, uint32_t group);
+hipError_t launch_rowbins(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                          uint32_t group, void* workspace);
 
 // Bytes of device workspace a path needs (split-k partials, counters).
 size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,

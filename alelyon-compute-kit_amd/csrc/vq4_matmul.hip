@@ -166,10 +166,13 @@ constexpr uint32_t kWindow = 1024;                              // rows per inte
 constexpr uint32_t kXBytes = 16384;                             // LDS for staged x
 constexpr int kBinsPerThread = 16 * kTileGroups / kBinThreads;  // 16 bins per M row
 
+// Rows of x staged at once: whole batches (so a lane's 16 activations never
+// straddle a restage), restaged whenever the chunk is used up.
 template <int M>
 __host__ __device__ constexpr uint32_t x_chunk_rows() {
-  return (kXBytes / (4 * M)) / kWindow * kWindow;               // whole windows
+  return (kXBytes / (4 * M)) / kBatchRows * kBatchRows;
 }
+static_assert(x_chunk_rows<kGemvMaxM>() >= kBatchRows, "staged x must hold one batch per row");
 
 // Byte offset of bin (e, q) for nibble NIB of w inside one M row's bins.
 template <int NIB>
@@ -337,18 +340,22 @@ __global__ __launch_bounds__(kBinThreads) void k_gemv_bins(Operands o, uint32_t 
         }
       }
       const uint32_t done = kb + kBatchRows;
-      if (done >= kend || (done - k0) % kWindow == 0) {
-        // flush the window: integer bins -> FP32 accumulators, bins reset
+      const bool flush = done >= kend || (done - k0) % kWindow == 0;
+      const bool restage = done < kend && done - xbase >= kXRows;
+      if (flush || restage) {
         __syncthreads();
+        if (flush) {
+          // the window ends: integer bins -> FP32 accumulators, bins reset
 #pragma unroll
-        for (int r = 0; r < M; ++r)
+          for (int r = 0; r < M; ++r)
 #pragma unroll
-          for (int i = 0; i < kBinsPerThread; ++i) {
-            const uint32_t b = r * 16 * kTileGroups + tid + i * kBinThreads;
-            acc[r][i] += float(bins[b]);
-            bins[b] = 0;
-          }
-        if (done < kend && done - xbase >= kXRows) {
+            for (int i = 0; i < kBinsPerThread; ++i) {
+              const uint32_t b = r * 16 * kTileGroups + tid + i * kBinThreads;
+              acc[r][i] += float(bins[b]);
+              bins[b] = 0;
+            }
+        }
+        if (restage) {
           xbase = done;
           stage_x<G, M>(a_codes, sa_book, k, flags, xbase, kend, kXRows, shift, sxq);
         }
@@ -502,14 +509,15 @@ const char* matmul_path_name(MatmulPath p) {
     case MatmulPath::GemvBins: return "gemv-bins";
     case MatmulPath::GemvTable: return "gemv-table";
     case MatmulPath::Mfma: return "mfma";
+    case MatmulPath::RowBins: return "row-bins";
   }
   return "unknown";
 }
 
 MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
-                              uint32_t policy) {
-  (void)k;
+                              uint32_t count, uint32_t policy) {
   if (policy == 1) return MatmulPath::General;
+  if (count == 1 && rowbins_applies(m, n, k, group, flags)) return MatmulPath::RowBins;
   if (m <= kGemvMaxM && (flags & 2u) == 0 && n % (8 * group) == 0) return MatmulPath::GemvBins;
   return MatmulPath::General;
 }
@@ -517,6 +525,7 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
 size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                               uint32_t flags, uint32_t count) {
   (void)flags;
+  if (p == MatmulPath::RowBins) return rowbins_workspace_bytes(n, k, group);
   if (p != MatmulPath::GemvBins) return 0;
   const uint32_t splits = gemv_splits(n, k, group, count);
   if (splits == 1) return 0;
@@ -528,6 +537,7 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
                          uint32_t group, uint32_t flags, MatmulPath path, void* workspace,
                          size_t workspace_bytes) {
   (void)workspace_bytes;
+  if (path == MatmulPath::RowBins) return launch_rowbins(s, o, m, n, k, group, workspace);
   if (path == MatmulPath::GemvBins) {
     if (group == 8) return launch_bins<8>(s, o, m, n, k, flags, workspace);
     if (group == 16) return launch_bins<16>(s, o, m, n, k, flags, workspace);

@@ -266,7 +266,7 @@ def main(argv=None) -> int:
         line["extra"] = {"prefill": {
             "workload": "config 4: X 2048x4096 . W 4096x14336 g32 (forward), dY 2048x14336 . W^T "
                         "(backward)",
-            **{f"{k}_{f}": (round(v[f], 4) if isinstance(v[f], float) else v[f])
+            **{f"{k}_{f}": (float(f"{v[f]:.4g}") if isinstance(v[f], float) else v[f])
                for k, v in prefill.items() for f in v},
             "roofline": {"bound": "mfma", "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "achieved": round(min(v["tflops"] for v in prefill.values()), 3),

@@ -78,7 +78,7 @@ GEMV_SHAPES = [(256, 256, 16), (4096, 4096, 16), (512, 1024, 8), (1024, 768, 32)
                (100, 512, 16), (3000, 2048, 8)]
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_gemv_bins_within_tolerance(vqdev, oracle, m):
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(50 + m)
@@ -119,6 +119,25 @@ def test_gemv_bins_batched(vqdev, oracle):
     for i, it in enumerate(items):
         ref, _ = oracle.matmul(*it, m, n, k, group, 0)
         assert o.max_rel(out[i], ref) <= TOL
+
+
+@pytest.mark.parametrize("m", [3, 5, 8])
+def test_gemv_bins_long_slices(vqdev, oracle, m):
+    """256 instances fill the chip without splitting k, so each block walks
+    all 2600 rows: several integer windows, and the staged activations are
+    restaged at chunk ends that do not coincide with window ends."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(90 + m)
+    k, n, group, count = 2600, 128, 16, 256
+    items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
+    ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
+    say("gemv-bins long slices", m, count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    for i in (0, 1, 128, 255):
+        ref, _ = oracle.matmul(*items[i], m, n, k, group, 0)
+        assert o.max_rel(out[i], ref) <= TOL
+        assert o.max_rel(out[i], _ref64(items[i], m, n, k, group, 0)) <= TOL
 
 
 def test_config1_matmul(vqdev, oracle):
@@ -164,3 +183,43 @@ def test_transposed_products_agree_with_float64(vqdev):
         out, status = _gpu(vqdev, ops, m, n, k, group, flags)
         assert status == 0
         assert o.max_rel(out, _ref64(ops, m, n, k, group, flags)) <= TOL
+
+
+ROW_BINS_SHAPES = [(64, 256, 64, 16), (100, 512, 96, 32), (130, 2048, 256, 16),
+                   (256, 1024, 512, 32), (333, 768, 1024, 16)]
+
+
+@pytest.mark.parametrize("m,n,k,group", ROW_BINS_SHAPES)
+def test_row_bins_within_tolerance(vqdev, oracle, m, n, k, group):
+    """Large-m product with B's groups along n: wave-uniform codes, bins in
+    registers (rows past m in the last wave are masked)."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(m + n + k)
+    words = (2, m, n, k, group, 16, 0, 0)
+    assert vqdev.path_name(words) == "row-bins"
+    say("row-bins", m, n, k, group)
+    ops = _operands(rng, m, n, k, group, 1.0, 0.02)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0)
+    assert status == 0
+    ref, _ = oracle.matmul(*ops, m, n, k, group, 0)
+    assert o.max_rel(out, ref) <= TOL
+    assert o.max_rel(out, _ref64(ops, m, n, k, group, 0)) <= TOL
+
+
+def test_config4_forward_rows_against_float64(vqdev):
+    """BASELINE config 4 forward at full size: X 2048x4096 . W 4096x14336 at
+    group 32; 16 rows checked against float64, all rows finite."""
+    from alelyon_compute_kit import vq
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(4)
+    w = (rng.standard_normal((4096, 14336)) * 0.02).astype(np.float32)
+    w_img = vqdev.encode(w, vq.fit_codebook(w, group=32), group=32)
+    x = rng.standard_normal((2048, 4096)).astype(np.float32)
+    x_img = vqdev.encode(x, vq.fit_codebook(x, group=32), group=32)
+    assert vqdev.path_name((2, 2048, 14336, 4096, 32, 16, 0, 0)) == "row-bins"
+    say("config4 forward")
+    y = vqdev.matmul(x_img, w_img)
+    rows = np.r_[0:8, 2040:2048]
+    ref = x_img.decode()[rows].astype(np.float64) @ w_img.decode().astype(np.float64)
+    assert o.max_rel(y[rows], ref) <= TOL
+    assert np.isfinite(y).all()
