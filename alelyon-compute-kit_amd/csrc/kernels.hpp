@@ -26,7 +26,7 @@ enum class MatmulPath : int {
   General = 0,    // tiled, sequential FP32 per output: bit-identical to vq4.comp
   GemvBins = 1,   // B groups along n: codebook-factorised bins, small m
   GemvTable = 2,  // B groups along k (B stored (n,k)): dot-product table, small m
-  Mfma = 3,       // reserved
+  GramMfma = 3,   // both operands grouped along k: one-hot x Gram table on fp16 MFMA
   RowBins = 4,    // large m, B groups along n: wave-uniform codes, bins in VGPRs
 };
 
@@ -35,6 +35,10 @@ const char* matmul_path_name(MatmulPath p);
 // Chooses the path for a product; `policy` 1 forces General.
 MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                               uint32_t count, uint32_t policy);
+
+bool gram_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
+hipError_t launch_gram(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                       uint32_t group);
 
 bool rowbins_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
 size_t rowbins_workspace_bytes(uint32_t n, uint32_t k, uint32_t group);

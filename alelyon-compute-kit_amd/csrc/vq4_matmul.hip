@@ -508,7 +508,7 @@ const char* matmul_path_name(MatmulPath p) {
     case MatmulPath::General: return "general";
     case MatmulPath::GemvBins: return "gemv-bins";
     case MatmulPath::GemvTable: return "gemv-table";
-    case MatmulPath::Mfma: return "mfma";
+    case MatmulPath::GramMfma: return "gram-mfma";
     case MatmulPath::RowBins: return "row-bins";
   }
   return "unknown";
@@ -518,6 +518,7 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
                               uint32_t count, uint32_t policy) {
   if (policy == 1) return MatmulPath::General;
   if (count == 1 && rowbins_applies(m, n, k, group, flags)) return MatmulPath::RowBins;
+  if (gram_applies(m, n, k, group, flags)) return MatmulPath::GramMfma;
   if (m <= kGemvMaxM && (flags & 2u) == 0 && n % (8 * group) == 0) return MatmulPath::GemvBins;
   return MatmulPath::General;
 }
@@ -538,6 +539,7 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
                          size_t workspace_bytes) {
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins(s, o, m, n, k, group, workspace);
+  if (path == MatmulPath::GramMfma) return launch_gram(s, o, m, n, k, group);
   if (path == MatmulPath::GemvBins) {
     if (group == 8) return launch_bins<8>(s, o, m, n, k, flags, workspace);
     if (group == 16) return launch_bins<16>(s, o, m, n, k, flags, workspace);

@@ -223,3 +223,69 @@ def test_config4_forward_rows_against_float64(vqdev):
     ref = x_img.decode()[rows].astype(np.float64) @ w_img.decode().astype(np.float64)
     assert o.max_rel(y[rows], ref) <= TOL
     assert np.isfinite(y).all()
+
+
+# (m, n, k, group): k / group of 12, 17 and 33 start rows mid-word
+GRAM_SHAPES = [(1, 256, 256, 16), (37, 53, 96, 8), (64, 96, 128, 32), (130, 200, 272, 16),
+               (256, 384, 1024, 32), (100, 64, 264, 8), (300, 129, 512, 16)]
+
+
+@pytest.mark.parametrize("m,n,k,group", GRAM_SHAPES)
+def test_gram_mfma_within_tolerance(vqdev, oracle, m, n, k, group):
+    """B stored (n, k) with both operands grouped along k: one-hot A times the
+    codebooks' Gram table on fp16 MFMA (hi + lo split)."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(m * 7 + n + k)
+    words = (2, m, n, k, group, 16, 2, 0)
+    assert vqdev.path_name(words) == "gram-mfma"
+    say("gram-mfma", m, n, k, group)
+    ops = _operands(rng, m, n, k, group, 0.1, 0.02)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 2)
+    assert status == 0
+    ref, _ = oracle.matmul(*ops, m, n, k, group, 2)
+    assert o.max_rel(out, ref) <= TOL
+    assert o.max_rel(out, _ref64(ops, m, n, k, group, 2)) <= TOL
+
+
+def test_gram_mfma_batched(vqdev, oracle):
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(123)
+    m, n, k, group, count = 70, 96, 160, 16, 5
+    items = [_operands(rng, m, n, k, group, 1.0 + i, 0.5) for i in range(count)]
+    ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
+    say("gram-mfma batch", count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 2, count=count)
+    assert status == 0
+    for i, it in enumerate(items):
+        ref, _ = oracle.matmul(*it, m, n, k, group, 2)
+        assert o.max_rel(out[i], ref) <= TOL
+
+
+def test_gram_mfma_status_on_overflow(vqdev, oracle):
+    from oracle import vq4_numpy as o
+    codes = o.pack_indices(np.zeros(4, np.int64))
+    book = np.full((16, 8), 3e19, np.float32)
+    say("gram-mfma overflow")
+    _, status = _gpu(vqdev, (codes, book, codes, book), 4, 4, 8, 8, 2)
+    assert status == oracle.matmul(codes, book, codes, book, 4, 4, 8, 8, 2)[1] == 1
+
+
+def test_config4_backward_rows_against_float64(vqdev):
+    """BASELINE config 4 backward at full size: dY 2048x14336 ~ N(0, 1e-2) .
+    W^T with W 4096x14336 stored (n, k) at group 32; 16 rows checked against
+    float64, all rows finite."""
+    from alelyon_compute_kit import vq
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((4096, 14336)) * 0.02).astype(np.float32)
+    w_img = vqdev.encode(w, vq.fit_codebook(w, group=32), group=32)
+    dy = (rng.standard_normal((2048, 14336)) * 0.1).astype(np.float32)
+    dy_img = vqdev.encode(dy, vq.fit_codebook(dy, group=32), group=32)
+    assert vqdev.path_name((2, 2048, 4096, 14336, 32, 16, 2, 0)) == "gram-mfma"
+    say("config4 backward")
+    y = vqdev.matmul(dy_img, w_img, transpose_b=True)
+    assert y.shape == (2048, 4096)
+    rows = np.r_[0:8, 2040:2048]
+    ref = dy_img.decode()[rows].astype(np.float64) @ w_img.decode().astype(np.float64).T
+    assert o.max_rel(y[rows], ref) <= TOL
+    assert np.isfinite(y).all()
