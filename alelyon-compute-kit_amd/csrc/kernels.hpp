@@ -28,6 +28,7 @@ enum class MatmulPath : int {
   GemvTable = 2,  // B groups along k (B stored (n,k)): dot-product table, small m
   GramMfma = 3,   // both operands grouped along k: one-hot x Gram table on fp16 MFMA
   RowBins = 4,    // large m, B groups along n: wave-uniform codes, bins in VGPRs
+  GemvPairs = 5,  // m = 1, B groups along n: one atomic per byte into 256-way pair bins
 };
 
 const char* matmul_path_name(MatmulPath p);

@@ -449,6 +449,296 @@ __global__ __launch_bounds__(256) void k_gemv_bins_finish(Operands o, uint32_t n
   }
 }
 
+// ---- GemvPairs (m = 1) -----------------------------------------------------
+// The two nibbles of a byte of a B row are the codes of two output groups of
+// the same inner row, so they receive the same x. One integer atomic into a
+// 256-way "pair bin" indexed by the whole byte replaces GemvBins' two:
+//   S[2p][e]   = sum over hi of P[p][16 hi + e]   (low nibble = group 8q+2p)
+//   S[2p+1][e] = sum over lo of P[p][16 e + lo]   (high nibble = group 8q+2p+1)
+// Pair bins are laid out [byte value][pair p][word q] (128 KiB for a 32-word
+// tile), so a bin address is (byte << 9) | (p << 7) | 4q: p is an immediate
+// offset and the 32 lanes of a half-wave hit 32 distinct banks.
+//
+// Integer windows are kPairWindow rows: x is scaled so that
+// max|x| * 2^shift * kPairWindow < 2^30 (a quantisation step of 2^-20 of
+// max|x|), and the bins are flushed into FP32 registers once per window.
+// Every load of the main loop is unconditional: rows past the slice read as
+// zero words through the buffer descriptor's range and meet x = 0; dead words
+// are clamped to the last word and never binned.
+constexpr int kPairThreads = 512;
+constexpr int kPairWaves = kPairThreads / 64;
+constexpr uint32_t kPairBatchRows = kPairWaves * 2 * kRowsPerLane;  // 256 rows per batch
+constexpr uint32_t kPairBins = 256 * 4 * kTileWords;                // 32768
+constexpr uint32_t kPairXRows = 8 * kPairThreads;                   // staged x rows (16 KiB)
+constexpr uint32_t kPairWindow = 2048;
+constexpr int kPairVec = kPairBins / (4 * kPairThreads);            // int4 bins per thread
+static_assert(kPairWindow % kPairBatchRows == 0 && kPairXRows % kPairBatchRows == 0, "batches");
+static_assert(kPairXRows >= 16 * kTileGroups, "S reuses the x staging area");
+
+template <int BYTE>
+__device__ __forceinline__ uint32_t pair_addr(uint32_t w, uint32_t q4) {
+  return ((__builtin_amdgcn_ubfe(w, 8 * BYTE, 8) << 9) | q4) + BYTE * 128;
+}
+
+// Buffer descriptor over the first `rows` rows of a code matrix: raw buffer
+// loads past it return zero, which is how rows past a slice read.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t code_rows(const uint32_t* codes, uint32_t rows,
+                                                            uint32_t row_words) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(codes), 0,
+                                           int(rows * row_words * 4u), 0x00020000);
+}
+
+// This lane's 16 words of a batch from word column `col`, rows first ..
+// first+15: one 32-bit byte offset per load (a matrix holds fewer than 2^30
+// words), no 64-bit address arithmetic.
+__device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t rs, uint32_t col,
+                                          uint32_t row_words, uint32_t first,
+                                          uint32_t (&w)[kRowsPerLane]) {
+  const uint32_t base = (first * row_words + col) * 4u;
+#pragma unroll
+  for (int u = 0; u < kRowsPerLane; ++u)
+    w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, base + u * row_words * 4u, 0, 0));
+}
+
+// Largest |value| of a 16 x G book in LDS, per wave.
+template <int G>
+__device__ float wave_book_absmax(const float* sbook) {
+  float v = 0.0f;
+  for (uint32_t i = threadIdx.x % 64; i < 16 * G; i += 64) v = fmaxf(v, fabsf(sbook[i]));
+  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+// x rows [xbase, xbase + kPairXRows) of the single row of A, scaled by
+// 2^shift and rounded, into sxq; rows at or past kend are zero. Thread t
+// stages rows 8t .. 8t+7, which lie in one group of A (8 divides G and
+// xbase); `a_word` is the code word holding that group's nibble.
+template <int G>
+__device__ void stage_x1(uint32_t a_word, const float* sa_book, uint32_t xbase, uint32_t kend,
+                         int shift, int32_t* sxq) {
+  const uint32_t r0 = xbase + 8 * threadIdx.x;
+  int32_t v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (r0 < kend) {
+    const uint32_t code = (a_word >> (((r0 / G) & 7u) * 4u)) & 15u;
+    const float4* c = reinterpret_cast<const float4*>(sa_book + code * G + r0 % G);
+    const float4 c0 = c[0], c1 = c[1];
+    const float x[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      v[i] = (r0 + i < kend) ? int32_t(rintf(ldexpf(x[i], shift))) : 0;
+  }
+  int4* dst = reinterpret_cast<int4*>(sxq + 8 * threadIdx.x);
+  dst[0] = make_int4(v[0], v[1], v[2], v[3]);
+  dst[1] = make_int4(v[4], v[5], v[6], v[7]);
+}
+
+__device__ __forceinline__ uint32_t stage_word(const uint32_t* a_codes, uint32_t xbase,
+                                               uint32_t kend, uint32_t group) {
+  const uint32_t r0 = xbase + 8 * threadIdx.x;
+  return r0 < kend ? a_codes[(r0 / group) >> 3] : 0u;
+}
+
+// What an instance's set-up reads from global memory besides its first batch
+// of B words, loaded during the previous instance: this thread's staging code
+// word and one entry of each book (16 * G <= kPairThreads).
+struct PairAhead {
+  uint32_t a_word;
+  float a_entry, b_entry;
+};
+
+template <int G>
+__device__ __forceinline__ void pair_setup_loads(const Operands& o, uint32_t item, uint32_t k0,
+                                                 uint32_t kend, PairAhead& ah) {
+  const uint32_t* a_codes = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
+  const float* a_book = item_ptr<float>(o.in[1], o.stride[1], item);
+  const float* b_book = item_ptr<float>(o.in[3], o.stride[3], item);
+  ah.a_word = stage_word(a_codes, k0, kend, G);
+  const uint32_t i = threadIdx.x < 16 * G ? threadIdx.x : 0;
+  ah.a_entry = a_book[i];
+  ah.b_entry = b_book[i];
+}
+
+// grid: (n tiles, k splits, z); block z serves instances z, z + gridDim.z, ...
+// ks is a multiple of kPairBatchRows. Dynamic shared memory: pair bins,
+// staged x (later S), the A and B books.
+template <int G>
+__global__ __launch_bounds__(kPairThreads) void k_gemv_pairs(Operands o, uint32_t n, uint32_t k,
+                                                             uint32_t ks, float* partial) {
+  static_assert(16 * G <= kPairThreads, "one book entry per thread");
+  extern __shared__ int32_t smem[];
+  int32_t* bins = smem;
+  int32_t* sxq = smem + kPairBins;
+  float* ss = reinterpret_cast<float*>(sxq);  // S after the main loop: [e][n8][q]
+  float* sa_book = reinterpret_cast<float*>(sxq + kPairXRows);
+  float* sb_book = sa_book + 16 * G;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t tile = blockIdx.x, split = blockIdx.y;
+  const uint32_t row_words = n / (8 * G);
+  const uint32_t k0 = split * ks;
+  const uint32_t kend = (k0 + ks) < k ? (k0 + ks) : k;
+  const uint32_t lane = tid % 64, wave = tid / 64;
+  const uint32_t q = lane % 32, half = lane / 32;
+  const uint32_t q4 = q * 4;
+  const uint32_t lane_row = wave * 32 + half * kRowsPerLane;
+  const bool live = tile * kTileWords + q < row_words;
+  const uint32_t word_col = live ? tile * kTileWords + q : row_words - 1;
+  if (static_cast<uint32_t>(reinterpret_cast<size_t>((lds_i32*)bins)) != 0) {
+    if (tid == 0) atomicOr(o.status, 2u);
+    return;
+  }
+  int4* bins4 = reinterpret_cast<int4*>(bins);
+  PairAhead ah;
+  uint32_t wn[kRowsPerLane];  // the next batch's words
+  if (blockIdx.z < o.count) {
+    pair_setup_loads<G>(o, blockIdx.z, k0, kend, ah);
+    load_rows(code_rows(item_ptr<uint32_t>(o.in[2], o.stride[2], blockIdx.z), kend, row_words),
+              word_col, row_words, k0 + lane_row, wn);
+  }
+  for (uint32_t item = blockIdx.z; item < o.count; item += gridDim.z) {
+    const uint32_t* a_codes = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
+    const __amdgpu_buffer_rsrc_t b_rows =
+        code_rows(item_ptr<uint32_t>(o.in[2], o.stride[2], item), kend, row_words);
+    // The last batch loads the next instance's first batch (this one's when
+    // there is none, unused): the batch loads never sit behind a branch, so
+    // the wait before binning a batch leaves the following batch in flight.
+    const uint32_t next = item + gridDim.z;
+    const bool has_next = next < o.count;
+    const __amdgpu_buffer_rsrc_t next_rows =
+        code_rows(item_ptr<uint32_t>(o.in[2], o.stride[2], has_next ? next : item), kend,
+                  row_words);
+    const uint32_t a_word = ah.a_word;
+    __syncthreads();  // the previous instance's S and books are no longer read
+    if (tid < 16 * G) {
+      sa_book[tid] = ah.a_entry;
+      sb_book[tid] = ah.b_entry;
+    }
+#pragma unroll
+    for (int i = 0; i < kPairVec; ++i) bins4[tid + i * kPairThreads] = make_int4(0, 0, 0, 0);
+    __syncthreads();
+    if (tile == 0 && split == 0) sweep_books(sa_book, sb_book, 16 * G, o.status);
+    const float xmax = wave_book_absmax<G>(sa_book);
+    int shift = 0;
+    if (xmax > 0.0f) {
+      int ex;
+      frexpf(xmax, &ex);  // xmax < 2^ex, so xmax * kPairWindow < 2^(ex + 11)
+      shift = 30 - (ex + 11);
+      shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
+    }
+    const float unscale = ldexpf(1.0f, -shift);
+    float acc[kPairVec][4];
+#pragma unroll
+    for (int i = 0; i < kPairVec; ++i) acc[i][0] = acc[i][1] = acc[i][2] = acc[i][3] = 0.0f;
+
+    uint32_t xbase = k0;
+    stage_x1<G>(a_word, sa_book, xbase, kend, shift, sxq);
+    __syncthreads();
+    for (uint32_t kb = k0; kb < kend; kb += kPairBatchRows) {
+      uint32_t w[kRowsPerLane];
+#pragma unroll
+      for (int u = 0; u < kRowsPerLane; ++u) w[u] = wn[u];
+      const bool last = kb + kPairBatchRows >= kend;
+      load_rows(last ? next_rows : b_rows, word_col, row_words,
+                (last ? k0 : kb + kPairBatchRows) + lane_row, wn);
+      if (live) {
+        const int4* xr = reinterpret_cast<const int4*>(sxq + (kb + lane_row - xbase));
+        int32_t xs[kRowsPerLane];
+#pragma unroll
+        for (int i = 0; i < kRowsPerLane / 4; ++i) {
+          const int4 v = xr[i];
+          xs[4 * i] = v.x; xs[4 * i + 1] = v.y; xs[4 * i + 2] = v.z; xs[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int u = 0; u < kRowsPerLane; ++u) {
+          const int32_t xv = xs[u];
+          const uint32_t ww = w[u];
+          lds_add(pair_addr<0>(ww, q4), xv);
+          lds_add(pair_addr<1>(ww, q4), xv);
+          lds_add(pair_addr<2>(ww, q4), xv);
+          lds_add(pair_addr<3>(ww, q4), xv);
+        }
+      }
+      if (last && has_next) pair_setup_loads<G>(o, next, k0, kend, ah);
+      const uint32_t done = kb + kPairBatchRows;
+      const bool flush = done >= kend || (done - k0) % kPairWindow == 0;
+      const bool restage = done < kend && done - xbase >= kPairXRows;
+      if (flush || restage) {
+        // a restage reads its code word before the barrier
+        const uint32_t rword = restage ? stage_word(a_codes, done, kend, G) : 0u;
+        __syncthreads();
+        if (flush) {
+#pragma unroll
+          for (int i = 0; i < kPairVec; ++i) {
+            const int4 v = bins4[tid + i * kPairThreads];
+            acc[i][0] += float(v.x);
+            acc[i][1] += float(v.y);
+            acc[i][2] += float(v.z);
+            acc[i][3] += float(v.w);
+            if (done < kend) bins4[tid + i * kPairThreads] = make_int4(0, 0, 0, 0);
+          }
+        }
+        if (restage) {
+          xbase = done;
+          stage_x1<G>(rword, sa_book, xbase, kend, shift, sxq);
+        }
+        __syncthreads();
+      }
+    }
+    // pair bins in FP32, in place; then S for the tile's groups
+    float4* fb4 = reinterpret_cast<float4*>(smem);
+#pragma unroll
+    for (int i = 0; i < kPairVec; ++i)
+      fb4[tid + i * kPairThreads] = make_float4(acc[i][0] * unscale, acc[i][1] * unscale,
+                                                acc[i][2] * unscale, acc[i][3] * unscale);
+    __syncthreads();
+    // Thread idx takes word qq = idx % 32 (consecutive lanes read consecutive
+    // banks) and nibble n8 = 2p + s, code e of the rest: group j = 8 qq + n8.
+    const float* fb = reinterpret_cast<const float*>(smem);
+    float* pp = partial + ((uint64_t(item) * gridDim.x + tile) * gridDim.y + split) *
+                              (16 * kTileGroups);
+    for (uint32_t idx = tid; idx < 16 * kTileGroups; idx += kPairThreads) {
+      const uint32_t qq = idx % kTileWords, rest = idx / kTileWords;
+      const uint32_t n8 = rest % 8, e = rest / 8;
+      const uint32_t p = n8 / 2;
+      const uint32_t stride = (n8 & 1u) ? 1u : 16u;   // the other nibble's step in the byte
+      const uint32_t v0 = (n8 & 1u) ? 16u * e : e;
+      float sum = 0.0f;
+#pragma unroll
+      for (uint32_t other = 0; other < 16; ++other)
+        sum += fb[((v0 + stride * other) * 4 + p) * kTileWords + qq];
+      if (gridDim.y == 1) ss[idx] = sum;
+      else pp[(qq * 8 + n8) * 16 + e] = sum;  // the finish kernel's [j][e]
+    }
+    __syncthreads();
+
+    const uint32_t groups = (row_words - tile * kTileWords) < kTileWords
+                                ? (row_words - tile * kTileWords) * 8
+                                : kTileGroups;
+    if (gridDim.y == 1) {
+      // thread tid always takes column t = tid % G: its 16 book entries stay in registers
+      const uint32_t t = tid % G;
+      float cb[16];
+#pragma unroll
+      for (uint32_t c = 0; c < 16; ++c) cb[c] = sb_book[c * G + t];
+      float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
+      bool bad = false;
+      for (uint32_t e = tid; e < groups * G; e += kPairThreads) {
+        const uint32_t j = e / G;
+        const float* sj = ss + (j % 8) * kTileWords + j / 8;
+        float y = 0.0f;
+#pragma unroll
+        for (uint32_t c = 0; c < 16; ++c) y = fmaf(cb[c], sj[c * kTileGroups], y);
+        out[tile * kTileGroups * G + e] = y;
+        bad |= !finite_f32(y);
+      }
+      if (__any(bad) && (tid % warpSize) == 0) atomicOr(o.status, 1u);
+    }
+  }
+}
+
+size_t pairs_shmem(uint32_t g) {
+  return size_t(kPairBins) * 4 + kPairXRows * 4 + 2 * 16 * g * 4;
+}
+
 uint32_t gemv_splits(uint32_t n, uint32_t k, uint32_t group, uint32_t count) {
   const uint32_t tiles = (n / (8 * group) + kTileWords - 1) / kTileWords;
   const uint64_t blocks = uint64_t(tiles) * count;
@@ -456,6 +746,16 @@ uint32_t gemv_splits(uint32_t n, uint32_t k, uint32_t group, uint32_t count) {
   uint32_t splits = 1;
   while (blocks * splits < 256 && k / (splits * 2) >= 256) splits *= 2;
   return splits;
+}
+
+// Slices of k for GemvPairs: gemv_splits' count, each slice rounded up to
+// whole batches, and only the slices that hold rows.
+void pairs_slices(uint32_t n, uint32_t k, uint32_t group, uint32_t count, uint32_t* ks,
+                  uint32_t* splits) {
+  const uint32_t want = gemv_splits(n, k, group, count);
+  const uint32_t per = (k + want - 1) / want;
+  *ks = (per + kPairBatchRows - 1) / kPairBatchRows * kPairBatchRows;
+  *splits = (k + *ks - 1) / *ks;
 }
 
 size_t bins_shmem(uint32_t m, uint32_t g) {
@@ -487,6 +787,32 @@ hipError_t launch_bins_m(hipStream_t s, const Operands& o, uint32_t n, uint32_t 
 }
 
 template <int G>
+hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k, uint32_t flags,
+                        void* workspace) {
+  (void)flags;  // m = 1: A's flat index is the inner index either way
+  const uint32_t tiles = (n / (8 * G) + kTileWords - 1) / kTileWords;
+  uint32_t ks, splits;
+  pairs_slices(n, k, G, o.count, &ks, &splits);
+  // about one block per compute unit; each block walks its instances and
+  // loads the next one's set-up while it finishes the current one
+  const uint32_t per_z = tiles * splits;
+  uint32_t zc = per_z >= 256 ? 1u : 256u / per_z;
+  zc = zc < o.count ? zc : o.count;
+  const size_t shmem = pairs_shmem(G);
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_pairs<G>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
+  if (e != hipSuccess) return e;
+  dim3 grid(tiles, splits, zc);
+  k_gemv_pairs<G><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, static_cast<float*>(workspace));
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || splits == 1) return err;
+  dim3 fgrid(tiles * kFinishParts, 1, zc);
+  k_gemv_bins_finish<G, 1><<<fgrid, 256, 0, s>>>(o, n, splits, tiles,
+                                                 static_cast<const float*>(workspace));
+  return hipGetLastError();
+}
+
+template <int G>
 hipError_t launch_bins(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t flags, void* workspace) {
   switch (m) {
@@ -507,6 +833,7 @@ const char* matmul_path_name(MatmulPath p) {
   switch (p) {
     case MatmulPath::General: return "general";
     case MatmulPath::GemvBins: return "gemv-bins";
+    case MatmulPath::GemvPairs: return "gemv-pairs";
     case MatmulPath::GemvTable: return "gemv-table";
     case MatmulPath::GramMfma: return "gram-mfma";
     case MatmulPath::RowBins: return "row-bins";
@@ -519,7 +846,8 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
   if (policy == 1) return MatmulPath::General;
   if (count == 1 && rowbins_applies(m, n, k, group, flags)) return MatmulPath::RowBins;
   if (gram_applies(m, n, k, group, flags)) return MatmulPath::GramMfma;
-  if (m <= kGemvMaxM && (flags & 2u) == 0 && n % (8 * group) == 0) return MatmulPath::GemvBins;
+  if (m <= kGemvMaxM && (flags & 2u) == 0 && n % (8 * group) == 0)
+    return m == 1 ? MatmulPath::GemvPairs : MatmulPath::GemvBins;
   return MatmulPath::General;
 }
 
@@ -527,8 +855,12 @@ size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, 
                               uint32_t flags, uint32_t count) {
   (void)flags;
   if (p == MatmulPath::RowBins) return rowbins_workspace_bytes(n, k, group);
-  if (p != MatmulPath::GemvBins) return 0;
-  const uint32_t splits = gemv_splits(n, k, group, count);
+  if (p != MatmulPath::GemvBins && p != MatmulPath::GemvPairs) return 0;
+  uint32_t splits = gemv_splits(n, k, group, count);
+  if (p == MatmulPath::GemvPairs) {
+    uint32_t ks;
+    pairs_slices(n, k, group, count, &ks, &splits);
+  }
   if (splits == 1) return 0;
   const uint32_t tiles = (n / (8 * group) + kTileWords - 1) / kTileWords;
   return size_t(count) * splits * tiles * m * 16 * kTileGroups * sizeof(float);
@@ -540,6 +872,11 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins(s, o, m, n, k, group, workspace);
   if (path == MatmulPath::GramMfma) return launch_gram(s, o, m, n, k, group);
+  if (path == MatmulPath::GemvPairs) {
+    if (group == 8) return launch_pairs<8>(s, o, n, k, flags, workspace);
+    if (group == 16) return launch_pairs<16>(s, o, n, k, flags, workspace);
+    return launch_pairs<32>(s, o, n, k, flags, workspace);
+  }
   if (path == MatmulPath::GemvBins) {
     if (group == 8) return launch_bins<8>(s, o, m, n, k, flags, workspace);
     if (group == 16) return launch_bins<16>(s, o, m, n, k, flags, workspace);

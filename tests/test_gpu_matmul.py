@@ -84,8 +84,8 @@ def test_gemv_bins_within_tolerance(vqdev, oracle, m):
     rng = np.random.default_rng(50 + m)
     for k, n, group in GEMV_SHAPES:
         words = (2, m, n, k, group, 16, 0, 0)
-        assert vqdev.path_name(words) == "gemv-bins"
-        say("gemv-bins", m, k, n, group)
+        assert vqdev.path_name(words) == ("gemv-pairs" if m == 1 else "gemv-bins")
+        say("gemv", m, k, n, group)
         ops = _operands(rng, m, n, k, group, 1.0, 0.02)
         out, status = _gpu(vqdev, ops, m, n, k, group, 0)
         assert status == 0
@@ -121,7 +121,7 @@ def test_gemv_bins_batched(vqdev, oracle):
         assert o.max_rel(out[i], ref) <= TOL
 
 
-@pytest.mark.parametrize("m", [3, 5, 8])
+@pytest.mark.parametrize("m", [1, 3, 5, 8])
 def test_gemv_bins_long_slices(vqdev, oracle, m):
     """256 instances fill the chip without splitting k, so each block walks
     all 2600 rows: several integer windows, and the staged activations are
@@ -135,6 +135,24 @@ def test_gemv_bins_long_slices(vqdev, oracle, m):
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
     for i in (0, 1, 128, 255):
+        ref, _ = oracle.matmul(*items[i], m, n, k, group, 0)
+        assert o.max_rel(out[i], ref) <= TOL
+        assert o.max_rel(out[i], _ref64(items[i], m, n, k, group, 0)) <= TOL
+
+
+def test_gemv_pairs_restaged_activations(vqdev, oracle):
+    """m = 1 over 9000 rows in one slice: nine integer windows and two
+    restages of the 4096-row activation chunk."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(91)
+    m, k, n, group, count = 1, 9000, 256, 16, 256
+    items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
+    ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
+    say("gemv-pairs restaged", count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    for i in (0, 77, 255):
         ref, _ = oracle.matmul(*items[i], m, n, k, group, 0)
         assert o.max_rel(out[i], ref) <= TOL
         assert o.max_rel(out[i], _ref64(items[i], m, n, k, group, 0)) <= TOL
