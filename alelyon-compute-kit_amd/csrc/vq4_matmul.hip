@@ -455,273 +455,389 @@ __global__ __launch_bounds__(256) void k_gemv_bins_finish(Operands o, uint32_t n
 // 256-way "pair bin" indexed by the whole byte replaces GemvBins' two:
 //   S[2p][e]   = sum over hi of P[p][16 hi + e]   (low nibble = group 8q+2p)
 //   S[2p+1][e] = sum over lo of P[p][16 e + lo]   (high nibble = group 8q+2p+1)
-// Pair bins are laid out [byte value][pair p][word q] (128 KiB for a 32-word
-// tile), so a bin address is (byte << 9) | (p << 7) | 4q: p is an immediate
-// offset and the 32 lanes of a half-wave hit 32 distinct banks.
 //
-// Integer windows are kPairWindow rows: x is scaled so that
-// max|x| * 2^shift * kPairWindow < 2^30 (a quantisation step of 2^-20 of
-// max|x|), and the bins are flushed into FP32 registers once per window.
-// Every load of the main loop is unconditional: rows past the slice read as
-// zero words through the buffer descriptor's range and meet x = 0; dead words
-// are clamped to the last word and never binned.
+// Bin of byte value v at byte position p of word column q (32-word tile):
+//   dword (p >> 1) * 16384 + v * 64 + (p & 1) * 32 + q
+// so the 32 lanes of a half-wave (one word column each) hit 32 distinct banks,
+// and the byte address is a single v_perm of the code word with a per-lane
+// constant: byte 0 = 4q (+128 for odd p), byte 1 = v, byte 2 = the region.
+//
+// Pipeline: each lane owns R rows of its word column per batch; D register
+// buffers form a ring (the loop is unrolled by D, so no in-flight register is
+// ever copied and the compiler never waits for more than the batch it bins).
+// The last D batches of an instance refill with the next instance's first D,
+// and an instance's set-up data (A words of the slice, one entry of each
+// book) is requested one instance ahead, so loads stay in flight across set-up
+// and finalisation. x is staged per row as int32 in LDS; the next batch's x is
+// read before the current batch's atomics (LDS ops complete in order, so a
+// read issued after them would wait for them).
+//
+// Integer windows are kPairWindow rows: x is scaled so that max|x| * 2^shift
+// < 2^19 and rounded values are capped at 2^19 - 1, so a window's sums stay
+// inside int32 (|sum| <= 4096 * 2^19 = 2^31 only for negative sums). The
+// quantisation step is at most 2^-19 of max|x|.
+//
+// Finalisation: each thread flushes one 8 x 8 (or SH x SL) sub-block of the
+// 16 x 16 pair-bin matrix of one (p, q), conflict-free (lanes are word
+// columns); row and column sums are taken in registers and only those
+// partials go through LDS.
 constexpr int kPairThreads = 512;
 constexpr int kPairWaves = kPairThreads / 64;
-constexpr uint32_t kPairBatchRows = kPairWaves * 2 * kRowsPerLane;  // 256 rows per batch
+constexpr int kPairR = 16;                                          // rows per lane per batch
+constexpr int kPairD = 4;                                           // batches in the ring
+constexpr uint32_t kPairBatchRows = kPairWaves * 2 * kPairR;        // 256 rows per batch
 constexpr uint32_t kPairBins = 256 * 4 * kTileWords;                // 32768
-constexpr uint32_t kPairXRows = 8 * kPairThreads;                   // staged x rows (16 KiB)
-constexpr uint32_t kPairWindow = 2048;
-constexpr int kPairVec = kPairBins / (4 * kPairThreads);            // int4 bins per thread
+constexpr uint32_t kPairXRows = 4096;                               // staged x rows (16 KiB)
+constexpr uint32_t kPairWindow = 4096;
+constexpr uint32_t kPairMaxAWords = 2 * kPairThreads;               // A words of one slice
+constexpr int kPairHB = 2, kPairLB = 2;                             // sub-blocks per (p, q)
+constexpr int kPairSH = 16 / kPairHB, kPairSL = 16 / kPairLB;
 static_assert(kPairWindow % kPairBatchRows == 0 && kPairXRows % kPairBatchRows == 0, "batches");
+static_assert(kPairSH * kPairSL * kPairThreads == int(kPairBins), "every bin flushed once");
+static_assert(kPairThreads / kTileWords == 4 * kPairHB * kPairLB, "thread roles");
 static_assert(kPairXRows >= 16 * kTileGroups, "S reuses the x staging area");
 
-template <int BYTE>
-__device__ __forceinline__ uint32_t pair_addr(uint32_t w, uint32_t q4) {
-  return ((__builtin_amdgcn_ubfe(w, 8 * BYTE, 8) << 9) | q4) + BYTE * 128;
-}
-
-// Buffer descriptor over the first `rows` rows of a code matrix: raw buffer
-// loads past it return zero, which is how rows past a slice read.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t code_rows(const uint32_t* codes, uint32_t rows,
-                                                            uint32_t row_words) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(codes), 0,
-                                           int(rows * row_words * 4u), 0x00020000);
-}
-
-// This lane's 16 words of a batch from word column `col`, rows first ..
-// first+15: one 32-bit byte offset per load (a matrix holds fewer than 2^30
-// words), no 64-bit address arithmetic.
-__device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t rs, uint32_t col,
-                                          uint32_t row_words, uint32_t first,
-                                          uint32_t (&w)[kRowsPerLane]) {
-  const uint32_t base = (first * row_words + col) * 4u;
-#pragma unroll
-  for (int u = 0; u < kRowsPerLane; ++u)
-    w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, base + u * row_words * 4u, 0, 0));
-}
-
-// Largest |value| of a 16 x G book in LDS, per wave.
+// LDS layout (bytes): bins | staged x (later S) | A book | B book | A words | row maxima.
 template <int G>
-__device__ float wave_book_absmax(const float* sbook) {
-  float v = 0.0f;
-  for (uint32_t i = threadIdx.x % 64; i < 16 * G; i += 64) v = fmaxf(v, fabsf(sbook[i]));
-  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
-  return v;
-}
-
-// x rows [xbase, xbase + kPairXRows) of the single row of A, scaled by
-// 2^shift and rounded, into sxq; rows at or past kend are zero. Thread t
-// stages rows 8t .. 8t+7, which lie in one group of A (8 divides G and
-// xbase); `a_word` is the code word holding that group's nibble.
-template <int G>
-__device__ void stage_x1(uint32_t a_word, const float* sa_book, uint32_t xbase, uint32_t kend,
-                         int shift, int32_t* sxq) {
-  const uint32_t r0 = xbase + 8 * threadIdx.x;
-  int32_t v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  if (r0 < kend) {
-    const uint32_t code = (a_word >> (((r0 / G) & 7u) * 4u)) & 15u;
-    const float4* c = reinterpret_cast<const float4*>(sa_book + code * G + r0 % G);
-    const float4 c0 = c[0], c1 = c[1];
-    const float x[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      v[i] = (r0 + i < kend) ? int32_t(rintf(ldexpf(x[i], shift))) : 0;
-  }
-  int4* dst = reinterpret_cast<int4*>(sxq + 8 * threadIdx.x);
-  dst[0] = make_int4(v[0], v[1], v[2], v[3]);
-  dst[1] = make_int4(v[4], v[5], v[6], v[7]);
-}
-
-__device__ __forceinline__ uint32_t stage_word(const uint32_t* a_codes, uint32_t xbase,
-                                               uint32_t kend, uint32_t group) {
-  const uint32_t r0 = xbase + 8 * threadIdx.x;
-  return r0 < kend ? a_codes[(r0 / group) >> 3] : 0u;
-}
-
-// What an instance's set-up reads from global memory besides its first batch
-// of B words, loaded during the previous instance: this thread's staging code
-// word and one entry of each book (16 * G <= kPairThreads).
-struct PairAhead {
-  uint32_t a_word;
-  float a_entry, b_entry;
+struct PairLds {
+  static constexpr uint32_t xs = kPairBins * 4;
+  static constexpr uint32_t af = xs + kPairXRows * 4;
+  static constexpr uint32_t bb = af + 16 * G * 4;
+  static constexpr uint32_t aw = bb + 16 * G * 4;
+  static constexpr uint32_t rmax = aw + kPairMaxAWords * 4;
+  static constexpr uint32_t total = rmax + 16 * 4;
 };
 
-template <int G>
-__device__ __forceinline__ void pair_setup_loads(const Operands& o, uint32_t item, uint32_t k0,
-                                                 uint32_t kend, PairAhead& ah) {
-  const uint32_t* a_codes = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
-  const float* a_book = item_ptr<float>(o.in[1], o.stride[1], item);
-  const float* b_book = item_ptr<float>(o.in[3], o.stride[3], item);
-  ah.a_word = stage_word(a_codes, k0, kend, G);
-  const uint32_t i = threadIdx.x < 16 * G ? threadIdx.x : 0;
-  ah.a_entry = a_book[i];
-  ah.b_entry = b_book[i];
+__device__ __forceinline__ uint32_t pair_dword(uint32_t v, uint32_t p, uint32_t q) {
+  return (p >> 1) * 16384 + v * 64 + (p & 1) * 32 + q;
 }
 
+// Buffer descriptor over the first `bytes` of an array: raw buffer loads past
+// it return zero, which is how rows past a slice (or a missing instance) read.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t words_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+
+struct PairAhead {
+  uint32_t w0, w1;  // A words tid and tid + kPairThreads of the slice
+  float a, b;       // entry tid of the A and B books
+};
+
 // grid: (n tiles, k splits, z); block z serves instances z, z + gridDim.z, ...
-// ks is a multiple of kPairBatchRows. Dynamic shared memory: pair bins,
-// staged x (later S), the A and B books.
+// ks is a multiple of kPairBatchRows.
 template <int G>
-__global__ __launch_bounds__(kPairThreads) void k_gemv_pairs(Operands o, uint32_t n, uint32_t k,
-                                                             uint32_t ks, float* partial) {
+__global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint32_t n,
+                                                                uint32_t k, uint32_t ks,
+                                                                float* partial) {
+  constexpr uint32_t R = kPairR, D = kPairD, BR = kPairBatchRows;
+  constexpr int kSPer = 16 * kTileGroups / kPairThreads;
   static_assert(16 * G <= kPairThreads, "one book entry per thread");
+  static_assert(D % 2 == 0, "x buffers alternate by batch parity");
+  using L = PairLds<G>;
   extern __shared__ int32_t smem[];
+  char* lds = reinterpret_cast<char*>(smem);
   int32_t* bins = smem;
-  int32_t* sxq = smem + kPairBins;
-  float* ss = reinterpret_cast<float*>(sxq);  // S after the main loop: [e][n8][q]
-  float* sa_book = reinterpret_cast<float*>(sxq + kPairXRows);
-  float* sb_book = sa_book + 16 * G;
-  const uint32_t tid = threadIdx.x;
-  const uint32_t tile = blockIdx.x, split = blockIdx.y;
-  const uint32_t row_words = n / (8 * G);
-  const uint32_t k0 = split * ks;
-  const uint32_t kend = (k0 + ks) < k ? (k0 + ks) : k;
-  const uint32_t lane = tid % 64, wave = tid / 64;
-  const uint32_t q = lane % 32, half = lane / 32;
-  const uint32_t q4 = q * 4;
-  const uint32_t lane_row = wave * 32 + half * kRowsPerLane;
-  const bool live = tile * kTileWords + q < row_words;
-  const uint32_t word_col = live ? tile * kTileWords + q : row_words - 1;
-  if (static_cast<uint32_t>(reinterpret_cast<size_t>((lds_i32*)bins)) != 0) {
-    if (tid == 0) atomicOr(o.status, 2u);
+  int4* bins4 = reinterpret_cast<int4*>(smem);
+  int32_t* sx = reinterpret_cast<int32_t*>(lds + L::xs);
+  float* af = reinterpret_cast<float*>(lds + L::af);
+  float* bb = reinterpret_cast<float*>(lds + L::bb);
+  uint32_t* aw = reinterpret_cast<uint32_t*>(lds + L::aw);
+  float* rmax = reinterpret_cast<float*>(lds + L::rmax);
+  // Defensive: the perm-built bin addresses assume the bins start at LDS 0.
+  if (static_cast<uint32_t>(reinterpret_cast<size_t>((lds_i32*)smem)) != 0) {
+    if (threadIdx.x == 0) atomicOr(o.status, 2u);
     return;
   }
-  int4* bins4 = reinterpret_cast<int4*>(bins);
-  PairAhead ah;
-  uint32_t wn[kRowsPerLane];  // the next batch's words
-  if (blockIdx.z < o.count) {
-    pair_setup_loads<G>(o, blockIdx.z, k0, kend, ah);
-    load_rows(code_rows(item_ptr<uint32_t>(o.in[2], o.stride[2], blockIdx.z), kend, row_words),
-              word_col, row_words, k0 + lane_row, wn);
-  }
-  for (uint32_t item = blockIdx.z; item < o.count; item += gridDim.z) {
-    const uint32_t* a_codes = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
-    const __amdgpu_buffer_rsrc_t b_rows =
-        code_rows(item_ptr<uint32_t>(o.in[2], o.stride[2], item), kend, row_words);
-    // The last batch loads the next instance's first batch (this one's when
-    // there is none, unused): the batch loads never sit behind a branch, so
-    // the wait before binning a batch leaves the following batch in flight.
-    const uint32_t next = item + gridDim.z;
-    const bool has_next = next < o.count;
-    const __amdgpu_buffer_rsrc_t next_rows =
-        code_rows(item_ptr<uint32_t>(o.in[2], o.stride[2], has_next ? next : item), kend,
-                  row_words);
-    const uint32_t a_word = ah.a_word;
-    __syncthreads();  // the previous instance's S and books are no longer read
-    if (tid < 16 * G) {
-      sa_book[tid] = ah.a_entry;
-      sb_book[tid] = ah.b_entry;
-    }
+  const uint32_t tid = threadIdx.x;
+  const uint32_t tile = blockIdx.x, split = blockIdx.y, zn = gridDim.z;
+  const uint32_t rw = n / (8 * G);
+  const uint32_t k0 = split * ks;
+  const uint32_t kend = (k0 + ks) < k ? (k0 + ks) : k;
+  const uint32_t nb = (kend - k0 + BR - 1) / BR;
+  const uint32_t nbp = (nb + D - 1) / D * D;  // padded batches read zero words and x
+  const uint32_t lane = tid % 64, wave = tid / 64;
+  const uint32_t q = lane % 32, half = lane / 32;
+  const uint32_t lane_row = (wave * 2 + half) * R;
+  // dead word columns (rw not a multiple of the tile) bin the last column into
+  // bins no output reads
+  const uint32_t col = (tile * kTileWords + q < rw) ? tile * kTileWords + q : rw - 1;
+  const uint32_t lc = (q * 4) | ((q * 4 + 128) << 8) | (1u << 16);
+  constexpr uint32_t kSel[4] = {0x0c0c0400u, 0x0c0c0501u, 0x0c020600u, 0x0c020701u};
+  const uint32_t a_w0 = k0 / G / 8;
+  const uint32_t a_words = (kend - 1) / G / 8 - a_w0 + 1;
+
+  // Opaque copies of the thread index keep per-phase addresses from being
+  // hoisted out of the instance loop and held live through the main loop.
+  auto opaque = [](uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+  };
+  auto setup_loads = [&](uint32_t item) {
+    const uint32_t lt = opaque(tid);
+    const __amdgpu_buffer_rsrc_t ars =
+        words_rsrc(item_ptr<uint32_t>(o.in[0], o.stride[0], item) + a_w0, a_words * 4u);
+    const __amdgpu_buffer_rsrc_t abk = words_rsrc(item_ptr<float>(o.in[1], o.stride[1], item), 64u * G);
+    const __amdgpu_buffer_rsrc_t bbk = words_rsrc(item_ptr<float>(o.in[3], o.stride[3], item), 64u * G);
+    PairAhead h;
+    h.a = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(abk, lt * 4u, 0, 0)));
+    h.b = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(bbk, lt * 4u, 0, 0)));
+    h.w0 = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(ars, lt * 4u, 0, 0));
+    h.w1 = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(ars, (lt + kPairThreads) * 4u, 0, 0));
+    return h;
+  };
+  auto batch_rsrc = [&](uint32_t item) {
+    const bool real = item < o.count;
+    return words_rsrc(item_ptr<uint32_t>(o.in[2], o.stride[2], real ? item : 0),
+                      real ? kend * rw * 4u : 0u);
+  };
+  const uint32_t voff_lane = (lane_row * rw + col) * 4u;
+  auto load_batch = [&](__amdgpu_buffer_rsrc_t rs, uint32_t b, uint32_t (&w)[R]) {
+    uint32_t off = voff_lane + (k0 + b * BR) * rw * 4u;
+    asm volatile("" : "+v"(off));  // per-row offsets formed next to each load
 #pragma unroll
-    for (int i = 0; i < kPairVec; ++i) bins4[tid + i * kPairThreads] = make_int4(0, 0, 0, 0);
+    for (uint32_t u = 0; u < R; ++u)
+      w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, off + u * rw * 4u, 0, 0));
+  };
+
+  uint32_t buf[D][R];
+  int32_t xa[R], xb[R];
+  float acc[kPairSH][kPairSL];
+  int shift = 0;
+  uint32_t xbase = k0;
+
+  // rows [xb0, xb0 + kPairXRows) of A's single row, quantised; zero past kend
+  auto stage_x = [&](uint32_t xb0) __attribute__((always_inline)) {
+    for (uint32_t r4 = opaque(tid) * 4; r4 < kPairXRows; r4 += 4 * kPairThreads) {
+      const uint32_t row = xb0 + r4;
+      int4 v = make_int4(0, 0, 0, 0);
+      if (row < kend) {
+        const uint32_t u = row / G;
+        const uint32_t code = (aw[(u >> 3) - a_w0] >> ((u & 7u) * 4u)) & 15u;
+        const float4 f = *reinterpret_cast<const float4*>(af + code * G + row % G);
+        const float lim = 524287.0f;  // 2^19 - 1
+        v.x = int32_t(fminf(rintf(ldexpf(f.x, shift)), lim));
+        v.y = row + 1 < kend ? int32_t(fminf(rintf(ldexpf(f.y, shift)), lim)) : 0;
+        v.z = row + 2 < kend ? int32_t(fminf(rintf(ldexpf(f.z, shift)), lim)) : 0;
+        v.w = row + 3 < kend ? int32_t(fminf(rintf(ldexpf(f.w, shift)), lim)) : 0;
+      }
+      *reinterpret_cast<int4*>(sx + r4) = v;
+    }
+  };
+  auto read_x = [&](uint32_t b, int32_t (&xs)[R]) __attribute__((always_inline)) {
+    asm volatile("" : "+s"(b));
+    if (k0 + b * BR >= kend) {  // a padding batch: nothing staged for it
+#pragma unroll
+      for (uint32_t u = 0; u < R; ++u) xs[u] = 0;
+      return;
+    }
+    const int4* xr = reinterpret_cast<const int4*>(sx + (k0 + b * BR + lane_row - xbase));
+#pragma unroll
+    for (uint32_t c4 = 0; c4 < R / 4; ++c4) {
+      const int4 v = xr[c4];
+      xs[4 * c4] = v.x; xs[4 * c4 + 1] = v.y; xs[4 * c4 + 2] = v.z; xs[4 * c4 + 3] = v.w;
+    }
+  };
+  // this thread's sub-block: word column fq, byte position fp, sub-block (fh, fl)
+  auto flush = [&](bool clear) __attribute__((always_inline)) {
+    const uint32_t ft = opaque(tid);
+    const uint32_t fq = ft % kTileWords, fc = ft / kTileWords;
+    const uint32_t fp = fc % 4, fs = fc / 4;
+    const uint32_t fh = fs % kPairHB, fl = fs / kPairHB;
+#pragma unroll
+    for (int a = 0; a < kPairSH; ++a)
+#pragma unroll
+      for (int c = 0; c < kPairSL; ++c) {
+        const uint32_t d = pair_dword(16 * (fh * kPairSH + a) + fl * kPairSL + c, fp, fq);
+        acc[a][c] += float(bins[d]);
+        if (clear) bins[d] = 0;
+      }
+  };
+  auto stage = [&](uint32_t (&w)[R], uint32_t b, int32_t (&xs)[R], int32_t (&xn)[R],
+                   __amdgpu_buffer_rsrc_t rs_refill, uint32_t b_refill)
+                   __attribute__((always_inline)) {
+    asm volatile("" : "+s"(b));  // row arithmetic is redone per batch, not strength-reduced
+    const uint32_t done = (b + 1) * BR;
+    const bool last = b + 1 == nbp;
+    const bool restage = k0 + done < kend && k0 + done - xbase >= kPairXRows;
+    const bool wend = done % kPairWindow == 0 || last;
+    if (!restage && !last) read_x(b + 1, xn);
+    if (b < nb) {  // padding batches (past the slice) bin nothing
+#pragma unroll
+      for (uint32_t u = 0; u < R; ++u) {
+        const uint32_t ww = w[u];
+        const int32_t xv = xs[u];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) lds_add(__builtin_amdgcn_perm(ww, lc, kSel[p]), xv);
+      }
+    }
+    load_batch(rs_refill, b_refill, w);
+    __builtin_amdgcn_sched_barrier(0);
+    if (wend) {
+      __syncthreads();
+      flush(!last);
+      if (!last && !restage) __syncthreads();
+    }
+    if (restage) {
+      if (!wend) __syncthreads();
+      xbase = k0 + done;
+      stage_x(xbase);
+      __syncthreads();
+      read_x(b + 1, xn);
+      // settle here, so at the join the common path's x (read a batch
+      // earlier) needs no wait behind this batch's atomics
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+    }
+  };
+
+  uint32_t item = blockIdx.z;
+  PairAhead cur{}, nxt{};
+  if (item < o.count) {
+    cur = setup_loads(item);
+    nxt = setup_loads(item + zn < o.count ? item + zn : item);
+    const __amdgpu_buffer_rsrc_t r0 = batch_rsrc(item);
+#pragma unroll
+    for (uint32_t d = 0; d < D; ++d) load_batch(r0, d, buf[d]);
+  }
+  for (; item < o.count; item += zn) {
+    const uint32_t next = item + zn;
+    const __amdgpu_buffer_rsrc_t cur_rs = batch_rsrc(item);
+    const __amdgpu_buffer_rsrc_t next_rs = batch_rsrc(next);
+    // ---- set-up ----
+    const uint32_t st = opaque(tid);
+    __syncthreads();  // the previous instance's S and books are no longer read
+    if (st < 16 * G) { af[st] = cur.a; bb[st] = cur.b; }
+    if (st < a_words) aw[st] = cur.w0;
+    if (st + kPairThreads < a_words) aw[st + kPairThreads] = cur.w1;
+#pragma unroll
+    for (uint32_t i = 0; i < kPairBins / (4 * kPairThreads); ++i)
+      bins4[st + i * kPairThreads] = make_int4(0, 0, 0, 0);
     __syncthreads();
-    if (tile == 0 && split == 0) sweep_books(sa_book, sb_book, 16 * G, o.status);
-    const float xmax = wave_book_absmax<G>(sa_book);
-    int shift = 0;
-    if (xmax > 0.0f) {
+    if (tile == 0 && split == 0) sweep_books(af, bb, 16 * G, o.status);
+    // largest |A book entry|: 16 row maxima, then every thread reads them
+    if (st < 16) {
+      float m = 0.0f;
+#pragma unroll
+      for (int t = 0; t < G; t += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(af + st * G + t);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+      }
+      rmax[st] = m;
+    }
+    __syncthreads();
+    float amax = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 16; t += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(rmax + t);
+      amax = fmaxf(amax, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+    }
+    shift = 0;
+    if (amax > 0.0f) {
       int ex;
-      frexpf(xmax, &ex);  // xmax < 2^ex, so xmax * kPairWindow < 2^(ex + 11)
-      shift = 30 - (ex + 11);
+      frexpf(amax, &ex);  // amax < 2^ex: max|x| * 2^shift < 2^19
+      shift = 31 - (ex + 12);
       shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
     }
     const float unscale = ldexpf(1.0f, -shift);
-    float acc[kPairVec][4];
-#pragma unroll
-    for (int i = 0; i < kPairVec; ++i) acc[i][0] = acc[i][1] = acc[i][2] = acc[i][3] = 0.0f;
-
-    uint32_t xbase = k0;
-    stage_x1<G>(a_word, sa_book, xbase, kend, shift, sxq);
+    xbase = k0;
+    stage_x(xbase);
     __syncthreads();
-    for (uint32_t kb = k0; kb < kend; kb += kPairBatchRows) {
-      uint32_t w[kRowsPerLane];
+    read_x(0, xa);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // settle the first x before the loop
+    // the next instance's set-up data moves up; the one after is requested now
+    cur = nxt;
+    nxt = setup_loads(next + zn < o.count ? next + zn : item);
 #pragma unroll
-      for (int u = 0; u < kRowsPerLane; ++u) w[u] = wn[u];
-      const bool last = kb + kPairBatchRows >= kend;
-      load_rows(last ? next_rows : b_rows, word_col, row_words,
-                (last ? k0 : kb + kPairBatchRows) + lane_row, wn);
-      if (live) {
-        const int4* xr = reinterpret_cast<const int4*>(sxq + (kb + lane_row - xbase));
-        int32_t xs[kRowsPerLane];
+    for (int a = 0; a < kPairSH; ++a)
 #pragma unroll
-        for (int i = 0; i < kRowsPerLane / 4; ++i) {
-          const int4 v = xr[i];
-          xs[4 * i] = v.x; xs[4 * i + 1] = v.y; xs[4 * i + 2] = v.z; xs[4 * i + 3] = v.w;
-        }
+      for (int c = 0; c < kPairSL; ++c) acc[a][c] = 0.0f;
+
+    // ---- main loop: all but the last D batches refill from this instance ----
+    for (uint32_t b0 = 0; b0 + D < nbp; b0 += D) {
 #pragma unroll
-        for (int u = 0; u < kRowsPerLane; ++u) {
-          const int32_t xv = xs[u];
-          const uint32_t ww = w[u];
-          lds_add(pair_addr<0>(ww, q4), xv);
-          lds_add(pair_addr<1>(ww, q4), xv);
-          lds_add(pair_addr<2>(ww, q4), xv);
-          lds_add(pair_addr<3>(ww, q4), xv);
-        }
-      }
-      if (last && has_next) pair_setup_loads<G>(o, next, k0, kend, ah);
-      const uint32_t done = kb + kPairBatchRows;
-      const bool flush = done >= kend || (done - k0) % kPairWindow == 0;
-      const bool restage = done < kend && done - xbase >= kPairXRows;
-      if (flush || restage) {
-        // a restage reads its code word before the barrier
-        const uint32_t rword = restage ? stage_word(a_codes, done, kend, G) : 0u;
-        __syncthreads();
-        if (flush) {
-#pragma unroll
-          for (int i = 0; i < kPairVec; ++i) {
-            const int4 v = bins4[tid + i * kPairThreads];
-            acc[i][0] += float(v.x);
-            acc[i][1] += float(v.y);
-            acc[i][2] += float(v.z);
-            acc[i][3] += float(v.w);
-            if (done < kend) bins4[tid + i * kPairThreads] = make_int4(0, 0, 0, 0);
-          }
-        }
-        if (restage) {
-          xbase = done;
-          stage_x1<G>(rword, sa_book, xbase, kend, shift, sxq);
-        }
-        __syncthreads();
+      for (uint32_t d = 0; d < D; d += 2) {
+        stage(buf[d], b0 + d, xa, xb, cur_rs, b0 + d + D);
+        stage(buf[d + 1], b0 + d + 1, xb, xa, cur_rs, b0 + d + 1 + D);
       }
     }
-    // pair bins in FP32, in place; then S for the tile's groups
-    float4* fb4 = reinterpret_cast<float4*>(smem);
 #pragma unroll
-    for (int i = 0; i < kPairVec; ++i)
-      fb4[tid + i * kPairThreads] = make_float4(acc[i][0] * unscale, acc[i][1] * unscale,
-                                                acc[i][2] * unscale, acc[i][3] * unscale);
-    __syncthreads();
-    // Thread idx takes word qq = idx % 32 (consecutive lanes read consecutive
-    // banks) and nibble n8 = 2p + s, code e of the rest: group j = 8 qq + n8.
-    const float* fb = reinterpret_cast<const float*>(smem);
-    float* pp = partial + ((uint64_t(item) * gridDim.x + tile) * gridDim.y + split) *
-                              (16 * kTileGroups);
-    for (uint32_t idx = tid; idx < 16 * kTileGroups; idx += kPairThreads) {
-      const uint32_t qq = idx % kTileWords, rest = idx / kTileWords;
-      const uint32_t n8 = rest % 8, e = rest / 8;
-      const uint32_t p = n8 / 2;
-      const uint32_t stride = (n8 & 1u) ? 1u : 16u;   // the other nibble's step in the byte
-      const uint32_t v0 = (n8 & 1u) ? 16u * e : e;
-      float sum = 0.0f;
+    for (uint32_t d = 0; d < D; d += 2) {
+      stage(buf[d], nbp - D + d, xa, xb, next_rs, d);
+      stage(buf[d + 1], nbp - D + d + 1, xb, xa, next_rs, d + 1);
+    }
+
+    // ---- finalise: sub-block row/column sums, one exchange, S, outputs ----
+    const uint32_t ft = opaque(tid);
+    const uint32_t fq = ft % kTileWords, fc = ft / kTileWords;
+    const uint32_t fp = fc % 4, fs = fc / 4;
+    const uint32_t fh = fs % kPairHB, fl = fs / kPairHB;
+    float* pl = reinterpret_cast<float*>(smem);           // [HB][4][16 lo][32 q]
+    float* ph = pl + kPairHB * 4 * 16 * kTileWords;       // [LB][4][16 hi][32 q]
+    __syncthreads();  // every thread has flushed its bins
 #pragma unroll
-      for (uint32_t other = 0; other < 16; ++other)
-        sum += fb[((v0 + stride * other) * 4 + p) * kTileWords + qq];
-      if (gridDim.y == 1) ss[idx] = sum;
-      else pp[(qq * 8 + n8) * 16 + e] = sum;  // the finish kernel's [j][e]
+    for (int c = 0; c < kPairSL; ++c) {
+      float s = 0.0f;
+#pragma unroll
+      for (int a = 0; a < kPairSH; ++a) s += acc[a][c];
+      pl[((fh * 4 + fp) * 16 + fl * kPairSL + c) * kTileWords + fq] = s * unscale;
+    }
+#pragma unroll
+    for (int a = 0; a < kPairSH; ++a) {
+      float s = 0.0f;
+#pragma unroll
+      for (int c = 0; c < kPairSL; ++c) s += acc[a][c];
+      ph[((fl * 4 + fp) * 16 + fh * kPairSH + a) * kTileWords + fq] = s * unscale;
     }
     __syncthreads();
-
-    const uint32_t groups = (row_words - tile * kTileWords) < kTileWords
-                                ? (row_words - tile * kTileWords) * 8
-                                : kTileGroups;
+    float sv[kSPer];
+#pragma unroll
+    for (int j = 0; j < kSPer; ++j) {
+      // S entry (e, nibble n8 = 2 p + kind, word column qq)
+      const uint32_t s_ = ft + j * kPairThreads;
+      const uint32_t qq = s_ % kTileWords, rest = s_ / kTileWords;
+      const uint32_t e = rest % 16, n8 = rest / 16;
+      const uint32_t pp_ = n8 / 2;
+      float v = 0.0f;
+      if ((n8 & 1u) == 0) {
+#pragma unroll
+        for (int h = 0; h < kPairHB; ++h) v += pl[((h * 4 + pp_) * 16 + e) * kTileWords + qq];
+      } else {
+#pragma unroll
+        for (int l = 0; l < kPairLB; ++l) v += ph[((l * 4 + pp_) * 16 + e) * kTileWords + qq];
+      }
+      sv[j] = v;
+    }
+    float* ss = reinterpret_cast<float*>(sx);  // [e][n8][q]
     if (gridDim.y == 1) {
-      // thread tid always takes column t = tid % G: its 16 book entries stay in registers
-      const uint32_t t = tid % G;
+#pragma unroll
+      for (int j = 0; j < kSPer; ++j) {
+        const uint32_t s_ = ft + j * kPairThreads;
+        const uint32_t qq = s_ % kTileWords, rest = s_ / kTileWords;
+        ss[((rest % 16) * 8 + rest / 16) * kTileWords + qq] = sv[j];
+      }
+    } else {
+      // the finish kernel's [j][e] with j = 8 qq + n8
+      float* pp = partial + ((uint64_t(item) * gridDim.x + tile) * gridDim.y + split) *
+                                (16 * kTileGroups);
+#pragma unroll
+      for (int j = 0; j < kSPer; ++j) {
+        const uint32_t s_ = ft + j * kPairThreads;
+        const uint32_t qq = s_ % kTileWords, rest = s_ / kTileWords;
+        pp[(qq * 8 + rest / 16) * 16 + rest % 16] = sv[j];
+      }
+    }
+    __syncthreads();
+    if (gridDim.y == 1) {
+      const uint32_t groups = (rw - tile * kTileWords) < kTileWords
+                                  ? (rw - tile * kTileWords) * 8
+                                  : kTileGroups;
+      // thread ft always takes column t = ft % G: its 16 book entries stay in registers
+      const uint32_t t = ft % G;
       float cb[16];
 #pragma unroll
-      for (uint32_t c = 0; c < 16; ++c) cb[c] = sb_book[c * G + t];
+      for (uint32_t c = 0; c < 16; ++c) cb[c] = bb[c * G + t];
       float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
       bool bad = false;
-      for (uint32_t e = tid; e < groups * G; e += kPairThreads) {
+      for (uint32_t e = ft; e < groups * G; e += kPairThreads) {
         const uint32_t j = e / G;
         const float* sj = ss + (j % 8) * kTileWords + j / 8;
         float y = 0.0f;
@@ -730,13 +846,13 @@ __global__ __launch_bounds__(kPairThreads) void k_gemv_pairs(Operands o, uint32_
         out[tile * kTileGroups * G + e] = y;
         bad |= !finite_f32(y);
       }
-      if (__any(bad) && (tid % warpSize) == 0) atomicOr(o.status, 1u);
+      if (__any(bad) && (ft % warpSize) == 0) atomicOr(o.status, 1u);
     }
   }
 }
 
 size_t pairs_shmem(uint32_t g) {
-  return size_t(kPairBins) * 4 + kPairXRows * 4 + 2 * 16 * g * 4;
+  return g == 8 ? PairLds<8>::total : (g == 16 ? PairLds<16>::total : PairLds<32>::total);
 }
 
 uint32_t gemv_splits(uint32_t n, uint32_t k, uint32_t group, uint32_t count) {
@@ -793,8 +909,8 @@ hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k
   const uint32_t tiles = (n / (8 * G) + kTileWords - 1) / kTileWords;
   uint32_t ks, splits;
   pairs_slices(n, k, G, o.count, &ks, &splits);
-  // about one block per compute unit; each block walks its instances and
-  // loads the next one's set-up while it finishes the current one
+  // about one block per compute unit; each block walks its instances with the
+  // next instance's first batches and set-up data already in flight
   const uint32_t per_z = tiles * splits;
   uint32_t zc = per_z >= 256 ? 1u : 256u / per_z;
   zc = zc < o.count ? zc : o.count;

@@ -195,7 +195,7 @@ def cpu_baseline(x_img, w_img, budget_s=10.0):
 
 
 def load_traffic():
-    path = ROOT / "profiles" / "gemv_bins_config3_traffic.json"
+    path = ROOT / "profiles" / "gemv_pairs_config3_traffic.json"
     if path.is_file():
         try:
             return json.loads(path.read_text()).get("traffic_bytes_per_launch")

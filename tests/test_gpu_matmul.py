@@ -141,8 +141,8 @@ def test_gemv_bins_long_slices(vqdev, oracle, m):
 
 
 def test_gemv_pairs_restaged_activations(vqdev, oracle):
-    """m = 1 over 9000 rows in one slice: nine integer windows and two
-    restages of the 4096-row activation chunk."""
+    """m = 1 over 9000 rows in one slice: three 4096-row integer windows and
+    two restages of the 4096-row activation chunk."""
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(91)
     m, k, n, group, count = 1, 9000, 256, 16, 256
@@ -156,6 +156,49 @@ def test_gemv_pairs_restaged_activations(vqdev, oracle):
         ref, _ = oracle.matmul(*items[i], m, n, k, group, 0)
         assert o.max_rel(out[i], ref) <= TOL
         assert o.max_rel(out[i], _ref64(items[i], m, n, k, group, 0)) <= TOL
+
+
+@pytest.mark.parametrize("k,group", [(300, 16), (4352, 8), (7936, 32), (12500, 16)])
+def test_gemv_pairs_padding_batches(vqdev, oracle, k, group):
+    """m = 1 with slice lengths that are not a whole number of ring turns:
+    the last turn carries padding batches past the slice, which must add
+    nothing (and, past a restage, read no stale activations)."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(k)
+    m, n, count = 1, 256, 256
+    items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
+    ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
+    say("gemv-pairs padding", k, group, count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    for i in (0, 100, 255):
+        ref, _ = oracle.matmul(*items[i], m, n, k, group, 0)
+        assert o.max_rel(out[i], ref) <= TOL
+        assert o.max_rel(out[i], _ref64(items[i], m, n, k, group, 0)) <= TOL
+
+
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_gemv_pairs_saturated_window(vqdev, sign):
+    """Every row of a 4096-row window puts the same byte, with the largest
+    activation, into one pair bin: the integer sum reaches 4096 * (2^19 - 1)
+    (or -2^31) and must not wrap."""
+    from oracle import vq4_numpy as o
+    m, n, k, group = 1, 512, 4096, 16
+    a_book = np.full((16, group), sign * np.nextafter(np.float32(1), np.float32(0)), np.float32)
+    a_codes = o.pack_indices(np.zeros(k // group, np.int64))
+    b_book = (np.arange(16 * group, dtype=np.float32).reshape(16, group) / 256.0).astype(np.float32)
+    b_codes = o.pack_indices(np.full(k * n // group, 5, np.int64))
+    one = (a_codes, a_book, b_codes, b_book)
+    count = 256  # enough instances that no block splits k: one slice holds the window
+    ops = tuple(np.tile(a.reshape(-1), count) for a in one)
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
+    say("gemv-pairs saturated", sign)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    ref = _ref64(one, m, n, k, group, 0)
+    for i in (0, 255):
+        assert o.max_rel(out[i], ref) <= TOL
 
 
 def test_config1_matmul(vqdev, oracle):
