@@ -14,14 +14,20 @@ genuinely encoded weight with a different relabelling of its 16 entries
 each (codes permuted, book rows permuted back): every item decodes to the
 same matrix, so all R outputs must agree, while no two items share bytes.
 
-Secondary (`extra.prefill`): BASELINE config 4, X 2048x4096 times W
-4096x14336 at group 32 and dY 2048x14336 times W^T, TFLOP/s = 2*M*N*K / time.
+Secondary lines (`extra`):
+* `prefill`: BASELINE config 4, X 2048x4096 times W 4096x14336 at group 32 and
+  dY 2048x14336 times W^T: algorithmic TFLOP/s = 2*M*N*K / time, plus each
+  kernel's executed-work rate against its own peak;
+* `gemv_m4`, `gemv_m8`: config 3 at M = 4 and 8, the same cache-cold batch;
+* `config5`: BASELINE config 5, an 8192x8192 row-normalised weight at group 8:
+  GPU encode (read GB/s and FP32 VALU fraction), decode, op-3 AdamW, and one
+  fused VQAdamW step end to end.
 
 `cpu_baseline`: the oracle's numpy CPU path for config 3 (decode the weight
 with a gather, then numpy matmul) on a bounded sample of matrices, timed on
 this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--items R]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--items R] [--no-extra]
 """
 from __future__ import annotations
 
@@ -41,6 +47,10 @@ for p in (str(ROOT / "alelyon-compute-kit_amd"), str(ROOT)):
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+FP16_MFMA_PEAK_TFLOPS = 2500.0     # dense
+# FP32 VALU: 256 CUs x 64 lanes x 2.4 GHz, one non-fused add or multiply per lane
+# and clock (157.3 TFLOP/s counts packed FMAs: 2 lanes x 2 flops)
+FP32_VALU_OPS_PEAK_T = 256 * 64 * 2.4e9 / 1e12
 W_BYTES = 524288 + 1024           # packed codes + codebook of one 4096x4096 g16 weight
 
 
@@ -74,14 +84,16 @@ def timed(device, fn, steps, warmup):
     return ms / steps
 
 
-def bench_gemv(device, dev, items, steps, warmup):
+def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
+    """Config 3 at activation height m: one batched launch over `items`
+    relabelled 4096x4096 g16 weights, HIP-event timed on the library stream."""
     from alelyon_compute_kit import vq
     from oracle.vq4_numpy import ShaderOracle, max_rel
     rng = np.random.default_rng(3)
-    log("encoding the 4096x4096 weight")
+    log(f"encoding the 4096x4096 weight (m={m})")
     w = (rng.standard_normal((4096, 4096)) * 0.02).astype(np.float32)
     w_img = dev.encode(w, vq.fit_codebook(w, group=16), group=16)
-    x = rng.standard_normal((1, 4096)).astype(np.float32)
+    x = rng.standard_normal((m, 4096)).astype(np.float32)
     x_img = dev.encode(x, vq.fit_codebook(x, group=16), group=16)
     log(f"building {items} relabelled weights")
     codes, books = relabelled_items(w_img.codes, w_img.codebook, items, 4)
@@ -90,38 +102,40 @@ def bench_gemv(device, dev, items, steps, warmup):
     bufs = [device.buffer(a.nbytes) for a in (xa, xb, codes, books)]
     for b, a in zip(bufs, (xa, xb, codes, books)):
         b.upload(a)
-    out = device.buffer(items * 4096 * 4)
+    out = device.buffer(items * m * 4096 * 4)
     status = device.buffer(4)
     status.upload(np.zeros(1, np.uint32))
-    words = (2, 1, 4096, 4096, 16, 16, 0, 0)
+    words = (2, m, 4096, 4096, 16, 16, 0, 0)
     path = dev.path_name(words)
+    single_ms = None
     try:
         def launch():
             dev.run(words, bufs, out, status, count=items)
-        log(f"timing {steps} launches of {items} items, path {path}")
+        log(f"timing {steps} launches of {items} items, m={m}, path {path}")
         ms = timed(device, launch, steps, warmup)
         flags = int(status.download(np.uint32)[0])
-        y = out.download(np.float32).reshape(items, 4096)
-        # single-matrix latency (resident, cache-warm): one ack_vq of item 0
-        s_bufs = [device.buffer(a.nbytes) for a in (x_img.codes, x_img.codebook, w_img.codes,
-                                                    w_img.codebook)]
-        for b, a in zip(s_bufs, (x_img.codes, x_img.codebook, w_img.codes, w_img.codebook)):
-            b.upload(a)
-        s_out = device.buffer(4096 * 4)
-        single_ms = timed(device, lambda: dev.run(words, s_bufs, s_out, status), 50, 5)
-        for b in s_bufs + [s_out]:
-            b.free()
+        y = out.download(np.float32).reshape(items, m, 4096)
+        if single:
+            # single-matrix latency (resident, cache-warm): one ack_vq of item 0
+            arrays = (x_img.codes, x_img.codebook, w_img.codes, w_img.codebook)
+            s_bufs = [device.buffer(a.nbytes) for a in arrays]
+            for b, a in zip(s_bufs, arrays):
+                b.upload(a)
+            s_out = device.buffer(m * 4096 * 4)
+            single_ms = timed(device, lambda: dev.run(words, s_bufs, s_out, status), 50, 5)
+            for b in s_bufs + [s_out]:
+                b.free()
     finally:
         for b in bufs + [out, status]:
             b.free()
     if flags:
-        raise SystemExit(f"status word {flags} after the timed GEMV launches")
+        raise SystemExit(f"status word {flags} after the timed GEMV launches (m={m})")
     oracle = ShaderOracle()
     ref, _ = oracle.matmul(x_img.codes, x_img.codebook, w_img.codes, w_img.codebook,
-                           1, 4096, 4096, 16, 0)
-    err = max(max_rel(y[0], ref[0]), float(np.max(np.abs(y - y[0]))) / float(np.max(np.abs(ref))))
+                           m, 4096, 4096, 16, 0)
+    err = max(max_rel(y[0], ref), float(np.max(np.abs(y - y[0]))) / float(np.max(np.abs(ref))))
     return {"ms": ms, "single_ms": single_ms, "path": path, "max_rel": err,
-            "x_img": x_img, "w_img": w_img}
+            "gbs": items * W_BYTES / (ms * 1e-3) / 1e9, "x_img": x_img, "w_img": w_img}
 
 
 def bench_prefill(device, dev, steps, warmup):
@@ -163,9 +177,100 @@ def bench_prefill(device, dev, steps, warmup):
         ref = a_dense @ (wd if flags == 0 else wd.T)
         err = float(np.max(np.abs(sample - ref)) / np.max(np.abs(ref)))
         flop = 2.0 * m * nn * kk
-        results[name] = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "path": dev.path_name(words),
-                         "max_rel_first_rows": err}
+        path = dev.path_name(words)
+        entry = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "path": path,
+                 "max_rel_first_rows": err}
+        # what the kernel actually executes
+        if path == "row-bins":      # one FP32 add per (row of A, nibble of B)
+            ops = float(m) * kk * (nn // 32)
+            entry["executed"] = {"what": "FP32 VALU adds", "tops": ops / (ms * 1e-3) / 1e12,
+                                 "peak": FP32_VALU_OPS_PEAK_T,
+                                 "frac": ops / (ms * 1e-3) / 1e12 / FP32_VALU_OPS_PEAK_T}
+        elif path == "gram-mfma":   # one-hot x Gram GEMM, inner 16 k/g, hi + lo halves
+            ops = 2.0 * m * nn * (2 * 16 * kk // 32)
+            entry["executed"] = {"what": "fp16 MFMA flops", "tflops": ops / (ms * 1e-3) / 1e12,
+                                 "peak": FP16_MFMA_PEAK_TFLOPS,
+                                 "frac": ops / (ms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS}
+        results[name] = entry
     return results
+
+
+def bench_config5(device, dev, steps, warmup):
+    """Config 5: 8192x8192 row-normalised N(0,1) weight at group 8 -- GPU
+    encode and decode throughput, op-3 AdamW, and the fused VQAdamW step
+    (re-encoding weight and both moments) on N(0, 1e-3) gradients."""
+    from alelyon_compute_kit import vq
+    n, g = 8192, 8
+    m = n * n
+    rng = np.random.default_rng(5)
+    log("config 5: building the 8192x8192 weight")
+    w = rng.standard_normal((n, n), dtype=np.float32)
+    w /= np.linalg.norm(w, axis=1, keepdims=True).astype(np.float32)
+    book = vq.fit_codebook(w, group=g)
+    words = vq.storage_layout((n, n), g)["code_bytes"] // 4
+    out = {}
+    wb = device.buffer(w.nbytes)
+    bk = device.buffer(book.nbytes)
+    codes = device.buffer(words * 4)
+    dense = device.buffer(w.nbytes)
+    status = device.buffer(4)
+    try:
+        wb.upload(w)
+        bk.upload(book)
+        status.upload(np.zeros(1, np.uint32))
+        enc = (0, m, 1, 1, g, 16, 0, 0)
+        ms = timed(device, lambda: dev.run(enc, [wb, bk], codes, status), steps, warmup)
+        read = 4.0 * m
+        vec_ops = 3.0 * 16 * g * (m // g)   # sub, mul, add per component and entry
+        out["encode"] = {"ms": ms, "read_gbs": read / (ms * 1e-3) / 1e9,
+                         "hbm_frac": read / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                         "valu_tops": vec_ops / (ms * 1e-3) / 1e12,
+                         "valu_frac": vec_ops / (ms * 1e-3) / 1e12 / FP32_VALU_OPS_PEAK_T,
+                         "path": dev.path_name(enc)}
+        dec = (1, m, 1, 1, g, 16, 0, 0)
+        ms = timed(device, lambda: dev.run(dec, [codes, bk], dense, status), steps, warmup)
+        moved = 4.0 * m + 4.0 * words
+        out["decode"] = {"ms": ms, "gbs": moved / (ms * 1e-3) / 1e9,
+                         "hbm_frac": moved / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        flags = int(status.download(np.uint32)[0])
+        if flags:
+            raise SystemExit(f"status word {flags} after the config-5 codec launches")
+        w_codes = codes.download(np.uint32)
+    finally:
+        for b in (wb, bk, codes, dense, status):
+            b.free()
+    del w
+    w_img = vq.VQArray((n, n), g, w_codes, book)
+    grad = (rng.standard_normal((n, n), dtype=np.float32) * np.float32(np.sqrt(1e-3)))
+    g_img = dev.encode(grad, vq.fit_codebook(grad, group=g), group=g)
+    del grad
+    opt = vq.VQAdamW(dev, w_img, lr=1e-3, betas=(0.9, 0.999))
+    # op-3 AdamW to dense scratch, resident
+    count, c4, b4, coeff = vq.VQDevice._adamw_inputs(
+        opt.weight, opt.momentum, opt.variance, g_img, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1)
+    bufs = [device.buffer(a.nbytes) for a in (c4, b4, coeff)]
+    scratch = device.buffer(3 * count * 4)
+    status = device.buffer(4)
+    try:
+        for b, a in zip(bufs, (c4, b4, coeff)):
+            b.upload(a)
+        status.upload(np.zeros(1, np.uint32))
+        op3 = (3, count, 1, 1, g, 16, 0, 0)
+        ms = timed(device, lambda: dev.run(op3, bufs, scratch, status), steps, warmup)
+        moved = 12.0 * count + float(c4.nbytes + b4.nbytes)
+        out["adamw_op3"] = {"ms": ms, "gbs": moved / (ms * 1e-3) / 1e9,
+                            "hbm_frac": moved / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    finally:
+        for b in bufs + [scratch, status]:
+            b.free()
+    # the fused step end to end (host images in, host images out: PCIe included)
+    t0 = time.perf_counter()
+    report = opt.step(g_img)
+    out["fused_step"] = {"seconds_end_to_end": time.perf_counter() - t0,
+                         "changed_weight_values": report["changed_weight_values"],
+                         "note": "uploads of the four packed states, device AdamW passes, "
+                                 "native host refits, downloads of three packed states"}
+    return out
 
 
 def cpu_baseline(x_img, w_img, budget_s=10.0):
@@ -211,6 +316,8 @@ def main(argv=None) -> int:
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--items", type=int, default=1024)
     parser.add_argument("--no-prefill", action="store_true")
+    parser.add_argument("--no-extra", action="store_true",
+                        help="skip the secondary lines (config 3 at m=4/8, config 5)")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a 512 MiB device-to-device copy (the reference for "
@@ -237,6 +344,14 @@ def main(argv=None) -> int:
         gemv = bench_gemv(device, dev, args.items, args.steps, args.warmup)
         prefill = None if args.no_prefill else bench_prefill(device, dev, max(3, args.steps // 4),
                                                               1)
+        wide = {}
+        c5 = None
+        if not args.no_extra:
+            for m in (4, 8):
+                r = bench_gemv(device, dev, args.items, max(3, args.steps // 2), 1, m=m,
+                               single=False)
+                wide[m] = r
+            c5 = bench_config5(device, dev, max(3, args.steps // 4), 1)
     gbs = args.items * W_BYTES / (gemv["ms"] * 1e-3) / 1e9
     line = {
         "metric": "vq4 packed matmul: packed-weight GB/s (% HBM peak) at M=1; TFLOP/s at M=2048",
@@ -262,16 +377,36 @@ def main(argv=None) -> int:
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic()},
     }
+    def tidy(v):
+        if isinstance(v, float):
+            return float(f"{v:.4g}")
+        if isinstance(v, dict):
+            return {k: tidy(x) for k, x in v.items()}
+        return v
+
+    extra = {}
     if prefill:
-        line["extra"] = {"prefill": {
+        extra["prefill"] = {
             "workload": "config 4: X 2048x4096 . W 4096x14336 g32 (forward), dY 2048x14336 . W^T "
                         "(backward)",
-            **{f"{k}_{f}": (float(f"{v[f]:.4g}") if isinstance(v[f], float) else v[f])
-               for k, v in prefill.items() for f in v},
+            **{f"{k}_{f}": tidy(v[f]) for k, v in prefill.items() for f in v},
+            # Algorithmic TFLOP/s (2 M N K per direction) against the FP32 matrix peak: above
+            # 1 because the codebook factorisation executes far fewer operations; the
+            # *_executed entries give each kernel's own executed-work fraction.
             "roofline": {"bound": "mfma", "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "achieved": round(min(v["tflops"] for v in prefill.values()), 3),
                          "frac": round(min(v["tflops"] for v in prefill.values())
-                                       / FP32_MFMA_PEAK_TFLOPS, 4)}}}
+                                       / FP32_MFMA_PEAK_TFLOPS, 4)}}
+    for m, r in wide.items():
+        extra[f"gemv_m{m}"] = {"workload": f"config 3 at M={m}, same cache-cold batch",
+                               "gbs": tidy(r["gbs"]), "hbm_frac": tidy(r["gbs"] / HBM_PEAK_GBS),
+                               "path": r["path"], "max_rel_vs_oracle": tidy(r["max_rel"])}
+    if c5:
+        extra["config5"] = {"workload": "config 5: 8192x8192 row-normalised N(0,1) weight, "
+                                        "group 8; N(0,1e-3) gradient",
+                            **tidy(c5)}
+    if extra:
+        line["extra"] = extra
     if not args.no_cpu:
         log("timing the CPU baseline")
         line["cpu_baseline"] = cpu_baseline(gemv["x_img"], gemv["w_img"])

@@ -1,0 +1,253 @@
+"""The expert bank (on-disk generations) and the harness that trains through it.
+
+CPU tests pin the bank's format against the reference's seeded payloads
+(tests/golden/expert_payloads.npz, written from the reference's own
+ExpertBank.initialize_expert), its commit counters and refusals, and the
+harness flow with a host backend. GPU tests run the harness step and the
+BASELINE config-2 flow on the MI355X and require every committed image to be
+byte-identical to the same flow computed by the CPU oracle.
+"""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+
+from alelyon_compute_kit import expert_bank, harness, vq
+from conftest import golden
+
+
+class HostBackend:
+    """numpy arithmetic on decoded operands (the reference's test fake,
+    tests/test_harness.py:7-28, restated)."""
+
+    def encode(self, values, codebook, *, group):
+        return vq.encode(values, codebook, group=group)
+
+    def decode(self, value):
+        return value.decode()
+
+    def matmul(self, left, right, *, transpose_a=False, transpose_b=False):
+        a, b = left.decode(), right.decode()
+        return (a.T if transpose_a else a) @ (b.T if transpose_b else b)
+
+    def adamw(self, weight, momentum, variance, gradient, *, lr, beta1, beta2, eps,
+              weight_decay, step):
+        w, m, v, g = (s.decode() for s in (weight, momentum, variance, gradient))
+        m = beta1 * m + (1.0 - beta1) * g
+        v = beta2 * v + (1.0 - beta2) * np.square(g)
+        w = w - lr * ((m / (1.0 - beta1 ** step)) / (np.sqrt(v / (1.0 - beta2 ** step)) + eps)
+                      + weight_decay * w)
+        return w.astype(np.float32), m.astype(np.float32), v.astype(np.float32)
+
+
+def _small_bank(tmp_path, name="bank"):
+    bank = expert_bank.ExpertBank.create(
+        tmp_path / name, expert_bank.BankConfig(1, 1, ((4, 3), (4, 3), (4, 3)), 8))
+    bank.initialize_expert(0, 0, seed=4, zero_optimizer_state=True)
+    return bank
+
+
+# ---- bank ----------------------------------------------------------------------
+def test_bank_metadata_is_canonical_and_reopens(tmp_path):
+    config = expert_bank.BankConfig(2, 3, ((8, 16), (16, 8)), 8)
+    bank = expert_bank.ExpertBank.create(tmp_path / "b", config)
+    data = (tmp_path / "b" / "bank.json").read_bytes()
+    assert data == json.dumps({"schema": "ack-expert-bank/v1", "config": config.to_dict()},
+                              sort_keys=True, separators=(",", ":")).encode()
+    again = expert_bank.ExpertBank.open(tmp_path / "b")
+    assert again.config == bank.config and again.config.parameters_per_expert == 256
+    with pytest.raises(FileExistsError):
+        expert_bank.ExpertBank.create(tmp_path / "b", config)
+    (tmp_path / "b" / "bank.json").write_bytes(data.replace(b":", b": ", 1))
+    with pytest.raises(expert_bank.ExpertBankError, match="noncanonical"):
+        expert_bank.ExpertBank.open(tmp_path / "b")
+
+
+@pytest.mark.parametrize("bad", [
+    dict(layers=0, experts_per_layer=1, matrix_shapes=((4, 4),)),
+    dict(layers=1, experts_per_layer=1, matrix_shapes=((4, 4),), group=12),
+    dict(layers=1, experts_per_layer=1, matrix_shapes=()),
+    dict(layers=1, experts_per_layer=1, matrix_shapes=((4, 4, 4),)),
+    dict(layers=True, experts_per_layer=1, matrix_shapes=((4, 4),)),
+])
+def test_bank_config_refusals(bad):
+    with pytest.raises(expert_bank.ExpertBankError):
+        expert_bank.BankConfig(**bad)
+
+
+def test_initialize_expert_matches_the_reference_payloads(tmp_path):
+    g = golden("expert_payloads.npz")
+    bank = expert_bank.ExpertBank.create(
+        tmp_path / "c2", expert_bank.BankConfig(1, 1, ((128, 128),) * 3, 16))
+    bank.initialize_expert(0, 0, seed=7)
+    for i, t in enumerate(bank.read_expert(0, 0)):
+        assert np.array_equal(t.codes, g[f"c2_{i}_codes"])
+        assert np.array_equal(t.codebook.view(np.uint32), g[f"c2_{i}_book"].view(np.uint32))
+    small = _small_bank(tmp_path)
+    for i, t in enumerate(small.read_expert(0, 0)):
+        assert np.array_equal(t.codes, g[f"h_{i}_codes"])
+        assert np.array_equal(t.codebook.view(np.uint32), g[f"h_{i}_book"].view(np.uint32))
+    with pytest.raises(expert_bank.ExpertBankError, match="already"):
+        small.initialize_expert(0, 0, seed=4)
+
+
+def test_write_counters_generations_and_refusals(tmp_path):
+    bank = _small_bank(tmp_path)
+    state = bank.read_expert_state(0, 0)
+    assert (state.revision, state.optimizer_step, state.parameter_update_applications) == (1, 0, 0)
+    receipt = bank.write_expert(0, 0, state.tensors, updated_count=12, optimizer_step=3)
+    assert receipt["revision"] == 2 and receipt["parameter_update_applications"] == 12
+    after = bank.read_expert_state(0, 0)
+    assert (after.revision, after.optimizer_step) == (2, 3)
+    pointer = json.loads((bank.root / "expert-0-0.json").read_bytes())
+    assert pointer["update_commits"] == 1
+    with pytest.raises(expert_bank.ExpertBankError, match="regress"):
+        bank.write_expert(0, 0, state.tensors, optimizer_step=2)
+    wrong = vq.VQArray((3, 4), 8, state.tensors[0].codes, state.tensors[0].codebook)
+    with pytest.raises(expert_bank.ExpertBankError, match="geometry"):
+        bank.write_expert(0, 0, (wrong,) + state.tensors[1:])
+    with pytest.raises(expert_bank.ExpertBankError):
+        bank.write_expert(0, 1, state.tensors)
+    # refused writes leave no pending pointer and no new shards behind
+    names = sorted(p.name for p in bank.root.iterdir())
+    assert not any(n.startswith("pending-") for n in names)
+    assert sum(n.endswith(".vq") for n in names) == 6  # two generations x three shards
+    stats = bank.stats()
+    assert stats["materialized_experts"] == 1 and stats["updated_experts"] == 1
+    assert stats["committed_payload_bytes"] == sum(t.layout["serialized_bytes"]
+                                                   for t in state.tensors)
+
+
+def test_a_changed_shard_is_refused(tmp_path):
+    bank = _small_bank(tmp_path)
+    pointer = json.loads((bank.root / "expert-0-0.json").read_bytes())
+    shard = bank.root / f"expert-0-0-g{pointer['generation']}-t0.vq"
+    data = bytearray(shard.read_bytes())
+    data[-1] ^= 1
+    shard.write_bytes(bytes(data))
+    with pytest.raises(expert_bank.ExpertBankError, match="checksum"):
+        bank.read_expert_state(0, 0)
+    zero = vq.VQArray((4, 3), 8, np.zeros(1, np.uint32), np.zeros((16, 8), np.float32))
+    with pytest.raises(expert_bank.ExpertBankError, match="checksum"):
+        bank.write_expert(0, 0, (zero, zero, zero))  # never builds on corrupt state
+
+
+# ---- harness with a host backend ------------------------------------------------
+def test_forward_is_the_packed_product_and_checks_width(tmp_path):
+    bank = _small_bank(tmp_path)
+    runner = harness.VulkanExpertHarness(bank, backend=HostBackend())
+    x = np.arange(8, dtype=np.float32).reshape(2, 4)
+    expected = x @ bank.read_expert_state(0, 0).tensors[0].decode()
+    np.testing.assert_array_equal(runner.forward(x), expected)
+    with pytest.raises(harness.HarnessError, match="width"):
+        runner.forward(np.zeros((2, 5), np.float32))
+    with pytest.raises(harness.HarnessError, match="rank-2 float32"):
+        runner.forward(np.zeros((2, 4), np.float64))
+
+
+def test_train_step_commits_the_optimizer_state(tmp_path):
+    bank = _small_bank(tmp_path)
+    runner = harness.ExpertHarness(bank, backend=HostBackend())
+    before = bank.read_expert_state(0, 0)
+    step = runner.train_step(np.ones((2, 4), np.float32), np.zeros((2, 3), np.float32),
+                             max_grad_norm=0.01)
+    after = bank.read_expert_state(0, 0)
+    assert (step.optimizer_step, step.revision) == (1, 2)
+    assert after.optimizer_step == 1 and after.parameter_update_applications == 12
+    assert step.clipped and step.persistent_state_bytes > 0
+    assert before.tensors[0].to_bytes() != after.tensors[0].to_bytes()
+    assert set(step.to_dict()) >= {"loss", "gradient_norm_before_clip", "clipped"}
+    with pytest.raises(harness.HarnessError, match="finite"):
+        runner.forward(np.full((2, 4), np.nan, np.float32))
+    with pytest.raises(harness.HarnessError, match="row count"):
+        runner.train_step(np.ones((2, 4), np.float32), np.zeros((3, 3), np.float32))
+    with pytest.raises(harness.HarnessError, match="positive"):
+        runner.train_step(np.ones((2, 4), np.float32), np.zeros((2, 3), np.float32),
+                          max_grad_norm=0.0)
+    steps = runner.train(np.ones((2, 4), np.float32), np.zeros((2, 3), np.float32), steps=2)
+    assert [s.optimizer_step for s in steps] == [2, 3]
+    assert bank.read_expert_state(0, 0).revision == 4
+
+
+def test_harness_refuses_bad_construction(tmp_path):
+    bank = _small_bank(tmp_path)
+    with pytest.raises(harness.HarnessError, match="ExpertBank"):
+        harness.ExpertHarness(object(), backend=HostBackend())
+    with pytest.raises(harness.HarnessError, match="not both"):
+        harness.ExpertHarness(bank, backend=HostBackend(), device=object())
+
+
+# ---- GPU parity of whole flows ----------------------------------------------------
+def _twin_banks(tmp_path, shapes, group, seed, zero):
+    banks = []
+    for name in ("gpu", "cpu"):
+        b = expert_bank.ExpertBank.create(tmp_path / name,
+                                          expert_bank.BankConfig(1, 1, shapes, group))
+        b.initialize_expert(0, 0, seed=seed, zero_optimizer_state=zero)
+        banks.append(b)
+    return banks
+
+
+@pytest.mark.gpu
+def test_harness_step_on_the_gpu_commits_the_oracle_images(tmp_path, vqdev):
+    """Two steps of the harness on config-2-sized matrices (128 x 128, group
+    16, seed 7, zero moments; x 32 x 128 ~ N(0,1), targets ~ N(0, 1e-2)):
+    the GPU run and the CPU-oracle run commit byte-identical generations."""
+    from gpu_util import say
+    from oracle_backend import OracleBackend
+    gpu_bank, cpu_bank = _twin_banks(tmp_path, ((128, 128),) * 3, 16, 7, True)
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((32, 128)).astype(np.float32)
+    t = (rng.standard_normal((32, 128)) * 0.1).astype(np.float32)
+    say("harness step parity")
+    gpu = harness.ExpertHarness(gpu_bank, backend=vqdev)
+    cpu = harness.ExpertHarness(cpu_bank, backend=OracleBackend())
+    for _ in range(2):
+        a = gpu.train_step(x, t, lr=1e-3, beta1=0.9, beta2=0.999, max_grad_norm=1.0)
+        b = cpu.train_step(x, t, lr=1e-3, beta1=0.9, beta2=0.999, max_grad_norm=1.0)
+        assert (a.loss, a.gradient_norm_before_clip, a.clipped) == \
+               (b.loss, b.gradient_norm_before_clip, b.clipped)
+        for ta, tb in zip(gpu_bank.read_expert(0, 0), cpu_bank.read_expert(0, 0)):
+            assert ta.to_bytes() == tb.to_bytes()
+    np.testing.assert_array_equal(gpu.forward(x), cpu.forward(x))
+
+
+@pytest.mark.gpu
+def test_config2_chain_and_clipped_step_match_the_oracle(vqdev):
+    """three 128 x 128 matrices from initialize_expert(0, 0,
+    seed=7) at group 16; x 32 x 128 ~ N(0,1) fitted and encoded and pushed
+    through the three packed products in sequence (each output re-fitted and
+    re-encoded); then one VQAdamW step (lr 1e-3, betas (0.9, 0.999)) per matrix
+    on N(0, 1e-2) gradients clipped to global norm 1.0. Every image and output
+    equals the CPU oracle's, bit for bit."""
+    from gpu_util import say
+    from oracle.vq4_numpy import clip_scale, expert_payload
+    from oracle_backend import OracleBackend
+    cpu = OracleBackend()
+    weights = [vq.VQArray((128, 128), 16, *expert_payload((128, 128), 16, 7, 0, 0, i))
+               for i in range(3)]
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((32, 128)).astype(np.float32)
+    say("config2 chain")
+    ha = hb = x
+    for w in weights:
+        ia = vqdev.encode(ha, vq.fit_codebook(ha, group=16), group=16)
+        ib = cpu.encode(hb, vq.fit_codebook(hb, group=16), group=16)
+        assert ia == ib
+        ha, hb = vqdev.matmul(ia, w), cpu.matmul(ib, w)
+        np.testing.assert_array_equal(ha.view(np.uint32), hb.view(np.uint32))
+    grads = [(rng.standard_normal((128, 128)) * 0.1).astype(np.float32) for _ in range(3)]
+    norm_scale = clip_scale(np.concatenate([g.reshape(-1) for g in grads]), 1.0)
+    say("config2 step")
+    for w, g in zip(weights, grads):
+        g = g * np.float32(norm_scale)
+        gi = vq.encode(g, vq.fit_codebook(g, group=16), group=16)
+        opt_a = vq.VQAdamW(vqdev, w, lr=1e-3, betas=(0.9, 0.999))
+        opt_b = vq.VQAdamW(cpu, w, lr=1e-3, betas=(0.9, 0.999))
+        ra, rb = opt_a.step(gi), opt_b.step(gi)
+        assert ra["changed_weight_values"] == rb["changed_weight_values"]
+        for sa, sb in ((opt_a.weight, opt_b.weight), (opt_a.momentum, opt_b.momentum),
+                       (opt_a.variance, opt_b.variance)):
+            assert sa.to_bytes() == sb.to_bytes()
