@@ -24,7 +24,7 @@ struct Operands {
 // Which implementation serves an op-2 product.
 enum class MatmulPath : int {
   General = 0,    // tiled, sequential FP32 per output: bit-identical to vq4.comp
-  GemvBins = 1,   // B groups along n: codebook-factorised bins, small m
+  GemvRows = 1,   // 2 <= m <= 8, B groups along n: nibble bins, two rows per 64-bit atomic
   GemvTable = 2,  // B groups along k (B stored (n,k)): dot-product table, small m
   GramMfma = 3,   // both operands grouped along k: one-hot x Gram table on fp16 MFMA
   RowBins = 4,    // large m, B groups along n: wave-uniform codes, bins in VGPRs

@@ -9,14 +9,15 @@
 //   rounded -- the shader's order, so its results are bit-identical to
 //   vq4.comp. Serves every shape and layout.
 //
-// * GemvBins (small m, B stored (k,n) with each row a whole number of
-//   words): per output group j and code e the kernel accumulates
-//   S[r][j][e] = sum over rows k with code(k,j) = e of x[r][k] with one LDS
-//   atomic add per nibble, then y[r][j*G+t] = sum_e C_B[e][t] * S[r][j][e].
-//   That is G times fewer additions than decoding the weight, which is what
-//   lets a product that reads only half a byte per G weights run at the
-//   packed-weight bandwidth instead of the FP32 FMA rate. The summation
-//   order differs from the shader's; results agree within FP32 rounding.
+// * The GEMV paths (m <= 8, B stored (k,n) with each row a whole number of
+//   words): per output group j and code e they accumulate
+//   S[r][j][e] = sum over rows k with code(k,j) = e of x[r][k] with integer
+//   LDS atomics, then y[r][j*G+t] = sum_e C_B[e][t] * S[r][j][e]. That is G
+//   times fewer additions than decoding the weight, which is what lets a
+//   product that reads only half a byte per G weights run at the packed-weight
+//   bandwidth instead of the FP32 FMA rate. GemvPairs (m = 1) bins whole bytes,
+//   GemvRows (2..8) bins nibbles two rows at a time. The summation order
+//   differs from the shader's; results agree within FP32 rounding.
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
@@ -138,268 +139,25 @@ __global__ __launch_bounds__(kGThreads) void k_matmul_general(Operands o, uint32
   }
 }
 
-// ---- GemvBins ------------------------------------------------------------
-// Tile: kTileWords words of each B row (8 * kTileWords output groups), all m
-// rows of A, a slice of k. In one batch each wave covers 32 rows: lane
-// (q = lane % 32, half = lane / 32) reads word q of rows base + half*16 + u,
-// u < 16, so every load instruction of a wave reads two whole 128-byte tile
-// rows and a lane's 16 activations are contiguous in LDS. The next batch's
-// words are loaded while the current batch is binned.
-//
-// The bins are 32-bit fixed point: x is scaled by 2^s (s from the A
-// codebook's largest magnitude) and rounded to an integer once, when it is
-// staged in LDS, and the bins are summed with integer LDS atomics -- exact,
-// and on gfx950 some thirty times the rate of FP32 LDS atomics. Every
-// kWindow rows the integer bins are flushed into FP32 accumulators held in
-// registers, which bounds |bin| < 2^30 (no overflow) while keeping the
-// rounding of x to 2^-s at most 2^-23 of the largest |x|.
-// Bins are laid out [r][nibble][e][q]: the 32 lanes of a half-wave hit 32
-// distinct banks for any codes.
+// ---- shared by the GEMV paths ------------------------------------------------
+// A tile is kTileWords words of each B row (8 * kTileWords output groups);
+// the bins are 32-bit (or paired 64-bit) fixed point in LDS: x is scaled by
+// 2^s from the A codebook's largest magnitude and rounded once, and integer
+// LDS atomics -- exact, and on gfx950 about fifty times the rate of FP32 LDS
+// atomics -- accumulate it; windows of rows are flushed into FP32 registers
+// before an int32 sum could overflow.
 constexpr int kTileWords = 32;
 constexpr int kTileGroups = kTileWords * 8;
-constexpr int kBinThreads = 256;
-constexpr int kBinWaves = kBinThreads / 64;
-constexpr int kRowsPerLane = 16;
-constexpr uint32_t kBatchRows = kBinWaves * 2 * kRowsPerLane;   // 128 rows per batch
 constexpr uint32_t kGemvMaxM = 8;
-constexpr uint32_t kWindow = 1024;                              // rows per integer window
-constexpr uint32_t kXBytes = 16384;                             // LDS for staged x
-constexpr int kBinsPerThread = 16 * kTileGroups / kBinThreads;  // 16 bins per M row
-
-// Rows of x staged at once: whole batches (so a lane's 16 activations never
-// straddle a restage), restaged whenever the chunk is used up.
-template <int M>
-__host__ __device__ constexpr uint32_t x_chunk_rows() {
-  return (kXBytes / (4 * M)) / kBatchRows * kBatchRows;
-}
-static_assert(x_chunk_rows<kGemvMaxM>() >= kBatchRows, "staged x must hold one batch per row");
-
-// Byte offset of bin (e, q) for nibble NIB of w inside one M row's bins.
-template <int NIB>
-__device__ __forceinline__ uint32_t bin_byte(uint32_t w, uint32_t q4) {
-  return (__builtin_amdgcn_ubfe(w, 4 * NIB, 4) << 7) | q4;
-}
 
 typedef __attribute__((address_space(3))) int32_t lds_i32;
 
 // Integer add into LDS at an absolute byte address. The bins sit at LDS
-// address 0 (the kernel has no static LDS), so a bin's address is known to
-// the compiler bit for bit and needs no base addition.
+// address 0 (the kernels have no static LDS), so a bin's address is known
+// to the compiler bit for bit and needs no base addition.
 __device__ __forceinline__ void lds_add(uint32_t byte_addr, int32_t v) {
   __hip_atomic_fetch_add(reinterpret_cast<lds_i32*>(static_cast<size_t>(byte_addr)), v,
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-__device__ __forceinline__ uint32_t bin_index(uint32_t r, uint32_t nib, uint32_t e, uint32_t q) {
-  return ((r * 8 + nib) * 16 + e) * kTileWords + q;
-}
-
-// x[r][kk] for rows r < m and inner rows [k0, kend), decoded from A by flat
-// index, scaled by 2^shift and rounded to int32 into sxq[r * rows + kk].
-template <int G, int M>
-__device__ void stage_x(const uint32_t* a_codes, const float* sa_book, uint32_t k, uint32_t flags,
-                        uint32_t k0, uint32_t kend, uint32_t rows, int shift, int32_t* sxq) {
-  for (uint32_t e = threadIdx.x; e < M * rows; e += blockDim.x) {
-    const uint32_t r = e / rows, kk = e % rows;
-    const uint32_t inner = k0 + kk;
-    int32_t v = 0;
-    if (inner < kend) {
-      const uint32_t flat = (flags & 1u) ? inner * M + r : r * k + inner;
-      v = int32_t(rintf(ldexpf(sa_book[nibble(a_codes, flat / G) * G + flat % G], shift)));
-    }
-    sxq[e] = v;
-  }
-}
-
-// Largest |value| of a 16 x G book, reduced over the block.
-template <int G>
-__device__ float book_absmax(const float* sbook, float* sred) {
-  float v = 0.0f;
-  for (uint32_t i = threadIdx.x; i < 16 * G; i += blockDim.x) v = fmaxf(v, fabsf(sbook[i]));
-  for (int off = 1; off < warpSize; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
-  if (threadIdx.x % warpSize == 0) sred[threadIdx.x / warpSize] = v;
-  __syncthreads();
-  float m = 0.0f;
-  for (uint32_t i = 0; i < blockDim.x / warpSize; ++i) m = fmaxf(m, sred[i]);
-  __syncthreads();
-  return m;
-}
-
-// Load this lane's 16 words of a batch (zero past kend or off the tile).
-__device__ __forceinline__ void load_batch(const uint32_t* col_codes, uint32_t row_words,
-                                           uint32_t first, uint32_t kend, bool live,
-                                           uint32_t (&w)[kRowsPerLane]) {
-#pragma unroll
-  for (int u = 0; u < kRowsPerLane; ++u) {
-    const uint32_t row = first + u;
-    w[u] = (live && row < kend) ? col_codes[uint64_t(row) * row_words] : 0u;
-  }
-}
-
-// grid: (n tiles, k splits, instances). Dynamic shared memory: the integer
-// bins (M * 16 * kTileGroups) then the staged x (M * x_chunk_rows int32).
-template <int G, int M>
-__global__ __launch_bounds__(kBinThreads) void k_gemv_bins(Operands o, uint32_t n, uint32_t k,
-                                                           uint32_t flags, uint32_t ks,
-                                                           float* partial) {
-  constexpr uint32_t kXRows = x_chunk_rows<M>();
-  // All LDS is dynamic so the bins start at address 0: a bin address is then
-  // (e << 7) | q4 with disjoint bits, one AND-OR per nibble.
-  extern __shared__ int32_t smem[];
-  int32_t* bins = smem;
-  int32_t* sxq = smem + M * 16 * kTileGroups;
-  float* fbins = reinterpret_cast<float*>(smem);
-  float* sa_book = reinterpret_cast<float*>(sxq + kXBytes / 4);
-  float* sb_book = sa_book + 16 * G;
-  float* sred = sb_book + 16 * G;
-  const uint32_t tid = threadIdx.x;
-  const uint32_t tile = blockIdx.x, split = blockIdx.y;
-  const uint32_t row_words = n / (8 * G);
-  const uint32_t k0 = split * ks;
-  const uint32_t kend = (k0 + ks) < k ? (k0 + ks) : k;
-  const uint32_t lane = tid % 64, wave = tid / 64;
-  const uint32_t q = lane % 32, half = lane / 32;
-  const uint32_t q4 = q * 4;
-  const uint32_t lane_row = wave * 32 + half * kRowsPerLane;  // first row of this lane in a batch
-  const uint32_t word_col = tile * kTileWords + q;
-  const bool live = word_col < row_words;
-  // Defensive: absolute bin addresses assume the bins start at LDS 0.
-  if (static_cast<uint32_t>(reinterpret_cast<size_t>((lds_i32*)bins)) != 0) {
-    if (tid == 0) atomicOr(o.status, 2u);
-    return;
-  }
-  for (uint32_t item = blockIdx.z; item < o.count; item += gridDim.z) {
-    const uint32_t* a_codes = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
-    const float* a_book = item_ptr<float>(o.in[1], o.stride[1], item);
-    const uint32_t* b_codes = item_ptr<uint32_t>(o.in[2], o.stride[2], item);
-    const float* b_book = item_ptr<float>(o.in[3], o.stride[3], item);
-    const uint32_t* col_codes = b_codes + word_col;
-    // the first batch's words are in flight while the block sets up
-    uint32_t wn[kRowsPerLane];
-    load_batch(col_codes, row_words, k0 + lane_row, kend, live, wn);
-    __syncthreads();
-    for (uint32_t i = tid; i < 16 * G; i += kBinThreads) {
-      sa_book[i] = a_book[i];
-      sb_book[i] = b_book[i];
-    }
-    for (uint32_t i = tid; i < M * 16 * kTileGroups; i += kBinThreads) bins[i] = 0;
-    if (tile == 0 && split == 0) sweep_books(a_book, b_book, 16 * G, o.status);
-    __syncthreads();
-    // 2^shift * max|x| * kWindow < 2^30: no window sum can overflow int32.
-    const float xmax = book_absmax<G>(sa_book, sred);
-    int shift = 0;
-    if (xmax > 0.0f) {
-      int ex;
-      frexpf(xmax, &ex);  // xmax < 2^ex, so xmax * kWindow < 2^(ex + 10)
-      shift = 30 - (ex + 10);
-      shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
-    }
-    const float unscale = ldexpf(1.0f, -shift);
-    float acc[M][kBinsPerThread];
-#pragma unroll
-    for (int r = 0; r < M; ++r)
-#pragma unroll
-      for (int i = 0; i < kBinsPerThread; ++i) acc[r][i] = 0.0f;
-
-    uint32_t xbase = k0;  // first row of the staged x chunk
-    stage_x<G, M>(a_codes, sa_book, k, flags, xbase, kend, kXRows, shift, sxq);
-    __syncthreads();
-    for (uint32_t kb = k0; kb < kend; kb += kBatchRows) {
-      uint32_t w[kRowsPerLane];
-#pragma unroll
-      for (int u = 0; u < kRowsPerLane; ++u) w[u] = wn[u];
-      if (kb + kBatchRows < kend)
-        load_batch(col_codes, row_words, kb + kBatchRows + lane_row, kend, live, wn);
-      if (live) {
-        const uint32_t first = kb + lane_row;
-#pragma unroll
-        for (int r = 0; r < M; ++r) {
-          const uint32_t base = r * (16 * kTileGroups * 4);
-          // the lane's 16 activations, 16-byte aligned; rows past kend are
-          // staged as zero (and carry w = 0), so their adds are no-ops
-          const int4* xr = reinterpret_cast<const int4*>(sxq + r * kXRows + (first - xbase));
-          int32_t xs[kRowsPerLane];
-#pragma unroll
-          for (int i = 0; i < kRowsPerLane / 4; ++i) {
-            const int4 v = xr[i];
-            xs[4 * i] = v.x; xs[4 * i + 1] = v.y; xs[4 * i + 2] = v.z; xs[4 * i + 3] = v.w;
-          }
-#pragma unroll
-          for (int u = 0; u < kRowsPerLane; ++u) {
-            const int32_t xv = xs[u];
-            const uint32_t ww = w[u];
-            lds_add(base + 0 * 2048 + bin_byte<0>(ww, q4), xv);
-            lds_add(base + 1 * 2048 + bin_byte<1>(ww, q4), xv);
-            lds_add(base + 2 * 2048 + bin_byte<2>(ww, q4), xv);
-            lds_add(base + 3 * 2048 + bin_byte<3>(ww, q4), xv);
-            lds_add(base + 4 * 2048 + bin_byte<4>(ww, q4), xv);
-            lds_add(base + 5 * 2048 + bin_byte<5>(ww, q4), xv);
-            lds_add(base + 6 * 2048 + bin_byte<6>(ww, q4), xv);
-            lds_add(base + 7 * 2048 + bin_byte<7>(ww, q4), xv);
-          }
-        }
-      }
-      const uint32_t done = kb + kBatchRows;
-      const bool flush = done >= kend || (done - k0) % kWindow == 0;
-      const bool restage = done < kend && done - xbase >= kXRows;
-      if (flush || restage) {
-        __syncthreads();
-        if (flush) {
-          // the window ends: integer bins -> FP32 accumulators, bins reset
-#pragma unroll
-          for (int r = 0; r < M; ++r)
-#pragma unroll
-            for (int i = 0; i < kBinsPerThread; ++i) {
-              const uint32_t b = r * 16 * kTileGroups + tid + i * kBinThreads;
-              acc[r][i] += float(bins[b]);
-              bins[b] = 0;
-            }
-        }
-        if (restage) {
-          xbase = done;
-          stage_x<G, M>(a_codes, sa_book, k, flags, xbase, kend, kXRows, shift, sxq);
-        }
-        __syncthreads();
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < M; ++r)
-#pragma unroll
-      for (int i = 0; i < kBinsPerThread; ++i)
-        fbins[r * 16 * kTileGroups + tid + i * kBinThreads] = acc[r][i] * unscale;
-    __syncthreads();
-
-    // Finalise this tile: y[r][j*G+t] = sum_e C_B[e][t] * S[r][j][e].
-    const uint32_t groups = (row_words - tile * kTileWords) < kTileWords
-                                ? (row_words - tile * kTileWords) * 8
-                                : kTileGroups;
-    if (gridDim.y == 1) {
-      float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
-      bool bad = false;
-      for (uint32_t e = tid; e < M * groups * G; e += kBinThreads) {
-        const uint32_t r = e / (groups * G);
-        const uint32_t jt = e % (groups * G);
-        const uint32_t j = jt / G, t = jt % G;
-        float y = 0.0f;
-#pragma unroll
-        for (uint32_t c = 0; c < 16; ++c)
-          y = fmaf(sb_book[c * G + t], fbins[bin_index(r, j % 8, c, j / 8)], y);
-        out[uint64_t(r) * n + tile * kTileGroups * G + jt] = y;
-        bad |= !finite_f32(y);
-      }
-      if (__any(bad) && (tid % warpSize) == 0) atomicOr(o.status, 1u);
-    } else {
-      // partial[item][tile][split][r][j][e]
-      float* p = partial + ((uint64_t(item) * gridDim.x + tile) * gridDim.y + split) *
-                               (M * 16 * kTileGroups);
-      for (uint32_t e = tid; e < M * 16 * kTileGroups; e += kBinThreads) {
-        const uint32_t r = e / (16 * kTileGroups);
-        const uint32_t je = e % (16 * kTileGroups);
-        const uint32_t j = je / 16, c = je % 16;
-        p[e] = fbins[bin_index(r, j % 8, c, j / 8)];
-      }
-    }
-  }
 }
 
 // Sum the split-k bins in split order (one thread per bin), then apply the B
@@ -409,7 +167,7 @@ constexpr uint32_t kFinishParts = 16;
 constexpr uint32_t kFinishGroups = kTileGroups / kFinishParts;  // 16 groups, 256 bins
 
 template <int G, int M>
-__global__ __launch_bounds__(256) void k_gemv_bins_finish(Operands o, uint32_t n, uint32_t splits,
+__global__ __launch_bounds__(256) void k_gemv_finish(Operands o, uint32_t n, uint32_t splits,
                                                           uint32_t tiles, const float* partial) {
   __shared__ float sb_book[16 * G];
   __shared__ float ssum[M][kFinishGroups * 16];
@@ -855,6 +613,369 @@ size_t pairs_shmem(uint32_t g) {
   return g == 8 ? PairLds<8>::total : (g == 16 ? PairLds<16>::total : PairLds<32>::total);
 }
 
+// ---- GemvRows (2 <= m <= 8) -------------------------------------------------
+// Nibble bins, two rows of A per atomic: for word column q, nibble n8 (output
+// group 8q + n8) and code e, the bin pair (S[2rp][j][e], S[2rp+1][j][e]) is
+// one 64-bit LDS word that a single ds_add_u64 updates with the 64-bit value
+// x_hi * 2^32 + x_lo (x_lo sign-extended). Integer addition then carries the
+// two int32 sums exactly side by side: the low word is S_lo, the high word is
+// S_hi - [S_lo < 0], recovered at the flush. Odd m pads a zero row.
+//
+// Bin (e, n8, rp, q) is the 8-byte word ((e * 8 + n8) * MP + rp) * 32 + q, so
+// one nibble's MP row pairs sit at immediate offsets from one address (one
+// bfe and one shift-add per nibble), and the 32 lanes of a half-wave (one word
+// column each) touch 32 consecutive 8-byte words.
+//
+// The pipeline is GemvPairs': a register ring of D batches of R rows per lane,
+// the next instance's first batches and set-up data requested during the
+// current one, x staged per row in LDS (as the 64-bit pair values) and read
+// one row ahead of that row's atomics. The staged chunk holds kRowXBytes; a
+// slice longer than that is restaged, from A's words and codebook in LDS.
+constexpr int kRowThreads = 512;
+constexpr int kRowR = 8;                                           // rows per lane per batch
+constexpr int kRowD = 4;
+constexpr uint32_t kRowBatchRows = (kRowThreads / 64) * 2 * kRowR;  // 128
+constexpr uint32_t kRowWindow = 4096;
+constexpr uint32_t kRowXBytes = 16384;
+constexpr uint32_t kRowAWords = 2048;                              // A words of a slice
+
+// Rows of x per staged chunk for MP row pairs: whole batches.
+__host__ __device__ constexpr uint32_t row_x_rows(uint32_t mp) {
+  return kRowXBytes / (8 * mp) / kRowBatchRows * kRowBatchRows;
+}
+
+template <int G, int MP>
+struct RowLds {
+  static constexpr uint32_t bins = 8 * 16 * MP * kTileWords * 8;  // bytes of 64-bit bins
+  static constexpr uint32_t xr = row_x_rows(MP);
+  static constexpr uint32_t xs = bins;
+  static constexpr uint32_t af = xs + xr * MP * 8;
+  static constexpr uint32_t bb = af + 16 * G * 4;
+  static constexpr uint32_t aw = bb + 16 * G * 4;
+  static constexpr uint32_t rmax = aw + kRowAWords * 4;
+  static constexpr uint32_t total = rmax + 16 * 4;
+};
+
+typedef __attribute__((address_space(3))) int64_t lds_i64;
+
+__device__ __forceinline__ void lds_add64(uint32_t byte_addr, int64_t v) {
+  __hip_atomic_fetch_add(reinterpret_cast<lds_i64*>(static_cast<size_t>(byte_addr)), v,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Words of A one slice needs: per row of A (flags 0) or one run (flags 1).
+struct RowAWords {
+  uint32_t per_row;   // words reserved per row (flags 0)
+  uint32_t total;     // words staged
+};
+
+__host__ __device__ inline RowAWords row_a_words(uint32_t m, uint32_t ks, uint32_t group,
+                                                 uint32_t flags) {
+  RowAWords w;
+  w.per_row = ks / (8 * group) + 2;
+  w.total = (flags & 1u) ? ks * m / (8 * group) + 2 : m * w.per_row;
+  return w;
+}
+
+struct RowAhead {
+  uint32_t w[4];   // A words tid + j * kRowThreads
+  float a, b;      // entry tid of the A and B books
+};
+
+template <int G, int MP>
+__global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32_t m, uint32_t n,
+                                                              uint32_t k, uint32_t flags,
+                                                              uint32_t ks, float* partial) {
+  constexpr uint32_t R = kRowR, D = kRowD, BR = kRowBatchRows;
+  constexpr uint32_t kBins64 = 8 * 16 * MP * kTileWords;
+  constexpr int kPer = kBins64 / kRowThreads;     // 64-bit bins per thread
+  static_assert(kBins64 % kRowThreads == 0, "bins per thread");
+  static_assert(16 * G <= kRowThreads, "one book entry per thread");
+  static_assert(kRowAWords <= 4 * kRowThreads, "A words per thread");
+  using L = RowLds<G, MP>;
+  constexpr uint32_t XR = L::xr;
+  static_assert(XR >= BR && kRowWindow % BR == 0, "staging");
+  extern __shared__ int32_t smem[];
+  char* lds = reinterpret_cast<char*>(smem);
+  int64_t* bins = reinterpret_cast<int64_t*>(smem);
+  int2* sx = reinterpret_cast<int2*>(lds + L::xs);
+  float* af = reinterpret_cast<float*>(lds + L::af);
+  float* bb = reinterpret_cast<float*>(lds + L::bb);
+  uint32_t* aw = reinterpret_cast<uint32_t*>(lds + L::aw);
+  float* rmax = reinterpret_cast<float*>(lds + L::rmax);
+  if (static_cast<uint32_t>(reinterpret_cast<size_t>((lds_i32*)smem)) != 0) {
+    if (threadIdx.x == 0) atomicOr(o.status, 2u);
+    return;
+  }
+  const uint32_t tid = threadIdx.x;
+  const uint32_t tile = blockIdx.x, split = blockIdx.y, zn = gridDim.z;
+  const uint32_t rw = n / (8 * G);
+  const uint32_t k0 = split * ks;
+  const uint32_t kend = (k0 + ks) < k ? (k0 + ks) : k;
+  const uint32_t nb = (kend - k0 + BR - 1) / BR;
+  const uint32_t nbp = (nb + D - 1) / D * D;
+  const uint32_t lane = tid % 64, wave = tid / 64;
+  const uint32_t q = lane % 32, half = lane / 32;
+  const uint32_t lane_row = (wave * 2 + half) * R;
+  const uint32_t col = (tile * kTileWords + q < rw) ? tile * kTileWords + q : rw - 1;
+  const uint32_t q8 = q * 8;
+  const RowAWords awn = row_a_words(m, ks, G, flags);
+  const uint32_t a_vec_elems = m * k;  // A's flat extent
+
+  auto opaque = [](uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+  };
+  // first A word staged for row r (flags 0) or for the slice (flags 1)
+  auto a_base = [&](uint32_t r) {
+    return (flags & 1u) ? (k0 * m / G) >> 3 : ((r * k + k0) / G) >> 3;
+  };
+  auto setup_loads = [&](uint32_t item) {
+    const uint32_t lt = opaque(tid);
+    const uint32_t a_words_all = ((a_vec_elems + G - 1) / G + 7) / 8;
+    const __amdgpu_buffer_rsrc_t ars =
+        words_rsrc(item_ptr<uint32_t>(o.in[0], o.stride[0], item), a_words_all * 4u);
+    const __amdgpu_buffer_rsrc_t abk = words_rsrc(item_ptr<float>(o.in[1], o.stride[1], item), 64u * G);
+    const __amdgpu_buffer_rsrc_t bbk = words_rsrc(item_ptr<float>(o.in[3], o.stride[3], item), 64u * G);
+    RowAhead h;
+    h.a = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(abk, lt * 4u, 0, 0)));
+    h.b = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(bbk, lt * 4u, 0, 0)));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t idx = lt + j * kRowThreads;
+      // staged word idx: row idx / per_row, word idx % per_row of that row (flags 0)
+      const uint32_t r = (flags & 1u) ? 0u : idx / awn.per_row;
+      const uint32_t i = (flags & 1u) ? idx : idx % awn.per_row;
+      const bool want = idx < awn.total && r < m;
+      h.w[j] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(
+          ars, want ? (a_base(r) + i) * 4u : 0xfffffff0u, 0, 0));
+    }
+    return h;
+  };
+  auto batch_rsrc = [&](uint32_t item) {
+    const bool real = item < o.count;
+    return words_rsrc(item_ptr<uint32_t>(o.in[2], o.stride[2], real ? item : 0),
+                      real ? kend * rw * 4u : 0u);
+  };
+  const uint32_t voff_lane = (lane_row * rw + col) * 4u;
+  auto load_batch = [&](__amdgpu_buffer_rsrc_t rs, uint32_t b, uint32_t (&w)[R]) {
+    uint32_t off = voff_lane + (k0 + b * BR) * rw * 4u;
+    asm volatile("" : "+v"(off));
+#pragma unroll
+    for (uint32_t u = 0; u < R; ++u)
+      w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, off + u * rw * 4u, 0, 0));
+  };
+
+  uint32_t buf[D][R];
+  float acc[kPer][2];
+  int shift = 0;
+  uint32_t xbase = k0;
+
+  // one quantised activation of A
+  auto x_of = [&](uint32_t r, uint32_t kk) -> int32_t {
+    const uint32_t flat = (flags & 1u) ? kk * m + r : r * k + kk;
+    const uint32_t v = flat / G;
+    const uint32_t slot = (flags & 1u) ? (v >> 3) - a_base(0) : r * awn.per_row + (v >> 3) - a_base(r);
+    const uint32_t code = (aw[slot] >> ((v & 7u) * 4u)) & 15u;
+    const float lim = 524287.0f;  // 2^19 - 1: a 4096-row window of sums fits int32
+    return int32_t(fminf(rintf(ldexpf(af[code * G + flat % G], shift)), lim));
+  };
+  // rows [xb0, xb0 + XR): per row and row pair, the 64-bit addend's two halves
+  auto stage_x = [&](uint32_t xb0) __attribute__((always_inline)) {
+    for (uint32_t idx = opaque(tid); idx < XR * MP; idx += kRowThreads) {
+      const uint32_t kk = xb0 + idx / MP, rp = idx % MP;
+      int32_t lo = 0, hi = 0;
+      if (kk < kend) {
+        if (2 * rp < m) lo = x_of(2 * rp, kk);
+        if (2 * rp + 1 < m) hi = x_of(2 * rp + 1, kk);
+      }
+      sx[idx] = make_int2(lo, hi + (lo >> 31));
+    }
+  };
+  // x pairs of one row of this lane's batch
+  auto read_row = [&](uint32_t row, int2 (&xp)[MP]) __attribute__((always_inline)) {
+    const int2* p = sx + (row - xbase) * MP;
+#pragma unroll
+    for (int rp = 0; rp < MP; ++rp) xp[rp] = p[rp];
+  };
+  auto flush = [&](bool clear) __attribute__((always_inline)) {
+    const uint32_t ft = opaque(tid);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const uint32_t bi = ft + i * kRowThreads;
+      const int64_t v = bins[bi];
+      const uint32_t lo = uint32_t(uint64_t(v)), hi = uint32_t(uint64_t(v) >> 32);
+      acc[i][0] += float(int32_t(lo));
+      acc[i][1] += float(int32_t(hi + (lo >> 31)));
+      if (clear) bins[bi] = 0;
+    }
+  };
+  // x pairs alternate between two register sets by row parity (R is even, so
+  // the next batch's first row is read during this batch's last row)
+  int2 xa[MP], xb[MP];
+  auto stage = [&](uint32_t (&w)[R], uint32_t b, __amdgpu_buffer_rsrc_t rs_refill,
+                   uint32_t b_refill) __attribute__((always_inline)) {
+    asm volatile("" : "+s"(b));
+    const uint32_t done = (b + 1) * BR;
+    const bool last = b + 1 == nbp;
+    const bool restage = k0 + done < kend && k0 + done - xbase >= XR;
+    const bool wend = done % kRowWindow == 0 || last;
+    if (b < nb) {  // padding batches (past the slice) bin nothing
+      const uint32_t first = k0 + b * BR + lane_row;
+#pragma unroll
+      for (uint32_t u = 0; u < R; ++u) {
+        int2 (&cur)[MP] = (u & 1u) ? xb : xa;
+        int2 (&nxt)[MP] = (u & 1u) ? xa : xb;
+        // the next row's x is read ahead of this row's atomics (LDS operations
+        // complete in order)
+        if (u + 1 < R) read_row(first + u + 1, nxt);
+        else if (b + 1 < nb && !restage) read_row(first + BR, nxt);
+        const uint32_t ww = w[u];
+        int64_t add[MP];
+#pragma unroll
+        for (int rp = 0; rp < MP; ++rp)
+          add[rp] = int64_t((uint64_t(uint32_t(cur[rp].y)) << 32) | uint32_t(cur[rp].x));
+#pragma unroll
+        for (uint32_t n8 = 0; n8 < 8; ++n8) {
+          const uint32_t base = __builtin_amdgcn_ubfe(ww, 4 * n8, 4) * (2048u * MP) + q8;
+#pragma unroll
+          for (int rp = 0; rp < MP; ++rp) lds_add64(base + (n8 * MP + rp) * 256, add[rp]);
+        }
+      }
+    }
+    load_batch(rs_refill, b_refill, w);
+    __builtin_amdgcn_sched_barrier(0);
+    if (wend) {
+      __syncthreads();
+      flush(!last);
+      if (!last && !restage) __syncthreads();
+    }
+    if (restage) {
+      if (!wend) __syncthreads();
+      xbase = k0 + done;
+      stage_x(xbase);
+      __syncthreads();
+      read_row(k0 + done + lane_row, xa);
+      // settle here, so at the join the common path's x needs no wait behind
+      // this batch's atomics
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+    }
+  };
+
+  uint32_t item = blockIdx.z;
+  RowAhead cur{}, nxt{};
+  if (item < o.count) {
+    cur = setup_loads(item);
+    nxt = setup_loads(item + zn < o.count ? item + zn : item);
+    const __amdgpu_buffer_rsrc_t r0 = batch_rsrc(item);
+#pragma unroll
+    for (uint32_t d = 0; d < D; ++d) load_batch(r0, d, buf[d]);
+  }
+  for (; item < o.count; item += zn) {
+    const uint32_t next = item + zn;
+    const __amdgpu_buffer_rsrc_t cur_rs = batch_rsrc(item);
+    const __amdgpu_buffer_rsrc_t next_rs = batch_rsrc(next);
+    // ---- set-up ----
+    const uint32_t st = opaque(tid);
+    __syncthreads();
+    if (st < 16 * G) { af[st] = cur.a; bb[st] = cur.b; }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (st + j * kRowThreads < kRowAWords) aw[st + j * kRowThreads] = cur.w[j];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) bins[st + i * kRowThreads] = 0;
+    __syncthreads();
+    if (tile == 0 && split == 0) sweep_books(af, bb, 16 * G, o.status);
+    if (st < 16) {
+      float mx = 0.0f;
+#pragma unroll
+      for (int t = 0; t < G; t += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(af + st * G + t);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+      }
+      rmax[st] = mx;
+    }
+    __syncthreads();
+    float amax = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 16; t += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(rmax + t);
+      amax = fmaxf(amax, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+    }
+    shift = 0;
+    if (amax > 0.0f) {
+      int ex;
+      frexpf(amax, &ex);  // max|x| * 2^shift < 2^19
+      shift = 31 - (ex + 12);
+      shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
+    }
+    const float unscale = ldexpf(1.0f, -shift);
+    xbase = k0;
+    stage_x(xbase);
+    __syncthreads();
+    read_row(k0 + lane_row, xa);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // settle the first row's x before the loop
+    cur = nxt;
+    nxt = setup_loads(next + zn < o.count ? next + zn : item);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) acc[i][0] = acc[i][1] = 0.0f;
+
+    for (uint32_t b0 = 0; b0 + D < nbp; b0 += D) {
+#pragma unroll
+      for (uint32_t d = 0; d < D; ++d) stage(buf[d], b0 + d, cur_rs, b0 + d + D);
+    }
+#pragma unroll
+    for (uint32_t d = 0; d < D; ++d) stage(buf[d], nbp - D + d, next_rs, d);
+
+    // ---- finalise: S[r][e][n8][q] in LDS, then y = C_B^T S per group ----
+    const uint32_t ft = opaque(tid);
+    float* ss = reinterpret_cast<float*>(smem);
+    __syncthreads();  // every thread has flushed its bins
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const uint32_t bi = ft + i * kRowThreads;
+      const uint32_t qq = bi % kTileWords, rest = bi / kTileWords;
+      const uint32_t rp = rest % MP, rest2 = rest / MP;
+      const uint32_t n8 = rest2 % 8, e = rest2 / 8;
+#pragma unroll
+      for (uint32_t h = 0; h < 2; ++h) {
+        const uint32_t r = 2 * rp + h;
+        const float s = acc[i][h] * unscale;
+        if (gridDim.y == 1) {
+          ss[((r * 16 + e) * 8 + n8) * kTileWords + qq] = s;
+        } else if (r < m) {
+          float* pp = partial + ((uint64_t(item) * gridDim.x + tile) * gridDim.y + split) *
+                                    (m * 16 * kTileGroups);
+          pp[r * 16 * kTileGroups + (qq * 8 + n8) * 16 + e] = s;
+        }
+      }
+    }
+    __syncthreads();
+    if (gridDim.y == 1) {
+      const uint32_t groups = (rw - tile * kTileWords) < kTileWords
+                                  ? (rw - tile * kTileWords) * 8
+                                  : kTileGroups;
+      const uint32_t t = ft % G;
+      float cb[16];
+#pragma unroll
+      for (uint32_t c = 0; c < 16; ++c) cb[c] = bb[c * G + t];
+      float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
+      bool bad = false;
+      for (uint32_t idx = ft; idx < m * groups * G; idx += kRowThreads) {
+        const uint32_t r = idx / (groups * G), rem = idx % (groups * G);
+        const uint32_t j = rem / G;
+        const float* sj = ss + (r * 16 * 8 + j % 8) * kTileWords + j / 8;
+        float y = 0.0f;
+#pragma unroll
+        for (uint32_t c = 0; c < 16; ++c) y = fmaf(cb[c], sj[c * kTileGroups], y);
+        out[uint64_t(r) * n + tile * kTileGroups * G + rem] = y;
+        bad |= !finite_f32(y);
+      }
+      if (__any(bad) && (ft % warpSize) == 0) atomicOr(o.status, 1u);
+    }
+  }
+}
+
 uint32_t gemv_splits(uint32_t n, uint32_t k, uint32_t group, uint32_t count) {
   const uint32_t tiles = (n / (8 * group) + kTileWords - 1) / kTileWords;
   const uint64_t blocks = uint64_t(tiles) * count;
@@ -872,34 +993,6 @@ void pairs_slices(uint32_t n, uint32_t k, uint32_t group, uint32_t count, uint32
   const uint32_t per = (k + want - 1) / want;
   *ks = (per + kPairBatchRows - 1) / kPairBatchRows * kPairBatchRows;
   *splits = (k + *ks - 1) / *ks;
-}
-
-size_t bins_shmem(uint32_t m, uint32_t g) {
-  return size_t(m) * 16 * kTileGroups * 4 + kXBytes + 2 * 16 * g * 4 + kBinWaves * 4;
-}
-
-template <int G, int M>
-hipError_t launch_bins_m(hipStream_t s, const Operands& o, uint32_t n, uint32_t k, uint32_t flags,
-                         void* workspace) {
-  const uint32_t tiles = (n / (8 * G) + kTileWords - 1) / kTileWords;
-  const uint32_t splits = gemv_splits(n, k, G, o.count);
-  const uint32_t ks = (k + splits - 1) / splits;
-  const uint32_t zc = o.count < 65535 ? o.count : 65535;
-  const size_t shmem = bins_shmem(M, G);
-  if (shmem > 65536) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_bins<G, M>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
-    if (e != hipSuccess) return e;
-  }
-  dim3 grid(tiles, splits, zc);
-  k_gemv_bins<G, M><<<grid, kBinThreads, shmem, s>>>(o, n, k, flags, ks,
-                                                     static_cast<float*>(workspace));
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess || splits == 1) return err;
-  dim3 fgrid(tiles * kFinishParts, 1, zc);
-  k_gemv_bins_finish<G, M><<<fgrid, 256, 0, s>>>(o, n, splits, tiles,
-                                                 static_cast<const float*>(workspace));
-  return hipGetLastError();
 }
 
 template <int G>
@@ -923,23 +1016,64 @@ hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || splits == 1) return err;
   dim3 fgrid(tiles * kFinishParts, 1, zc);
-  k_gemv_bins_finish<G, 1><<<fgrid, 256, 0, s>>>(o, n, splits, tiles,
+  k_gemv_finish<G, 1><<<fgrid, 256, 0, s>>>(o, n, splits, tiles,
                                                  static_cast<const float*>(workspace));
   return hipGetLastError();
 }
 
-template <int G>
-hipError_t launch_bins(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
-                       uint32_t flags, void* workspace) {
+// Slices of k for GemvRows: gemv_splits' count in whole batches, and short
+// enough that one slice's A words fit the staging area.
+void rows_slices(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                 uint32_t count, uint32_t* ks, uint32_t* splits) {
+  const uint32_t want = gemv_splits(n, k, group, count);
+  uint32_t per = (k + want - 1) / want;
+  per = (per + kRowBatchRows - 1) / kRowBatchRows * kRowBatchRows;
+  while (per > kRowBatchRows && row_a_words(m, per, group, flags).total > kRowAWords)
+    per = (per / 2 + kRowBatchRows - 1) / kRowBatchRows * kRowBatchRows;
+  *ks = per;
+  *splits = (k + per - 1) / per;
+}
+
+template <int G, int MP>
+hipError_t launch_rows_mp(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                          uint32_t flags, void* workspace) {
+  const uint32_t tiles = (n / (8 * G) + kTileWords - 1) / kTileWords;
+  uint32_t ks, splits;
+  rows_slices(m, n, k, G, flags, o.count, &ks, &splits);
+  const uint32_t per_z = tiles * splits;
+  uint32_t zc = per_z >= 256 ? 1u : 256u / per_z;
+  zc = zc < o.count ? zc : o.count;
+  const size_t shmem = RowLds<G, MP>::total;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_rows<G, MP>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
+  if (e != hipSuccess) return e;
+  dim3 grid(tiles, splits, zc);
+  k_gemv_rows<G, MP><<<grid, kRowThreads, shmem, s>>>(o, m, n, k, flags, ks,
+                                                      static_cast<float*>(workspace));
+  e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  dim3 fgrid(tiles * kFinishParts, 1, zc);
+  const float* part = static_cast<const float*>(workspace);
   switch (m) {
-    case 1: return launch_bins_m<G, 1>(s, o, n, k, flags, workspace);
-    case 2: return launch_bins_m<G, 2>(s, o, n, k, flags, workspace);
-    case 3: return launch_bins_m<G, 3>(s, o, n, k, flags, workspace);
-    case 4: return launch_bins_m<G, 4>(s, o, n, k, flags, workspace);
-    case 5: return launch_bins_m<G, 5>(s, o, n, k, flags, workspace);
-    case 6: return launch_bins_m<G, 6>(s, o, n, k, flags, workspace);
-    case 7: return launch_bins_m<G, 7>(s, o, n, k, flags, workspace);
-    default: return launch_bins_m<G, 8>(s, o, n, k, flags, workspace);
+    case 2: k_gemv_finish<G, 2><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
+    case 3: k_gemv_finish<G, 3><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
+    case 4: k_gemv_finish<G, 4><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
+    case 5: k_gemv_finish<G, 5><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
+    case 6: k_gemv_finish<G, 6><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
+    case 7: k_gemv_finish<G, 7><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
+    default: k_gemv_finish<G, 8><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
+  }
+  return hipGetLastError();
+}
+
+template <int G>
+hipError_t launch_rows(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                       uint32_t flags, void* workspace) {
+  switch ((m + 1) / 2) {
+    case 1: return launch_rows_mp<G, 1>(s, o, m, n, k, flags, workspace);
+    case 2: return launch_rows_mp<G, 2>(s, o, m, n, k, flags, workspace);
+    case 3: return launch_rows_mp<G, 3>(s, o, m, n, k, flags, workspace);
+    default: return launch_rows_mp<G, 4>(s, o, m, n, k, flags, workspace);
   }
 }
 
@@ -948,7 +1082,7 @@ hipError_t launch_bins(hipStream_t s, const Operands& o, uint32_t m, uint32_t n,
 const char* matmul_path_name(MatmulPath p) {
   switch (p) {
     case MatmulPath::General: return "general";
-    case MatmulPath::GemvBins: return "gemv-bins";
+    case MatmulPath::GemvRows: return "gemv-rows";
     case MatmulPath::GemvPairs: return "gemv-pairs";
     case MatmulPath::GemvTable: return "gemv-table";
     case MatmulPath::GramMfma: return "gram-mfma";
@@ -963,20 +1097,17 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
   if (count == 1 && rowbins_applies(m, n, k, group, flags)) return MatmulPath::RowBins;
   if (gram_applies(m, n, k, group, flags)) return MatmulPath::GramMfma;
   if (m <= kGemvMaxM && (flags & 2u) == 0 && n % (8 * group) == 0)
-    return m == 1 ? MatmulPath::GemvPairs : MatmulPath::GemvBins;
+    return m == 1 ? MatmulPath::GemvPairs : MatmulPath::GemvRows;
   return MatmulPath::General;
 }
 
 size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                               uint32_t flags, uint32_t count) {
-  (void)flags;
   if (p == MatmulPath::RowBins) return rowbins_workspace_bytes(n, k, group);
-  if (p != MatmulPath::GemvBins && p != MatmulPath::GemvPairs) return 0;
-  uint32_t splits = gemv_splits(n, k, group, count);
-  if (p == MatmulPath::GemvPairs) {
-    uint32_t ks;
-    pairs_slices(n, k, group, count, &ks, &splits);
-  }
+  if (p != MatmulPath::GemvRows && p != MatmulPath::GemvPairs) return 0;
+  uint32_t ks, splits;
+  if (p == MatmulPath::GemvPairs) pairs_slices(n, k, group, count, &ks, &splits);
+  else rows_slices(m, n, k, group, flags, count, &ks, &splits);
   if (splits == 1) return 0;
   const uint32_t tiles = (n / (8 * group) + kTileWords - 1) / kTileWords;
   return size_t(count) * splits * tiles * m * 16 * kTileGroups * sizeof(float);
@@ -993,10 +1124,10 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
     if (group == 16) return launch_pairs<16>(s, o, n, k, flags, workspace);
     return launch_pairs<32>(s, o, n, k, flags, workspace);
   }
-  if (path == MatmulPath::GemvBins) {
-    if (group == 8) return launch_bins<8>(s, o, m, n, k, flags, workspace);
-    if (group == 16) return launch_bins<16>(s, o, m, n, k, flags, workspace);
-    return launch_bins<32>(s, o, m, n, k, flags, workspace);
+  if (path == MatmulPath::GemvRows) {
+    if (group == 8) return launch_rows<8>(s, o, m, n, k, flags, workspace);
+    if (group == 16) return launch_rows<16>(s, o, m, n, k, flags, workspace);
+    return launch_rows<32>(s, o, m, n, k, flags, workspace);
   }
   const uint32_t zc = o.count < 65535 ? o.count : 65535;
   dim3 grid((n + kGT - 1) / kGT, (m + kGT - 1) / kGT, zc);

@@ -79,12 +79,12 @@ GEMV_SHAPES = [(256, 256, 16), (4096, 4096, 16), (512, 1024, 8), (1024, 768, 32)
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8])
-def test_gemv_bins_within_tolerance(vqdev, oracle, m):
+def test_gemv_within_tolerance(vqdev, oracle, m):
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(50 + m)
     for k, n, group in GEMV_SHAPES:
         words = (2, m, n, k, group, 16, 0, 0)
-        assert vqdev.path_name(words) == ("gemv-pairs" if m == 1 else "gemv-bins")
+        assert vqdev.path_name(words) == ("gemv-pairs" if m == 1 else "gemv-rows")
         say("gemv", m, k, n, group)
         ops = _operands(rng, m, n, k, group, 1.0, 0.02)
         out, status = _gpu(vqdev, ops, m, n, k, group, 0)
@@ -95,25 +95,26 @@ def test_gemv_bins_within_tolerance(vqdev, oracle, m):
         assert o.max_rel(out, _ref64(ops, m, n, k, group, 0)) <= TOL
 
 
-def test_gemv_bins_transposed_a(vqdev, oracle):
+def test_gemv_transposed_a(vqdev, oracle):
     """A stored (k, m): the activation decode follows the flat index."""
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(77)
-    for m, k, n, group in ((1, 256, 256, 16), (4, 200, 512, 8), (3, 96, 1024, 32)):
-        say("gemv-bins a^T", m, k, n, group)
+    for m, k, n, group in ((1, 256, 256, 16), (4, 200, 512, 8), (3, 96, 1024, 32),
+                           (8, 3000, 256, 16), (7, 1100, 512, 8)):
+        say("gemv a^T", m, k, n, group)
         ops = _operands(rng, m, n, k, group)
         out, status = _gpu(vqdev, ops, m, n, k, group, 1)
         ref, _ = oracle.matmul(*ops, m, n, k, group, 1)
         assert status == 0 and o.max_rel(out, ref) <= TOL
 
 
-def test_gemv_bins_batched(vqdev, oracle):
+def test_gemv_batched(vqdev, oracle):
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(88)
     m, k, n, group, count = 1, 512, 512, 16, 6
     items = [_operands(rng, m, n, k, group) for _ in range(count)]
     ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
-    say("gemv-bins batch", count)
+    say("gemv batch", count)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
     for i, it in enumerate(items):
@@ -122,7 +123,7 @@ def test_gemv_bins_batched(vqdev, oracle):
 
 
 @pytest.mark.parametrize("m", [1, 3, 5, 8])
-def test_gemv_bins_long_slices(vqdev, oracle, m):
+def test_gemv_long_slices(vqdev, oracle, m):
     """256 instances fill the chip without splitting k, so each block walks
     all 2600 rows: several integer windows, and the staged activations are
     restaged at chunk ends that do not coincide with window ends."""
@@ -131,7 +132,7 @@ def test_gemv_bins_long_slices(vqdev, oracle, m):
     k, n, group, count = 2600, 128, 16, 256
     items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
     ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
-    say("gemv-bins long slices", m, count)
+    say("gemv long slices", m, count)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
     for i in (0, 1, 128, 255):
@@ -194,6 +195,49 @@ def test_gemv_pairs_saturated_window(vqdev, sign):
     ops = tuple(np.tile(a.reshape(-1), count) for a in one)
     assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
     say("gemv-pairs saturated", sign)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    ref = _ref64(one, m, n, k, group, 0)
+    for i in (0, 255):
+        assert o.max_rel(out[i], ref) <= TOL
+
+
+@pytest.mark.parametrize("m,k,group,flags", [(2, 20000, 8, 0), (8, 20000, 8, 0),
+                                             (5, 12000, 16, 1), (6, 700, 32, 0)])
+def test_gemv_rows_split_slices(vqdev, m, k, group, flags):
+    """One product (no batch) over long k: k is split across blocks, and for
+    g = 8, m = 8 the slices are also capped so one slice's A words fit the
+    staging area; the split partials are summed by the finish kernel."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(k + m)
+    n = 512
+    ops = _operands(rng, m, n, k, group, 1.0, 0.02)
+    assert vqdev.path_name((2, m, n, k, group, 16, flags, 0)) == "gemv-rows"
+    say("gemv-rows split", m, k, group, flags)
+    out, status = _gpu(vqdev, ops, m, n, k, group, flags)
+    assert status == 0
+    assert o.max_rel(out, _ref64(ops, m, n, k, group, flags)) <= TOL
+
+
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_gemv_rows_saturated_window(vqdev, sign):
+    """Both rows of a 64-bit bin pair at the largest activation over a full
+    4096-row window into one bin: each int32 half reaches 4096 * (2^19 - 1)
+    (or -2^31) and the carry between the halves must stay exact."""
+    from oracle import vq4_numpy as o
+    m, n, k, group = 2, 512, 4096, 16
+    a_book = np.full((16, group), sign * np.nextafter(np.float32(1), np.float32(0)), np.float32)
+    a_book[1] = -a_book[1]
+    # row 0 uses entry 0, row 1 entry 1: opposite signs in the two halves
+    a_idx = np.concatenate([np.zeros(k // group, np.int64), np.ones(k // group, np.int64)])
+    a_codes = o.pack_indices(a_idx)
+    b_book = (np.arange(16 * group, dtype=np.float32).reshape(16, group) / 256.0).astype(np.float32)
+    b_codes = o.pack_indices(np.full(k * n // group, 9, np.int64))
+    one = (a_codes, a_book, b_codes, b_book)
+    count = 256
+    ops = tuple(np.tile(a.reshape(-1), count) for a in one)
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-rows"
+    say("gemv-rows saturated", sign)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
     ref = _ref64(one, m, n, k, group, 0)
