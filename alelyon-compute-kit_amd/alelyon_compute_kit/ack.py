@@ -130,6 +130,8 @@ _SIGNATURES = {
                            _c.c_int32),
     "ack_vq_host_fit_codebook": ([_c.c_void_p, _c.c_uint64, _c.c_uint32, _c.c_uint32,
                                   _c.c_uint32, _c.c_void_p, _c.c_void_p], _c.c_int32),
+    "ack_vq_fit_codebook": ([_c.c_void_p] * 5 + [_c.c_uint64, _c.c_uint32, _c.c_uint32,
+                                                 _c.c_uint32], _c.c_int32),
 }
 
 

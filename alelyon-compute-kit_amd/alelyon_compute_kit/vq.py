@@ -296,6 +296,58 @@ class VQDevice:
                 raise ack.AckError(f"vq device arithmetic refused: status={flags}")
             return out.download(dtype)
 
+    def fit_resident(self, values: ack.Buffer, elements: int, book: ack.Buffer,
+                     status: ack.Buffer, *, group: int = 16, iterations: int = 4,
+                     sample_vectors: int = 4096, init: ack.Buffer | None = None) -> None:
+        """Enqueue ``fit_codebook`` of ``elements`` FP32 values held in a device
+        buffer; the 16 x group book lands in ``book``. Does not wait or check
+        status (bit 1: a nonfinite sampled value or init entry)."""
+        group = _group(group)
+        iterations = _integer(iterations, "iterations", 0, 32)
+        sample_vectors = _integer(sample_vectors, "sample_vectors", ENTRIES, 65536)
+        device = self.device
+        with device._lock:
+            device._require_open()
+            rc = self._lib.cdll.ack_vq_fit_codebook(
+                device._handle, values._handle, None if init is None else init._handle,
+                book._handle, status._handle, elements, group, iterations, sample_vectors)
+            if rc != ack.ACK_OK:
+                raise ack._kit_error("fit_codebook", rc, self._lib.last_error())
+
+    def fit_codebook(self, values, *, group: int = 16, iterations: int = 4,
+                     sample_vectors: int = 4096, init=None) -> np.ndarray:
+        """``fit_codebook`` (vq.py:182-257) computed on the GPU: the same
+        refusals and the same book, bit for bit."""
+        group = _group(group)
+        iterations = _integer(iterations, "iterations", 0, 32)
+        sample_vectors = _integer(sample_vectors, "sample_vectors", ENTRIES, 65536)
+        x = _float_array(values, "values").reshape(-1)
+        if x.size < group:
+            raise ValueError("codebook calibration needs at least one complete vector")
+        warm = None if init is None else _book(init, group)
+        device = self.device
+        with device._lock, ExitStack() as cleanup:
+            device._require_open()
+
+            def upload(array):
+                b = device.buffer(array.nbytes)
+                cleanup.callback(b.free)
+                b.upload(array)
+                return b
+
+            values_buf = upload(x)
+            init_buf = None if warm is None else upload(warm)
+            book = device.buffer(ENTRIES * group * 4)
+            cleanup.callback(book.free)
+            status = upload(np.zeros(1, dtype=np.uint32))
+            self.fit_resident(values_buf, x.size, book, status, group=group,
+                              iterations=iterations, sample_vectors=sample_vectors,
+                              init=init_buf)
+            flags = int(status.download(np.uint32)[0])
+            if flags:
+                raise ack.AckError(f"vq device arithmetic refused: status={flags}")
+            return book.download(np.float32).reshape(ENTRIES, group)
+
     def path_name(self, words) -> str:
         """The kernel path the library takes for a plan."""
         buf = ctypes.create_string_buffer(64)
@@ -376,6 +428,26 @@ class VQDevice:
                            (codes, books, coefficients), count * 3 * 4, np.float32)
         return tuple(x.reshape(weight.shape) for x in np.split(result, 3))
 
+    def adamw_step_resident(self, codes: ack.Buffer, books: ack.Buffer, coefficients: ack.Buffer,
+                            out_codes: ack.Buffer, out_books: ack.Buffer, changed: ack.Buffer,
+                            status: ack.Buffer, *, count: int, group: int,
+                            iterations: int = 4, sample_vectors: int = 4096) -> None:
+        """Enqueue the fused step on resident buffers (the op-3 inputs as
+        ``adamw`` lays them out); does not wait or check status."""
+        group = _group(group)
+        iterations = _integer(iterations, "iterations", 0, 32)
+        sample_vectors = _integer(sample_vectors, "sample_vectors", ENTRIES, 65536)
+        device = self.device
+        with device._lock:
+            device._require_open()
+            plan = _plan((3, count, 1, 1, group, ENTRIES, 0, 0))
+            rc = self._lib.cdll.ack_vq_adamw_step(
+                device._handle, codes._handle, books._handle, coefficients._handle,
+                out_codes._handle, out_books._handle, changed._handle, status._handle,
+                plan, len(plan), iterations, sample_vectors)
+            if rc != ack.ACK_OK:
+                raise ack._kit_error("vq", rc, self._lib.last_error())
+
     def adamw_step(self, weight: VQArray, momentum: VQArray, variance: VQArray,
                    gradient: VQArray, *, lr: float, beta1: float, beta2: float,
                    eps: float, weight_decay: float, step: int, iterations: int = 4,
@@ -408,17 +480,12 @@ class VQDevice:
             cleanup.callback(out_books.free)
             changed = device.buffer(4)
             cleanup.callback(changed.free)
-            changed.upload(np.zeros(1, dtype=np.uint32))
             status = device.buffer(4)
             cleanup.callback(status.free)
             status.upload(np.zeros(1, dtype=np.uint32))
-            plan = _plan((3, count, 1, 1, group, ENTRIES, 0, 0))
-            rc = self._lib.cdll.ack_vq_adamw_step(
-                device._handle, *(b._handle for b in bufs), out_codes._handle,
-                out_books._handle, changed._handle, status._handle, plan, len(plan),
-                iterations, sample_vectors)
-            if rc != ack.ACK_OK:
-                raise ack._kit_error("vq", rc, self._lib.last_error())
+            self.adamw_step_resident(*bufs, out_codes, out_books, changed, status, count=count,
+                                     group=group, iterations=iterations,
+                                     sample_vectors=sample_vectors)
             flags = int(status.download(np.uint32)[0])
             if flags:
                 raise ack.AckError(f"vq device arithmetic refused: status={flags}")

@@ -153,6 +153,8 @@ int32_t parse_plan(const uint8_t* plan, size_t plan_len, ackvq::Bounds bounds, a
   return ACK_OK;
 }
 
+size_t round_up(size_t bytes) { return (bytes + 255) / 256 * 256; }
+
 int32_t ensure_workspace(Device& dev, size_t bytes) {
   if (bytes <= dev.workspace_bytes) return ACK_OK;
   if (dev.workspace) {
@@ -597,6 +599,69 @@ int32_t ack_vq_host_fit_codebook(const float* values, uint64_t m, uint32_t group
   return ACK_OK;
 }
 
+int32_t ack_vq_fit_codebook(const AckDevice* handle, const AckBuffer* values,
+                            const AckBuffer* init, const AckBuffer* book_out,
+                            const AckBuffer* status, uint64_t m, uint32_t group,
+                            uint32_t iterations, uint32_t sample_vectors) {
+  if (!(group == 8 || group == 16 || group == 32)) {
+    set_error("vq fit: group must be 8, 16 or 32");
+    return ACK_ERR_SHAPE;
+  }
+  if (m < group || m > ackvq::kMaxValues) {
+    set_error("codebook calibration needs at least one complete vector");
+    return ACK_ERR_SIZE;
+  }
+  if (iterations > 32 || sample_vectors < 16 || sample_vectors > 65536) {
+    set_error("vq fit: iterations must be in 0..32 and sample_vectors in 16..65536");
+    return ACK_ERR_SHAPE;
+  }
+  std::shared_ptr<Device> dev;
+  std::unique_lock<std::mutex> lock;
+  if (int32_t rc = enter(handle, &dev, &lock)) return rc;
+  const AckBuffer* slots[4] = {values, init, book_out, status};
+  BufferRec* bufs[4] = {nullptr, nullptr, nullptr, nullptr};
+  for (int i = 0; i < 4; ++i) {
+    if (i == 1 && init == nullptr) continue;
+    if (int32_t rc = lookup_buffer(*dev, slots[i], &bufs[i])) return rc;
+  }
+  const uint64_t need[4] = {m * 4, uint64_t(16) * group * 4, uint64_t(16) * group * 4, 4};
+  for (int i = 0; i < 4; ++i) {
+    if (bufs[i] != nullptr && bufs[i]->bytes < need[i]) {
+      set_error("vq fit: buffer " + std::to_string(i) + " is too small");
+      return ACK_ERR_SIZE;
+    }
+  }
+  for (int w = 2; w < 4; ++w)
+    for (int i = 0; i < w; ++i)
+      if (bufs[i] != nullptr && bufs[w]->id == bufs[i]->id) {
+        set_error("vq fit: write slot " + std::to_string(w) + " aliases slot " +
+                  std::to_string(i));
+        return ACK_ERR_SHAPE;
+      }
+  const uint64_t complete = m / group;
+  const uint32_t count = uint32_t(complete < sample_vectors ? complete : sample_vectors);
+  const size_t sample_bytes = round_up(size_t(count) * group * 4);
+  const size_t idx_bytes = round_up(count);
+  if (int32_t rc = ensure_workspace(*dev, sample_bytes + idx_bytes + 256)) return rc;
+  char* ws = static_cast<char*>(dev->workspace);
+  ackvq::FitArgs fit;
+  fit.sample = reinterpret_cast<float*>(ws);
+  fit.idx = reinterpret_cast<uint8_t*>(ws + sample_bytes);
+  fit.flags = reinterpret_cast<uint32_t*>(ws + sample_bytes + idx_bytes);
+  fit.book = static_cast<float*>(bufs[2]->ptr);
+  fit.count = count;
+  fit.complete = complete;
+  fit.status = static_cast<uint32_t*>(bufs[3]->ptr);
+  ackvq::FitWhole whole;
+  whole.values = static_cast<const float*>(bufs[0]->ptr);
+  hipError_t e = ackvq::launch_fit_sample_dense(dev->stream, whole.values, group, fit);
+  if (e == hipSuccess)
+    e = ackvq::launch_fit(dev->stream, fit, group, 1, iterations,
+                          bufs[1] ? static_cast<const float*>(bufs[1]->ptr) : nullptr, whole);
+  if (e != hipSuccess) return hip_failure(*dev, "vq fit: launch", e, true);
+  return ACK_OK;
+}
+
 int32_t ack_vq_adamw_step(const AckDevice* handle, const AckBuffer* b0, const AckBuffer* b1,
                           const AckBuffer* b2, const AckBuffer* out_codes,
                           const AckBuffer* out_books, const AckBuffer* changed,
@@ -650,74 +715,32 @@ int32_t ack_vq_adamw_step(const AckDevice* handle, const AckBuffer* b0, const Ac
   uint32_t* st = static_cast<uint32_t*>(bufs[6]->ptr);
   hipStream_t s = dev->stream;
 
-  // fit_codebook's strided sample of complete vectors (vq.py:206-207).
+  // fit_codebook's strided sample of complete vectors (vq.py:206-207), the
+  // three fits on the device, then the encode pass; no host round trip.
   const uint64_t complete = m / g;
   const uint32_t count = uint32_t(complete < sample_vectors ? complete : sample_vectors);
-  std::vector<uint32_t> sample_idx(count);
-  ackvq::linspace_index(complete, count, sample_idx.data());
-  // Workspace: sample indices, sample values (3 x count x g), three books,
-  // a used mask.
-  const size_t idx_bytes = (size_t(count) * 4 + 255) / 256 * 256;
-  const size_t val_bytes = (size_t(3) * count * g * 4 + 255) / 256 * 256;
-  const size_t book_bytes = 256 * ((3 * 16 * g * 4 + 255) / 256);
-  if (int32_t rc = ensure_workspace(*dev, idx_bytes + val_bytes + book_bytes + 256)) return rc;
+  const size_t sample_bytes = round_up(size_t(3) * count * g * 4);
+  const size_t idx_bytes = round_up(size_t(3) * count);
+  if (int32_t rc = ensure_workspace(*dev, sample_bytes + idx_bytes + 256)) return rc;
   char* ws = static_cast<char*>(dev->workspace);
-  uint32_t* d_idx = reinterpret_cast<uint32_t*>(ws);
-  float* d_vals = reinterpret_cast<float*>(ws + idx_bytes);
-  float* d_books = reinterpret_cast<float*>(ws + idx_bytes + val_bytes);
-  uint32_t* d_mask = reinterpret_cast<uint32_t*>(ws + idx_bytes + val_bytes + book_bytes);
+  ackvq::FitArgs fit;
+  fit.sample = reinterpret_cast<float*>(ws);
+  fit.idx = reinterpret_cast<uint8_t*>(ws + sample_bytes);
+  fit.flags = reinterpret_cast<uint32_t*>(ws + sample_bytes + idx_bytes);
+  fit.book = static_cast<float*>(bufs[4]->ptr);
+  fit.count = count;
+  fit.complete = complete;
+  fit.status = st;
+  ackvq::FitWhole whole;
+  whole.adamw = &in;
 
-  hipError_t e = hipMemcpyAsync(d_idx, sample_idx.data(), size_t(count) * 4,
-                                hipMemcpyHostToDevice, s);
-  if (e == hipSuccess) e = ackvq::launch_adamw_gather(s, in, d_idx, count, d_vals, st);
-  std::vector<float> vals(size_t(3) * count * g);
-  std::vector<float> init(size_t(3) * 16 * g);
+  hipError_t e = ackvq::launch_adamw_gather(s, in, count, const_cast<float*>(fit.sample),
+                                               static_cast<uint32_t*>(bufs[5]->ptr), st);
+  if (e == hipSuccess) e = ackvq::launch_fit(s, fit, g, 3, iterations, in.books4, whole);
   if (e == hipSuccess)
-    e = hipMemcpyAsync(vals.data(), d_vals, vals.size() * 4, hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(init.data(), in.books4, init.size() * 4, hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (e != hipSuccess) return hip_failure(*dev, "vq adamw step: sample pass", e, true);
-
-  std::vector<float> books(size_t(3) * 16 * g);
-  for (uint32_t state = 0; state < 3; ++state) {
-    struct Ctx {
-      Device* dev;
-      ackvq::AdamwInputs in;
-      float* d_book;
-      uint32_t* d_mask;
-      uint32_t* status;
-      uint32_t state;
-      hipError_t err;
-    } ctx{dev.get(), in, d_books, d_mask, st, state, hipSuccess};
-    auto used = [](void* p, const float* book, uint32_t* mask) -> int32_t {
-      Ctx& c = *static_cast<Ctx*>(p);
-      hipStream_t st2 = c.dev->stream;
-      const uint32_t zero = 0;
-      hipError_t err = hipMemcpyAsync(c.d_book, book, size_t(16) * c.in.group * 4,
-                                      hipMemcpyHostToDevice, st2);
-      if (err == hipSuccess) err = hipMemcpyAsync(c.d_mask, &zero, 4, hipMemcpyHostToDevice, st2);
-      if (err == hipSuccess)
-        err = ackvq::launch_adamw_used(st2, c.in, c.d_book, c.state, c.d_mask, c.status);
-      if (err == hipSuccess) err = hipMemcpyAsync(mask, c.d_mask, 4, hipMemcpyDeviceToHost, st2);
-      if (err == hipSuccess) err = hipStreamSynchronize(st2);
-      c.err = err;
-      return err == hipSuccess ? 0 : -1;
-    };
-    ackvq::host_fit_sample(vals.data() + size_t(state) * count * g, count, complete, g,
-                           iterations, init.data() + size_t(state) * 16 * g, used, &ctx,
-                           books.data() + size_t(state) * 16 * g);
-    if (ctx.err != hipSuccess)
-      return hip_failure(*dev, "vq adamw step: whole-tensor pass", ctx.err, true);
-  }
-  e = hipMemcpyAsync(d_books, books.data(), books.size() * 4, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess)
-    e = ackvq::launch_adamw_encode(s, in, d_books, static_cast<uint32_t*>(bufs[3]->ptr),
+    e = ackvq::launch_adamw_encode(s, in, fit.book, static_cast<uint32_t*>(bufs[3]->ptr),
                                    static_cast<uint32_t*>(bufs[5]->ptr), st);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(bufs[4]->ptr, books.data(), books.size() * 4, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (e != hipSuccess) return hip_failure(*dev, "vq adamw step: encode pass", e, true);
+  if (e != hipSuccess) return hip_failure(*dev, "vq adamw step: launch", e, true);
   return ACK_OK;
 }
 

@@ -1,0 +1,57 @@
+// Device helpers of the codebook calibration (fit_codebook,
+// src/alelyon_compute_kit/_kit/python/vq.py:182-257), shared by the fit
+// kernels and the AdamW keep pass. Every float64 step is ordered as numpy
+// orders the reference's expressions, and the library is compiled with
+// -ffp-contract=off, so results are bit-identical to the host restatement
+// (host_fit.cpp) and to the reference's Python.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace ackvq {
+namespace fitdev {
+
+// Row i of floor(numpy.linspace(0, n - 1, num)) (vq.py:206-207): i * ((n -
+// 1) / (num - 1)) in float64, the last element exactly n - 1.
+__device__ __forceinline__ uint32_t linspace_at(uint64_t n, uint32_t num, uint32_t i) {
+  if (num <= 1) return 0;
+  const double delta = double(n - 1);
+  const double div = double(num - 1);
+  const double step = delta / div;
+  double y = step == 0.0 ? (double(i) / div) * delta : double(i) * step;
+  y = y + 0.0;
+  if (i == num - 1) y = delta;
+  return uint32_t(floor(y));
+}
+
+// The float64 CPU encode's argmin for one complete vector (vq.py:166-174):
+// d = d + (x_j - c_j)^2 over j ascending, every operation rounded; the first
+// minimum wins, and a NaN distance wins at once (np.argmin). `book` holds the
+// 16 x G entries as float64.
+template <int G>
+__device__ __forceinline__ uint32_t nearest64(const double (&x)[G], const double* book) {
+  double best = 0.0;
+  uint32_t sel = 0;
+#pragma unroll 1
+  for (uint32_t e = 0; e < 16; ++e) {
+    double d = 0.0;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const double delta = x[j] - book[e * G + j];
+      const double sq = delta * delta;
+      d = d + sq;
+    }
+    const bool nan = d != d;
+    if (e == 0 || nan || d < best) {
+      best = d;
+      sel = e;
+      if (nan) break;
+    }
+  }
+  return sel;
+}
+
+}  // namespace fitdev
+}  // namespace ackvq

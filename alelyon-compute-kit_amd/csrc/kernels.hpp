@@ -67,13 +67,47 @@ struct AdamwInputs {
   uint32_t group;
 };
 
-// AdamW at whole vectors `vectors[0..count)`: out = [3][count][group].
-hipError_t launch_adamw_gather(hipStream_t s, const AdamwInputs& in, const uint32_t* vectors,
-                               uint32_t count, float* out, uint32_t* status);
-// Entries of `book` selected by complete vectors of state `state` under the
-// float64 rule; OR-ed into *mask.
-hipError_t launch_adamw_used(hipStream_t s, const AdamwInputs& in, const float* book,
-                             uint32_t state, uint32_t* mask, uint32_t* status);
+// Device codebook calibration (fit_codebook, vq.py:182-257) for `problems`
+// independent fits that share one geometry. Per problem p the buffers are
+// laid out back to back: sample [count][G] FP32 (the strided sample of
+// complete vectors), idx [count] entry indices, book [16][G] (the working
+// and final book), flags [4] (used mask, kept mask, keep-pass switch, spare).
+struct FitArgs {
+  const float* sample = nullptr;
+  uint8_t* idx = nullptr;
+  float* book = nullptr;
+  uint32_t* flags = nullptr;
+  uint32_t count = 0;         // sample vectors per problem
+  uint64_t complete = 0;      // complete vectors of the tensor being fitted
+  uint32_t* status = nullptr;
+};
+
+// What the warm-start keep rule re-encodes when it needs the whole tensor.
+struct FitWhole {
+  const float* values = nullptr;   // dense tensor (one problem), or
+  const AdamwInputs* adamw = nullptr;  // the three AdamW states (problems 0..2)
+};
+
+// Samples rows linspace(0, complete-1, count) of a dense tensor into
+// a.sample; a nonfinite sampled value sets status bit 1.
+hipError_t launch_fit_sample_dense(hipStream_t s, const float* values, uint32_t group,
+                                   const FitArgs& a);
+// The Lloyd iterations: book = init (problem p at init + p * 16 * group) or
+// sample rows linspace(0, count-1, 16), then `iterations` rounds of assign,
+// optional keep pass over `whole`, and update. Enqueue only; allocates
+// nothing.
+hipError_t launch_fit(hipStream_t s, const FitArgs& a, uint32_t group, uint32_t problems,
+                      uint32_t iterations, const float* init, const FitWhole& whole);
+
+// AdamW at fit_codebook's strided sample of whole vectors (rows
+// linspace(0, m/group - 1, count)): out = [3][count][group]. Also clears
+// *changed, which the encode pass counts into.
+hipError_t launch_adamw_gather(hipStream_t s, const AdamwInputs& in, uint32_t count, float* out,
+                               uint32_t* changed, uint32_t* status);
+// Keep pass of the fit over the three recomputed states (FitArgs problems
+// 0..2): entries selected by complete vectors under the float64 rule, OR-ed
+// into each problem's kept mask when its keep-pass switch is set.
+hipError_t launch_adamw_keep(hipStream_t s, const AdamwInputs& in, const FitArgs& a);
 // Recompute and encode all three states against books3; count changed W.
 hipError_t launch_adamw_encode(hipStream_t s, const AdamwInputs& in, const float* books3,
                                uint32_t* out_codes, uint32_t* changed, uint32_t* status);

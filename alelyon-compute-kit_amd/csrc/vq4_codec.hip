@@ -10,6 +10,7 @@
 #include <cfloat>
 #include <cstdint>
 
+#include "fit_device.hpp"
 #include "kernels.hpp"
 
 namespace ackvq {
@@ -197,21 +198,14 @@ struct AdamwOut {
   bool write;      // the shader writes the element (vq4.comp:92-115)
 };
 
-// unpack_state (vq4.comp:74-78) and adamw_value (:80-116) for element i.
-template <int G>
-__device__ __forceinline__ AdamwOut adamw_element(const uint32_t* codes4, const float* books4,
-                                                  uint32_t words, uint32_t i, const Coeffs& c) {
+// adamw_value (vq4.comp:80-116) for one element given its four decoded state
+// values.
+__device__ __forceinline__ AdamwOut adamw_value(float weight, float moment, float variance,
+                                                float gradient, const Coeffs& c) {
   AdamwOut r;
   r.flags = 0;
   r.write = false;
   r.w = r.m = r.v = 0.0f;
-  const uint32_t vector = i / G;
-  const uint32_t t = i % G;
-  float s[4];
-#pragma unroll
-  for (int st = 0; st < 4; ++st)
-    s[st] = books4[st * 16 * G + nibble(codes4 + st * words, vector) * G + t];
-  const float weight = s[0], moment = s[1], variance = s[2], gradient = s[3];
   if (!finite_f32(weight) || !finite_f32(moment) || !finite_f32(variance) || !finite_f32(gradient)) {
     r.flags = 1;
     return r;
@@ -238,6 +232,23 @@ __device__ __forceinline__ AdamwOut adamw_element(const uint32_t* codes4, const 
   return r;
 }
 
+// unpack_state (vq4.comp:74-78) then adamw_value for element i.
+template <int G>
+__device__ __forceinline__ AdamwOut adamw_element(const uint32_t* codes4, const float* books4,
+                                                  uint32_t words, uint32_t i, const Coeffs& c) {
+  const uint32_t vector = i / G;
+  const uint32_t t = i % G;
+  float s[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+    s[st] = books4[st * 16 * G + nibble(codes4 + st * words, vector) * G + t];
+  return adamw_value(s[0], s[1], s[2], s[3], c);
+}
+
+// Op 3. The four books sit in LDS; with m a multiple of 4 and an aligned
+// output each lane takes four consecutive elements (one vector's quad: G is a
+// multiple of 4), reads each state's code word once and stores 16-byte
+// quads; otherwise one element per lane.
 template <int G>
 __global__ __launch_bounds__(kThreads) void k_adamw(Operands o, uint32_t m) {
   const uint32_t item = blockIdx.y;
@@ -245,7 +256,10 @@ __global__ __launch_bounds__(kThreads) void k_adamw(Operands o, uint32_t m) {
   const float* books4 = item_ptr<float>(o.in[1], o.stride[1], item);
   const float* coeff = item_ptr<float>(o.in[2], o.stride[2], item);
   float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
+  __shared__ __align__(16) float sbook[4 * 16 * G];
+  for (uint32_t i = threadIdx.x; i < 4 * 16 * G; i += kThreads) sbook[i] = books4[i];
   if (blockIdx.x == 0) sweep_book(books4, 64 * G, o.status);
+  __syncthreads();
   const Coeffs c = load_coeffs(coeff);
   if (c.fail) {
     if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(o.status, c.fail);
@@ -253,13 +267,47 @@ __global__ __launch_bounds__(kThreads) void k_adamw(Operands o, uint32_t m) {
   }
   const uint32_t words = words_for(m, G);
   uint32_t flags = 0;
-  for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < m; i += gridDim.x * kThreads) {
-    const AdamwOut r = adamw_element<G>(codes4, books4, words, i, c);
-    flags |= r.flags;
-    if (r.write) {
-      out[i] = r.w;
-      out[m + i] = r.m;
-      out[2 * m + i] = r.v;
+  if (m % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
+    const uint32_t quads = m / 4;
+    for (uint32_t q = blockIdx.x * kThreads + threadIdx.x; q < quads; q += gridDim.x * kThreads) {
+      const uint32_t i = q * 4;
+      const uint32_t vector = i / G;
+      const uint32_t t = i % G;
+      float4 s[4];
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const uint32_t code = nibble(codes4 + st * words, vector);
+        s[st] = *reinterpret_cast<const float4*>(sbook + (st * 16 + code) * G + t);
+      }
+      const AdamwOut r0 = adamw_value(s[0].x, s[1].x, s[2].x, s[3].x, c);
+      const AdamwOut r1 = adamw_value(s[0].y, s[1].y, s[2].y, s[3].y, c);
+      const AdamwOut r2 = adamw_value(s[0].z, s[1].z, s[2].z, s[3].z, c);
+      const AdamwOut r3 = adamw_value(s[0].w, s[1].w, s[2].w, s[3].w, c);
+      flags |= r0.flags | r1.flags | r2.flags | r3.flags;
+      if (r0.write && r1.write && r2.write && r3.write) {
+        *reinterpret_cast<float4*>(out + i) = make_float4(r0.w, r1.w, r2.w, r3.w);
+        *reinterpret_cast<float4*>(out + m + i) = make_float4(r0.m, r1.m, r2.m, r3.m);
+        *reinterpret_cast<float4*>(out + 2 * m + i) = make_float4(r0.v, r1.v, r2.v, r3.v);
+      } else {
+        const AdamwOut rs[4] = {r0, r1, r2, r3};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (!rs[u].write) continue;
+          out[i + u] = rs[u].w;
+          out[m + i + u] = rs[u].m;
+          out[2 * m + i + u] = rs[u].v;
+        }
+      }
+    }
+  } else {
+    for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < m; i += gridDim.x * kThreads) {
+      const AdamwOut r = adamw_element<G>(codes4, sbook, words, i, c);
+      flags |= r.flags;
+      if (r.write) {
+        out[i] = r.w;
+        out[m + i] = r.m;
+        out[2 * m + i] = r.v;
+      }
     }
   }
   // Wave-reduce the bits before touching the status word.
@@ -268,10 +316,13 @@ __global__ __launch_bounds__(kThreads) void k_adamw(Operands o, uint32_t m) {
 }
 
 // ---- fused VQAdamW passes -------------------------------------------------
+// AdamW at fit_codebook's strided sample: sample vector e is complete vector
+// linspace(0, m/G - 1, count)[e] (vq.py:206-207).
 template <int G>
-__global__ __launch_bounds__(kThreads) void k_adamw_gather(AdamwInputs in, const uint32_t* vectors,
-                                                           uint32_t count, float* out,
+__global__ __launch_bounds__(kThreads) void k_adamw_gather(AdamwInputs in, uint32_t count,
+                                                           float* out, uint32_t* changed,
                                                            uint32_t* status) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *changed = 0;  // the encode pass counts into it
   const Coeffs c = load_coeffs(in.coeffs);
   if (c.fail) {
     if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(status, c.fail);
@@ -279,9 +330,10 @@ __global__ __launch_bounds__(kThreads) void k_adamw_gather(AdamwInputs in, const
   }
   const uint32_t words = words_for(in.m, G);
   const uint32_t total = count * G;
+  const uint64_t complete = in.m / G;
   uint32_t flags = 0;
   for (uint32_t e = blockIdx.x * kThreads + threadIdx.x; e < total; e += gridDim.x * kThreads) {
-    const uint32_t i = vectors[e / G] * G + e % G;
+    const uint32_t i = fitdev::linspace_at(complete, count, e / G) * G + e % G;
     const AdamwOut r = adamw_element<G>(in.codes4, in.books4, words, i, c);
     flags |= r.flags;
     out[e] = r.w;
@@ -292,17 +344,19 @@ __global__ __launch_bounds__(kThreads) void k_adamw_gather(AdamwInputs in, const
   if (flags && (threadIdx.x % warpSize) == 0) atomicOr(status, flags);
 }
 
-// The float64 CPU encode (vq.py:166-174): d = d + (x - c)^2 in float64 with
-// every operation rounded, j ascending; argmin keeps the first minimum.
+// The fit's keep pass over the recomputed state blockIdx.y (0 W', 1 M',
+// 2 V'): the entries its complete vectors select under the float64 rule,
+// when that fit's keep-pass switch is set.
 template <int G>
-__global__ __launch_bounds__(kThreads) void k_adamw_used(AdamwInputs in, const float* book,
-                                                         uint32_t state, uint32_t* mask,
-                                                         uint32_t* status) {
+__global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs a) {
+  const uint32_t state = blockIdx.y;
+  if (a.flags[state * 4 + 2] == 0) return;
   __shared__ double sbook[16 * G];
-  for (uint32_t i = threadIdx.x; i < 16 * G; i += kThreads) sbook[i] = double(book[i]);
+  for (uint32_t i = threadIdx.x; i < 16 * G; i += kThreads)
+    sbook[i] = double(a.book[state * 16 * G + i]);
   __syncthreads();
   const Coeffs c = load_coeffs(in.coeffs);
-  if (c.fail) return;  // the encode pass reports coefficient failures
+  if (c.fail) return;  // the gather and encode passes report coefficient failures
   const uint32_t words = words_for(in.m, G);
   const uint32_t complete = in.m / G;
   uint32_t used = 0;
@@ -313,26 +367,10 @@ __global__ __launch_bounds__(kThreads) void k_adamw_used(AdamwInputs in, const f
       const AdamwOut r = adamw_element<G>(in.codes4, in.books4, words, v * G + j, c);
       x[j] = double(state == 0 ? r.w : state == 1 ? r.m : r.v);
     }
-    double best = 0.0;
-    uint32_t sel = 0;
-    for (uint32_t code = 0; code < 16; ++code) {
-      double d = 0.0;
-#pragma unroll
-      for (int j = 0; j < G; ++j) {
-        const double delta = x[j] - sbook[code * G + j];
-        const double sq = delta * delta;
-        d = d + sq;
-      }
-      if (code == 0 || d < best) {
-        best = d;
-        sel = code;
-      }
-    }
-    used |= 1u << sel;
+    used |= 1u << fitdev::nearest64<G>(x, sbook);
   }
   for (int off = 1; off < warpSize; off <<= 1) used |= __shfl_xor(used, off);
-  if (used && (threadIdx.x % warpSize) == 0) atomicOr(mask, used);
-  (void)status;
+  if (used && (threadIdx.x % warpSize) == 0) atomicOr(&a.flags[state * 4 + 1], used);
 }
 
 // Recompute W', M', V' per vector and encode each against its new book with
@@ -342,9 +380,9 @@ __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const
                                                            uint32_t* out_codes, uint32_t* changed,
                                                            uint32_t* status) {
   __shared__ float sbook[3 * 16 * G];
-  __shared__ float soldw[16 * G];
+  __shared__ float sold[4 * 16 * G];  // the op-3 input books; W's is the old weight book
   for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) sbook[i] = books3[i];
-  for (uint32_t i = threadIdx.x; i < 16 * G; i += kThreads) soldw[i] = in.books4[i];
+  for (uint32_t i = threadIdx.x; i < 4 * 16 * G; i += kThreads) sold[i] = in.books4[i];
   if (blockIdx.x == 0) sweep_book(books3, 3 * 16 * G, status);
   __syncthreads();
   const Coeffs c = load_coeffs(in.coeffs);
@@ -364,11 +402,16 @@ __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const
     if (v < vectors) {
       const uint32_t start = v * G;
       const uint32_t valid = (m - start) < G ? (m - start) : G;
+      uint32_t in_code[4];
+#pragma unroll
+      for (int st = 0; st < 4; ++st) in_code[st] = nibble(in.codes4 + st * words, v);
       float xs[3][G];
 #pragma unroll
       for (int j = 0; j < G; ++j) {
         if (uint32_t(j) < valid) {
-          const AdamwOut r = adamw_element<G>(in.codes4, in.books4, words, start + j, c);
+          const AdamwOut r = adamw_value(sold[in_code[0] * G + j], sold[(16 + in_code[1]) * G + j],
+                                         sold[(32 + in_code[2]) * G + j],
+                                         sold[(48 + in_code[3]) * G + j], c);
           flags |= r.flags;
           xs[0][j] = r.w; xs[1][j] = r.m; xs[2][j] = r.v;
           bad |= !finite_f32(r.w) || !finite_f32(r.m) || !finite_f32(r.v);
@@ -381,9 +424,8 @@ __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const
         code[st] = valid == G ? argmin32<G, true>(xs[st], G, sbook + st * 16 * G, bad)
                               : argmin32<G, false>(xs[st], valid, sbook + st * 16 * G, bad);
       }
-      const uint32_t old_code = nibble(in.codes4, v);
       for (uint32_t j = 0; j < valid; ++j)
-        moved += sbook[code[0] * G + j] != soldw[old_code * G + j];
+        moved += sbook[code[0] * G + j] != sold[in_code[0] * G + j];
     }
 #pragma unroll
     for (int st = 0; st < 3; ++st) {
@@ -436,28 +478,27 @@ hipError_t launch_decode(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
 }
 
 hipError_t launch_adamw(hipStream_t s, const Operands& o, uint32_t m, uint32_t group) {
-  dim3 grid(grid_for(m, kThreads), o.count);
+  dim3 grid(grid_for((m + 3) / 4, kThreads), o.count);
   if (group == 8) k_adamw<8><<<grid, kThreads, 0, s>>>(o, m);
   else if (group == 16) k_adamw<16><<<grid, kThreads, 0, s>>>(o, m);
   else k_adamw<32><<<grid, kThreads, 0, s>>>(o, m);
   return hipGetLastError();
 }
 
-hipError_t launch_adamw_gather(hipStream_t s, const AdamwInputs& in, const uint32_t* vectors,
-                               uint32_t count, float* out, uint32_t* status) {
+hipError_t launch_adamw_gather(hipStream_t s, const AdamwInputs& in, uint32_t count, float* out,
+                               uint32_t* changed, uint32_t* status) {
   dim3 grid(grid_for(uint64_t(count) * in.group, kThreads));
-  if (in.group == 8) k_adamw_gather<8><<<grid, kThreads, 0, s>>>(in, vectors, count, out, status);
-  else if (in.group == 16) k_adamw_gather<16><<<grid, kThreads, 0, s>>>(in, vectors, count, out, status);
-  else k_adamw_gather<32><<<grid, kThreads, 0, s>>>(in, vectors, count, out, status);
+  if (in.group == 8) k_adamw_gather<8><<<grid, kThreads, 0, s>>>(in, count, out, changed, status);
+  else if (in.group == 16) k_adamw_gather<16><<<grid, kThreads, 0, s>>>(in, count, out, changed, status);
+  else k_adamw_gather<32><<<grid, kThreads, 0, s>>>(in, count, out, changed, status);
   return hipGetLastError();
 }
 
-hipError_t launch_adamw_used(hipStream_t s, const AdamwInputs& in, const float* book,
-                             uint32_t state, uint32_t* mask, uint32_t* status) {
-  dim3 grid(grid_for(in.m / in.group, kThreads));
-  if (in.group == 8) k_adamw_used<8><<<grid, kThreads, 0, s>>>(in, book, state, mask, status);
-  else if (in.group == 16) k_adamw_used<16><<<grid, kThreads, 0, s>>>(in, book, state, mask, status);
-  else k_adamw_used<32><<<grid, kThreads, 0, s>>>(in, book, state, mask, status);
+hipError_t launch_adamw_keep(hipStream_t s, const AdamwInputs& in, const FitArgs& a) {
+  dim3 grid(grid_for(in.m / in.group, kThreads), 3);
+  if (in.group == 8) k_adamw_keep<8><<<grid, kThreads, 0, s>>>(in, a);
+  else if (in.group == 16) k_adamw_keep<16><<<grid, kThreads, 0, s>>>(in, a);
+  else k_adamw_keep<32><<<grid, kThreads, 0, s>>>(in, a);
   return hipGetLastError();
 }
 

@@ -1,0 +1,361 @@
+// Codebook calibration on the device: fit_codebook
+// (src/alelyon_compute_kit/_kit/python/vq.py:182-257) as a chain of kernels
+// that needs no host round trip, bit-identical to the reference's Python and
+// to host_fit.cpp.
+//
+// One fit (a "problem") per blockIdx.y (assign) or blockIdx.x (the
+// single-block kernels); the fused VQAdamW step runs its three state fits as
+// three problems of the same launches. Per iteration:
+//   assign  one lane per sample vector: float64 nearest entry, the used mask;
+//   decide  the warm-start keep rule's condition (vq.py:216-222): some entry
+//           the sample never selected is not a copy of an earlier entry;
+//   keep    (only when a warm start fits a sample smaller than the tensor)
+//           the whole tensor's float64 nearest entries, when decide said so;
+//   update  one 1024-lane block: each wave owns one entry and sums its
+//           members in sample order, in float64 (numpy's axis-0 mean);
+//           then entries in ascending order take their mean, or, when empty
+//           and not kept, the sample vector farthest from the book as it
+//           stands at that moment (vq.py:232-257).
+// The mean's sum order is sequential per component, as numpy sums axis 0.
+// The reseed distance sums the G squared differences in numpy's pairwise
+// order (eight interleaved partial sums), and its argmax takes the first
+// maximum or the first NaN.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "fit_device.hpp"
+#include "kernels.hpp"
+
+namespace ackvq {
+namespace {
+
+using fitdev::linspace_at;
+using fitdev::nearest64;
+
+constexpr uint32_t kAssignThreads = 256;
+constexpr uint32_t kUpdateThreads = 1024;  // 16 waves: wave e owns entry e
+constexpr uint32_t kStageBytes = 32768;     // sample rows staged per round in update
+
+__device__ __forceinline__ bool finite_f32(float x) { return fabsf(x) <= FLT_MAX; }
+
+template <int G>
+__device__ __forceinline__ const float* sample_of(const FitArgs& a, uint32_t p) {
+  return a.sample + uint64_t(p) * a.count * G;
+}
+
+// Rows linspace(0, complete-1, count) of a dense tensor; one lane per value.
+template <int G>
+__global__ __launch_bounds__(256) void k_fit_sample_dense(const float* values, FitArgs a) {
+  float* out = const_cast<float*>(a.sample);
+  const uint32_t total = a.count * G;
+  bool bad = false;
+  for (uint32_t e = blockIdx.x * 256 + threadIdx.x; e < total; e += gridDim.x * 256) {
+    const uint32_t row = linspace_at(a.complete, a.count, e / G);
+    const float v = values[uint64_t(row) * G + e % G];
+    bad |= !finite_f32(v);
+    out[e] = v;
+  }
+  if (__any(bad) && (threadIdx.x % warpSize) == 0) atomicOr(a.status, 1u);
+}
+
+// Starting book: init, or sample rows linspace(0, count-1, 16) (vq.py:208-213);
+// clears the masks. One block per problem.
+template <int G>
+__global__ __launch_bounds__(256) void k_fit_init(FitArgs a, const float* init) {
+  const uint32_t p = blockIdx.x;
+  float* book = a.book + p * 16 * G;
+  const float* sample = sample_of<G>(a, p);
+  bool bad = false;
+  for (uint32_t i = threadIdx.x; i < 16 * G; i += 256) {
+    float v;
+    if (init != nullptr) {
+      v = init[p * 16 * G + i];
+      bad |= !finite_f32(v);
+    } else {
+      v = sample[uint64_t(linspace_at(a.count, 16, i / G)) * G + i % G];
+    }
+    book[i] = v;
+  }
+  if (threadIdx.x < 4) a.flags[p * 4 + threadIdx.x] = 0;
+  if (__any(bad) && (threadIdx.x % warpSize) == 0) atomicOr(a.status, 1u);
+}
+
+template <int G>
+__device__ __forceinline__ void load_book64(const float* book, double* sbook) {
+  for (uint32_t i = threadIdx.x; i < 16 * G; i += blockDim.x) sbook[i] = double(book[i]);
+}
+
+// Nearest entry of every sample vector (vq.py:214); the used mask.
+template <int G>
+__global__ __launch_bounds__(kAssignThreads) void k_fit_assign(FitArgs a) {
+  const uint32_t p = blockIdx.y;
+  __shared__ double sbook[16 * G];
+  load_book64<G>(a.book + p * 16 * G, sbook);
+  __syncthreads();
+  const float* sample = sample_of<G>(a, p);
+  uint8_t* idx = a.idx + uint64_t(p) * a.count;
+  uint32_t used = 0;
+  for (uint32_t i = blockIdx.x * kAssignThreads + threadIdx.x; i < a.count;
+       i += gridDim.x * kAssignThreads) {
+    double x[G];
+    const float4* row = reinterpret_cast<const float4*>(sample + uint64_t(i) * G);
+#pragma unroll
+    for (int q = 0; q < G / 4; ++q) {
+      const float4 v = row[q];
+      x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+    }
+    const uint32_t e = nearest64<G>(x, sbook);
+    idx[i] = uint8_t(e);
+    used |= 1u << e;
+  }
+  for (int off = 1; off < warpSize; off <<= 1) used |= __shfl_xor(used, off);
+  if (used && (threadIdx.x % warpSize) == 0) atomicOr(&a.flags[p * 4], used);
+}
+
+// vq.py:216-222's condition: an entry the sample left unused that is not a
+// copy of an earlier entry (float compare: -0 equals 0, NaN equals nothing).
+// One wave per problem; lane e tests entry e.
+template <int G>
+__global__ __launch_bounds__(64) void k_fit_decide(FitArgs a) {
+  const uint32_t p = blockIdx.x;
+  const float* book = a.book + p * 16 * G;
+  const uint32_t used = a.flags[p * 4];
+  const uint32_t e = threadIdx.x;
+  bool candidate = false;
+  if (e < 16 && !(used & (1u << e))) {
+    bool duplicate = false;
+    for (uint32_t j = 0; j < e && !duplicate; ++j) {
+      bool equal = true;
+      for (int t = 0; t < G; ++t) equal &= book[e * G + t] == book[j * G + t];
+      duplicate = equal;
+    }
+    candidate = !duplicate;
+  }
+  const bool reachable = __any(candidate);
+  if (threadIdx.x == 0) a.flags[p * 4 + 2] = reachable ? 1u : 0u;
+}
+
+// The keep pass over a dense tensor (one problem): entries its complete
+// vectors select under the current book.
+template <int G>
+__global__ __launch_bounds__(256) void k_fit_keep_dense(FitArgs a, const float* values) {
+  if (a.flags[2] == 0) return;
+  __shared__ double sbook[16 * G];
+  load_book64<G>(a.book, sbook);
+  __syncthreads();
+  uint32_t used = 0;
+  for (uint64_t v = uint64_t(blockIdx.x) * 256 + threadIdx.x; v < a.complete;
+       v += uint64_t(gridDim.x) * 256) {
+    double x[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) x[j] = double(values[v * G + j]);
+    used |= 1u << nearest64<G>(x, sbook);
+  }
+  for (int off = 1; off < warpSize; off <<= 1) used |= __shfl_xor(used, off);
+  if (used && (threadIdx.x % warpSize) == 0) atomicOr(&a.flags[1], used);
+}
+
+// numpy's pairwise sum of the G >= 8 squared differences (G a multiple of
+// 8) between x and an entry: eight interleaved partial sums r[j % 8] taken in
+// j order, combined ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)).
+template <int G>
+__device__ __forceinline__ double pairwise_gap(const float (&x)[G], const float* entry) {
+  double r[8];
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    const double d = double(x[j]) - double(entry[j]);
+    const double sq = d * d;
+    r[j % 8] = j < 8 ? sq : r[j % 8] + sq;
+  }
+  return ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+}
+
+struct Far {
+  double gap;
+  uint32_t row;  // 0xffffffff: none
+  uint32_t nan;
+};
+
+// The argmax rule of vq.py:257 as a commutative choice: the first NaN if
+// any, else the largest gap, ties to the lower row.
+__device__ __forceinline__ Far farther(Far a, Far b) {
+  if (a.row == 0xffffffffu) return b;
+  if (b.row == 0xffffffffu) return a;
+  if (a.nan != b.nan) return a.nan ? a : b;
+  if (a.nan) return a.row < b.row ? a : b;
+  if (a.gap != b.gap) return a.gap > b.gap ? a : b;
+  return a.row < b.row ? a : b;
+}
+
+// _reseed (vq.py:232-257) for the whole block: the sample row whose nearest
+// entry of `cur` is farthest. Every thread returns the same row.
+template <int G>
+__device__ uint32_t reseed_row(const float* sample, uint32_t count, const float* cur,
+                               Far* scratch) {
+  Far best{0.0, 0xffffffffu, 0};
+  for (uint32_t i = threadIdx.x; i < count; i += kUpdateThreads) {
+    float x[G];
+    const float4* row = reinterpret_cast<const float4*>(sample + uint64_t(i) * G);
+#pragma unroll
+    for (int q = 0; q < G / 4; ++q) {
+      const float4 v = row[q];
+      x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+    }
+    double gap = 0.0;
+#pragma unroll 1
+    for (uint32_t e = 0; e < 16; ++e) {
+      const double s = pairwise_gap<G>(x, cur + e * G);
+      if (e == 0 || s != s || s < gap) gap = s;
+      if (gap != gap) break;
+    }
+    best = farther(best, Far{gap, i, gap != gap ? 1u : 0u});
+  }
+  for (int off = 1; off < warpSize; off <<= 1) {
+    Far o;
+    o.gap = __shfl_xor(best.gap, off);
+    o.row = __shfl_xor(best.row, off);
+    o.nan = __shfl_xor(best.nan, off);
+    best = farther(best, o);
+  }
+  const uint32_t wave = threadIdx.x / warpSize;
+  if (threadIdx.x % warpSize == 0) scratch[wave] = best;
+  __syncthreads();
+  Far all = scratch[0];
+  for (uint32_t w = 1; w < kUpdateThreads / warpSize; ++w) all = farther(all, scratch[w]);
+  __syncthreads();  // scratch is reused by the next reseed
+  return all.row;
+}
+
+// Means and reseeds of one iteration (vq.py:223-229). One block per problem.
+template <int G>
+__global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
+  constexpr uint32_t kRows = kStageBytes / (4 * G);  // rows per staged round
+  __shared__ float4 xs4[kStageBytes / 16];
+  __shared__ uint8_t ids[kRows];
+  __shared__ float cur[16 * G];
+  __shared__ float mean[16 * G];
+  __shared__ uint32_t members[16];
+  __shared__ Far scratch[kUpdateThreads / 64];
+
+  const uint32_t p = blockIdx.x;
+  const uint32_t t = threadIdx.x;
+  const uint32_t wave = t / warpSize;  // the entry this wave sums
+  const uint32_t lane = t % warpSize;
+  const uint32_t count = a.count;
+  const float* sample = sample_of<G>(a, p);
+  const uint8_t* idx = a.idx + uint64_t(p) * count;
+  float* book = a.book + p * 16 * G;
+  uint32_t* flags = a.flags + p * 4;
+  for (uint32_t i = t; i < 16 * G; i += kUpdateThreads) cur[i] = book[i];
+
+  // Per-entry sums in sample order. Adding +0.0 for a skipped slot is exact:
+  // a sum that starts at +0 is never -0, and NaN and infinities pass through.
+  double sum = 0.0;
+  uint32_t n = 0;
+  const float* xs = reinterpret_cast<const float*>(xs4);
+  for (uint32_t c0 = 0; c0 < count; c0 += kRows) {
+    const uint32_t rows = count - c0 < kRows ? count - c0 : kRows;
+    __syncthreads();
+    const float4* src = reinterpret_cast<const float4*>(sample + uint64_t(c0) * G);
+    for (uint32_t q = t; q < rows * G / 4; q += kUpdateThreads) xs4[q] = src[q];
+    for (uint32_t q = t; q < rows; q += kUpdateThreads) ids[q] = idx[c0 + q];
+    __syncthreads();
+    for (uint32_t sb = 0; sb < rows; sb += 64) {
+      const uint32_t r = sb + lane;
+      uint64_t bits = __ballot(r < rows && ids[r] == wave);
+      n += __popcll(bits);
+      const float* block = xs + sb * G;
+      const uint32_t j = lane < G ? lane : 0;
+      while (bits) {
+        const uint32_t b0 = __builtin_ctzll(bits);
+        bits &= bits - 1;
+        const bool h1 = bits != 0;
+        const uint32_t b1 = h1 ? __builtin_ctzll(bits) : b0;
+        bits &= bits - 1;
+        const bool h2 = bits != 0;
+        const uint32_t b2 = h2 ? __builtin_ctzll(bits) : b0;
+        bits &= bits - 1;
+        const bool h3 = bits != 0;
+        const uint32_t b3 = h3 ? __builtin_ctzll(bits) : b0;
+        bits &= bits - 1;
+        const float x0 = block[b0 * G + j], x1 = block[b1 * G + j];
+        const float x2 = block[b2 * G + j], x3 = block[b3 * G + j];
+        sum = sum + double(x0);
+        sum = sum + (h1 ? double(x1) : 0.0);
+        sum = sum + (h2 ? double(x2) : 0.0);
+        sum = sum + (h3 ? double(x3) : 0.0);
+      }
+    }
+  }
+  if (lane < G && n > 0) mean[wave * G + lane] = float(sum / double(n));
+  if (lane == 0) members[wave] = n;
+  __syncthreads();
+
+  // Entries in ascending order; a reseed sees the book as updated so far.
+  const uint32_t kept = flags[1];
+  for (uint32_t e = 0; e < 16; ++e) {
+    if (members[e] > 0) {
+      if (t < G) cur[e * G + t] = mean[e * G + t];
+      continue;
+    }
+    if (kept & (1u << e)) continue;
+    __syncthreads();
+    const uint32_t row = reseed_row<G>(sample, count, cur, scratch);
+    if (t < G) cur[e * G + t] = sample[uint64_t(row) * G + t];
+  }
+  __syncthreads();
+  for (uint32_t i = t; i < 16 * G; i += kUpdateThreads) book[i] = cur[i];
+  if (t < 4) flags[t] = 0;
+}
+
+uint32_t blocks_for(uint64_t items, uint32_t per_block, uint32_t cap) {
+  uint64_t b = (items + per_block - 1) / per_block;
+  if (b == 0) b = 1;
+  return b > cap ? cap : uint32_t(b);
+}
+
+template <int G>
+hipError_t fit_group(hipStream_t s, const FitArgs& a, uint32_t problems, uint32_t iterations,
+                     const float* init, const FitWhole& whole) {
+  k_fit_init<G><<<problems, 256, 0, s>>>(a, init);
+  // The keep pass can only be due for a warm start on a sample smaller than
+  // the tensor (vq.py:219).
+  const bool keep = init != nullptr && a.count < a.complete;
+  const dim3 assign_grid(blocks_for(a.count, kAssignThreads, 4096), problems);
+  for (uint32_t it = 0; it < iterations; ++it) {
+    k_fit_assign<G><<<assign_grid, kAssignThreads, 0, s>>>(a);
+    if (keep) {
+      k_fit_decide<G><<<problems, 64, 0, s>>>(a);
+      if (whole.adamw != nullptr) {
+        hipError_t e = launch_adamw_keep(s, *whole.adamw, a);
+        if (e != hipSuccess) return e;
+      } else {
+        k_fit_keep_dense<G><<<blocks_for(a.complete, 256, 16384), 256, 0, s>>>(a, whole.values);
+      }
+    }
+    k_fit_update<G><<<problems, kUpdateThreads, 0, s>>>(a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_fit_sample_dense(hipStream_t s, const float* values, uint32_t group,
+                                   const FitArgs& a) {
+  const dim3 grid(blocks_for(uint64_t(a.count) * group, 256, 4096));
+  if (group == 8) k_fit_sample_dense<8><<<grid, 256, 0, s>>>(values, a);
+  else if (group == 16) k_fit_sample_dense<16><<<grid, 256, 0, s>>>(values, a);
+  else k_fit_sample_dense<32><<<grid, 256, 0, s>>>(values, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fit(hipStream_t s, const FitArgs& a, uint32_t group, uint32_t problems,
+                      uint32_t iterations, const float* init, const FitWhole& whole) {
+  if (group == 8) return fit_group<8>(s, a, problems, iterations, init, whole);
+  if (group == 16) return fit_group<16>(s, a, problems, iterations, init, whole);
+  return fit_group<32>(s, a, problems, iterations, init, whole);
+}
+
+}  // namespace ackvq

@@ -129,22 +129,38 @@ int32_t ack_vq_batch(const AckDevice* dev, const AckBuffer* b0, const AckBuffer*
  * books; b2 = seven FP32 coefficients; plan = the op-3 plan) are decoded and
  * updated per element exactly as op 3 computes them, but no dense scratch is
  * written. Instead: AdamW is evaluated at fit_codebook's strided sample of
- * whole vectors, each of W', M', V' gets a codebook from the host fit warm-
- * started from its current book (vq.py:182-229, `iterations` and
- * `sample_vectors` as there; the whole-tensor keep pass runs on the device),
- * and a second device pass recomputes every element and encodes it against
- * its new book (op 0's FP32 rule) straight into `out_codes` (3 x words(m)
- * u32: W', M', V'). `out_books` receives the three books (3 x 16 x group
- * FP32), `changed` (one u32) the number of W values whose decoded value
- * differs from the old W's. Synchronous: returns after the device finished.
- * Status bits as op 3 and op 0; a nonzero status means the outputs must be
- * discarded. Both write slots and the status word must be distinct buffers
- * that alias no input. */
+ * whole vectors, each of W', M', V' gets a codebook fitted on the device
+ * warm-started from its current book (vq.py:182-229, `iterations` and
+ * `sample_vectors` as there, including the whole-tensor keep pass; the same
+ * books as the CPU fit, bit for bit), and a last pass recomputes every
+ * element and encodes it against its new book (op 0's FP32 rule) straight
+ * into `out_codes` (3 x words(m) u32: W', M', V'). `out_books` receives the
+ * three books (3 x 16 x group FP32), `changed` (one u32, cleared by the step)
+ * the number of W values whose decoded value differs from the old W's.
+ * Enqueued on the device stream like ack_vq: ACK_OK means accepted, and a
+ * download waits for it. Status bits as op 3 and op 0; a nonzero status
+ * means the outputs must be discarded. Both write slots and the status word
+ * must be distinct buffers that alias no input. */
 int32_t ack_vq_adamw_step(const AckDevice* dev, const AckBuffer* b0, const AckBuffer* b1,
                           const AckBuffer* b2, const AckBuffer* out_codes,
                           const AckBuffer* out_books, const AckBuffer* changed,
                           const AckBuffer* status, const uint8_t* plan, size_t plan_len,
                           uint32_t iterations, uint32_t sample_vectors);
+
+/* Codebook calibration on the device (fit_codebook, vq.py:182-257) of the m
+ * FP32 values in `values`: bounded Lloyd on the strided sample of at most
+ * `sample_vectors` complete vectors, farthest-point reseed, and, with a warm
+ * start `init` (16 x group FP32; null for a cold start) on a sample smaller
+ * than the tensor, the whole-tensor keep pass. `book_out` receives 16 x group
+ * FP32, bit-identical to ack_vq_host_fit_codebook and the reference's
+ * Python. The reference refuses nonfinite input before fitting; here a
+ * nonfinite sampled value or init entry sets status bit 1, so read status
+ * first. Enqueued like ack_vq. book_out and status must be distinct and
+ * alias no input. For callers whose values already live on the device (the
+ * optimizer's refit, a resident harness). */
+int32_t ack_vq_fit_codebook(const AckDevice* dev, const AckBuffer* values, const AckBuffer* init,
+                            const AckBuffer* book_out, const AckBuffer* status, uint64_t m,
+                            uint32_t group, uint32_t iterations, uint32_t sample_vectors);
 
 /* Stream timer for benchmarks: phase 0 records a start event on the device
  * stream, phase 1 records a stop event, waits for it and writes the elapsed
