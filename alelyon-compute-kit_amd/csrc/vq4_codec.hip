@@ -199,21 +199,12 @@ struct AdamwOut {
 };
 
 // adamw_value (vq4.comp:80-116) for one element given its four decoded state
-// values.
+// values. Branch-free: the arithmetic always runs (a GPU raises no traps) and
+// the shader's early returns become the flags and the write decision.
 __device__ __forceinline__ AdamwOut adamw_value(float weight, float moment, float variance,
                                                 float gradient, const Coeffs& c) {
-  AdamwOut r;
-  r.flags = 0;
-  r.write = false;
-  r.w = r.m = r.v = 0.0f;
-  if (!finite_f32(weight) || !finite_f32(moment) || !finite_f32(variance) || !finite_f32(gradient)) {
-    r.flags = 1;
-    return r;
-  }
-  if (variance < 0.0f) {
-    r.flags = 4;
-    return r;
-  }
+  const bool inputs_finite =
+      finite_f32(weight) && finite_f32(moment) && finite_f32(variance) && finite_f32(gradient);
   const float next_m = c.beta1 * moment + (1.0f - c.beta1) * gradient;
   const float next_v = c.beta2 * variance + (1.0f - c.beta2) * (gradient * gradient);
   const float corrected_m = next_m / c.c1;
@@ -221,14 +212,16 @@ __device__ __forceinline__ AdamwOut adamw_value(float weight, float moment, floa
   const float denominator = sqrtf(corrected_v) + c.eps;
   const float decayed = weight * (1.0f - c.lr * c.decay);
   const float next_w = decayed - c.lr * corrected_m / denominator;
-  if (!finite_f32(next_m) || !finite_f32(next_v) || !finite_f32(corrected_m) ||
-      !finite_f32(corrected_v) || !finite_f32(denominator) || !finite_f32(decayed) ||
-      !finite_f32(next_w))
-    r.flags = 1;
-  r.w = next_w;
-  r.m = next_m;
-  r.v = next_v;
-  r.write = true;
+  const bool results_finite = finite_f32(next_m) && finite_f32(next_v) &&
+                              finite_f32(corrected_m) && finite_f32(corrected_v) &&
+                              finite_f32(denominator) && finite_f32(decayed) && finite_f32(next_w);
+  AdamwOut r;
+  r.write = inputs_finite && !(variance < 0.0f);
+  r.flags = !inputs_finite ? 1u : (variance < 0.0f ? 4u : (results_finite ? 0u : 1u));
+  // An element the shader leaves unwritten reads as zero to the fused passes.
+  r.w = r.write ? next_w : 0.0f;
+  r.m = r.write ? next_m : 0.0f;
+  r.v = r.write ? next_v : 0.0f;
   return r;
 }
 
@@ -344,33 +337,47 @@ __global__ __launch_bounds__(kThreads) void k_adamw_gather(AdamwInputs in, uint3
   if (flags && (threadIdx.x % warpSize) == 0) atomicOr(status, flags);
 }
 
-// The fit's keep pass over the recomputed state blockIdx.y (0 W', 1 M',
-// 2 V'): the entries its complete vectors select under the float64 rule,
-// when that fit's keep-pass switch is set.
+// The fit's keep pass over the recomputed states: for each state whose fit
+// set its keep-pass switch, the entries its complete vectors select under
+// the float64 rule. AdamW is evaluated once per element for all three.
 template <int G>
 __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs a) {
-  const uint32_t state = blockIdx.y;
-  if (a.flags[state * 4 + 2] == 0) return;
-  __shared__ double sbook[16 * G];
-  for (uint32_t i = threadIdx.x; i < 16 * G; i += kThreads)
-    sbook[i] = double(a.book[state * 16 * G + i]);
+  const uint32_t active = (a.flags[2] ? 1u : 0u) | (a.flags[6] ? 2u : 0u) |
+                          (a.flags[10] ? 4u : 0u);
+  if (active == 0) return;
+  __shared__ double sbook[3 * 16 * G];
+  __shared__ float sold[4 * 16 * G];
+  for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) sbook[i] = double(a.book[i]);
+  for (uint32_t i = threadIdx.x; i < 4 * 16 * G; i += kThreads) sold[i] = in.books4[i];
   __syncthreads();
   const Coeffs c = load_coeffs(in.coeffs);
   if (c.fail) return;  // the gather and encode passes report coefficient failures
   const uint32_t words = words_for(in.m, G);
   const uint32_t complete = in.m / G;
-  uint32_t used = 0;
+  uint32_t used[3] = {0, 0, 0};
   for (uint32_t v = blockIdx.x * kThreads + threadIdx.x; v < complete; v += gridDim.x * kThreads) {
-    double x[G];
+    uint32_t code[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) code[st] = nibble(in.codes4 + st * words, v);
+    double x[3][G];
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-      const AdamwOut r = adamw_element<G>(in.codes4, in.books4, words, v * G + j, c);
-      x[j] = double(state == 0 ? r.w : state == 1 ? r.m : r.v);
+      const AdamwOut r = adamw_value(sold[code[0] * G + j], sold[(16 + code[1]) * G + j],
+                                     sold[(32 + code[2]) * G + j], sold[(48 + code[3]) * G + j],
+                                     c);
+      x[0][j] = double(r.w);
+      x[1][j] = double(r.m);
+      x[2][j] = double(r.v);
     }
-    used |= 1u << fitdev::nearest64<G>(x, sbook);
+#pragma unroll
+    for (int st = 0; st < 3; ++st)
+      if (active & (1u << st)) used[st] |= 1u << fitdev::nearest64<G>(x[st], sbook + st * 16 * G);
   }
-  for (int off = 1; off < warpSize; off <<= 1) used |= __shfl_xor(used, off);
-  if (used && (threadIdx.x % warpSize) == 0) atomicOr(&a.flags[state * 4 + 1], used);
+#pragma unroll
+  for (int st = 0; st < 3; ++st) {
+    for (int off = 1; off < warpSize; off <<= 1) used[st] |= __shfl_xor(used[st], off);
+    if (used[st] && (threadIdx.x % warpSize) == 0) atomicOr(&a.flags[st * 4 + 1], used[st]);
+  }
 }
 
 // Recompute W', M', V' per vector and encode each against its new book with
@@ -406,26 +413,39 @@ __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const
 #pragma unroll
       for (int st = 0; st < 4; ++st) in_code[st] = nibble(in.codes4 + st * words, v);
       float xs[3][G];
+      if (valid == G) {
 #pragma unroll
-      for (int j = 0; j < G; ++j) {
-        if (uint32_t(j) < valid) {
+        for (int j = 0; j < G; ++j) {
           const AdamwOut r = adamw_value(sold[in_code[0] * G + j], sold[(16 + in_code[1]) * G + j],
                                          sold[(32 + in_code[2]) * G + j],
                                          sold[(48 + in_code[3]) * G + j], c);
           flags |= r.flags;
           xs[0][j] = r.w; xs[1][j] = r.m; xs[2][j] = r.v;
           bad |= !finite_f32(r.w) || !finite_f32(r.m) || !finite_f32(r.v);
-        } else {
-          xs[0][j] = xs[1][j] = xs[2][j] = 0.0f;
         }
+#pragma unroll
+        for (int st = 0; st < 3; ++st)
+          code[st] = argmin32<G, true>(xs[st], G, sbook + st * 16 * G, bad);
+      } else {
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          const AdamwOut r = adamw_value(sold[in_code[0] * G + j], sold[(16 + in_code[1]) * G + j],
+                                         sold[(32 + in_code[2]) * G + j],
+                                         sold[(48 + in_code[3]) * G + j], c);
+          const bool live = uint32_t(j) < valid;
+          flags |= live ? r.flags : 0u;
+          xs[0][j] = live ? r.w : 0.0f;
+          xs[1][j] = live ? r.m : 0.0f;
+          xs[2][j] = live ? r.v : 0.0f;
+          bad |= live && (!finite_f32(r.w) || !finite_f32(r.m) || !finite_f32(r.v));
+        }
+#pragma unroll
+        for (int st = 0; st < 3; ++st)
+          code[st] = argmin32<G, false>(xs[st], valid, sbook + st * 16 * G, bad);
       }
 #pragma unroll
-      for (int st = 0; st < 3; ++st) {
-        code[st] = valid == G ? argmin32<G, true>(xs[st], G, sbook + st * 16 * G, bad)
-                              : argmin32<G, false>(xs[st], valid, sbook + st * 16 * G, bad);
-      }
-      for (uint32_t j = 0; j < valid; ++j)
-        moved += sbook[code[0] * G + j] != sold[in_code[0] * G + j];
+      for (int j = 0; j < G; ++j)
+        moved += uint32_t(j) < valid && sbook[code[0] * G + j] != sold[in_code[0] * G + j];
     }
 #pragma unroll
     for (int st = 0; st < 3; ++st) {
@@ -495,7 +515,7 @@ hipError_t launch_adamw_gather(hipStream_t s, const AdamwInputs& in, uint32_t co
 }
 
 hipError_t launch_adamw_keep(hipStream_t s, const AdamwInputs& in, const FitArgs& a) {
-  dim3 grid(grid_for(in.m / in.group, kThreads), 3);
+  dim3 grid(grid_for(in.m / in.group, kThreads));
   if (in.group == 8) k_adamw_keep<8><<<grid, kThreads, 0, s>>>(in, a);
   else if (in.group == 16) k_adamw_keep<16><<<grid, kThreads, 0, s>>>(in, a);
   else k_adamw_keep<32><<<grid, kThreads, 0, s>>>(in, a);
