@@ -132,6 +132,8 @@ _SIGNATURES = {
                                   _c.c_uint32, _c.c_void_p, _c.c_void_p], _c.c_int32),
     "ack_vq_fit_codebook": ([_c.c_void_p] * 5 + [_c.c_uint64, _c.c_uint32, _c.c_uint32,
                                                  _c.c_uint32], _c.c_int32),
+    "ack_vq_matmul_dense": ([_c.c_void_p] * 6 + [_c.c_void_p, _c.c_size_t], _c.c_int32),
+    "ack_vq_dense_path_name": ([_c.c_void_p, _c.c_size_t, _c.c_char_p, _c.c_size_t], _c.c_int32),
 }
 
 

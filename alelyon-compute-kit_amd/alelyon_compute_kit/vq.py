@@ -394,6 +394,69 @@ class VQDevice:
         return out.reshape(m, n)
 
     @staticmethod
+    def _dense_geometry(x: np.ndarray, b: VQArray, transpose_a, transpose_b):
+        if type(transpose_a) is not bool or type(transpose_b) is not bool:
+            raise ValueError("transpose flags must be boolean")
+        if x.ndim != 2 or len(b.shape) != 2:
+            raise ValueError("vq dense matmul requires a dense matrix and a vq matrix")
+        m, k = x.shape[::-1] if transpose_a else x.shape
+        k2, n = b.shape[::-1] if transpose_b else b.shape
+        if k != k2 or max(m, n, k) > 65536 or m * n > MAX_ELEMENTS or m * k > MAX_ELEMENTS:
+            raise ValueError("vq matmul dimensions are incompatible or exceed bounds")
+        if m * n * k > MAX_MATMUL_MACS:
+            raise ValueError("vq-matmul-work-limit: split the product into bounded calls")
+        return m, n, k, int(transpose_a) | (int(transpose_b) << 1)
+
+    def matmul_dense(self, x, b: VQArray, *, transpose_a=False, transpose_b=False) -> np.ndarray:
+        """``op(x) @ op(b)`` with ``x`` a dense float32 matrix: the packed
+        product without encoding the activations (an extension; ``matmul``
+        keeps the reference's semantics)."""
+        x = _float_array(x, "dense operand")
+        m, n, k, flags = self._dense_geometry(x, b, transpose_a, transpose_b)
+        device = self.device
+        with device._lock, ExitStack() as cleanup:
+            device._require_open()
+            bufs = []
+            for array in (x, b.codes, b.codebook):
+                buf = device.buffer(array.nbytes)
+                cleanup.callback(buf.free)
+                buf.upload(array)
+                bufs.append(buf)
+            out = device.buffer(m * n * 4)
+            cleanup.callback(out.free)
+            status = device.buffer(4)
+            cleanup.callback(status.free)
+            status.upload(np.zeros(1, dtype=np.uint32))
+            self.run_dense((2, m, n, k, b.group, ENTRIES, flags, 0), *bufs, out, status)
+            flags_out = int(status.download(np.uint32)[0])
+            if flags_out:
+                raise ack.AckError(f"vq device arithmetic refused: status={flags_out}")
+            return out.download(np.float32).reshape(m, n)
+
+    def run_dense(self, words, x: ack.Buffer, b_codes: ack.Buffer, b_book: ack.Buffer,
+                  out: ack.Buffer, status: ack.Buffer) -> None:
+        """Enqueue the dense-activation product on resident buffers (an op-2
+        plan; ``x`` holds m x k float32); does not wait or check status."""
+        device = self.device
+        with device._lock:
+            device._require_open()
+            plan = _plan(words)
+            rc = self._lib.cdll.ack_vq_matmul_dense(device._handle, x._handle, b_codes._handle,
+                                                    b_book._handle, out._handle, status._handle,
+                                                    plan, len(plan))
+            if rc != ack.ACK_OK:
+                raise ack._kit_error("vq", rc, self._lib.last_error())
+
+    def dense_path_name(self, words) -> str:
+        """The kernel path the dense-activation product takes for an op-2 plan."""
+        buf = ctypes.create_string_buffer(64)
+        plan = _plan(words)
+        rc = self._lib.cdll.ack_vq_dense_path_name(plan, len(plan), buf, len(buf))
+        if rc != ack.ACK_OK:
+            raise ack._kit_error("vq", rc, self._lib.last_error())
+        return buf.value.decode()
+
+    @staticmethod
     def _adamw_inputs(weight, momentum, variance, gradient, lr, beta1, beta2, eps,
                       weight_decay, step):
         states = (weight, momentum, variance, gradient)

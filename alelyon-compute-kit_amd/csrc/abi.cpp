@@ -599,6 +599,68 @@ int32_t ack_vq_host_fit_codebook(const float* values, uint64_t m, uint32_t group
   return ACK_OK;
 }
 
+int32_t ack_vq_matmul_dense(const AckDevice* handle, const AckBuffer* x, const AckBuffer* b_codes,
+                            const AckBuffer* b_book, const AckBuffer* out, const AckBuffer* status,
+                            const uint8_t* plan_bytes, size_t plan_len) {
+  ackvq::Plan plan;
+  if (int32_t rc = parse_plan(plan_bytes, plan_len, ackvq::Bounds::Library, &plan)) return rc;
+  if (plan.op != ackvq::Op::Matmul) {
+    set_error("vq dense matmul: plan op must be 2 (matmul)");
+    return ACK_ERR_SHAPE;
+  }
+  std::shared_ptr<Device> dev;
+  std::unique_lock<std::mutex> lock;
+  if (int32_t rc = enter(handle, &dev, &lock)) return rc;
+  // Slot 0 holds the dense m x k activations; slot 1 (A's codebook in op 2)
+  // is not read and aliases slot 0. The output and status rules are op 2's.
+  const AckBuffer* slots[6] = {x, x, b_codes, b_book, out, status};
+  BufferRec* bufs[6];
+  uint64_t capacities[6], ids[6];
+  for (int i = 0; i < 6; ++i) {
+    if (int32_t rc = lookup_buffer(*dev, slots[i], &bufs[i])) return rc;
+    capacities[i] = bufs[i]->bytes;
+    ids[i] = bufs[i]->id;
+  }
+  const uint32_t m = plan.m(), n = plan.n(), k = plan.k(), g = plan.group();
+  ackvq::Plan dense = plan;
+  dense.required_bytes[0] = uint64_t(m) * k * 4;
+  dense.required_bytes[1] = 0;
+  int slot = 0;
+  ackvq::PlanError e = ackvq::validate_buffers(dense, capacities, ids, &slot);
+  if (e != ackvq::PlanError::None) {
+    set_error("vq dense matmul: plan refused: " + ackvq::plan_error_name(e, slot));
+    return plan_code(e);
+  }
+  ackvq::Operands o;
+  for (int i = 0; i < 4; ++i) o.in[i] = bufs[i]->ptr;
+  o.out = bufs[4]->ptr;
+  o.status = static_cast<uint32_t*>(bufs[5]->ptr);
+  const ackvq::MatmulPath path =
+      ackvq::choose_dense_path(m, n, k, g, plan.flags(), 1, dev->policy);
+  const size_t ws = ackvq::dense_workspace_bytes(path, m, n, k, g, plan.flags(), 1);
+  if (int32_t rc = ensure_workspace(*dev, ws)) return rc;
+  hipError_t he = ackvq::launch_matmul_dense(dev->stream, o, m, n, k, g, plan.flags(), path,
+                                             dev->workspace, dev->workspace_bytes);
+  if (he != hipSuccess) return hip_failure(*dev, "vq dense matmul: kernel launch refused", he, false);
+  return ACK_OK;
+}
+
+int32_t ack_vq_dense_path_name(const uint8_t* plan, size_t plan_len, char* out, size_t len) {
+  if (out == nullptr || len == 0) return ACK_ERR_NULL;
+  ackvq::Plan p;
+  if (int32_t rc = parse_plan(plan, plan_len, ackvq::Bounds::Library, &p)) return rc;
+  if (p.op != ackvq::Op::Matmul) {
+    set_error("vq dense matmul: plan op must be 2 (matmul)");
+    return ACK_ERR_SHAPE;
+  }
+  const char* name = ackvq::matmul_path_name(
+      ackvq::choose_dense_path(p.m(), p.n(), p.k(), p.group(), p.flags(), 1, 0));
+  const size_t n = std::strlen(name) < len - 1 ? std::strlen(name) : len - 1;
+  std::memcpy(out, name, n);
+  out[n] = '\0';
+  return ACK_OK;
+}
+
 int32_t ack_vq_fit_codebook(const AckDevice* handle, const AckBuffer* values,
                             const AckBuffer* init, const AckBuffer* book_out,
                             const AckBuffer* status, uint64_t m, uint32_t group,

@@ -42,9 +42,12 @@ hipError_t launch_gram(hipStream_t s, const Operands& o, uint32_t m, uint32_t n,
                        uint32_t group);
 
 bool rowbins_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
+bool rowbins_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
 size_t rowbins_workspace_bytes(uint32_t n, uint32_t k, uint32_t group);
 hipError_t launch_rowbins(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                           uint32_t group, void* workspace);
+hipError_t launch_rowbins_dense(hipStream_t s, const Operands& o, uint32_t m, uint32_t n,
+                                uint32_t k, uint32_t group, void* workspace);
 
 // Bytes of device workspace a path needs (split-k partials, counters).
 size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
@@ -56,6 +59,17 @@ hipError_t launch_adamw(hipStream_t s, const Operands& o, uint32_t m, uint32_t g
 hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                          uint32_t group, uint32_t flags, MatmulPath path, void* workspace,
                          size_t workspace_bytes);
+
+// The dense-activation product: op 2's geometry and flags with A a dense FP32
+// array in in[0] (in[1] unused). Paths: row-bins (m >= 64), the GEMV paths
+// (m <= 8, after a pass that takes max |x|), else General.
+MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                             uint32_t count, uint32_t policy);
+size_t dense_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
+                             uint32_t flags, uint32_t count);
+hipError_t launch_matmul_dense(hipStream_t s, const Operands& o, uint32_t m, uint32_t n,
+                               uint32_t k, uint32_t group, uint32_t flags, MatmulPath path,
+                               void* workspace, size_t workspace_bytes);
 
 // Fused VQAdamW passes (ack_vq_adamw_step). codes4/books4/coeffs are the
 // op-3 inputs.

@@ -55,7 +55,9 @@ constexpr int kGT = 64;   // output tile edge
 constexpr int kGK = 16;   // inner step
 constexpr int kGThreads = 256;
 
-template <int G>
+// AD: A is a dense FP32 array in in[0] (the dense-activation product), read
+// at the same flat index the packed A would be decoded at.
+template <int G, bool AD>
 __global__ __launch_bounds__(kGThreads) void k_matmul_general(Operands o, uint32_t m, uint32_t n,
                                                               uint32_t k, uint32_t flags) {
   __shared__ float sa_book[16 * G];
@@ -71,12 +73,14 @@ __global__ __launch_bounds__(kGThreads) void k_matmul_general(Operands o, uint32
     const uint32_t* b_codes = item_ptr<uint32_t>(o.in[2], o.stride[2], item);
     const float* b_book = item_ptr<float>(o.in[3], o.stride[3], item);
     float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
+    const float* a_dense = item_ptr<float>(o.in[0], o.stride[0], item);
     __syncthreads();
     for (uint32_t i = tid; i < 16 * G; i += kGThreads) {
-      sa_book[i] = a_book[i];
+      if (!AD) sa_book[i] = a_book[i];
       sb_book[i] = b_book[i];
     }
-    if (blockIdx.x == 0 && blockIdx.y == 0) sweep_books(a_book, b_book, 16 * G, o.status);
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+      sweep_books(AD ? b_book : a_book, b_book, 16 * G, o.status);
     float acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -94,7 +98,7 @@ __global__ __launch_bounds__(kGThreads) void k_matmul_general(Operands o, uint32
           const uint32_t row = m0 + r;
           if (row < m) {
             const uint32_t flat = (flags & 1u) ? inner * m + row : row * k + inner;
-            av = sa_book[nibble(a_codes, flat / G) * G + flat % G];
+            av = AD ? a_dense[flat] : sa_book[nibble(a_codes, flat / G) * G + flat % G];
           }
           const uint32_t col = n0 + r;
           if (col < n) {
@@ -158,6 +162,34 @@ typedef __attribute__((address_space(3))) int32_t lds_i32;
 __device__ __forceinline__ void lds_add(uint32_t byte_addr, int32_t v) {
   __hip_atomic_fetch_add(reinterpret_cast<lds_i32*>(static_cast<size_t>(byte_addr)), v,
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Dense A (the dense-activation product): the largest |x| of each instance's
+// m x k values sets the fixed-point scale of the GEMV bins. kAmaxParts blocks
+// per instance each write the maximum of their share; the GEMV set-up takes
+// the maximum of the parts. A nonfinite value sets status bit 1.
+constexpr uint32_t kAmaxParts = 16;
+
+__global__ __launch_bounds__(256) void k_dense_amax(Operands o, uint32_t values, float* parts) {
+  __shared__ float wmax[4];
+  for (uint32_t item = blockIdx.y; item < o.count; item += gridDim.y) {
+    const float* x = item_ptr<float>(o.in[0], o.stride[0], item);
+    float mx = 0.0f;
+    bool bad = false;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < values; i += kAmaxParts * 256) {
+      const float v = x[i];
+      bad |= !finite_f32(v);
+      mx = fmaxf(mx, fabsf(v));
+    }
+    for (int off = 1; off < warpSize; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    __syncthreads();  // the previous instance's maxima are read
+    if (threadIdx.x % warpSize == 0) wmax[threadIdx.x / warpSize] = mx;
+    if (__any(bad) && (threadIdx.x % warpSize) == 0) atomicOr(o.status, 1u);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      parts[uint64_t(item) * kAmaxParts + blockIdx.x] =
+          fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  }
 }
 
 // Sum the split-k bins in split order (one thread per bin), then apply the B
@@ -282,8 +314,9 @@ struct PairAhead {
 };
 
 // grid: (n tiles, k splits, z); block z serves instances z, z + gridDim.z, ...
-// ks is a multiple of kPairBatchRows.
-template <int G>
+// ks is a multiple of kPairBatchRows. AD: x is dense FP32 in in[0] and in[1]
+// holds the kAmaxParts partial maxima of |x| per instance (k_dense_amax).
+template <int G, bool AD>
 __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint32_t n,
                                                                 uint32_t k, uint32_t ks,
                                                                 float* partial) {
@@ -334,13 +367,18 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     const uint32_t lt = opaque(tid);
     const __amdgpu_buffer_rsrc_t ars =
         words_rsrc(item_ptr<uint32_t>(o.in[0], o.stride[0], item) + a_w0, a_words * 4u);
-    const __amdgpu_buffer_rsrc_t abk = words_rsrc(item_ptr<float>(o.in[1], o.stride[1], item), 64u * G);
+    const __amdgpu_buffer_rsrc_t abk = words_rsrc(item_ptr<float>(o.in[1], o.stride[1], item),
+                                                  AD ? kAmaxParts * 4u : 64u * G);
     const __amdgpu_buffer_rsrc_t bbk = words_rsrc(item_ptr<float>(o.in[3], o.stride[3], item), 64u * G);
     PairAhead h;
-    h.a = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(abk, lt * 4u, 0, 0)));
+    h.a = __uint_as_float(uint32_t(
+        __builtin_amdgcn_raw_buffer_load_b32(abk, (AD ? lt % kAmaxParts : lt) * 4u, 0, 0)));
     h.b = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(bbk, lt * 4u, 0, 0)));
-    h.w0 = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(ars, lt * 4u, 0, 0));
-    h.w1 = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(ars, (lt + kPairThreads) * 4u, 0, 0));
+    h.w0 = h.w1 = 0;
+    if (!AD) {
+      h.w0 = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(ars, lt * 4u, 0, 0));
+      h.w1 = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(ars, (lt + kPairThreads) * 4u, 0, 0));
+    }
     return h;
   };
   auto batch_rsrc = [&](uint32_t item) {
@@ -362,13 +400,21 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   float acc[kPairSH][kPairSL];
   int shift = 0;
   uint32_t xbase = k0;
+  __amdgpu_buffer_rsrc_t x_rs = words_rsrc(nullptr, 0u);  // AD: this instance's x[0, kend)
 
   // rows [xb0, xb0 + kPairXRows) of A's single row, quantised; zero past kend
   auto stage_x = [&](uint32_t xb0) __attribute__((always_inline)) {
     for (uint32_t r4 = opaque(tid) * 4; r4 < kPairXRows; r4 += 4 * kPairThreads) {
       const uint32_t row = xb0 + r4;
       int4 v = make_int4(0, 0, 0, 0);
-      if (row < kend) {
+      if (AD) {
+        const float lim = 524287.0f;  // 2^19 - 1; reads past kend return zero
+        auto quant = [&](uint32_t rr) {
+          const float f = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(x_rs, rr * 4u, 0, 0)));
+          return int32_t(fminf(rintf(ldexpf(f, shift)), lim));
+        };
+        v = make_int4(quant(row), quant(row + 1), quant(row + 2), quant(row + 3));
+      } else if (row < kend) {
         const uint32_t u = row / G;
         const uint32_t code = (aw[(u >> 3) - a_w0] >> ((u & 7u) * 4u)) & 15u;
         const float4 f = *reinterpret_cast<const float4*>(af + code * G + row % G);
@@ -463,21 +509,30 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     // ---- set-up ----
     const uint32_t st = opaque(tid);
     __syncthreads();  // the previous instance's S and books are no longer read
-    if (st < 16 * G) { af[st] = cur.a; bb[st] = cur.b; }
-    if (st < a_words) aw[st] = cur.w0;
-    if (st + kPairThreads < a_words) aw[st + kPairThreads] = cur.w1;
+    if (st < 16 * G) {
+      if (!AD) af[st] = cur.a;
+      bb[st] = cur.b;
+    }
+    if (!AD && st < a_words) aw[st] = cur.w0;
+    if (!AD && st + kPairThreads < a_words) aw[st + kPairThreads] = cur.w1;
+    if (AD) x_rs = words_rsrc(item_ptr<float>(o.in[0], o.stride[0], item), kend * 4u);
 #pragma unroll
     for (uint32_t i = 0; i < kPairBins / (4 * kPairThreads); ++i)
       bins4[st + i * kPairThreads] = make_int4(0, 0, 0, 0);
     __syncthreads();
-    if (tile == 0 && split == 0) sweep_books(af, bb, 16 * G, o.status);
-    // largest |A book entry|: 16 row maxima, then every thread reads them
+    if (tile == 0 && split == 0) sweep_books(AD ? bb : af, bb, 16 * G, o.status);
+    // largest |A book entry| (AD: largest |x|): 16 partial maxima, then every
+    // thread reads them
     if (st < 16) {
       float m = 0.0f;
+      if (AD) {
+        m = cur.a;
+      } else {
 #pragma unroll
-      for (int t = 0; t < G; t += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(af + st * G + t);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        for (int t = 0; t < G; t += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(af + st * G + t);
+          m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
       }
       rmax[st] = m;
     }
@@ -609,6 +664,8 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   }
 }
 
+static_assert(kAmaxParts == 16, "the GEMV set-up reduces 16 partial maxima");
+
 size_t pairs_shmem(uint32_t g) {
   return g == 8 ? PairLds<8>::total : (g == 16 ? PairLds<16>::total : PairLds<32>::total);
 }
@@ -682,7 +739,8 @@ struct RowAhead {
   float a, b;      // entry tid of the A and B books
 };
 
-template <int G, int MP>
+// AD: A is dense FP32 in in[0]; in[1] holds the partial maxima of |x|.
+template <int G, int MP, bool AD>
 __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32_t m, uint32_t n,
                                                               uint32_t k, uint32_t flags,
                                                               uint32_t ks, float* partial) {
@@ -735,13 +793,17 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
     const uint32_t a_words_all = ((a_vec_elems + G - 1) / G + 7) / 8;
     const __amdgpu_buffer_rsrc_t ars =
         words_rsrc(item_ptr<uint32_t>(o.in[0], o.stride[0], item), a_words_all * 4u);
-    const __amdgpu_buffer_rsrc_t abk = words_rsrc(item_ptr<float>(o.in[1], o.stride[1], item), 64u * G);
+    const __amdgpu_buffer_rsrc_t abk = words_rsrc(item_ptr<float>(o.in[1], o.stride[1], item),
+                                                  AD ? kAmaxParts * 4u : 64u * G);
     const __amdgpu_buffer_rsrc_t bbk = words_rsrc(item_ptr<float>(o.in[3], o.stride[3], item), 64u * G);
     RowAhead h;
-    h.a = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(abk, lt * 4u, 0, 0)));
+    h.a = __uint_as_float(uint32_t(
+        __builtin_amdgcn_raw_buffer_load_b32(abk, (AD ? lt % kAmaxParts : lt) * 4u, 0, 0)));
     h.b = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(bbk, lt * 4u, 0, 0)));
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      h.w[j] = 0;
+      if (AD) continue;
       const uint32_t idx = lt + j * kRowThreads;
       // staged word idx: row idx / per_row, word idx % per_row of that row (flags 0)
       const uint32_t r = (flags & 1u) ? 0u : idx / awn.per_row;
@@ -770,10 +832,15 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
   float acc[kPer][2];
   int shift = 0;
   uint32_t xbase = k0;
+  __amdgpu_buffer_rsrc_t x_rs = words_rsrc(nullptr, 0u);  // AD: this instance's m x k values
 
   // one quantised activation of A
   auto x_of = [&](uint32_t r, uint32_t kk) -> int32_t {
     const uint32_t flat = (flags & 1u) ? kk * m + r : r * k + kk;
+    if (AD) {
+      const float f = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(x_rs, flat * 4u, 0, 0)));
+      return int32_t(fminf(rintf(ldexpf(f, shift)), 524287.0f));
+    }
     const uint32_t v = flat / G;
     const uint32_t slot = (flags & 1u) ? (v >> 3) - a_base(0) : r * awn.per_row + (v >> 3) - a_base(r);
     const uint32_t code = (aw[slot] >> ((v & 7u) * 4u)) & 15u;
@@ -878,20 +945,28 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
     // ---- set-up ----
     const uint32_t st = opaque(tid);
     __syncthreads();
-    if (st < 16 * G) { af[st] = cur.a; bb[st] = cur.b; }
+    if (st < 16 * G) {
+      if (!AD) af[st] = cur.a;
+      bb[st] = cur.b;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (st + j * kRowThreads < kRowAWords) aw[st + j * kRowThreads] = cur.w[j];
+      if (!AD && st + j * kRowThreads < kRowAWords) aw[st + j * kRowThreads] = cur.w[j];
+    if (AD) x_rs = words_rsrc(item_ptr<float>(o.in[0], o.stride[0], item), m * k * 4u);
 #pragma unroll
     for (int i = 0; i < kPer; ++i) bins[st + i * kRowThreads] = 0;
     __syncthreads();
-    if (tile == 0 && split == 0) sweep_books(af, bb, 16 * G, o.status);
+    if (tile == 0 && split == 0) sweep_books(AD ? bb : af, bb, 16 * G, o.status);
     if (st < 16) {
       float mx = 0.0f;
+      if (AD) {
+        mx = cur.a;
+      } else {
 #pragma unroll
-      for (int t = 0; t < G; t += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(af + st * G + t);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        for (int t = 0; t < G; t += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(af + st * G + t);
+          mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
       }
       rmax[st] = mx;
     }
@@ -995,7 +1070,7 @@ void pairs_slices(uint32_t n, uint32_t k, uint32_t group, uint32_t count, uint32
   *splits = (k + *ks - 1) / *ks;
 }
 
-template <int G>
+template <int G, bool AD>
 hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k, uint32_t flags,
                         void* workspace) {
   (void)flags;  // m = 1: A's flat index is the inner index either way
@@ -1008,11 +1083,12 @@ hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k
   uint32_t zc = per_z >= 256 ? 1u : 256u / per_z;
   zc = zc < o.count ? zc : o.count;
   const size_t shmem = pairs_shmem(G);
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_pairs<G>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_pairs<G, AD>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
   if (e != hipSuccess) return e;
   dim3 grid(tiles, splits, zc);
-  k_gemv_pairs<G><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, static_cast<float*>(workspace));
+  k_gemv_pairs<G, AD><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks,
+                                                        static_cast<float*>(workspace));
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || splits == 1) return err;
   dim3 fgrid(tiles * kFinishParts, 1, zc);
@@ -1034,7 +1110,7 @@ void rows_slices(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t fl
   *splits = (k + per - 1) / per;
 }
 
-template <int G, int MP>
+template <int G, int MP, bool AD>
 hipError_t launch_rows_mp(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                           uint32_t flags, void* workspace) {
   const uint32_t tiles = (n / (8 * G) + kTileWords - 1) / kTileWords;
@@ -1044,12 +1120,12 @@ hipError_t launch_rows_mp(hipStream_t s, const Operands& o, uint32_t m, uint32_t
   uint32_t zc = per_z >= 256 ? 1u : 256u / per_z;
   zc = zc < o.count ? zc : o.count;
   const size_t shmem = RowLds<G, MP>::total;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_rows<G, MP>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_rows<G, MP, AD>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
   if (e != hipSuccess) return e;
   dim3 grid(tiles, splits, zc);
-  k_gemv_rows<G, MP><<<grid, kRowThreads, shmem, s>>>(o, m, n, k, flags, ks,
-                                                      static_cast<float*>(workspace));
+  k_gemv_rows<G, MP, AD><<<grid, kRowThreads, shmem, s>>>(o, m, n, k, flags, ks,
+                                                          static_cast<float*>(workspace));
   e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   dim3 fgrid(tiles * kFinishParts, 1, zc);
@@ -1066,15 +1142,28 @@ hipError_t launch_rows_mp(hipStream_t s, const Operands& o, uint32_t m, uint32_t
   return hipGetLastError();
 }
 
-template <int G>
+template <int G, bool AD>
 hipError_t launch_rows(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t flags, void* workspace) {
   switch ((m + 1) / 2) {
-    case 1: return launch_rows_mp<G, 1>(s, o, m, n, k, flags, workspace);
-    case 2: return launch_rows_mp<G, 2>(s, o, m, n, k, flags, workspace);
-    case 3: return launch_rows_mp<G, 3>(s, o, m, n, k, flags, workspace);
-    default: return launch_rows_mp<G, 4>(s, o, m, n, k, flags, workspace);
+    case 1: return launch_rows_mp<G, 1, AD>(s, o, m, n, k, flags, workspace);
+    case 2: return launch_rows_mp<G, 2, AD>(s, o, m, n, k, flags, workspace);
+    case 3: return launch_rows_mp<G, 3, AD>(s, o, m, n, k, flags, workspace);
+    default: return launch_rows_mp<G, 4, AD>(s, o, m, n, k, flags, workspace);
   }
+}
+
+template <bool AD>
+hipError_t launch_factorised(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                             uint32_t group, uint32_t flags, MatmulPath path, void* workspace) {
+  if (path == MatmulPath::GemvPairs) {
+    if (group == 8) return launch_pairs<8, AD>(s, o, n, k, flags, workspace);
+    if (group == 16) return launch_pairs<16, AD>(s, o, n, k, flags, workspace);
+    return launch_pairs<32, AD>(s, o, n, k, flags, workspace);
+  }
+  if (group == 8) return launch_rows<8, AD>(s, o, m, n, k, flags, workspace);
+  if (group == 16) return launch_rows<16, AD>(s, o, m, n, k, flags, workspace);
+  return launch_rows<32, AD>(s, o, m, n, k, flags, workspace);
 }
 
 }  // namespace
@@ -1119,21 +1208,56 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins(s, o, m, n, k, group, workspace);
   if (path == MatmulPath::GramMfma) return launch_gram(s, o, m, n, k, group);
-  if (path == MatmulPath::GemvPairs) {
-    if (group == 8) return launch_pairs<8>(s, o, n, k, flags, workspace);
-    if (group == 16) return launch_pairs<16>(s, o, n, k, flags, workspace);
-    return launch_pairs<32>(s, o, n, k, flags, workspace);
-  }
-  if (path == MatmulPath::GemvRows) {
-    if (group == 8) return launch_rows<8>(s, o, m, n, k, flags, workspace);
-    if (group == 16) return launch_rows<16>(s, o, m, n, k, flags, workspace);
-    return launch_rows<32>(s, o, m, n, k, flags, workspace);
+  if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows)
+    return launch_factorised<false>(s, o, m, n, k, group, flags, path, workspace);
+  const uint32_t zc = o.count < 65535 ? o.count : 65535;
+  dim3 grid((n + kGT - 1) / kGT, (m + kGT - 1) / kGT, zc);
+  if (group == 8) k_matmul_general<8, false><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
+  else if (group == 16) k_matmul_general<16, false><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
+  else k_matmul_general<32, false><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
+  return hipGetLastError();
+}
+
+MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                             uint32_t count, uint32_t policy) {
+  if (policy == 1) return MatmulPath::General;
+  if (count == 1 && rowbins_applies_dense(m, n, k, group, flags)) return MatmulPath::RowBins;
+  if (m <= kGemvMaxM && (flags & 2u) == 0 && n % (8 * group) == 0)
+    return m == 1 ? MatmulPath::GemvPairs : MatmulPath::GemvRows;
+  return MatmulPath::General;
+}
+
+// The factorised paths' split-k partials, then (256-byte aligned) the
+// partial maxima of |x|.
+size_t dense_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
+                             uint32_t flags, uint32_t count) {
+  const size_t base = matmul_workspace_bytes(p, m, n, k, group, flags, count);
+  if (p != MatmulPath::GemvRows && p != MatmulPath::GemvPairs) return base;
+  return (base + 255) / 256 * 256 + size_t(count) * kAmaxParts * sizeof(float);
+}
+
+hipError_t launch_matmul_dense(hipStream_t s, const Operands& o, uint32_t m, uint32_t n,
+                               uint32_t k, uint32_t group, uint32_t flags, MatmulPath path,
+                               void* workspace, size_t workspace_bytes) {
+  (void)workspace_bytes;
+  if (path == MatmulPath::RowBins) return launch_rowbins_dense(s, o, m, n, k, group, workspace);
+  if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows) {
+    const size_t base = matmul_workspace_bytes(path, m, n, k, group, flags, o.count);
+    float* parts = reinterpret_cast<float*>(static_cast<char*>(workspace) + (base + 255) / 256 * 256);
+    Operands od = o;
+    od.in[1] = parts;
+    od.stride[1] = kAmaxParts * sizeof(float);
+    const uint32_t zc = o.count < 65535 ? o.count : 65535;
+    k_dense_amax<<<dim3(kAmaxParts, zc), 256, 0, s>>>(od, m * k, parts);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_factorised<true>(s, od, m, n, k, group, flags, path, workspace);
   }
   const uint32_t zc = o.count < 65535 ? o.count : 65535;
   dim3 grid((n + kGT - 1) / kGT, (m + kGT - 1) / kGT, zc);
-  if (group == 8) k_matmul_general<8><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
-  else if (group == 16) k_matmul_general<16><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
-  else k_matmul_general<32><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
+  if (group == 8) k_matmul_general<8, true><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
+  else if (group == 16) k_matmul_general<16, true><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
+  else k_matmul_general<32, true><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);
   return hipGetLastError();
 }
 

@@ -104,7 +104,8 @@ __device__ __forceinline__ bool finish_group(const v16f sb, const float (*sbt)[1
   return bad && live;
 }
 
-template <int G>
+// AD: A is a dense FP32 m x k array in in[0] (the dense-activation product).
+template <int G, bool AD>
 __global__ __launch_bounds__(256) void k_rowbins(Operands o, uint32_t m, uint32_t n, uint32_t k,
                                                  const uint32_t* __restrict__ wt) {
   __shared__ __align__(16) float sbt[G][16];      // C_B transposed: sbt[t][e]
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(256) void k_rowbins(Operands o, uint32_t m, uint32_
   if (blockIdx.x == 0 && blockIdx.y == 0) {
     bool bad = false;
     for (uint32_t i = threadIdx.x; i < 16 * G; i += blockDim.x)
-      bad |= !finite_f32(a_book[i]) || !finite_f32(b_book[i]);
+      bad |= (!AD && !finite_f32(a_book[i])) || !finite_f32(b_book[i]);
     if (__any(bad) && lane == 0) atomicOr(o.status, 1u);
   }
   __syncthreads();
@@ -142,8 +143,9 @@ __global__ __launch_bounds__(256) void k_rowbins(Operands o, uint32_t m, uint32_
   // x comes from the A codebook in global memory (L1-resident, 16 x G
   // floats): reading it through LDS would share lgkmcnt with the scalar
   // prefetch and wait for it.
-  uint32_t a = row_live ? nibble(a_codes, r * groups) : 0u;
-  uint32_t a_next = (row_live && groups > 1) ? nibble(a_codes, r * groups + 1) : 0u;
+  uint32_t a = (!AD && row_live) ? nibble(a_codes, r * groups) : 0u;
+  uint32_t a_next = (!AD && row_live && groups > 1) ? nibble(a_codes, r * groups + 1) : 0u;
+  const float* x_row = static_cast<const float*>(o.in[0]) + uint64_t(row_live ? r : 0) * k;
   for (uint32_t run = 0; run < runs; ++run) {
     uint32_t w[kRun];
 #pragma unroll
@@ -154,12 +156,13 @@ __global__ __launch_bounds__(256) void k_rowbins(Operands o, uint32_t m, uint32_
     }
     const uint32_t kk0 = run * kRun;
     const uint32_t u = kk0 / G, s0 = kk0 % G;
-    if (s0 == 0 && u > 0) {
+    if (!AD && s0 == 0 && u > 0) {
       a = a_next;
       if (row_live && u + 1 < groups) a_next = nibble(a_codes, r * groups + u + 1);
     }
     float x[kRun];
-    const float4* xrow = reinterpret_cast<const float4*>(a_book + a * G + s0);
+    const float4* xrow = AD ? reinterpret_cast<const float4*>(x_row + kk0)
+                            : reinterpret_cast<const float4*>(a_book + a * G + s0);
 #pragma unroll
     for (int s = 0; s < kRun; s += 4) {
       const float4 v = xrow[s / 4];
@@ -199,6 +202,11 @@ __global__ __launch_bounds__(256) void k_rowbins(Operands o, uint32_t m, uint32_
 
 }  // namespace
 
+// Dense A has no groups to straddle: any group, k a multiple of 16 (runs).
+bool rowbins_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags) {
+  return flags == 0 && m >= 64 && n % (8 * group) == 0 && k % 16 == 0;
+}
+
 bool rowbins_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags) {
   // runs of 16 rows of B never straddle an A group: k % 16 == 0 and g >= 16
   // divides them, g = 8 takes two groups per run (handled: s0 + s < 16 < 2g).
@@ -210,7 +218,10 @@ size_t rowbins_workspace_bytes(uint32_t n, uint32_t k, uint32_t group) {
   return size_t(n / (8 * group)) * k * 4;
 }
 
-hipError_t launch_rowbins(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+namespace {
+
+template <bool AD>
+hipError_t rowbins_launch(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                           uint32_t group, void* workspace) {
   const uint32_t rw = n / (8 * group);
   uint32_t* wt = static_cast<uint32_t*>(workspace);
@@ -219,10 +230,22 @@ hipError_t launch_rowbins(hipStream_t s, const Operands& o, uint32_t m, uint32_t
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   dim3 grid((rw + kRBWaves - 1) / kRBWaves, (m + 63) / 64);
-  if (group == 8) k_rowbins<8><<<grid, 64 * kRBWaves, 0, s>>>(o, m, n, k, wt);
-  else if (group == 16) k_rowbins<16><<<grid, 64 * kRBWaves, 0, s>>>(o, m, n, k, wt);
-  else k_rowbins<32><<<grid, 64 * kRBWaves, 0, s>>>(o, m, n, k, wt);
+  if (group == 8) k_rowbins<8, AD><<<grid, 64 * kRBWaves, 0, s>>>(o, m, n, k, wt);
+  else if (group == 16) k_rowbins<16, AD><<<grid, 64 * kRBWaves, 0, s>>>(o, m, n, k, wt);
+  else k_rowbins<32, AD><<<grid, 64 * kRBWaves, 0, s>>>(o, m, n, k, wt);
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_rowbins(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                          uint32_t group, void* workspace) {
+  return rowbins_launch<false>(s, o, m, n, k, group, workspace);
+}
+
+hipError_t launch_rowbins_dense(hipStream_t s, const Operands& o, uint32_t m, uint32_t n,
+                                uint32_t k, uint32_t group, void* workspace) {
+  return rowbins_launch<true>(s, o, m, n, k, group, workspace);
 }
 
 }  // namespace ackvq

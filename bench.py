@@ -108,6 +108,7 @@ def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
     words = (2, m, 4096, 4096, 16, 16, 0, 0)
     path = dev.path_name(words)
     single_ms = None
+    dense = None
     try:
         def launch():
             dev.run(words, bufs, out, status, count=items)
@@ -123,7 +124,15 @@ def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
                 b.upload(a)
             s_out = device.buffer(m * 4096 * 4)
             single_ms = timed(device, lambda: dev.run(words, s_bufs, s_out, status), 50, 5)
-            for b in s_bufs + [s_out]:
+            # the dense-activation product on the same weight: x as float32
+            d_x = device.buffer(x.nbytes)
+            d_x.upload(x)
+            dense_ms = timed(device, lambda: dev.run_dense(words, d_x, s_bufs[2], s_bufs[3],
+                                                           s_out, status), 50, 5)
+            dense = {"single_us": dense_ms * 1e3, "path": dev.dense_path_name(words),
+                     "max_rel_vs_float64": None}
+            y_dense = s_out.download(np.float32).reshape(m, 4096)
+            for b in s_bufs + [s_out, d_x]:
                 b.free()
     finally:
         for b in bufs + [out, status]:
@@ -134,7 +143,10 @@ def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
     ref, _ = oracle.matmul(x_img.codes, x_img.codebook, w_img.codes, w_img.codebook,
                            m, 4096, 4096, 16, 0)
     err = max(max_rel(y[0], ref), float(np.max(np.abs(y - y[0]))) / float(np.max(np.abs(ref))))
-    return {"ms": ms, "single_ms": single_ms, "path": path, "max_rel": err,
+    if dense is not None:
+        exact = x.astype(np.float64) @ w_img.decode().astype(np.float64)
+        dense["max_rel_vs_float64"] = max_rel(y_dense, exact)
+    return {"ms": ms, "single_ms": single_ms, "path": path, "max_rel": err, "dense": dense,
             "gbs": items * W_BYTES / (ms * 1e-3) / 1e9, "x_img": x_img, "w_img": w_img}
 
 
@@ -150,7 +162,7 @@ def bench_prefill(device, dev, steps, warmup):
     x_img = dev.encode(x, vq.fit_codebook(x, group=32), group=32)
     dy = (rng.standard_normal((m, n)) * 0.1).astype(np.float32)
     dy_img = dev.encode(dy, vq.fit_codebook(dy, group=32), group=32)
-    del x, dy
+    del dy
     results = {}
     for name, a, flags, nn in (("forward", x_img, 0, n), ("backward", dy_img, 2, k)):
         kk = k if flags == 0 else n
@@ -192,6 +204,30 @@ def bench_prefill(device, dev, steps, warmup):
                                  "peak": FP16_MFMA_PEAK_TFLOPS,
                                  "frac": ops / (ms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS}
         results[name] = entry
+    # the forward product with X handed over dense (no activation encode)
+    words = (2, m, n, k, 32, 16, 0, 0)
+    bufs = [device.buffer(arr.nbytes) for arr in (x, w_img.codes, w_img.codebook)]
+    for b, arr in zip(bufs, (x, w_img.codes, w_img.codebook)):
+        b.upload(arr)
+    out = device.buffer(m * n * 4)
+    status = device.buffer(4)
+    status.upload(np.zeros(1, np.uint32))
+    try:
+        path = dev.dense_path_name(words)
+        log(f"timing the dense-activation forward: {m}x{n}x{k}, path {path}")
+        ms = timed(device, lambda: dev.run_dense(words, *bufs, out, status), steps, warmup)
+        flags_out = int(status.download(np.uint32)[0])
+        sample = out.download(np.float32).reshape(m, n)[:8]
+    finally:
+        for b in bufs + [out, status]:
+            b.free()
+    if flags_out:
+        raise SystemExit(f"status word {flags_out} after the dense forward launches")
+    ref = x[:8].astype(np.float64) @ w_img.decode().astype(np.float64)
+    flop = 2.0 * m * n * k
+    results["forward_dense_x"] = {
+        "ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "path": path,
+        "max_rel_first_rows": float(np.max(np.abs(sample - ref)) / np.max(np.abs(ref)))}
     return results
 
 
@@ -413,6 +449,10 @@ def main(argv=None) -> int:
         return v
 
     extra = {}
+    if gemv["dense"]:
+        extra["gemv_dense_x"] = {"workload": "config 3 weight, one 1x4096 float32 activation "
+                                             "row handed over dense (ack_vq_matmul_dense)",
+                                 **tidy(gemv["dense"])}
     if prefill:
         extra["prefill"] = {
             "workload": "config 4: X 2048x4096 . W 4096x14336 g32 (forward), dY 2048x14336 . W^T "

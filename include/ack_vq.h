@@ -147,6 +147,24 @@ int32_t ack_vq_adamw_step(const AckDevice* dev, const AckBuffer* b0, const AckBu
                           const AckBuffer* status, const uint8_t* plan, size_t plan_len,
                           uint32_t iterations, uint32_t sample_vectors);
 
+/* Dense-activation product: C = op(X) . op(B) with op 2's plan, geometry and
+ * flags (the 32-byte op-2 block), where X is a dense row-major FP32 array of
+ * m x k values (k x m with flags & 1) instead of a packed image, so the
+ * activations need no lossy encode (the harness encodes them,
+ * src/alelyon_compute_kit/harness.py:140-149). B is packed as in op 2. A
+ * separate entry: op 2 itself is unchanged. Status bit 1 on a nonfinite
+ * value of X, of B's book or of an output. Results: the General path is
+ * bit-identical to the op-2 loop with A read from X; the factorised paths
+ * (m <= 8, m >= 64) agree within FP32 rounding. Enqueued like ack_vq. The
+ * output and status must be distinct and alias no input. No counterpart in
+ * the reference: the next step its survey names for this path. */
+int32_t ack_vq_matmul_dense(const AckDevice* dev, const AckBuffer* x, const AckBuffer* b_codes,
+                            const AckBuffer* b_book, const AckBuffer* out, const AckBuffer* status,
+                            const uint8_t* plan, size_t plan_len);
+
+/* The kernel path ack_vq_matmul_dense takes for an op-2 plan. */
+int32_t ack_vq_dense_path_name(const uint8_t* plan, size_t plan_len, char* out, size_t len);
+
 /* Codebook calibration on the device (fit_codebook, vq.py:182-257) of the m
  * FP32 values in `values`: bounded Lloyd on the strided sample of at most
  * `sample_vectors` complete vectors, farthest-point reseed, and, with a warm

@@ -59,8 +59,10 @@ class ShaderOracle:
         lib.oracle_encode.argtypes = [p, u32, p, u32, p]
         lib.oracle_decode.argtypes = [p, p, u32, u32, p]
         lib.oracle_matmul.argtypes = [p, p, p, p, u32, u32, u32, u32, u32, p]
+        lib.oracle_matmul_dense.argtypes = [p, p, p, u32, u32, u32, u32, u32, p]
         lib.oracle_adamw.argtypes = [p, p, p, u32, u32, p]
-        for fn in (lib.oracle_encode, lib.oracle_decode, lib.oracle_matmul, lib.oracle_adamw):
+        for fn in (lib.oracle_encode, lib.oracle_decode, lib.oracle_matmul,
+                   lib.oracle_matmul_dense, lib.oracle_adamw):
             fn.restype = u32
         self.lib = lib
 
@@ -91,6 +93,16 @@ class ShaderOracle:
         out = np.zeros((m, n), dtype=np.float32)
         status = self.lib.oracle_matmul(pac, pab, pbc, pbb, m, n, k, group, flags,
                                         out.ctypes.data)
+        return out, int(status)
+
+    def matmul_dense(self, x, b_codes, b_book, m, n, k, group, flags):
+        """The dense-activation product: op 2 with A read from dense x."""
+        x, px = self._c(x, np.float32)
+        b_codes, pbc = self._c(b_codes, np.uint32)
+        b_book, pbb = self._c(b_book, np.float32)
+        out = np.zeros((m, n), dtype=np.float32)
+        status = self.lib.oracle_matmul_dense(px, pbc, pbb, m, n, k, group, flags,
+                                              out.ctypes.data)
         return out, int(status)
 
     def adamw(self, codes4, books4, coefficients, m, group, fill=np.nan):

@@ -112,6 +112,31 @@ uint32_t oracle_matmul(const uint32_t* a_codes, const float* a_book, const uint3
   return status;
 }
 
+/* The dense-activation product (libackvq's ack_vq_matmul_dense, an extension
+ * with no reference counterpart): op 2's loop (vq4.comp:165-176) with A read
+ * from a dense FP32 array at the flat index the packed A would be decoded at.
+ * Pinned by the op-2 oracle: with x = decode(A) it must equal oracle_matmul
+ * bit for bit (tests/test_oracle.py). */
+uint32_t oracle_matmul_dense(const float* x, const uint32_t* b_codes, const float* b_book,
+                             uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                             float* out) {
+  uint32_t status = sweep(b_book, 16u * group);
+  for (uint32_t row = 0; row < m; ++row) {
+    for (uint32_t col = 0; col < n; ++col) {
+      float total = 0.0f;
+      for (uint32_t inner = 0; inner < k; ++inner) {
+        uint32_t ai = (flags & 1u) ? inner * m + row : row * k + inner;
+        uint32_t bi = (flags & 2u) ? col * k + inner : inner * n + col;
+        float product = x[ai] * unpack(b_codes, b_book, bi, group);
+        total = total + product;
+        if (!finite_value(product) || !finite_value(total)) status |= 1u;
+      }
+      out[(size_t)row * n + col] = total;
+    }
+  }
+  return status;
+}
+
 /* op 3 (vq4.comp:80-116, :163-164). Elements the shader returns from early
  * are left unwritten in out (3m floats). */
 uint32_t oracle_adamw(const uint32_t* codes4, const float* books4, const float* b2, uint32_t m,

@@ -1,0 +1,126 @@
+"""The dense-activation product (ack_vq_matmul_dense): op 2's plan with the
+activations handed over as dense float32 instead of a vq4 image. The General
+path must equal the oracle's op-2 loop with A read from x bit for bit; the
+factorised paths (m = 1, 2..8, >= 64) must agree with the float64 product
+within 1e-5 max-rel and with the oracle within FP32 rounding."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+
+def _weight(rng, shape, group, scale=0.02):
+    from alelyon_compute_kit import vq
+    w = (rng.standard_normal(shape) * scale).astype(np.float32)
+    return vq.encode(w, vq.fit_codebook(w, group=group), group=group)
+
+
+def _check(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol=1e-5):
+    from alelyon_compute_kit import vq
+    from oracle import vq4_numpy as o
+    m, n, k, flags = vq.VQDevice._dense_geometry(x, w, transpose_a, transpose_b)
+    words = (2, m, n, k, w.group, 16, flags, 0)
+    assert vqdev.dense_path_name(words) == path
+    say("dense matmul", path, m, n, k, w.group, flags)
+    y = vqdev.matmul_dense(x, w, transpose_a=transpose_a, transpose_b=transpose_b)
+    ref, status = oracle.matmul_dense(x, w.codes, w.codebook, m, n, k, w.group, flags)
+    assert status == 0
+    if path == "general":
+        np.testing.assert_array_equal(y.view(np.uint32), ref.view(np.uint32))
+    b = w.decode()
+    exact = o.matmul64(x, b, transpose_a, transpose_b)
+    assert o.max_rel(y, exact) <= tol
+    return y
+
+
+@pytest.mark.parametrize("group", [8, 16, 32])
+@pytest.mark.parametrize("m", [1, 2, 5, 8])
+def test_dense_gemv_paths(vqdev, oracle, group, m):
+    rng = np.random.default_rng(m * 100 + group)
+    k, n = 1536, 8 * group * 40            # 40 word columns: one full tile and a ragged one
+    w = _weight(rng, (k, n), group)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    _check(vqdev, oracle, x, w, False, False, "gemv-pairs" if m == 1 else "gemv-rows")
+
+
+@pytest.mark.parametrize("m,k,group", [(1, 20000, 16), (4, 20000, 8), (3, 700, 32)])
+def test_dense_gemv_split_and_ragged_k(vqdev, oracle, m, k, group):
+    rng = np.random.default_rng(k + m)
+    n = 8 * group * 32
+    w = _weight(rng, (k, n), group)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    _check(vqdev, oracle, x, w, False, False, "gemv-pairs" if m == 1 else "gemv-rows")
+
+
+def test_dense_gemv_transposed_activations(vqdev, oracle):
+    rng = np.random.default_rng(5)
+    w = _weight(rng, (1024, 8 * 16 * 32), 16)
+    x = rng.standard_normal((1024, 6)).astype(np.float32)     # stored k x m
+    _check(vqdev, oracle, x, w, True, False, "gemv-rows")
+
+
+def test_dense_gemv_outliers_and_zero_rows(vqdev, oracle):
+    rng = np.random.default_rng(6)
+    w = _weight(rng, (2048, 8 * 16 * 32), 16)
+    x = rng.standard_normal((4, 2048)).astype(np.float32)
+    x[1] = 0.0                                              # an all-zero row
+    x[2, 7] = 30.0                                          # one outlier sets the scale
+    _check(vqdev, oracle, x, w, False, False, "gemv-rows", tol=2e-5)
+    zero = np.zeros((1, 2048), np.float32)
+    y = vqdev.matmul_dense(zero, w)
+    assert not np.any(y)
+
+
+@pytest.mark.parametrize("group", [8, 16, 32])
+def test_dense_row_bins(vqdev, oracle, group):
+    rng = np.random.default_rng(group + 1)
+    m, k, n = 128, 512, 8 * group * 6
+    w = _weight(rng, (k, n), group)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    _check(vqdev, oracle, x, w, False, False, "row-bins")
+
+
+@pytest.mark.parametrize("m,n,k,ta,tb", [(3, 40, 100, False, True), (20, 64, 48, True, True),
+                                         (17, 130, 96, False, False), (9, 256, 64, True, False)])
+def test_dense_general_is_bit_exact(vqdev, oracle, m, n, k, ta, tb):
+    rng = np.random.default_rng(m + n + k)
+    w = _weight(rng, (n, k) if tb else (k, n), 16)
+    x = rng.standard_normal((k, m) if ta else (m, k)).astype(np.float32)
+    _check(vqdev, oracle, x, w, ta, tb, "general")
+
+
+def test_dense_refusals_and_status(vqdev):
+    from alelyon_compute_kit import ack, vq
+    rng = np.random.default_rng(9)
+    w = _weight(rng, (256, 256), 16)
+    with pytest.raises(ValueError):
+        vqdev.matmul_dense(np.ones((2, 100), np.float32), w)       # inner sizes differ
+    with pytest.raises(ValueError):
+        vqdev.matmul_dense(np.full((1, 256), np.nan, np.float32), w)
+    with pytest.raises(ValueError):
+        vqdev.matmul_dense(np.ones((1, 256), np.float32), w, transpose_b=1)
+    device = vqdev.device
+    x = device.buffer(256 * 4)
+    codes, book = device.buffer(w.codes.nbytes), device.buffer(w.codebook.nbytes)
+    out, status = device.buffer(256 * 4), device.buffer(4)
+    try:
+        xs = np.ones(256, np.float32)
+        xs[3] = np.inf
+        x.upload(xs)
+        codes.upload(w.codes)
+        book.upload(w.codebook)
+        status.upload(np.zeros(1, np.uint32))
+        words = (2, 1, 256, 256, 16, 16, 0, 0)
+        vqdev.run_dense(words, x, codes, book, out, status)
+        assert int(status.download(np.uint32)[0]) & 1
+        with pytest.raises(ack.AckError):
+            vqdev.run_dense(words, x, codes, book, x, status)       # output aliases an input
+        with pytest.raises(ack.AckError):
+            vqdev.run_dense((2, 2, 256, 256, 16, 16, 0, 0), x, codes, book, out, status)
+    finally:
+        for b in (x, codes, book, out, status):
+            b.free()

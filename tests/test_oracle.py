@@ -157,6 +157,35 @@ def test_matmul_status_on_overflow(oracle):
     assert status == 1
 
 
+@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+def test_dense_matmul_reduces_to_op2_on_decoded_activations(oracle, flags):
+    """The dense-activation product's oracle is op 2's loop with A read from x:
+    fed x = decode(A) it must equal the op-2 oracle bit for bit, and a dense x
+    that no image can hold must match the sequential float32 sum."""
+    rng = np.random.default_rng(40 + flags)
+    m, n, k, group = 5, 24, 13, 8
+    a_codes, a_book, b_codes, b_book, a_shape, b_shape = _operands(rng, m, n, k, group, flags)
+    x = _dense(a_codes, a_book, a_shape, group)
+    want, s1 = oracle.matmul(a_codes, a_book, b_codes, b_book, m, n, k, group, flags)
+    got, s2 = oracle.matmul_dense(x, b_codes, b_book, m, n, k, group, flags)
+    assert s1 == s2 == 0
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    x = rng.standard_normal(a_shape).astype(np.float32)
+    got, _ = oracle.matmul_dense(x, b_codes, b_book, m, n, k, group, flags)
+    a = x.T if flags & 1 else x
+    b = _dense(b_codes, b_book, b_shape, group)
+    b = b.T if flags & 2 else b
+    f = np.float32
+    for r in range(m):
+        for c in range(n):
+            t = f(0)
+            for i in range(k):
+                t = f(t + f(a[r, i] * b[i, c]))
+            assert got[r, c].view(np.uint32) == t.view(np.uint32)
+    x[0, 0] = np.inf                            # a nonfinite activation raises bit 1
+    assert oracle.matmul_dense(x, b_codes, b_book, m, n, k, group, flags)[1] == 1
+
+
 def _adamw_f32(w, m, v, g, c):
     f = np.float32
     nm = f(f(c[1] * m) + f(f(f(1) - c[1]) * g))
