@@ -6,7 +6,8 @@ Run in the build container only, where the reference is mounted:
 
 It imports the reference's CPU functions -- ``encode``, ``fit_codebook``,
 ``VQArray``, ``VQAdamW`` (src/alelyon_compute_kit/_kit/python/vq.py) and
-``ExpertBank.initialize_expert`` (_kit/python/expert_bank.py:357-390) -- the
+``ExpertBank`` (_kit/python/expert_bank.py:148-430: ``initialize_expert``
+payloads and the files a short sequence of commits leaves on disk) -- the
 functions no closed form or known-answer test pins bit for bit, and records
 their inputs and outputs as .npz fixtures (no pickles). Nothing under
 /root/reference is needed, read or copied at test time.
@@ -192,12 +193,46 @@ def vqadamw_steps() -> dict:
     return out
 
 
+def bank_files() -> dict:
+    """Every file of a small bank the reference writes: create, three seeded
+    experts (one with zeroed optimizer state), then two committed updates of
+    expert (0, 1) carrying other experts' payloads. Generation ids are random
+    (uuid4), so the history of expert (0, 1)'s generations is recorded too."""
+    with tempfile.TemporaryDirectory() as tmp:
+        root = Path(tmp) / "bank"
+        config = ref_bank.BankConfig(2, 2, ((10, 13), (13, 10), (10, 13)), 8)
+        bank = ref_bank.ExpertBank.create(root, config)
+        history = []
+
+        def generation():
+            text = (root / "expert-0-1.json").read_text()
+            return text.split('"generation":"')[1].split('"')[0]
+
+        bank.initialize_expert(0, 1, seed=3)
+        history.append(generation())
+        bank.initialize_expert(1, 0, seed=5, zero_optimizer_state=True)
+        bank.initialize_expert(1, 1, seed=9)
+        bank.write_expert(0, 1, bank.read_expert(1, 0), updated_count=100, optimizer_step=1)
+        history.append(generation())
+        bank.write_expert(0, 1, bank.read_expert(1, 1), updated_count=17, optimizer_step=4)
+        history.append(generation())
+        stats = ref_bank._json(bank.stats())
+        names = sorted(p.name for p in root.iterdir())
+        blobs = [(root / n).read_bytes() for n in names]
+    offsets = np.cumsum([0] + [len(b) for b in blobs]).astype(np.int64)
+    return {"names": np.array(names), "offsets": offsets,
+            "blob": np.frombuffer(b"".join(blobs), dtype=np.uint8),
+            "history_0_1": np.array(history),
+            "stats": np.frombuffer(stats, dtype=np.uint8)}
+
+
 def main() -> int:
     np.savez_compressed(OUT / "encode_cpu.npz", **encode_cases())
     np.savez_compressed(OUT / "fit_codebook.npz", **fit_cases())
     np.savez_compressed(OUT / "config1.npz", **config1())
     np.savez_compressed(OUT / "expert_payloads.npz", **expert_payloads())
     np.savez_compressed(OUT / "vqadamw_steps.npz", **vqadamw_steps())
+    np.savez_compressed(OUT / "bank_files.npz", **bank_files())
     for p in sorted(OUT.glob("*.npz")):
         print(p.name, p.stat().st_size)
     return 0

@@ -120,6 +120,69 @@ def test_write_counters_generations_and_refusals(tmp_path):
                                                    for t in state.tensors)
 
 
+def _reference_bank():
+    """The files the reference's ExpertBank left after create, three seeded
+    experts and two updates of expert (0, 1) (tests/golden/make_golden.py)."""
+    g = golden("bank_files.npz")
+    blob, off = g["blob"].tobytes(), g["offsets"]
+    files = {str(n): blob[off[i]:off[i + 1]] for i, n in enumerate(g["names"])}
+    return files, [str(h) for h in g["history_0_1"]], g["stats"].tobytes()
+
+
+def test_a_reference_written_bank_opens_and_reads(tmp_path):
+    files, _, stats = _reference_bank()
+    root = tmp_path / "ref"
+    root.mkdir()
+    for name, data in files.items():
+        (root / name).write_bytes(data)
+    bank = expert_bank.ExpertBank.open(root)
+    state = bank.read_expert_state(0, 1)
+    assert (state.optimizer_step, state.revision, state.parameter_update_applications) == \
+        (4, 3, 117)
+    assert state.tensors == bank.read_expert(1, 1)       # the second update carried (1, 1)'s
+    zero = bank.read_expert(1, 0)
+    assert not zero[1].codes.any() and not zero[2].codebook.any()
+    assert expert_bank.canonical_json(bank.stats()) == stats
+
+
+def test_this_writer_leaves_the_reference_files(tmp_path):
+    """The same operations write the same bytes: bank.json, every shard and
+    every pointer, once generation ids (uuid4, random in both) are mapped."""
+    files, history, stats = _reference_bank()
+    root = tmp_path / "ours"
+    bank = expert_bank.ExpertBank.create(
+        root, expert_bank.BankConfig(2, 2, ((10, 13), (13, 10), (10, 13)), 8))
+    ours = []
+
+    def generation(base):
+        return json.loads((root / f"{base}.json").read_text())["generation"]
+
+    bank.initialize_expert(0, 1, seed=3)
+    ours.append(generation("expert-0-1"))
+    bank.initialize_expert(1, 0, seed=5, zero_optimizer_state=True)
+    bank.initialize_expert(1, 1, seed=9)
+    bank.write_expert(0, 1, bank.read_expert(1, 0), updated_count=100, optimizer_step=1)
+    ours.append(generation("expert-0-1"))
+    bank.write_expert(0, 1, bank.read_expert(1, 1), updated_count=17, optimizer_step=4)
+    ours.append(generation("expert-0-1"))
+    rename = dict(zip(ours, history))
+    for base in ("expert-1-0", "expert-1-1"):
+        rename[generation(base)] = json.loads(files[f"{base}.json"])["generation"]
+
+    def mapped(text: str) -> str:
+        for mine, theirs in rename.items():
+            text = text.replace(mine, theirs)
+        return text
+
+    written = {mapped(p.name): p.read_bytes() for p in root.iterdir()}
+    assert sorted(written) == sorted(files)
+    for name, data in written.items():
+        if name.endswith(".json"):
+            data = mapped(data.decode()).encode()
+        assert data == files[name], name
+    assert expert_bank.canonical_json(bank.stats()) == stats
+
+
 def test_a_changed_shard_is_refused(tmp_path):
     bank = _small_bank(tmp_path)
     pointer = json.loads((bank.root / "expert-0-0.json").read_bytes())
