@@ -316,7 +316,9 @@ struct PairAhead {
 // grid: (n tiles, k splits, z); block z serves instances z, z + gridDim.z, ...
 // ks is a multiple of kPairBatchRows. AD: x is dense FP32 in in[0] and in[1]
 // holds the kAmaxParts partial maxima of |x| per instance (k_dense_amax).
-template <int G, bool AD>
+// SW: the slice is one window (ks <= kPairWindow), so the bins are read out
+// once, at the end, and no FP32 accumulator lives through the main loop.
+template <int G, bool AD, bool SW>
 __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint32_t n,
                                                                 uint32_t k, uint32_t ks,
                                                                 float* partial) {
@@ -452,18 +454,19 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
 #pragma unroll
       for (int c = 0; c < kPairSL; ++c) {
         const uint32_t d = pair_dword(16 * (fh * kPairSH + a) + fl * kPairSL + c, fp, fq);
-        acc[a][c] += float(bins[d]);
-        if (clear) bins[d] = 0;
+        acc[a][c] = SW ? float(bins[d]) : acc[a][c] + float(bins[d]);
+        if (!SW && clear) bins[d] = 0;
       }
   };
+  // `tail`: a batch of the peeled last D, the only ones that can be the last
   auto stage = [&](uint32_t (&w)[R], uint32_t b, int32_t (&xs)[R], int32_t (&xn)[R],
-                   __amdgpu_buffer_rsrc_t rs_refill, uint32_t b_refill)
+                   __amdgpu_buffer_rsrc_t rs_refill, uint32_t b_refill, bool tail)
                    __attribute__((always_inline)) {
     asm volatile("" : "+s"(b));  // row arithmetic is redone per batch, not strength-reduced
     const uint32_t done = (b + 1) * BR;
-    const bool last = b + 1 == nbp;
-    const bool restage = k0 + done < kend && k0 + done - xbase >= kPairXRows;
-    const bool wend = done % kPairWindow == 0 || last;
+    const bool last = tail && b + 1 == nbp;
+    const bool restage = !SW && k0 + done < kend && k0 + done - xbase >= kPairXRows;
+    const bool wend = SW ? last : (done % kPairWindow == 0 || last);
     if (!restage && !last) read_x(b + 1, xn);
     if (b < nb) {  // padding batches (past the slice) bin nothing
 #pragma unroll
@@ -559,23 +562,25 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     // the next instance's set-up data moves up; the one after is requested now
     cur = nxt;
     nxt = setup_loads(next + zn < o.count ? next + zn : item);
+    if (!SW) {
 #pragma unroll
-    for (int a = 0; a < kPairSH; ++a)
+      for (int a = 0; a < kPairSH; ++a)
 #pragma unroll
-      for (int c = 0; c < kPairSL; ++c) acc[a][c] = 0.0f;
+        for (int c = 0; c < kPairSL; ++c) acc[a][c] = 0.0f;
+    }
 
     // ---- main loop: all but the last D batches refill from this instance ----
     for (uint32_t b0 = 0; b0 + D < nbp; b0 += D) {
 #pragma unroll
       for (uint32_t d = 0; d < D; d += 2) {
-        stage(buf[d], b0 + d, xa, xb, cur_rs, b0 + d + D);
-        stage(buf[d + 1], b0 + d + 1, xb, xa, cur_rs, b0 + d + 1 + D);
+        stage(buf[d], b0 + d, xa, xb, cur_rs, b0 + d + D, false);
+        stage(buf[d + 1], b0 + d + 1, xb, xa, cur_rs, b0 + d + 1 + D, false);
       }
     }
 #pragma unroll
     for (uint32_t d = 0; d < D; d += 2) {
-      stage(buf[d], nbp - D + d, xa, xb, next_rs, d);
-      stage(buf[d + 1], nbp - D + d + 1, xb, xa, next_rs, d + 1);
+      stage(buf[d], nbp - D + d, xa, xb, next_rs, d, true);
+      stage(buf[d + 1], nbp - D + d + 1, xb, xa, next_rs, d + 1, true);
     }
 
     // ---- finalise: sub-block row/column sums, one exchange, S, outputs ----
@@ -643,21 +648,35 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       const uint32_t groups = (rw - tile * kTileWords) < kTileWords
                                   ? (rw - tile * kTileWords) * 8
                                   : kTileGroups;
-      // thread ft always takes column t = ft % G: its 16 book entries stay in registers
-      const uint32_t t = ft % G;
-      float cb[16];
+      // thread ft always takes columns 4 tc .. 4 tc + 3 (tc = ft % (G / 4)) of its
+      // groups: their 16 x 4 book entries stay in registers, and each S value
+      // read serves four outputs
+      const uint32_t tc = ft % (G / 4);
+      float4 cb[16];
 #pragma unroll
-      for (uint32_t c = 0; c < 16; ++c) cb[c] = bb[c * G + t];
-      float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
+      for (uint32_t c = 0; c < 16; ++c) cb[c] = *reinterpret_cast<const float4*>(bb + c * G + 4 * tc);
+      float* out = item_ptr_mut<float>(o.out, o.stride[4], item) + tile * kTileGroups * G;
+      const bool vec = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
       bool bad = false;
-      for (uint32_t e = ft; e < groups * G; e += kPairThreads) {
-        const uint32_t j = e / G;
+      for (uint32_t e = ft; e < groups * (G / 4); e += kPairThreads) {
+        const uint32_t j = e / (G / 4);
         const float* sj = ss + (j % 8) * kTileWords + j / 8;
-        float y = 0.0f;
+        float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (uint32_t c = 0; c < 16; ++c) y = fmaf(cb[c], sj[c * kTileGroups], y);
-        out[tile * kTileGroups * G + e] = y;
-        bad |= !finite_f32(y);
+        for (uint32_t c = 0; c < 16; ++c) {
+          const float sv_ = sj[c * kTileGroups];
+          y.x = fmaf(cb[c].x, sv_, y.x);
+          y.y = fmaf(cb[c].y, sv_, y.y);
+          y.z = fmaf(cb[c].z, sv_, y.z);
+          y.w = fmaf(cb[c].w, sv_, y.w);
+        }
+        float* oy = out + j * G + 4 * tc;
+        if (vec) {
+          *reinterpret_cast<float4*>(oy) = y;
+        } else {
+          oy[0] = y.x; oy[1] = y.y; oy[2] = y.z; oy[3] = y.w;
+        }
+        bad |= !finite_f32(y.x) || !finite_f32(y.y) || !finite_f32(y.z) || !finite_f32(y.w);
       }
       if (__any(bad) && (ft % warpSize) == 0) atomicOr(o.status, 1u);
     }
@@ -1083,12 +1102,18 @@ hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k
   uint32_t zc = per_z >= 256 ? 1u : 256u / per_z;
   zc = zc < o.count ? zc : o.count;
   const size_t shmem = pairs_shmem(G);
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_pairs<G, AD>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
+  const bool one_window = ks <= kPairWindow;
+  const void* fn = one_window ? reinterpret_cast<const void*>(&k_gemv_pairs<G, AD, true>)
+                              : reinterpret_cast<const void*>(&k_gemv_pairs<G, AD, false>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
   if (e != hipSuccess) return e;
   dim3 grid(tiles, splits, zc);
-  k_gemv_pairs<G, AD><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks,
-                                                        static_cast<float*>(workspace));
+  if (one_window)
+    k_gemv_pairs<G, AD, true><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks,
+                                                                static_cast<float*>(workspace));
+  else
+    k_gemv_pairs<G, AD, false><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks,
+                                                                 static_cast<float*>(workspace));
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || splits == 1) return err;
   dim3 fgrid(tiles * kFinishParts, 1, zc);
