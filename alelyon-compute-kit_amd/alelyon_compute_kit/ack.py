@@ -134,6 +134,8 @@ _SIGNATURES = {
                                                  _c.c_uint32], _c.c_int32),
     "ack_vq_matmul_dense": ([_c.c_void_p] * 6 + [_c.c_void_p, _c.c_size_t], _c.c_int32),
     "ack_vq_dense_path_name": ([_c.c_void_p, _c.c_size_t, _c.c_char_p, _c.c_size_t], _c.c_int32),
+    "ack_buffer_copy": ([_c.c_void_p, _c.c_void_p, _c.c_uint64, _c.c_void_p, _c.c_uint64,
+                         _c.c_uint64], _c.c_int32),
 }
 
 
@@ -224,6 +226,18 @@ class Buffer:
             if rc != ACK_OK:
                 raise _kit_error("download", rc, lib.last_error())
             return out
+
+    def copy_from(self, src: "Buffer", nbytes: int, *, offset: int = 0,
+                  src_offset: int = 0) -> None:
+        """Enqueue a device-to-device copy of ``nbytes`` from ``src``."""
+        with self._device._lock:
+            self._require_live()
+            src._require_live()
+            lib = self._device._lib
+            rc = lib.cdll.ack_buffer_copy(self._device._handle, self._handle, offset,
+                                          src._handle, src_offset, nbytes)
+            if rc != ACK_OK:
+                raise _kit_error("copy", rc, lib.last_error())
 
     def free(self) -> None:
         with self._device._lock:

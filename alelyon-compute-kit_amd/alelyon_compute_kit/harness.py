@@ -15,8 +15,12 @@ bank's moments and step (:203-213), and the same commit (:217-223). Only the
 device differs; the reference's class name is kept as an alias so callers
 that import ``VulkanExpertHarness`` keep working.
 
-Diagnostic reductions (loss, gradient norm) and codebook calibration are CPU
-work here as there.
+Diagnostic reductions (loss, gradient norm) are host float64 work here as
+there. With ``resident=True`` the expert's weight, momentum and variance stay
+on the device between steps (in the fused optimizer step's input layout),
+codebooks are fitted on the device (the same books as the host fit), and only
+activation-sized arrays and the reductions' inputs cross the bus; a step
+commits the same images as the default path, byte for byte.
 """
 from __future__ import annotations
 
@@ -26,6 +30,7 @@ import math
 import os
 import tempfile
 import time
+from contextlib import ExitStack
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -83,19 +88,60 @@ def _positive(value, name: str) -> float:
     return number
 
 
+class _ResidentExpert:
+    """One expert's weight, momentum and variance on the device, laid out as
+    the fused optimizer step reads them: the codes of W, M, V and a gradient
+    slot back to back, then their four books. ``images`` are the host images
+    the buffers hold."""
+
+    def __init__(self, device: ack.Device, images):
+        w = images[0]
+        self.words = w.layout["code_bytes"] // 4
+        self.book = vq.ENTRIES * w.group
+        self.codes4 = device.buffer(4 * self.words * 4)
+        try:
+            self.books4 = device.buffer(4 * self.book * 4)
+        except BaseException:
+            self.codes4.free()
+            raise
+        self.load(images)
+
+    def load(self, images) -> None:
+        codes = np.zeros(4 * self.words, np.uint32)
+        books = np.zeros(4 * self.book, np.float32)
+        for i, t in enumerate(images[:3]):
+            codes[i * self.words:(i + 1) * self.words] = t.codes
+            books[i * self.book:(i + 1) * self.book] = t.codebook.reshape(-1)
+        self.codes4.upload(codes)
+        self.books4.upload(books)
+        self.images = tuple(images[:3])
+
+    def holds(self, images) -> bool:
+        return len(images) >= 3 and all(a == b for a, b in zip(self.images, images[:3]))
+
+    def free(self) -> None:
+        self.codes4.free()
+        self.books4.free()
+
+
 class ExpertHarness:
     """One durable linear expert driven through the vq4 kernels.
 
     ``backend`` may be any object with the ``VQDevice`` methods (host-only
     tests inject fakes). Without one, the harness opens an ``ack.Device``
-    itself -- importing this module opens nothing.
+    itself -- importing this module opens nothing. ``resident=True`` (a
+    ``VQDevice`` backend only) keeps each expert's optimizer state on the
+    device between steps and fits codebooks there.
     """
 
-    def __init__(self, bank: expert_bank.ExpertBank, *, backend=None, device=None):
+    def __init__(self, bank: expert_bank.ExpertBank, *, backend=None, device=None,
+                 resident: bool = False):
         if not isinstance(bank, expert_bank.ExpertBank):
             raise HarnessError("bank must be an ExpertBank")
         if backend is not None and device is not None:
             raise HarnessError("supply backend or device, not both")
+        if not isinstance(resident, bool):
+            raise HarnessError("resident must be a bool")
         self.bank = bank
         self._device = device
         self._owns_device = False
@@ -104,12 +150,17 @@ class ExpertHarness:
                 self._device = ack.Device()
                 self._owns_device = True
             backend = vq.VQDevice(self._device)
+        if resident and not isinstance(backend, vq.VQDevice):
+            raise HarnessError("a resident harness needs a VQDevice backend")
         self.backend = backend
+        self.resident = resident
+        self._residents: dict[tuple[int, int], _ResidentExpert] = {}
 
     @classmethod
-    def open(cls, root, *, device=None, backend=None) -> "ExpertHarness":
+    def open(cls, root, *, device=None, backend=None, resident=False) -> "ExpertHarness":
         """Open an existing bank; creates and initializes nothing."""
-        return cls(expert_bank.ExpertBank.open(root), backend=backend, device=device)
+        return cls(expert_bank.ExpertBank.open(root), backend=backend, device=device,
+                   resident=resident)
 
     def __enter__(self) -> "ExpertHarness":
         return self
@@ -118,6 +169,9 @@ class ExpertHarness:
         self.close()
 
     def close(self) -> None:
+        for res in self._residents.values():
+            res.free()
+        self._residents.clear()
         if self._owns_device and self._device is not None:
             self._device.close()
             self._device = None
@@ -143,13 +197,132 @@ class ExpertHarness:
             sample = np.pad(values.reshape(-1), (0, group - values.size))
         return self.backend.encode(values, vq.fit_codebook(sample, group=group), group=group)
 
+    # -- the resident path ---------------------------------------------------------
+    def _resident_for(self, layer: int, expert: int, state) -> _ResidentExpert:
+        res = self._residents.get((layer, expert))
+        if res is not None and res.holds(state.tensors):
+            return res
+        if res is not None:            # the bank moved on under us: reload
+            res.load(state.tensors)
+            return res
+        res = _ResidentExpert(self.backend.device, state.tensors)
+        self._residents[(layer, expert)] = res
+        return res
+
+    def _device_image(self, values: np.ndarray, group: int, buf, status):
+        """fit_codebook and encode on the device: the image ``_encode`` makes
+        (the same tiny-batch padding for the fit), left in device buffers."""
+        flat = values.reshape(-1)
+        sample = flat if flat.size >= group else np.pad(flat, (0, group - flat.size))
+        sample = np.ascontiguousarray(sample, dtype=np.float32)
+        vals = buf(sample.nbytes)
+        vals.upload(sample)
+        book = buf(vq.ENTRIES * group * 4)
+        self.backend.fit_resident(vals, sample.size, book, status, group=group)
+        codes = buf(vq.storage_layout(values.shape, group)["code_bytes"])
+        self.backend.run((0, flat.size, 1, 1, group, vq.ENTRIES, 0, 0), [vals, book], codes,
+                         status)
+        return codes, book
+
+    @staticmethod
+    def _checked(status) -> None:
+        flags = int(status.download(np.uint32)[0])
+        if flags:
+            raise HarnessError(f"expert device arithmetic refused: status={flags}")
+
+    def _forward_resident(self, x: np.ndarray, weight, res: _ResidentExpert) -> np.ndarray:
+        device, group = self.backend.device, weight.group
+        m, k = x.shape
+        n = weight.shape[1]
+        with ExitStack() as cleanup:
+            def buf(nbytes):
+                b = device.buffer(nbytes)
+                cleanup.callback(b.free)
+                return b
+            status = buf(4)
+            status.upload(np.zeros(1, np.uint32))
+            xc, xb = self._device_image(x, group, buf, status)
+            y = buf(m * n * 4)
+            self.backend.run((2, m, n, k, group, vq.ENTRIES, 0, 0),
+                             [xc, xb, res.codes4, res.books4], y, status)
+            self._checked(status)
+            return y.download(np.float32).reshape(m, n)
+
+    def _step_resident(self, x, target, state, res: _ResidentExpert, lr, beta1, beta2, eps,
+                       weight_decay, max_grad_norm):
+        """The train_step flow below on resident state; returns (loss, norm,
+        scale, new images, report bytes, input/activation/gradient layouts)."""
+        device = self.backend.device
+        weight = state.tensors[0]
+        group = weight.group
+        m, k = x.shape
+        n = weight.shape[1]
+        with ExitStack() as cleanup:
+            def buf(nbytes):
+                b = device.buffer(nbytes)
+                cleanup.callback(b.free)
+                return b
+            status = buf(4)
+            status.upload(np.zeros(1, np.uint32))
+            xc, xb = self._device_image(x, group, buf, status)
+            tc, tb = self._device_image(target, group, buf, status)
+            y, t_dec = buf(m * n * 4), buf(m * n * 4)
+            self.backend.run((2, m, n, k, group, vq.ENTRIES, 0, 0),
+                             [xc, xb, res.codes4, res.books4], y, status)
+            self.backend.run((1, m * n, 1, 1, group, vq.ENTRIES, 0, 0), [tc, tb], t_dec, status)
+            self._checked(status)
+            residual = y.download(np.float32).reshape(m, n) - \
+                t_dec.download(np.float32).reshape(m, n)
+            loss = float(np.mean(np.square(residual, dtype=np.float64)))
+            if not math.isfinite(loss):
+                raise HarnessError("expert loss is nonfinite")
+            residual *= np.float32(2.0 / residual.size)
+            rc, rb = self._device_image(residual, group, buf, status)
+            grad = buf(k * n * 4)
+            self.backend.run((2, k, n, m, group, vq.ENTRIES, 1, 0), [xc, xb, rc, rb], grad,
+                             status)
+            self._checked(status)
+            gradient = grad.download(np.float32).reshape(k, n)
+            norm = float(np.linalg.norm(gradient.astype(np.float64)))
+            if not math.isfinite(norm):
+                raise HarnessError("expert gradient norm is nonfinite")
+            scale = min(1.0, max_grad_norm / (norm + 1e-6))
+            gradient *= np.float32(scale)
+            gc, gb = self._device_image(gradient, group, buf, status)
+            res.codes4.copy_from(gc, res.words * 4, offset=3 * res.words * 4)
+            res.books4.copy_from(gb, res.book * 4, offset=3 * res.book * 4)
+            try:
+                coeff = vq.VQDevice.adamw_coefficients(lr, beta1, beta2, eps, weight_decay,
+                                                       state.optimizer_step + 1)
+            except ValueError as exc:
+                raise HarnessError(f"expert optimizer refused the update: {exc}") from exc
+            cb = buf(coeff.nbytes)
+            cb.upload(coeff)
+            out_codes, out_books = buf(3 * res.words * 4), buf(3 * res.book * 4)
+            changed = buf(4)
+            self.backend.adamw_step_resident(res.codes4, res.books4, cb, out_codes, out_books,
+                                             changed, status,
+                                             count=weight.layout["elements"], group=group)
+            self._checked(status)
+            codes = out_codes.download(np.uint32).reshape(3, res.words)
+            books = out_books.download(np.float32).reshape(3, vq.ENTRIES, group)
+            images = tuple(vq.VQArray(weight.shape, group, codes[i], books[i]) for i in range(3))
+            res.codes4.copy_from(out_codes, 3 * res.words * 4)
+            res.books4.copy_from(out_books, 3 * res.book * 4)
+            res.images = images
+        layouts = tuple(vq.storage_layout(a.shape, group) for a in (x, target, gradient))
+        return loss, norm, scale, images, layouts
+
     # -- the driver surface ------------------------------------------------------
     def forward(self, inputs, *, layer: int = 0, expert: int = 0) -> np.ndarray:
         """``inputs @ weight`` through the packed product."""
         x = _matrix(inputs, "inputs")
-        weight = self._state(layer, expert).tensors[0]
+        state = self._state(layer, expert)
+        weight = state.tensors[0]
         if x.shape[1] != weight.shape[0]:
             raise HarnessError(f"inputs have width {x.shape[1]}, expert expects {weight.shape[0]}")
+        if self.resident:
+            return self._forward_resident(x, weight, self._resident_for(layer, expert, state))
         return self.backend.matmul(self._encode(x, weight.group), weight)
 
     def train_step(self, inputs, targets, *, layer: int = 0, expert: int = 0,
@@ -167,6 +340,19 @@ class ExpertHarness:
         max_grad_norm = _positive(max_grad_norm, "max_grad_norm")
         group = weight.group
         t0 = time.perf_counter()
+        if self.resident:
+            res = self._resident_for(layer, expert, state)
+            try:
+                loss, norm, scale, images, layouts = self._step_resident(
+                    x, target, state, res, lr, beta1, beta2, eps, weight_decay, max_grad_norm)
+            except (ValueError, ack.AckError) as exc:
+                # a failed step leaves the device copy unknown: reload next time
+                self._residents.pop((layer, expert)).free()
+                if isinstance(exc, HarnessError):
+                    raise
+                raise HarnessError(f"expert step failed on the device: {exc}") from exc
+            return self._commit(layer, expert, weight, images, state.optimizer_step + 1, loss,
+                                norm, scale, t0, layouts)
         x_img = self._encode(x, group)
         t_img = self._encode(target, group)
         residual = self.backend.matmul(x_img, weight) - self.backend.decode(t_img)
@@ -190,22 +376,30 @@ class ExpertHarness:
             update = opt.step(g_img)
         except (TypeError, ValueError, ack.AckError) as exc:
             raise HarnessError(f"expert optimizer refused the update: {exc}") from exc
+        return self._commit(layer, expert, weight, (opt.weight, opt.momentum, opt.variance),
+                            opt.steps, loss, norm, scale, t0,
+                            (x_img.layout, t_img.layout, g_img.layout),
+                            update["persistent_state_bytes"])
+
+    def _commit(self, layer, expert, weight, images, optimizer_step, loss, norm, scale, t0,
+                layouts, state_bytes=None) -> ExpertStep:
         try:
-            receipt = self.bank.write_expert(
-                layer, expert, (opt.weight, opt.momentum, opt.variance),
-                updated_count=weight.layout["elements"], optimizer_step=opt.steps)
+            receipt = self.bank.write_expert(layer, expert, images,
+                                             updated_count=weight.layout["elements"],
+                                             optimizer_step=optimizer_step)
         except expert_bank.ExpertBankError as exc:
             raise HarnessError(f"expert update was not committed: {exc}") from exc
         elapsed = time.perf_counter() - t0
         if not (math.isfinite(elapsed) and elapsed > 0):
             raise HarnessError("expert step elapsed time is invalid")
-        return ExpertStep(layer=layer, expert=expert, optimizer_step=opt.steps,
+        if state_bytes is None:
+            state_bytes = sum(a.layout["serialized_bytes"] for a in images)
+        return ExpertStep(layer=layer, expert=expert, optimizer_step=optimizer_step,
                           revision=receipt["revision"], loss=loss,
                           gradient_norm_before_clip=norm, clipped=scale < 1.0,
-                          elapsed_seconds=elapsed,
-                          persistent_state_bytes=update["persistent_state_bytes"],
-                          input_layout=x_img.layout, activation_layout=t_img.layout,
-                          gradient_layout=g_img.layout)
+                          elapsed_seconds=elapsed, persistent_state_bytes=state_bytes,
+                          input_layout=layouts[0], activation_layout=layouts[1],
+                          gradient_layout=layouts[2])
 
     def train(self, inputs, targets, *, steps: int = 1, **kwargs) -> tuple[ExpertStep, ...]:
         """Bounded sequential steps, each committed before the next."""
@@ -261,12 +455,14 @@ def main(argv=None) -> int:
     parser.add_argument("--lr", type=float, default=1e-3)
     parser.add_argument("--max-grad-norm", type=float, default=1.0)
     parser.add_argument("--device", action="store_true", help="explicitly open the GPU")
+    parser.add_argument("--resident", action="store_true",
+                        help="keep the optimizer state on the device between steps")
     parser.add_argument("--force", action="store_true")
     args = parser.parse_args(argv)
     if not args.device:
         parser.error("--device is required; execution is never implicit")
     inputs = _load_matrix(args.input, "input")
-    with ExpertHarness.open(args.bank) as harness:
+    with ExpertHarness.open(args.bank, resident=args.resident) as harness:
         if args.target is None:
             result = harness.forward(inputs, layer=args.layer, expert=args.expert)
             report = {"mode": "forward", "shape": list(result.shape)}

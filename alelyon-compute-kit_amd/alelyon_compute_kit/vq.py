@@ -462,24 +462,31 @@ class VQDevice:
         states = (weight, momentum, variance, gradient)
         if any(s.shape != weight.shape or s.group != weight.group for s in states):
             raise ValueError("vq AdamW states must have identical shapes and groups")
+        count = weight.layout["elements"]
+        if count * 3 > MAX_ELEMENTS:
+            raise ValueError("vq AdamW active scratch exceeds element bound")
+        coefficients = VQDevice.adamw_coefficients(lr, beta1, beta2, eps, weight_decay, step)
+        codes = np.concatenate([s.codes for s in states])
+        books = np.concatenate([s.codebook.reshape(-1) for s in states])
+        return count, codes, books, coefficients
+
+    @staticmethod
+    def adamw_coefficients(lr, beta1, beta2, eps, weight_decay, step) -> np.ndarray:
+        """Op 3's seven float32 coefficients (vq.py:348-360), with the same
+        refusals."""
         step = _integer(step, "step", 1, 1 << 53)
         values = (lr, beta1, beta2, eps, weight_decay)
         if any(isinstance(x, (bool, np.bool_)) or not math.isfinite(float(x)) for x in values):
             raise ValueError("vq AdamW coefficients must be finite numbers")
         if lr < 0 or not 0 <= beta1 < 1 or not 0 <= beta2 < 1 or eps <= 0 or weight_decay < 0:
             raise ValueError("vq AdamW coefficients outside their domains")
-        count = weight.layout["elements"]
-        if count * 3 > MAX_ELEMENTS:
-            raise ValueError("vq AdamW active scratch exceeds element bound")
         # Bias corrections in Python float64, then rounded to float32 (vq.py:357-358).
         coefficients = np.array([lr, beta1, beta2, eps, weight_decay,
                                  1 - beta1 ** step, 1 - beta2 ** step], dtype=np.float32)
         if (not np.isfinite(coefficients).all() or coefficients[3] <= 0
                 or (coefficients[5:] <= 0).any()):
             raise ValueError("vq AdamW coefficients are not representable in float32")
-        codes = np.concatenate([s.codes for s in states])
-        books = np.concatenate([s.codebook.reshape(-1) for s in states])
-        return count, codes, books, coefficients
+        return coefficients
 
     def adamw(self, weight: VQArray, momentum: VQArray, variance: VQArray,
               gradient: VQArray, *, lr: float, beta1: float, beta2: float,
@@ -589,7 +596,7 @@ class VQAdamW:
                 self.weight, self.momentum, self.variance, gradient, **kwargs)
             words = self.weight.layout["code_bytes"] + ENTRIES * self.weight.group * 4
             native_bytes = 3 * words + 4
-            calibration = "native float64 fit on the strided sample; device keep pass"
+            calibration = "device float64 fit on the strided sample (the host fit's books)"
         else:
             scratch = self.backend.adamw(self.weight, self.momentum, self.variance, gradient,
                                          **kwargs)

@@ -477,6 +477,32 @@ int32_t ack_download(const AckDevice* handle, const AckBuffer* buf, uint8_t* dat
   return ACK_OK;
 }
 
+int32_t ack_buffer_copy(const AckDevice* handle, const AckBuffer* dst, uint64_t dst_offset,
+                        const AckBuffer* src, uint64_t src_offset, uint64_t bytes) {
+  std::shared_ptr<Device> dev;
+  std::unique_lock<std::mutex> lock;
+  if (int32_t rc = enter(handle, &dev, &lock)) return rc;
+  BufferRec* d = nullptr;
+  BufferRec* s = nullptr;
+  if (int32_t rc = lookup_buffer(*dev, dst, &d)) return rc;
+  if (int32_t rc = lookup_buffer(*dev, src, &s)) return rc;
+  if (dst_offset > d->bytes || bytes > d->bytes - dst_offset || src_offset > s->bytes ||
+      bytes > s->bytes - src_offset) {
+    set_error("copy of " + std::to_string(bytes) + " bytes outside a buffer");
+    return ACK_ERR_SIZE;
+  }
+  if (d->id == s->id && dst_offset < src_offset + bytes && src_offset < dst_offset + bytes) {
+    set_error("copy ranges overlap within one buffer");
+    return ACK_ERR_SHAPE;
+  }
+  if (bytes == 0) return ACK_OK;
+  hipError_t e = hipMemcpyAsync(static_cast<char*>(d->ptr) + dst_offset,
+                                static_cast<const char*>(s->ptr) + src_offset, bytes,
+                                hipMemcpyDeviceToDevice, dev->stream);
+  if (e != hipSuccess) return hip_failure(*dev, "copy", e, true);
+  return ACK_OK;
+}
+
 int32_t ack_sync(const AckDevice* handle) {
   std::shared_ptr<Device> dev;
   std::unique_lock<std::mutex> lock;

@@ -337,6 +337,41 @@ def bench_config5(device, dev, steps, warmup):
     return out
 
 
+def bench_harness(device, dev, steps=3):
+    """ExpertHarness.train_step on one expert, default (images uploaded per
+    call, host codebook fits) against resident (optimizer state kept on the
+    device, device fits): seconds per committed step, end to end."""
+    import tempfile
+    from alelyon_compute_kit import expert_bank, harness
+    out = {}
+    for name, shape, group, batch in (("config2", (128, 128), 16, 32),
+                                      ("w4096", (4096, 4096), 16, 32)):
+        rng = np.random.default_rng(21)
+        x = rng.standard_normal((batch, shape[0])).astype(np.float32)
+        t = (rng.standard_normal((batch, shape[1])) * 0.1).astype(np.float32)
+        entry = {"expert": f"{shape[0]}x{shape[1]} g{group}, batch {batch}"}
+        images = {}
+        for mode in ("default", "resident"):
+            with tempfile.TemporaryDirectory() as tmp:
+                bank = expert_bank.ExpertBank.create(
+                    Path(tmp) / "bank", expert_bank.BankConfig(1, 1, (shape,) * 3, group))
+                bank.initialize_expert(0, 0, seed=7, zero_optimizer_state=True)
+                h = harness.ExpertHarness(bank, backend=dev, resident=(mode == "resident"))
+                try:
+                    h.train_step(x, t)                       # warm-up (and first upload)
+                    t0 = time.perf_counter()
+                    for _ in range(steps):
+                        h.train_step(x, t)
+                    entry[f"{mode}_s_per_step"] = (time.perf_counter() - t0) / steps
+                    images[mode] = [a.to_bytes() for a in bank.read_expert(0, 0)]
+                finally:
+                    h.close()
+        entry["identical_commits"] = images["default"] == images["resident"]
+        out[name] = entry
+        log(f"harness {name}: {entry}")
+    return out
+
+
 def cpu_baseline(x_img, w_img, budget_s=10.0):
     """The oracle's numpy CPU path for config 3: decode + matmul per matrix."""
     from oracle import vq4_numpy as o
@@ -410,12 +445,14 @@ def main(argv=None) -> int:
                                                               1)
         wide = {}
         c5 = None
+        hstep = None
         if not args.no_extra:
             for m in (4, 8):
                 r = bench_gemv(device, dev, args.items, max(3, args.steps // 2), 1, m=m,
                                single=False)
                 wide[m] = r
             c5 = bench_config5(device, dev, max(3, args.steps // 4), 1)
+            hstep = bench_harness(device, dev)
     gbs = args.items * W_BYTES / (gemv["ms"] * 1e-3) / 1e9
     line = {
         "metric": "vq4 packed matmul: packed-weight GB/s (% HBM peak) at M=1; TFLOP/s at M=2048",
@@ -473,6 +510,10 @@ def main(argv=None) -> int:
         extra["config5"] = {"workload": "config 5: 8192x8192 row-normalised N(0,1) weight, "
                                         "group 8; N(0,1e-3) gradient",
                             **tidy(c5)}
+    if hstep:
+        extra["harness_step"] = {"workload": "ExpertHarness.train_step (MSE, clip 1.0, fused "
+                                             "VQAdamW, bank commit), seconds per step",
+                                 **tidy(hstep)}
     if extra:
         line["extra"] = extra
     if not args.no_cpu:

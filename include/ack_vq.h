@@ -185,6 +185,14 @@ int32_t ack_vq_fit_codebook(const AckDevice* dev, const AckBuffer* values, const
  * milliseconds to *ms_out. */
 int32_t ack_stream_timer(const AckDevice* dev, uint32_t phase, float* ms_out);
 
+/* Device-to-device copy of `bytes` from src + src_offset to dst + dst_offset,
+ * enqueued on the device stream. Ranges must lie inside their buffers and
+ * must not overlap. For callers that keep images resident and move one
+ * between the slots of a multi-image buffer (the resident harness places the
+ * gradient image into the fused optimizer step's input). */
+int32_t ack_buffer_copy(const AckDevice* dev, const AckBuffer* dst, uint64_t dst_offset,
+                        const AckBuffer* src, uint64_t src_offset, uint64_t bytes);
+
 /* Wait for every operation enqueued on the device. */
 int32_t ack_sync(const AckDevice* dev);
 

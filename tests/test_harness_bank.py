@@ -314,3 +314,51 @@ def test_config2_chain_and_clipped_step_match_the_oracle(vqdev):
         for sa, sb in ((opt_a.weight, opt_b.weight), (opt_a.momentum, opt_b.momentum),
                        (opt_a.variance, opt_b.variance)):
             assert sa.to_bytes() == sb.to_bytes()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,group,batch", [((128, 128), 16, 32), ((512, 384), 8, 64),
+                                               ((96, 256), 32, 3)])
+def test_resident_harness_commits_the_default_images(tmp_path, vqdev, shape, group, batch):
+    """The resident harness (optimizer state kept on the device, codebooks
+    fitted there) commits byte-identical generations to the default GPU
+    harness over three steps, the middle one clipped; a write by another
+    harness in between is picked up."""
+    from gpu_util import say
+    a_bank, b_bank = _twin_banks(tmp_path, (shape,) * 3, group, 11, True)
+    rng = np.random.default_rng(shape[0] + batch)
+    x = rng.standard_normal((batch, shape[0])).astype(np.float32)
+    t = (rng.standard_normal((batch, shape[1])) * 0.1).astype(np.float32)
+    say("resident harness", shape, group, batch)
+    res = harness.ExpertHarness(a_bank, backend=vqdev, resident=True)
+    plain = harness.ExpertHarness(b_bank, backend=vqdev)
+    try:
+        for norm in (10.0, 1e-3, 10.0):
+            a = res.train_step(x, t, lr=1e-3, beta1=0.9, beta2=0.999, max_grad_norm=norm)
+            b = plain.train_step(x, t, lr=1e-3, beta1=0.9, beta2=0.999, max_grad_norm=norm)
+            da, db = a.to_dict(), b.to_dict()
+            da.pop("elapsed_seconds"), db.pop("elapsed_seconds")
+            assert da == db
+            for ta, tb in zip(a_bank.read_expert(0, 0), b_bank.read_expert(0, 0)):
+                assert ta.to_bytes() == tb.to_bytes()
+        np.testing.assert_array_equal(res.forward(x), plain.forward(x))
+        # another writer commits to the resident expert: the next step reloads
+        other = harness.ExpertHarness(a_bank, backend=vqdev)
+        other.train_step(x, t, lr=1e-3)
+        plain.train_step(x, t, lr=1e-3)
+        a = res.train_step(x, t, lr=1e-3)
+        b = plain.train_step(x, t, lr=1e-3)
+        assert a.revision == b.revision == 6
+        for ta, tb in zip(a_bank.read_expert(0, 0), b_bank.read_expert(0, 0)):
+            assert ta.to_bytes() == tb.to_bytes()
+    finally:
+        res.close()
+
+
+def test_resident_harness_needs_a_device_backend(tmp_path):
+    bank = expert_bank.ExpertBank.create(
+        tmp_path / "r", expert_bank.BankConfig(1, 1, ((4, 3), (4, 3), (4, 3)), 8))
+    with pytest.raises(harness.HarnessError, match="VQDevice"):
+        harness.ExpertHarness(bank, backend=HostBackend(), resident=True)
+    with pytest.raises(harness.HarnessError, match="bool"):
+        harness.ExpertHarness(bank, backend=HostBackend(), resident=1)
