@@ -152,7 +152,17 @@ __global__ __launch_bounds__(kGThreads) void k_matmul_general(Operands o, uint32
 // before an int32 sum could overflow.
 constexpr int kTileWords = 32;
 constexpr int kTileGroups = kTileWords * 8;
-constexpr uint32_t kGemvMaxM = 8;
+constexpr uint32_t kGemvMaxM = 8;    // rows of A one GEMV launch bins
+constexpr uint32_t kRowsMaxM = 64;   // taller A runs GemvRows in chunks of kGemvMaxM rows
+// ... when B is large enough (n * k elements) that the general kernel's few
+// output tiles would leave the chip idle; smaller products keep the general
+// kernel, which reproduces the shader's sums bit for bit.
+constexpr uint64_t kRowsChunkMinWeight = 1ull << 20;
+
+bool rows_apply(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags) {
+  if ((flags & 2u) != 0 || n % (8 * group) != 0) return false;
+  return m <= kGemvMaxM || (m <= kRowsMaxM && uint64_t(n) * k >= kRowsChunkMinWeight);
+}
 
 typedef __attribute__((address_space(3))) int32_t lds_i32;
 
@@ -739,17 +749,18 @@ __device__ __forceinline__ void lds_add64(uint32_t byte_addr, int64_t v) {
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Words of A one slice needs: per row of A (flags 0) or one run (flags 1).
+// Words of A one slice needs: per row of A (flags 0) or one run over all
+// `mall` rows of A (flags 1, where the rows interleave along k).
 struct RowAWords {
   uint32_t per_row;   // words reserved per row (flags 0)
   uint32_t total;     // words staged
 };
 
-__host__ __device__ inline RowAWords row_a_words(uint32_t m, uint32_t ks, uint32_t group,
-                                                 uint32_t flags) {
+__host__ __device__ inline RowAWords row_a_words(uint32_t m, uint32_t mall, uint32_t ks,
+                                                 uint32_t group, uint32_t flags) {
   RowAWords w;
   w.per_row = ks / (8 * group) + 2;
-  w.total = (flags & 1u) ? ks * m / (8 * group) + 2 : m * w.per_row;
+  w.total = (flags & 1u) ? ks * mall / (8 * group) + 2 : m * w.per_row;
   return w;
 }
 
@@ -759,10 +770,13 @@ struct RowAhead {
 };
 
 // AD: A is dense FP32 in in[0]; in[1] holds the partial maxima of |x|.
+// The launch bins rows r0 .. r0 + m - 1 of A's `mall` rows (outputs are
+// written from o.out, which the caller offsets to row r0).
 template <int G, int MP, bool AD>
 __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32_t m, uint32_t n,
                                                               uint32_t k, uint32_t flags,
-                                                              uint32_t ks, float* partial) {
+                                                              uint32_t ks, float* partial,
+                                                              uint32_t r0, uint32_t mall) {
   constexpr uint32_t R = kRowR, D = kRowD, BR = kRowBatchRows;
   constexpr uint32_t kBins64 = 8 * 16 * MP * kTileWords;
   constexpr int kPer = kBins64 / kRowThreads;     // 64-bit bins per thread
@@ -796,8 +810,8 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
   const uint32_t lane_row = (wave * 2 + half) * R;
   const uint32_t col = (tile * kTileWords + q < rw) ? tile * kTileWords + q : rw - 1;
   const uint32_t q8 = q * 8;
-  const RowAWords awn = row_a_words(m, ks, G, flags);
-  const uint32_t a_vec_elems = m * k;  // A's flat extent
+  const RowAWords awn = row_a_words(m, mall, ks, G, flags);
+  const uint32_t a_vec_elems = mall * k;  // A's flat extent
 
   auto opaque = [](uint32_t v) {
     asm volatile("" : "+v"(v));
@@ -805,7 +819,7 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
   };
   // first A word staged for row r (flags 0) or for the slice (flags 1)
   auto a_base = [&](uint32_t r) {
-    return (flags & 1u) ? (k0 * m / G) >> 3 : ((r * k + k0) / G) >> 3;
+    return (flags & 1u) ? (k0 * mall / G) >> 3 : (((r0 + r) * k + k0) / G) >> 3;
   };
   auto setup_loads = [&](uint32_t item) {
     const uint32_t lt = opaque(tid);
@@ -855,7 +869,7 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
 
   // one quantised activation of A
   auto x_of = [&](uint32_t r, uint32_t kk) -> int32_t {
-    const uint32_t flat = (flags & 1u) ? kk * m + r : r * k + kk;
+    const uint32_t flat = (flags & 1u) ? kk * mall + r0 + r : (r0 + r) * k + kk;
     if (AD) {
       const float f = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(x_rs, flat * 4u, 0, 0)));
       return int32_t(fminf(rintf(ldexpf(f, shift)), 524287.0f));
@@ -971,7 +985,7 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (!AD && st + j * kRowThreads < kRowAWords) aw[st + j * kRowThreads] = cur.w[j];
-    if (AD) x_rs = words_rsrc(item_ptr<float>(o.in[0], o.stride[0], item), m * k * 4u);
+    if (AD) x_rs = words_rsrc(item_ptr<float>(o.in[0], o.stride[0], item), mall * k * 4u);
 #pragma unroll
     for (int i = 0; i < kPer; ++i) bins[st + i * kRowThreads] = 0;
     __syncthreads();
@@ -1124,12 +1138,12 @@ hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k
 
 // Slices of k for GemvRows: gemv_splits' count in whole batches, and short
 // enough that one slice's A words fit the staging area.
-void rows_slices(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
-                 uint32_t count, uint32_t* ks, uint32_t* splits) {
+void rows_slices(uint32_t m, uint32_t mall, uint32_t n, uint32_t k, uint32_t group,
+                 uint32_t flags, uint32_t count, uint32_t* ks, uint32_t* splits) {
   const uint32_t want = gemv_splits(n, k, group, count);
   uint32_t per = (k + want - 1) / want;
   per = (per + kRowBatchRows - 1) / kRowBatchRows * kRowBatchRows;
-  while (per > kRowBatchRows && row_a_words(m, per, group, flags).total > kRowAWords)
+  while (per > kRowBatchRows && row_a_words(m, mall, per, group, flags).total > kRowAWords)
     per = (per / 2 + kRowBatchRows - 1) / kRowBatchRows * kRowBatchRows;
   *ks = per;
   *splits = (k + per - 1) / per;
@@ -1137,10 +1151,10 @@ void rows_slices(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t fl
 
 template <int G, int MP, bool AD>
 hipError_t launch_rows_mp(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
-                          uint32_t flags, void* workspace) {
+                          uint32_t flags, void* workspace, uint32_t r0, uint32_t mall) {
   const uint32_t tiles = (n / (8 * G) + kTileWords - 1) / kTileWords;
   uint32_t ks, splits;
-  rows_slices(m, n, k, G, flags, o.count, &ks, &splits);
+  rows_slices(m, mall, n, k, G, flags, o.count, &ks, &splits);
   const uint32_t per_z = tiles * splits;
   uint32_t zc = per_z >= 256 ? 1u : 256u / per_z;
   zc = zc < o.count ? zc : o.count;
@@ -1148,34 +1162,48 @@ hipError_t launch_rows_mp(hipStream_t s, const Operands& o, uint32_t m, uint32_t
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_rows<G, MP, AD>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
   if (e != hipSuccess) return e;
+  Operands oc = o;  // this chunk's outputs start at row r0
+  oc.out = static_cast<char*>(o.out) + uint64_t(r0) * n * sizeof(float);
   dim3 grid(tiles, splits, zc);
-  k_gemv_rows<G, MP, AD><<<grid, kRowThreads, shmem, s>>>(o, m, n, k, flags, ks,
-                                                          static_cast<float*>(workspace));
+  k_gemv_rows<G, MP, AD><<<grid, kRowThreads, shmem, s>>>(oc, m, n, k, flags, ks,
+                                                          static_cast<float*>(workspace), r0,
+                                                          mall);
   e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   dim3 fgrid(tiles * kFinishParts, 1, zc);
   const float* part = static_cast<const float*>(workspace);
   switch (m) {
-    case 2: k_gemv_finish<G, 2><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
-    case 3: k_gemv_finish<G, 3><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
-    case 4: k_gemv_finish<G, 4><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
-    case 5: k_gemv_finish<G, 5><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
-    case 6: k_gemv_finish<G, 6><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
-    case 7: k_gemv_finish<G, 7><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
-    default: k_gemv_finish<G, 8><<<fgrid, 256, 0, s>>>(o, n, splits, tiles, part); break;
+    case 1: k_gemv_finish<G, 1><<<fgrid, 256, 0, s>>>(oc, n, splits, tiles, part); break;
+    case 2: k_gemv_finish<G, 2><<<fgrid, 256, 0, s>>>(oc, n, splits, tiles, part); break;
+    case 3: k_gemv_finish<G, 3><<<fgrid, 256, 0, s>>>(oc, n, splits, tiles, part); break;
+    case 4: k_gemv_finish<G, 4><<<fgrid, 256, 0, s>>>(oc, n, splits, tiles, part); break;
+    case 5: k_gemv_finish<G, 5><<<fgrid, 256, 0, s>>>(oc, n, splits, tiles, part); break;
+    case 6: k_gemv_finish<G, 6><<<fgrid, 256, 0, s>>>(oc, n, splits, tiles, part); break;
+    case 7: k_gemv_finish<G, 7><<<fgrid, 256, 0, s>>>(oc, n, splits, tiles, part); break;
+    default: k_gemv_finish<G, 8><<<fgrid, 256, 0, s>>>(oc, n, splits, tiles, part); break;
   }
   return hipGetLastError();
 }
 
+// A taller than kGemvMaxM rows runs as consecutive launches over chunks of
+// kGemvMaxM rows (each re-reads B: the packed weight is small next to the
+// general kernel's cost at these heights); the chunks share the workspace in
+// stream order.
 template <int G, bool AD>
 hipError_t launch_rows(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t flags, void* workspace) {
-  switch ((m + 1) / 2) {
-    case 1: return launch_rows_mp<G, 1, AD>(s, o, m, n, k, flags, workspace);
-    case 2: return launch_rows_mp<G, 2, AD>(s, o, m, n, k, flags, workspace);
-    case 3: return launch_rows_mp<G, 3, AD>(s, o, m, n, k, flags, workspace);
-    default: return launch_rows_mp<G, 4, AD>(s, o, m, n, k, flags, workspace);
+  for (uint32_t r0 = 0; r0 < m; r0 += kGemvMaxM) {
+    const uint32_t mc = (m - r0) < kGemvMaxM ? (m - r0) : kGemvMaxM;
+    hipError_t e;
+    switch ((mc + 1) / 2) {
+      case 1: e = launch_rows_mp<G, 1, AD>(s, o, mc, n, k, flags, workspace, r0, m); break;
+      case 2: e = launch_rows_mp<G, 2, AD>(s, o, mc, n, k, flags, workspace, r0, m); break;
+      case 3: e = launch_rows_mp<G, 3, AD>(s, o, mc, n, k, flags, workspace, r0, m); break;
+      default: e = launch_rows_mp<G, 4, AD>(s, o, mc, n, k, flags, workspace, r0, m); break;
+    }
+    if (e != hipSuccess) return e;
   }
+  return hipSuccess;
 }
 
 template <bool AD>
@@ -1210,7 +1238,7 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
   if (policy == 1) return MatmulPath::General;
   if (count == 1 && rowbins_applies(m, n, k, group, flags)) return MatmulPath::RowBins;
   if (gram_applies(m, n, k, group, flags)) return MatmulPath::GramMfma;
-  if (m <= kGemvMaxM && (flags & 2u) == 0 && n % (8 * group) == 0)
+  if (rows_apply(m, n, k, group, flags))
     return m == 1 ? MatmulPath::GemvPairs : MatmulPath::GemvRows;
   return MatmulPath::General;
 }
@@ -1220,11 +1248,22 @@ size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, 
   if (p == MatmulPath::RowBins) return rowbins_workspace_bytes(n, k, group);
   if (p != MatmulPath::GemvRows && p != MatmulPath::GemvPairs) return 0;
   uint32_t ks, splits;
-  if (p == MatmulPath::GemvPairs) pairs_slices(n, k, group, count, &ks, &splits);
-  else rows_slices(m, n, k, group, flags, count, &ks, &splits);
-  if (splits == 1) return 0;
+  // the largest chunk of rows one launch bins; chunks reuse the partials
+  const uint32_t mc = m < kGemvMaxM ? m : kGemvMaxM;
+  uint32_t most = 1;
+  if (p == MatmulPath::GemvPairs) {
+    pairs_slices(n, k, group, count, &ks, &splits);
+    most = splits;
+  } else {
+    for (uint32_t r0 = 0; r0 < m; r0 += kGemvMaxM) {
+      rows_slices((m - r0) < kGemvMaxM ? (m - r0) : kGemvMaxM, m, n, k, group, flags, count, &ks,
+                  &splits);
+      most = splits > most ? splits : most;
+    }
+  }
+  if (most == 1) return 0;
   const uint32_t tiles = (n / (8 * group) + kTileWords - 1) / kTileWords;
-  return size_t(count) * splits * tiles * m * 16 * kTileGroups * sizeof(float);
+  return size_t(count) * most * tiles * mc * 16 * kTileGroups * sizeof(float);
 }
 
 hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
@@ -1247,7 +1286,7 @@ MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                              uint32_t count, uint32_t policy) {
   if (policy == 1) return MatmulPath::General;
   if (count == 1 && rowbins_applies_dense(m, n, k, group, flags)) return MatmulPath::RowBins;
-  if (m <= kGemvMaxM && (flags & 2u) == 0 && n % (8 * group) == 0)
+  if (rows_apply(m, n, k, group, flags))
     return m == 1 ? MatmulPath::GemvPairs : MatmulPath::GemvRows;
   return MatmulPath::General;
 }

@@ -47,7 +47,8 @@ def test_dense_gemv_paths(vqdev, oracle, group, m):
     _check(vqdev, oracle, x, w, False, False, "gemv-pairs" if m == 1 else "gemv-rows")
 
 
-@pytest.mark.parametrize("m,k,group", [(1, 20000, 16), (4, 20000, 8), (3, 700, 32)])
+@pytest.mark.parametrize("m,k,group", [(1, 20000, 16), (4, 20000, 8), (3, 700, 32),
+                                       (32, 4096, 16), (19, 3072, 8)])
 def test_dense_gemv_split_and_ragged_k(vqdev, oracle, m, k, group):
     rng = np.random.default_rng(k + m)
     n = 8 * group * 32
@@ -85,7 +86,7 @@ def test_dense_row_bins(vqdev, oracle, group):
 
 
 @pytest.mark.parametrize("m,n,k,ta,tb", [(3, 40, 100, False, True), (20, 64, 48, True, True),
-                                         (17, 130, 96, False, False), (9, 256, 64, True, False)])
+                                         (17, 130, 96, False, False), (9, 200, 64, True, False)])
 def test_dense_general_is_bit_exact(vqdev, oracle, m, n, k, ta, tb):
     rng = np.random.default_rng(m + n + k)
     w = _weight(rng, (n, k) if tb else (k, n), 16)

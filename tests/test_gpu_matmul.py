@@ -95,6 +95,40 @@ def test_gemv_within_tolerance(vqdev, oracle, m):
         assert o.max_rel(out, _ref64(ops, m, n, k, group, 0)) <= TOL
 
 
+@pytest.mark.parametrize("m,flags", [(9, 0), (16, 0), (17, 1), (32, 0), (40, 1), (63, 0)])
+def test_gemv_rows_in_chunks_of_eight(vqdev, oracle, m, flags):
+    """9 <= m < 64 with a weight of at least 2^20 values runs the row-pair
+    kernel over consecutive chunks of 8 rows of A (the last one shorter), each
+    written at its own output rows; A transposed interleaves every row along
+    k. Smaller weights keep the general kernel."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(60 + m)
+    for k, n, group in ((1024, 1024, 16), (2048, 512, 8), (512, 2048, 32)):
+        words = (2, m, n, k, group, 16, flags, 0)
+        assert vqdev.path_name(words) == "gemv-rows"
+        say("gemv-rows chunks", m, k, n, group, flags)
+        ops = _operands(rng, m, n, k, group, 1.0, 0.02)
+        out, status = _gpu(vqdev, ops, m, n, k, group, flags)
+        assert status == 0
+        ref, _ = oracle.matmul(*ops, m, n, k, group, flags)
+        assert o.max_rel(out, ref) <= TOL
+        assert o.max_rel(out, _ref64(ops, m, n, k, group, flags)) <= TOL
+    assert vqdev.path_name((2, m, 512, 512, 16, 16, flags, 0)) == "general"
+
+
+def test_gemv_rows_chunks_with_split_k(vqdev):
+    """m = 24 over k = 20000 at g = 8: every chunk splits k and reuses the
+    partials workspace in stream order."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(123)
+    m, k, n, group = 24, 20000, 512, 8
+    ops = _operands(rng, m, n, k, group, 1.0, 0.02)
+    say("gemv-rows chunks split", m, k)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0)
+    assert status == 0
+    assert o.max_rel(out, _ref64(ops, m, n, k, group, 0)) <= TOL
+
+
 def test_gemv_transposed_a(vqdev, oracle):
     """A stored (k, m): the activation decode follows the flat index."""
     from oracle import vq4_numpy as o
