@@ -203,8 +203,9 @@ struct AdamwOut {
 // the shader's early returns become the flags and the write decision.
 __device__ __forceinline__ AdamwOut adamw_value(float weight, float moment, float variance,
                                                 float gradient, const Coeffs& c) {
+  // bitwise, not short-circuit: the checks compile to flag arithmetic, not branches
   const bool inputs_finite =
-      finite_f32(weight) && finite_f32(moment) && finite_f32(variance) && finite_f32(gradient);
+      finite_f32(weight) & finite_f32(moment) & finite_f32(variance) & finite_f32(gradient);
   const float next_m = c.beta1 * moment + (1.0f - c.beta1) * gradient;
   const float next_v = c.beta2 * variance + (1.0f - c.beta2) * (gradient * gradient);
   const float corrected_m = next_m / c.c1;
@@ -212,11 +213,11 @@ __device__ __forceinline__ AdamwOut adamw_value(float weight, float moment, floa
   const float denominator = sqrtf(corrected_v) + c.eps;
   const float decayed = weight * (1.0f - c.lr * c.decay);
   const float next_w = decayed - c.lr * corrected_m / denominator;
-  const bool results_finite = finite_f32(next_m) && finite_f32(next_v) &&
-                              finite_f32(corrected_m) && finite_f32(corrected_v) &&
-                              finite_f32(denominator) && finite_f32(decayed) && finite_f32(next_w);
+  const bool results_finite = finite_f32(next_m) & finite_f32(next_v) &
+                              finite_f32(corrected_m) & finite_f32(corrected_v) &
+                              finite_f32(denominator) & finite_f32(decayed) & finite_f32(next_w);
   AdamwOut r;
-  r.write = inputs_finite && !(variance < 0.0f);
+  r.write = inputs_finite & !(variance < 0.0f);
   r.flags = !inputs_finite ? 1u : (variance < 0.0f ? 4u : (results_finite ? 0u : 1u));
   // An element the shader leaves unwritten reads as zero to the fused passes.
   r.w = r.write ? next_w : 0.0f;
@@ -413,39 +414,30 @@ __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const
 #pragma unroll
       for (int st = 0; st < 4; ++st) in_code[st] = nibble(in.codes4 + st * words, v);
       float xs[3][G];
-      if (valid == G) {
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-          const AdamwOut r = adamw_value(sold[in_code[0] * G + j], sold[(16 + in_code[1]) * G + j],
-                                         sold[(32 + in_code[2]) * G + j],
-                                         sold[(48 + in_code[3]) * G + j], c);
-          flags |= r.flags;
-          xs[0][j] = r.w; xs[1][j] = r.m; xs[2][j] = r.v;
-          bad |= !finite_f32(r.w) || !finite_f32(r.m) || !finite_f32(r.v);
-        }
+      for (int j = 0; j < G; ++j) {
+        const AdamwOut r = adamw_value(sold[in_code[0] * G + j], sold[(16 + in_code[1]) * G + j],
+                                       sold[(32 + in_code[2]) * G + j],
+                                       sold[(48 + in_code[3]) * G + j], c);
+        // components past a tail vector's end are computed but neither
+        // reported nor compared (the tail argmin reads only the valid ones)
+        const bool live = uint32_t(j) < valid;
+        flags |= live ? r.flags : 0u;
+        xs[0][j] = r.w; xs[1][j] = r.m; xs[2][j] = r.v;
+        bad |= live & (!finite_f32(r.w) | !finite_f32(r.m) | !finite_f32(r.v));
+      }
+      if (valid == G) {
 #pragma unroll
         for (int st = 0; st < 3; ++st)
           code[st] = argmin32<G, true>(xs[st], G, sbook + st * 16 * G, bad);
       } else {
-#pragma unroll
-        for (int j = 0; j < G; ++j) {
-          const AdamwOut r = adamw_value(sold[in_code[0] * G + j], sold[(16 + in_code[1]) * G + j],
-                                         sold[(32 + in_code[2]) * G + j],
-                                         sold[(48 + in_code[3]) * G + j], c);
-          const bool live = uint32_t(j) < valid;
-          flags |= live ? r.flags : 0u;
-          xs[0][j] = live ? r.w : 0.0f;
-          xs[1][j] = live ? r.m : 0.0f;
-          xs[2][j] = live ? r.v : 0.0f;
-          bad |= live && (!finite_f32(r.w) || !finite_f32(r.m) || !finite_f32(r.v));
-        }
 #pragma unroll
         for (int st = 0; st < 3; ++st)
           code[st] = argmin32<G, false>(xs[st], valid, sbook + st * 16 * G, bad);
       }
 #pragma unroll
       for (int j = 0; j < G; ++j)
-        moved += uint32_t(j) < valid && sbook[code[0] * G + j] != sold[in_code[0] * G + j];
+        moved += (uint32_t(j) < valid) & (sbook[code[0] * G + j] != sold[in_code[0] * G + j]);
     }
 #pragma unroll
     for (int st = 0; st < 3; ++st) {
