@@ -85,12 +85,15 @@ struct AdamwInputs {
 // independent fits that share one geometry. Per problem p the buffers are
 // laid out back to back: sample [count][G] FP32 (the strided sample of
 // complete vectors), idx [count] entry indices, book [16][G] (the working
-// and final book), flags [4] (used mask, kept mask, keep-pass switch, spare).
+// and final book), flags [4] (used mask, kept mask, keep-pass switch, spare),
+// gaps [17][count] float64 (the reseeds' per-row gaps over updated entries and
+// their suffix minima over untouched ones).
 struct FitArgs {
   const float* sample = nullptr;
   uint8_t* idx = nullptr;
   float* book = nullptr;
   uint32_t* flags = nullptr;
+  double* gaps = nullptr;
   uint32_t count = 0;         // sample vectors per problem
   uint64_t complete = 0;      // complete vectors of the tensor being fitted
   uint32_t* status = nullptr;

@@ -189,12 +189,29 @@ __device__ __forceinline__ Far farther(Far a, Far b) {
   return a.row < b.row ? a : b;
 }
 
-// _reseed (vq.py:232-257) for the whole block: the sample row whose nearest
-// entry of `cur` is farthest. Every thread returns the same row.
+// The gap rule of vq.py:254-256 as a combination: a NaN distance wins, else
+// the smaller one. Gaps are sums of squares, never -0, so the result does not
+// depend on the order entries are combined in.
+__device__ __forceinline__ double nanmin(double a, double b) {
+  return a != a ? a : (b != b ? b : (b < a ? b : a));
+}
+
+// _reseed (vq.py:232-257) of entry e for the whole block: the sample row whose
+// nearest entry of `cur` (entries below e already updated this iteration,
+// the others as they were) is farthest. Every thread returns the same row.
+//
+// The first reseed of an iteration (`first`) measures every row against all
+// 16 entries and keeps, per row, near[i] = the gap over the updated entries
+// [0, e) and suffix[e'][i] = the gap over the untouched entries [e', 16) for
+// e' > e. A later reseed at e only measures the entries updated since the
+// previous one ([done, e)) and combines near with suffix[e]: the same gap
+// the full scan would find.
 template <int G>
 __device__ uint32_t reseed_row(const float* sample, uint32_t count, const float* cur,
-                               Far* scratch) {
+                               uint32_t e, uint32_t done, bool first, double* near,
+                               double* suffix, Far* scratch) {
   Far best{0.0, 0xffffffffu, 0};
+  const double inf = __longlong_as_double(0x7ff0000000000000ll);
   for (uint32_t i = threadIdx.x; i < count; i += kUpdateThreads) {
     float x[G];
     const float4* row = reinterpret_cast<const float4*>(sample + uint64_t(i) * G);
@@ -203,13 +220,23 @@ __device__ uint32_t reseed_row(const float* sample, uint32_t count, const float*
       const float4 v = row[q];
       x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
     }
-    double gap = 0.0;
+    double lo = first ? inf : near[i];
 #pragma unroll 1
-    for (uint32_t e = 0; e < 16; ++e) {
-      const double s = pairwise_gap<G>(x, cur + e * G);
-      if (e == 0 || s != s || s < gap) gap = s;
-      if (gap != gap) break;
+    for (uint32_t ee = first ? 0 : done; ee < e; ++ee)
+      lo = nanmin(lo, pairwise_gap<G>(x, cur + ee * G));
+    near[i] = lo;
+    double hi;
+    if (first) {
+      hi = inf;
+#pragma unroll 1
+      for (uint32_t ee = 16; ee-- > e;) {
+        hi = nanmin(pairwise_gap<G>(x, cur + ee * G), hi);
+        if (ee > e) suffix[uint64_t(ee) * count + i] = hi;
+      }
+    } else {
+      hi = suffix[uint64_t(e) * count + i];
     }
+    const double gap = nanmin(lo, hi);
     best = farther(best, Far{gap, i, gap != gap ? 1u : 0u});
   }
   for (int off = 1; off < warpSize; off <<= 1) {
@@ -295,6 +322,10 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
 
   // Entries in ascending order; a reseed sees the book as updated so far.
   const uint32_t kept = flags[1];
+  double* near = a.gaps + uint64_t(p) * count * 17;
+  double* suffix = near + count;
+  bool first = true;
+  uint32_t done = 0;
   for (uint32_t e = 0; e < 16; ++e) {
     if (members[e] > 0) {
       if (t < G) cur[e * G + t] = mean[e * G + t];
@@ -302,8 +333,10 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
     }
     if (kept & (1u << e)) continue;
     __syncthreads();
-    const uint32_t row = reseed_row<G>(sample, count, cur, scratch);
+    const uint32_t row = reseed_row<G>(sample, count, cur, e, done, first, near, suffix, scratch);
     if (t < G) cur[e * G + t] = sample[uint64_t(row) * G + t];
+    first = false;
+    done = e;
   }
   __syncthreads();
   for (uint32_t i = t; i < 16 * G; i += kUpdateThreads) book[i] = cur[i];
