@@ -85,3 +85,44 @@ def test_fused_step_refuses_bad_coefficients_and_keeps_state(vqdev):
     with pytest.raises(ack.AckError, match="status=4"):
         opt.step(weight)
     assert opt.steps == 0 and opt.weight is weight
+
+
+def test_config5_at_full_size(vqdev, oracle):
+    """W 8192 x 8192, rows ~ N(0,1) then L2-normalised,
+    group 8, book = fit_codebook(W). The GPU encode picks the oracle's code
+    for every vector of a strided 1/64 subset, decode is the exact gather, and
+    one fused VQAdamW step with an N(0, 1e-3) gradient equals the unfused
+    sequence (op 3, native fits, GPU encode) bit for bit at full size."""
+    from alelyon_compute_kit import vq
+    n, g = 8192, 8
+    rng = np.random.default_rng(5)
+    w = rng.standard_normal((n, n), dtype=np.float32)
+    w /= np.linalg.norm(w, axis=1, keepdims=True).astype(np.float32)
+    book = vq.fit_codebook(w, group=g)
+    say("config5 encode", n, g)
+    img = vqdev.encode(w, book, group=g)
+    vectors = w.reshape(-1, g)
+    pick = np.arange(0, vectors.shape[0], 64)
+    sub = vectors[pick]
+    ref_codes, status = oracle.encode(sub.reshape(-1), book, g)
+    assert status == 0
+    from oracle import vq4_numpy as o
+    got = o.unpack_indices(img.codes, vectors.shape[0])[pick]
+    np.testing.assert_array_equal(got, o.unpack_indices(ref_codes, sub.shape[0]))
+    say("config5 decode")
+    dense = vqdev.decode(img)
+    np.testing.assert_array_equal(dense.reshape(-1, g), book[o.unpack_indices(img.codes,
+                                                                              vectors.shape[0])])
+    del w, vectors, dense
+    grad = rng.standard_normal((n, n), dtype=np.float32) * np.float32(np.sqrt(1e-3))
+    g_img = vq.encode(grad, vq.fit_codebook(grad, group=g), group=g)
+    del grad
+    say("config5 fused step")
+    fused = vq.VQAdamW(vqdev, img, lr=1e-3, betas=(0.9, 0.999))
+    plain = vq.VQAdamW(Unfused(vqdev), img, lr=1e-3, betas=(0.9, 0.999))
+    r1, r2 = fused.step(g_img), plain.step(g_img)
+    assert r1["changed_weight_values"] == r2["changed_weight_values"]
+    for a, b in ((fused.weight, plain.weight), (fused.momentum, plain.momentum),
+                 (fused.variance, plain.variance)):
+        np.testing.assert_array_equal(a.codebook, b.codebook)
+        np.testing.assert_array_equal(a.codes, b.codes)
