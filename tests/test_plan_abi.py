@@ -255,3 +255,63 @@ def test_library_exports_every_declared_symbol(lib):
     assert {"ack_vq", "ack_vq_schema", "ack_open", "ack_download"} <= declared
     for name in sorted(declared):
         assert hasattr(lib.cdll, name), f"libackvq.so does not export {name}"
+
+
+# ---- this library's extensions ------------------------------------------------
+def _path(lib, entry, words):
+    out = ctypes.create_string_buffer(32)
+    p = block(words)
+    rc = getattr(lib.cdll, entry)(p, len(p), out, len(out))
+    return rc, out.value.decode()
+
+
+@pytest.mark.parametrize("words,path", [
+    ((2, 1, 4096, 4096, 16, 16, 0, 0), "gemv-pairs"),
+    ((2, 8, 4096, 4096, 16, 16, 1, 0), "gemv-rows"),
+    ((2, 32, 4096, 4096, 16, 16, 0, 0), "gemv-rows"),          # chunks of 8 rows
+    ((2, 32, 512, 512, 16, 16, 0, 0), "general"),              # small weight: bit-exact kernel
+    ((2, 2048, 14336, 4096, 32, 16, 0, 0), "row-bins"),
+    ((2, 2048, 4096, 14336, 32, 16, 2, 0), "gram-mfma"),
+    ((2, 4, 4096, 4096, 16, 16, 2, 0), "gram-mfma"),           # both grouped along k
+    ((2, 4, 4096, 4096, 16, 16, 3, 0), "general"),             # A along m, B along k
+    ((2, 1, 4100, 4096, 16, 16, 0, 0), "general"),             # n not whole words of groups
+    ((0, 100, 1, 1, 16, 16, 0, 0), "encode"), ((1, 100, 1, 1, 16, 16, 0, 0), "decode"),
+    ((3, 100, 1, 1, 16, 16, 0, 0), "adamw")])
+def test_kernel_path_choice(lib, words, path):
+    assert _path(lib, "ack_vq_path_name", words) == (0, path)
+
+
+@pytest.mark.parametrize("words,path", [
+    ((2, 1, 4096, 4096, 16, 16, 0, 0), "gemv-pairs"),
+    ((2, 19, 2048, 3072, 8, 16, 0, 0), "gemv-rows"),
+    ((2, 128, 768, 512, 8, 16, 0, 0), "row-bins"),            # dense A: group 8 admitted
+    ((2, 2048, 4096, 14336, 32, 16, 2, 0), "general"),         # no Gram path for dense A
+    ((2, 9, 200, 64, 16, 16, 1, 0), "general")])
+def test_dense_product_path_choice(lib, words, path):
+    assert _path(lib, "ack_vq_dense_path_name", words) == (0, path)
+
+
+def test_dense_product_refuses_before_any_device_lookup(lib):
+    b = FORGED
+    assert _path(lib, "ack_vq_dense_path_name", (0, 1, 1, 1, 8, 16, 0, 0))[0] == ACK_ERR_SHAPE
+    p = block([0, 1, 1, 1, 8, 16, 0, 0])
+    assert lib.cdll.ack_vq_matmul_dense(b, b, b, b, b, b, p, len(p)) == ACK_ERR_SHAPE
+    assert "plan op must be 2" in lib.last_error()
+    p = block([2, 1, 1, 1, 8, 16, 4, 0])
+    assert lib.cdll.ack_vq_matmul_dense(b, b, b, b, b, b, p, len(p)) == ACK_ERR_SHAPE
+    assert lib.cdll.ack_vq_matmul_dense(b, b, b, b, b, b, p, 31) == ACK_ERR_SIZE
+    p = block([2, 4, 64, 64, 16, 16, 0, 0])
+    assert lib.cdll.ack_vq_matmul_dense(FORGED, b, b, b, b, b, p, len(p)) == ACK_ERR_CLOSED
+
+
+def test_device_fit_and_copy_refuse_before_any_device_lookup(lib):
+    b = FORGED
+    fit = lib.cdll.ack_vq_fit_codebook
+    assert fit(b, b, None, b, b, 64, 12, 4, 4096) == ACK_ERR_SHAPE          # group
+    assert fit(b, b, None, b, b, 7, 8, 4, 4096) == ACK_ERR_SIZE             # no whole vector
+    assert "complete vector" in lib.last_error()
+    assert fit(b, b, None, b, b, (1 << 28) + 8, 8, 4, 4096) == ACK_ERR_SIZE
+    assert fit(b, b, None, b, b, 64, 8, 33, 4096) == ACK_ERR_SHAPE          # iterations
+    assert fit(b, b, None, b, b, 64, 8, 4, 15) == ACK_ERR_SHAPE             # sample size
+    assert fit(b, b, None, b, b, 64, 8, 4, 4096) == ACK_ERR_CLOSED
+    assert lib.cdll.ack_buffer_copy(b, b, 0, b, 0, 4) == ACK_ERR_CLOSED
