@@ -54,6 +54,46 @@ __device__ __forceinline__ uint32_t nibble(const uint32_t* codes, uint32_t vecto
                  : "scc");                                                          \
   } while (0)
 
+// The eight ROWBIN_ADDs of one code word in one indexing window: index
+// mode stays on across them and s_set_gpr_idx_idx moves the index to the
+// next nibble's code, so each add costs two scalar instructions, not three.
+// Only the adds run inside the window (SRC0 and DST are indexed; X, their
+// second source, is not).
+#define ROWBIN_ADD8(B0, B1, B2, B3, B4, B5, B6, B7, WORD, X)                        \
+  do {                                                                              \
+    uint32_t e_;                                                                    \
+    asm volatile("s_bfe_u32 %8, %9, 0x40000\n\t"                                  \
+                 "s_set_gpr_idx_on %8, gpr_idx(SRC0,DST)\n\t"                     \
+                 "v_add_f32 v0, v0, %10\n\t"                                       \
+                 "s_bfe_u32 %8, %9, 0x40004\n\t"                                  \
+                 "s_set_gpr_idx_idx %8\n\t"                                        \
+                 "v_add_f32 v16, v16, %10\n\t"                                     \
+                 "s_bfe_u32 %8, %9, 0x40008\n\t"                                  \
+                 "s_set_gpr_idx_idx %8\n\t"                                        \
+                 "v_add_f32 v32, v32, %10\n\t"                                     \
+                 "s_bfe_u32 %8, %9, 0x4000c\n\t"                                  \
+                 "s_set_gpr_idx_idx %8\n\t"                                        \
+                 "v_add_f32 v48, v48, %10\n\t"                                     \
+                 "s_bfe_u32 %8, %9, 0x40010\n\t"                                  \
+                 "s_set_gpr_idx_idx %8\n\t"                                        \
+                 "v_add_f32 v64, v64, %10\n\t"                                     \
+                 "s_bfe_u32 %8, %9, 0x40014\n\t"                                  \
+                 "s_set_gpr_idx_idx %8\n\t"                                        \
+                 "v_add_f32 v80, v80, %10\n\t"                                     \
+                 "s_bfe_u32 %8, %9, 0x40018\n\t"                                  \
+                 "s_set_gpr_idx_idx %8\n\t"                                        \
+                 "v_add_f32 v96, v96, %10\n\t"                                     \
+                 "s_bfe_u32 %8, %9, 0x4001c\n\t"                                  \
+                 "s_set_gpr_idx_idx %8\n\t"                                        \
+                 "v_add_f32 v112, v112, %10\n\t"                                   \
+                 "s_set_gpr_idx_off"                                                \
+                 : "+{v[0:15]}"(B0), "+{v[16:31]}"(B1), "+{v[32:47]}"(B2),          \
+                   "+{v[48:63]}"(B3), "+{v[64:79]}"(B4), "+{v[80:95]}"(B5),         \
+                   "+{v[96:111]}"(B6), "+{v[112:127]}"(B7), "=&s"(e_)               \
+                 : "s"(WORD), "v"(X)                                                \
+                 : "scc");                                                          \
+  } while (0)
+
 constexpr int kRBWaves = 4;  // word columns per block
 
 // Word column q of B's codes, contiguous: wt[q * k + kk] = codes[kk * rw + q].
@@ -175,14 +215,7 @@ __global__ __launch_bounds__(256) void k_rowbins(Operands o, uint32_t m, uint32_
     for (int s = 0; s < kRun; ++s) {
       const uint32_t ww = w[s];
       const float xv = x[s];
-      ROWBIN_ADD(b0, "v[0:15]", "v0", ww, 0x40000, xv);
-      ROWBIN_ADD(b1, "v[16:31]", "v16", ww, 0x40004, xv);
-      ROWBIN_ADD(b2, "v[32:47]", "v32", ww, 0x40008, xv);
-      ROWBIN_ADD(b3, "v[48:63]", "v48", ww, 0x4000c, xv);
-      ROWBIN_ADD(b4, "v[64:79]", "v64", ww, 0x40010, xv);
-      ROWBIN_ADD(b5, "v[80:95]", "v80", ww, 0x40014, xv);
-      ROWBIN_ADD(b6, "v[96:111]", "v96", ww, 0x40018, xv);
-      ROWBIN_ADD(b7, "v[112:127]", "v112", ww, 0x4001c, xv);
+      ROWBIN_ADD8(b0, b1, b2, b3, b4, b5, b6, b7, ww, xv);
     }
   }
 
