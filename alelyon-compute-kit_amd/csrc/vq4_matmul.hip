@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256) void k_gemv_finish(Operands o, uint32_t n, uin
 // ---- GemvPairs (m = 1) -----------------------------------------------------
 // The two nibbles of a byte of a B row are the codes of two output groups of
 // the same inner row, so they receive the same x. One integer atomic into a
-// 256-way "pair bin" indexed by the whole byte replaces GemvBins' two:
+// 256-way "pair bin" indexed by the whole byte replaces the two nibble bins:
 //   S[2p][e]   = sum over hi of P[p][16 hi + e]   (low nibble = group 8q+2p)
 //   S[2p+1][e] = sum over lo of P[p][16 e + lo]   (high nibble = group 8q+2p+1)
 //
