@@ -1063,21 +1063,35 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
       const uint32_t groups = (rw - tile * kTileWords) < kTileWords
                                   ? (rw - tile * kTileWords) * 8
                                   : kTileGroups;
-      const uint32_t t = ft % G;
-      float cb[16];
+      // thread ft always takes columns 4 tc .. 4 tc + 3 of its groups (tc = ft %
+      // (G / 4)): each S value read serves four outputs
+      const uint32_t tc = ft % (G / 4);
+      float4 cb[16];
 #pragma unroll
-      for (uint32_t c = 0; c < 16; ++c) cb[c] = bb[c * G + t];
-      float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
+      for (uint32_t c = 0; c < 16; ++c)
+        cb[c] = *reinterpret_cast<const float4*>(bb + c * G + 4 * tc);
+      float* out = item_ptr_mut<float>(o.out, o.stride[4], item) + tile * kTileGroups * G;
+      const bool vec = ((reinterpret_cast<uintptr_t>(out) | (uint64_t(n) * 4)) & 15u) == 0;
       bool bad = false;
-      for (uint32_t idx = ft; idx < m * groups * G; idx += kRowThreads) {
-        const uint32_t r = idx / (groups * G), rem = idx % (groups * G);
-        const uint32_t j = rem / G;
+      for (uint32_t idx = ft; idx < m * groups * (G / 4); idx += kRowThreads) {
+        const uint32_t r = idx / (groups * (G / 4)), j = idx % (groups * (G / 4)) / (G / 4);
         const float* sj = ss + (r * 16 * 8 + j % 8) * kTileWords + j / 8;
-        float y = 0.0f;
+        float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (uint32_t c = 0; c < 16; ++c) y = fmaf(cb[c], sj[c * kTileGroups], y);
-        out[uint64_t(r) * n + tile * kTileGroups * G + rem] = y;
-        bad |= !finite_f32(y);
+        for (uint32_t c = 0; c < 16; ++c) {
+          const float sv_ = sj[c * kTileGroups];
+          y.x = fmaf(cb[c].x, sv_, y.x);
+          y.y = fmaf(cb[c].y, sv_, y.y);
+          y.z = fmaf(cb[c].z, sv_, y.z);
+          y.w = fmaf(cb[c].w, sv_, y.w);
+        }
+        float* oy = out + uint64_t(r) * n + j * G + 4 * tc;
+        if (vec) {
+          *reinterpret_cast<float4*>(oy) = y;
+        } else {
+          oy[0] = y.x; oy[1] = y.y; oy[2] = y.z; oy[3] = y.w;
+        }
+        bad |= !finite_f32(y.x) || !finite_f32(y.y) || !finite_f32(y.z) || !finite_f32(y.w);
       }
       if (__any(bad) && (ft % warpSize) == 0) atomicOr(o.status, 1u);
     }
