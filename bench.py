@@ -372,30 +372,69 @@ def bench_harness(device, dev, steps=3):
     return out
 
 
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(x_img, w_img, budget_s=10.0):
-    """The oracle's numpy CPU path for config 3: decode + matmul per matrix."""
+    """The oracle's numpy CPU path for config 3: decode + matmul per matrix
+    (the value), with the other CPU phases of the path -- the codebook fit
+    and the float64 encode of the same weight -- timed beside it."""
     from oracle import vq4_numpy as o
+    blas = {}
     try:
         from threadpoolctl import threadpool_info
-        threads = max((i.get("num_threads", 1) for i in threadpool_info()
-                       if i.get("user_api") == "blas"), default=1)
+        for info in threadpool_info():
+            if info.get("user_api") == "blas":
+                blas = {"vendor": info.get("internal_api"), "threads": info.get("num_threads")}
+                break
     except Exception:  # pragma: no cover - threadpoolctl is optional
-        threads = os.cpu_count() or 1
+        pass
+    threads = int(blas.get("threads") or os.cpu_count() or 1)
     x = o.decode(x_img.codes, x_img.codebook, 4096, 16).reshape(1, 4096)
+
+    def median_of(fn, runs=5):
+        fn()                                           # warm-up
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times))
+
+    decode_s = median_of(lambda: o.decode(w_img.codes, w_img.codebook, 4096 * 4096, 16))
+    wd = o.decode(w_img.codes, w_img.codebook, 4096 * 4096, 16).reshape(4096, 4096)
+    matmul_s = median_of(lambda: x @ wd)
+    fit_s = median_of(lambda: o.fit_codebook(wd, 16), runs=3)
+    encode_s = median_of(lambda: o.encode64(wd.reshape(-1)[:1 << 20], w_img.codebook, 16),
+                         runs=3) * 16               # 1/16 of the weight, scaled
+    # the value: decode + matmul per matrix, repeated for about budget_s
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < 3 or time.perf_counter() < t_end:
+    while len(times) < 5 or time.perf_counter() < t_end:
         t0 = time.perf_counter()
-        wd = o.decode(w_img.codes, w_img.codebook, 4096 * 4096, 16).reshape(4096, 4096)
-        _ = x @ wd
+        w_dense = o.decode(w_img.codes, w_img.codebook, 4096 * 4096, 16).reshape(4096, 4096)
+        _ = x @ w_dense
         times.append(time.perf_counter() - t0)
         if len(times) >= 1000:
             break
     per = float(np.median(times))
-    return {"value": W_BYTES / per / 1e9, "unit": "GB/s", "cores": int(threads), "kind": "port",
+    return {"value": W_BYTES / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{len(times)} matrices of config 3 (numpy gather decode of the 4096x4096 "
                       f"g16 weight + numpy matmul with a 1x4096 row), median {per * 1e3:.1f} ms "
-                      f"per matrix; BLAS threads {threads}, os.cpu_count {os.cpu_count()}"}
+                      f"per matrix; BLAS threads {threads}",
+            "host": {"cpu": _cpu_model(), "os_cpu_count": os.cpu_count(),
+                     "affinity_cores": len(os.sched_getaffinity(0)), "blas": blas},
+            "phases_ms": {"decode": decode_s * 1e3, "matmul": matmul_s * 1e3,
+                          "fit_codebook": fit_s * 1e3, "encode_float64": encode_s * 1e3},
+            "phases_note": "one 4096x4096 g16 weight each; warm-up then median of 5 (fit and "
+                           "encode: 3; encode timed on 1/16 of the weight and scaled)"}
 
 
 def load_traffic():
