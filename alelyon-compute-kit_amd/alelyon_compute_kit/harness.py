@@ -325,6 +325,31 @@ class ExpertHarness:
             return self._forward_resident(x, weight, self._resident_for(layer, expert, state))
         return self.backend.matmul(self._encode(x, weight.group), weight)
 
+    def forward_batch(self, inputs, experts) -> np.ndarray:
+        """``inputs[i] @ weight(experts[i])`` for several experts of the bank at
+        once (``experts`` are (layer, expert) pairs; every input has the same
+        shape). On a ``VQDevice`` backend the products run as one batched
+        launch over the packed weights (``ack_vq_batch``); each result equals
+        ``forward`` of that input within FP32 rounding (the kernel may split
+        the sums differently for a batch than for one product)."""
+        pairs = [tuple(int(v) for v in e) for e in experts]
+        xs = [_matrix(v, "inputs") for v in inputs]
+        if not pairs or len(xs) != len(pairs):
+            raise HarnessError("one input matrix per expert is required")
+        if any(x.shape != xs[0].shape for x in xs):
+            raise HarnessError("batched inputs must share one shape")
+        weights = [self._state(layer, expert).tensors[0] for layer, expert in pairs]
+        if xs[0].shape[1] != weights[0].shape[0]:
+            raise HarnessError(f"inputs have width {xs[0].shape[1]}, "
+                               f"expert expects {weights[0].shape[0]}")
+        group = weights[0].group
+        if any(w.shape != weights[0].shape or w.group != group for w in weights):
+            raise HarnessError("batched experts must share one weight shape and group")
+        images = [self._encode(x, group) for x in xs]
+        if isinstance(self.backend, vq.VQDevice):
+            return self.backend.matmul_batch(images, weights)
+        return np.stack([self.backend.matmul(a, w) for a, w in zip(images, weights)])
+
     def train_step(self, inputs, targets, *, layer: int = 0, expert: int = 0,
                    lr: float = 1e-3, beta1: float = 0.9, beta2: float = 0.95,
                    eps: float = 1e-8, weight_decay: float = 0.0,

@@ -393,6 +393,26 @@ class VQDevice:
                         (a.codes, a.codebook, b.codes, b.codebook), m * n * 4, np.float32)
         return out.reshape(m, n)
 
+    def matmul_batch(self, a, b, *, transpose_a=False, transpose_b=False) -> np.ndarray:
+        """``[op(a[i]) @ op(b[i]) for i]`` as one batched launch
+        (``ack_vq_batch``): the operands of every instance share shapes and
+        group, their packed images are laid back to back. Returns
+        ``(count, m, n)`` float32."""
+        a, b = list(a), list(b)
+        if not a or len(a) != len(b):
+            raise ValueError("vq batched matmul needs one right operand per left operand")
+        if any(x.shape != a[0].shape or x.group != a[0].group for x in a) or \
+                any(y.shape != b[0].shape or y.group != b[0].group for y in b):
+            raise ValueError("vq batched matmul operands must share shapes and group")
+        m, n, k, flags = self._matmul_geometry(a[0], b[0], transpose_a, transpose_b)
+        arrays = (np.concatenate([x.codes for x in a]),
+                  np.concatenate([x.codebook.reshape(-1) for x in a]),
+                  np.concatenate([y.codes for y in b]),
+                  np.concatenate([y.codebook.reshape(-1) for y in b]))
+        out = self._run((2, m, n, k, a[0].group, ENTRIES, flags, 0), arrays,
+                        len(a) * m * n * 4, np.float32, count=len(a))
+        return out.reshape(len(a), m, n)
+
     @staticmethod
     def _dense_geometry(x: np.ndarray, b: VQArray, transpose_a, transpose_b):
         if type(transpose_a) is not bool or type(transpose_b) is not bool:

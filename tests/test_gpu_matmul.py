@@ -428,3 +428,28 @@ def test_config4_backward_rows_against_float64(vqdev):
     ref = dy_img.decode()[rows].astype(np.float64) @ w_img.decode().astype(np.float64).T
     assert o.max_rel(y[rows], ref) <= TOL
     assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("m,flags", [(1, 0), (6, 2), (48, 1), (200, 0)])
+def test_matmul_batch_method_matches_each_instance(vqdev, m, flags):
+    """``VQDevice.matmul_batch`` (one ``ack_vq_batch`` launch) against a
+    float64 product of each instance's decoded operands."""
+    from alelyon_compute_kit import vq
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(100 + m)
+    n, k, group, count = 384, 512, 16, 5
+    a_shape = (k, m) if flags & 1 else (m, k)
+    b_shape = (n, k) if flags & 2 else (k, n)
+    a_vals = [rng.standard_normal(a_shape).astype(np.float32) for _ in range(count)]
+    b_vals = [rng.standard_normal(b_shape).astype(np.float32) * 0.1 for _ in range(count)]
+    a = [vq.encode(v, vq.fit_codebook(v, group=group), group=group) for v in a_vals]
+    b = [vq.encode(v, vq.fit_codebook(v, group=group), group=group) for v in b_vals]
+    say("matmul_batch", m, n, k, flags, count)
+    got = vqdev.matmul_batch(a, b, transpose_a=bool(flags & 1), transpose_b=bool(flags & 2))
+    assert got.shape == (count, m, n)
+    for i in range(count):
+        exact = o.matmul64(a[i].decode(), b[i].decode(), bool(flags & 1), bool(flags & 2))
+        assert o.max_rel(got[i], exact) <= TOL
+    with pytest.raises(ValueError, match="share shapes"):
+        vqdev.matmul_batch(a[:2], [b[0], vq.encode(b_vals[1].T.copy(), b[1].codebook,
+                                                    group=group)])

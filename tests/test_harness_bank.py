@@ -362,3 +362,60 @@ def test_resident_harness_needs_a_device_backend(tmp_path):
         harness.ExpertHarness(bank, backend=HostBackend(), resident=True)
     with pytest.raises(harness.HarnessError, match="bool"):
         harness.ExpertHarness(bank, backend=HostBackend(), resident=1)
+
+
+def test_forward_batch_equals_per_expert_forward_on_a_host_backend(tmp_path):
+    bank = expert_bank.ExpertBank.create(
+        tmp_path / "many", expert_bank.BankConfig(2, 3, ((16, 24), (16, 24), (16, 24)), 8))
+    for layer in range(2):
+        for e in range(3):
+            bank.initialize_expert(layer, e, seed=layer * 10 + e)
+    h = harness.ExpertHarness(bank, backend=HostBackend())
+    rng = np.random.default_rng(1)
+    xs = [rng.standard_normal((5, 16)).astype(np.float32) for _ in range(4)]
+    experts = [(0, 2), (1, 0), (0, 2), (1, 1)]
+    got = h.forward_batch(xs, experts)
+    for x, (layer, e), y in zip(xs, experts, got):
+        np.testing.assert_array_equal(y, h.forward(x, layer=layer, expert=e))
+    with pytest.raises(harness.HarnessError, match="one input"):
+        h.forward_batch(xs[:2], experts)
+    with pytest.raises(harness.HarnessError, match="share one shape"):
+        h.forward_batch([xs[0], xs[1][:3]], experts[:2])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 4, 32])
+def test_forward_batch_is_one_launch_over_many_experts(tmp_path, vqdev, m):
+    """Eight experts of a 4096 x 4096 g16 bank in one batched launch: each
+    output agrees with that expert's own forward and with the float64 product
+    of the decoded operands within 1e-5."""
+    from gpu_util import say
+    from oracle import vq4_numpy as o
+    bank = expert_bank.ExpertBank.create(
+        tmp_path / "many", expert_bank.BankConfig(2, 4, ((4096, 4096),) * 3, 16))
+    experts = [(layer, e) for layer in range(2) for e in range(4)]
+    for layer, e in experts:
+        bank.initialize_expert(layer, e, seed=3 + layer * 4 + e, zero_optimizer_state=True)
+    h = harness.ExpertHarness(bank, backend=vqdev)
+    rng = np.random.default_rng(m)
+    xs = [rng.standard_normal((m, 4096)).astype(np.float32) for _ in experts]
+    say("forward_batch", m, len(experts))
+    got = h.forward_batch(xs, experts)
+    for x, (layer, e), y in zip(xs, experts, got):
+        one = h.forward(x, layer=layer, expert=e)
+        assert o.max_rel(y, one) <= 1e-5
+        x_img = h._encode(x, 16)
+        exact = o.matmul64(x_img.decode(), bank.read_expert(layer, e)[0].decode())
+        assert o.max_rel(y, exact) <= 1e-5
+
+
+def test_forward_batch_refuses_a_wrong_width(tmp_path):
+    bank = expert_bank.ExpertBank.create(
+        tmp_path / "mixed", expert_bank.BankConfig(2, 1, ((16, 24), (16, 24), (16, 24)), 8))
+    bank.initialize_expert(0, 0, seed=1)
+    bank.initialize_expert(1, 0, seed=2)
+    h = harness.ExpertHarness(bank, backend=HostBackend())
+    x = np.ones((2, 16), np.float32)
+    with pytest.raises(harness.HarnessError, match="width"):
+        h.forward_batch([x[:, :8]], [(0, 0)])
+    assert h.forward_batch([x, x], [(0, 0), (1, 0)]).shape == (2, 2, 24)
