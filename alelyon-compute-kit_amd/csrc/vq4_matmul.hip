@@ -285,6 +285,7 @@ constexpr int kPairThreads = 512;
 constexpr int kPairWaves = kPairThreads / 64;
 constexpr int kPairR = 16;                                          // rows per lane per batch
 constexpr int kPairD = 4;                                           // batches in the ring
+constexpr int kPairDX4 = 4;  // X4, one window: x takes 8 registers, and no accumulators
 constexpr uint32_t kPairBatchRows = kPairWaves * 2 * kPairR;        // 256 rows per batch
 constexpr uint32_t kPairBins = 256 * 4 * kTileWords;                // 32768
 constexpr uint32_t kPairXRows = 4096;                               // staged x rows (16 KiB)
@@ -297,19 +298,35 @@ static_assert(kPairSH * kPairSL * kPairThreads == int(kPairBins), "every bin flu
 static_assert(kPairThreads / kTileWords == 4 * kPairHB * kPairLB, "thread roles");
 static_assert(kPairXRows >= 16 * kTileGroups, "S reuses the x staging area");
 
-// LDS layout (bytes): bins | staged x (later S) | A book | B book | A words | row maxima.
+// LDS layout (bytes): bins | staged x (later S) | A book | B book x 2 | A words | row maxima.
+// The B book alternates between two copies by instance, so an instance's
+// set-up need not wait for the previous output phase, the book's only reader.
 template <int G>
 struct PairLds {
   static constexpr uint32_t xs = kPairBins * 4;
   static constexpr uint32_t af = xs + kPairXRows * 4;
   static constexpr uint32_t bb = af + 16 * G * 4;
-  static constexpr uint32_t aw = bb + 16 * G * 4;
+  static constexpr uint32_t aw = bb + 2 * 16 * G * 4;
   static constexpr uint32_t rmax = aw + kPairMaxAWords * 4;
   static constexpr uint32_t total = rmax + 16 * 4;
 };
 
 __device__ __forceinline__ uint32_t pair_dword(uint32_t v, uint32_t p, uint32_t q) {
   return (p >> 1) * 16384 + v * 64 + (p & 1) * 32 + q;
+}
+
+// Largest of the wave's values, for values that are >= 0 and not NaN (their
+// bit patterns then order as the floats do): DPP within each row of 16, then
+// the four row results.
+__device__ __forceinline__ float wave_max_nonneg(float m) {
+  int v = __float_as_int(m);
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false));  // row_mirror
+  const int r = max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+                    max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+  return __int_as_float(r);
 }
 
 // Buffer descriptor over the first `bytes` of an array: raw buffer loads past
@@ -328,11 +345,16 @@ struct PairAhead {
 // holds the kAmaxParts partial maxima of |x| per instance (k_dense_amax).
 // SW: the slice is one window (ks <= kPairWindow), so the bins are read out
 // once, at the end, and no FP32 accumulator lives through the main loop.
-template <int G, bool AD, bool SW>
+// X4 (rows of whole 32-word tiles): each lane loads 4 adjacent words of 4 rows
+// with 16-byte loads, a quarter of the load instructions. Eight lanes cover a
+// row, so the 32 lanes of a half-wave hold 4 rows; a lane rotates its 4 words
+// by its row slot so that at every atomic the half-wave still covers the 32
+// word columns once (32 distinct banks).
+template <int G, bool AD, bool SW, bool X4>
 __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint32_t n,
                                                                 uint32_t k, uint32_t ks,
                                                                 float* partial) {
-  constexpr uint32_t R = kPairR, D = kPairD, BR = kPairBatchRows;
+  constexpr uint32_t R = kPairR, D = (X4 && SW) ? kPairDX4 : kPairD, BR = kPairBatchRows;
   constexpr int kSPer = 16 * kTileGroups / kPairThreads;
   static_assert(16 * G <= kPairThreads, "one book entry per thread");
   static_assert(D % 2 == 0, "x buffers alternate by batch parity");
@@ -343,7 +365,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   int4* bins4 = reinterpret_cast<int4*>(smem);
   int32_t* sx = reinterpret_cast<int32_t*>(lds + L::xs);
   float* af = reinterpret_cast<float*>(lds + L::af);
-  float* bb = reinterpret_cast<float*>(lds + L::bb);
+  float* const bb0 = reinterpret_cast<float*>(lds + L::bb);
   uint32_t* aw = reinterpret_cast<uint32_t*>(lds + L::aw);
   float* rmax = reinterpret_cast<float*>(lds + L::rmax);
   // Defensive: the perm-built bin addresses assume the bins start at LDS 0.
@@ -360,11 +382,26 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   const uint32_t nbp = (nb + D - 1) / D * D;  // padded batches read zero words and x
   const uint32_t lane = tid % 64, wave = tid / 64;
   const uint32_t q = lane % 32, half = lane / 32;
-  const uint32_t lane_row = (wave * 2 + half) * R;
+  // X4: lane = 8 row slots x 8 four-word chunks; rx rows per lane per batch
+  constexpr uint32_t RX = X4 ? R / 4 : R;
+  const uint32_t chunk = lane % 8, slot = lane / 8;
+  const uint32_t lane_row = X4 ? wave * (2 * R) + slot * RX : (wave * 2 + half) * R;
   // dead word columns (rw not a multiple of the tile) bin the last column into
   // bins no output reads
-  const uint32_t col = (tile * kTileWords + q < rw) ? tile * kTileWords + q : rw - 1;
-  const uint32_t lc = (q * 4) | ((q * 4 + 128) << 8) | (1u << 16);
+  const uint32_t col = X4 ? tile * kTileWords + 4 * chunk
+                          : ((tile * kTileWords + q < rw) ? tile * kTileWords + q : rw - 1);
+  // byte 0: 4 x word column (+128 for odd byte positions), byte 2: region 1
+  uint32_t lcs[X4 ? 4 : 1];
+  if (X4) {
+#pragma unroll
+    for (uint32_t t = 0; t < 4; ++t) {
+      const uint32_t qt = 4 * chunk + ((t + slot) & 3u);
+      lcs[t] = (qt * 4) | ((qt * 4 + 128) << 8) | (1u << 16);
+    }
+  } else {
+    lcs[0] = (q * 4) | ((q * 4 + 128) << 8) | (1u << 16);
+  }
+  const bool rot1 = (slot & 1u) != 0, rot2 = (slot & 2u) != 0;
   constexpr uint32_t kSel[4] = {0x0c0c0400u, 0x0c0c0501u, 0x0c020600u, 0x0c020701u};
   const uint32_t a_w0 = k0 / G / 8;
   const uint32_t a_words = (kend - 1) / G / 8 - a_w0 + 1;
@@ -402,14 +439,25 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   auto load_batch = [&](__amdgpu_buffer_rsrc_t rs, uint32_t b, uint32_t (&w)[R]) {
     uint32_t off = voff_lane + (k0 + b * BR) * rw * 4u;
     asm volatile("" : "+v"(off));  // per-row offsets formed next to each load
+    if (X4) {
 #pragma unroll
-    for (uint32_t u = 0; u < R; ++u)
-      w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, off + u * rw * 4u, 0, 0));
+      for (uint32_t u = 0; u < RX; ++u) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + u * rw * 4u, 0, 0);
+        w[4 * u] = v[0]; w[4 * u + 1] = v[1]; w[4 * u + 2] = v[2]; w[4 * u + 3] = v[3];
+      }
+    } else {
+#pragma unroll
+      for (uint32_t u = 0; u < R; ++u)
+        w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, off + u * rw * 4u, 0, 0));
+    }
   };
 
   uint32_t buf[D][R];
-  int32_t xa[R], xb[R];
-  float acc[kPairSH][kPairSL];
+  int32_t xa[RX], xb[RX];
+  // multi-window: the sub-block's FP32 accumulators; one window: its row and
+  // column sums, formed as the bins are read (the same sums in the same order)
+  float acc[SW ? 1 : kPairSH][SW ? 1 : kPairSL];
+  float rsum[kPairSH], csum[kPairSL];
   int shift = 0;
   uint32_t xbase = k0;
   __amdgpu_buffer_rsrc_t x_rs = words_rsrc(nullptr, 0u);  // AD: this instance's x[0, kend)
@@ -439,16 +487,16 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       *reinterpret_cast<int4*>(sx + r4) = v;
     }
   };
-  auto read_x = [&](uint32_t b, int32_t (&xs)[R]) __attribute__((always_inline)) {
+  auto read_x = [&](uint32_t b, int32_t (&xs)[RX]) __attribute__((always_inline)) {
     asm volatile("" : "+s"(b));
     if (k0 + b * BR >= kend) {  // a padding batch: nothing staged for it
 #pragma unroll
-      for (uint32_t u = 0; u < R; ++u) xs[u] = 0;
+      for (uint32_t u = 0; u < RX; ++u) xs[u] = 0;
       return;
     }
     const int4* xr = reinterpret_cast<const int4*>(sx + (k0 + b * BR + lane_row - xbase));
 #pragma unroll
-    for (uint32_t c4 = 0; c4 < R / 4; ++c4) {
+    for (uint32_t c4 = 0; c4 < RX / 4; ++c4) {
       const int4 v = xr[c4];
       xs[4 * c4] = v.x; xs[4 * c4 + 1] = v.y; xs[4 * c4 + 2] = v.z; xs[4 * c4 + 3] = v.w;
     }
@@ -464,12 +512,18 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
 #pragma unroll
       for (int c = 0; c < kPairSL; ++c) {
         const uint32_t d = pair_dword(16 * (fh * kPairSH + a) + fl * kPairSL + c, fp, fq);
-        acc[a][c] = SW ? float(bins[d]) : acc[a][c] + float(bins[d]);
-        if (!SW && clear) bins[d] = 0;
+        if (SW) {
+          const float v = float(bins[d]);
+          csum[c] = a == 0 ? v : csum[c] + v;
+          rsum[a] = c == 0 ? v : rsum[a] + v;
+        } else {
+          acc[a][c] += float(bins[d]);
+          if (clear) bins[d] = 0;
+        }
       }
   };
   // `tail`: a batch of the peeled last D, the only ones that can be the last
-  auto stage = [&](uint32_t (&w)[R], uint32_t b, int32_t (&xs)[R], int32_t (&xn)[R],
+  auto stage = [&](uint32_t (&w)[R], uint32_t b, int32_t (&xs)[RX], int32_t (&xn)[RX],
                    __amdgpu_buffer_rsrc_t rs_refill, uint32_t b_refill, bool tail)
                    __attribute__((always_inline)) {
     asm volatile("" : "+s"(b));  // row arithmetic is redone per batch, not strength-reduced
@@ -479,12 +533,29 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     const bool wend = SW ? last : (done % kPairWindow == 0 || last);
     if (!restage && !last) read_x(b + 1, xn);
     if (b < nb) {  // padding batches (past the slice) bin nothing
+      if (X4) {
 #pragma unroll
-      for (uint32_t u = 0; u < R; ++u) {
-        const uint32_t ww = w[u];
-        const int32_t xv = xs[u];
+        for (uint32_t u = 0; u < RX; ++u) {
+          // word t of the rotated row is word (t + slot) % 4 of the chunk
+          const uint32_t a0 = rot1 ? w[4 * u + 1] : w[4 * u];
+          const uint32_t a1 = rot1 ? w[4 * u + 2] : w[4 * u + 1];
+          const uint32_t a2 = rot1 ? w[4 * u + 3] : w[4 * u + 2];
+          const uint32_t a3 = rot1 ? w[4 * u] : w[4 * u + 3];
+          const uint32_t r[4] = {rot2 ? a2 : a0, rot2 ? a3 : a1, rot2 ? a0 : a2, rot2 ? a1 : a3};
+          const int32_t xv = xs[u];
 #pragma unroll
-        for (int p = 0; p < 4; ++p) lds_add(__builtin_amdgcn_perm(ww, lc, kSel[p]), xv);
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int p = 0; p < 4; ++p) lds_add(__builtin_amdgcn_perm(r[t], lcs[t], kSel[p]), xv);
+        }
+      } else {
+#pragma unroll
+        for (uint32_t u = 0; u < R; ++u) {
+          const uint32_t ww = w[u];
+          const int32_t xv = xs[u];
+#pragma unroll
+          for (int p = 0; p < 4; ++p) lds_add(__builtin_amdgcn_perm(ww, lcs[0], kSel[p]), xv);
+        }
       }
     }
     load_batch(rs_refill, b_refill, w);
@@ -515,13 +586,21 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
 #pragma unroll
     for (uint32_t d = 0; d < D; ++d) load_batch(r0, d, buf[d]);
   }
+  // the bins start at zero; each instance clears them again once its finalise
+  // has read them (the set-up barriers order that before the next atomics)
+#pragma unroll
+  for (uint32_t i = 0; i < kPairBins / (4 * kPairThreads); ++i)
+    bins4[tid + i * kPairThreads] = make_int4(0, 0, 0, 0);
   for (; item < o.count; item += zn) {
     const uint32_t next = item + zn;
     const __amdgpu_buffer_rsrc_t cur_rs = batch_rsrc(item);
     const __amdgpu_buffer_rsrc_t next_rs = batch_rsrc(next);
     // ---- set-up ----
+    // No barrier first: the previous output phase reads only S (staging area)
+    // and the other copy of the B book, and its bin clears precede this
+    // instance's atomics by the barriers below.
     const uint32_t st = opaque(tid);
-    __syncthreads();  // the previous instance's S and books are no longer read
+    float* bb = bb0 + (((item - blockIdx.z) / zn) & 1u) * (16 * G);
     if (st < 16 * G) {
       if (!AD) af[st] = cur.a;
       bb[st] = cur.b;
@@ -529,30 +608,18 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     if (!AD && st < a_words) aw[st] = cur.w0;
     if (!AD && st + kPairThreads < a_words) aw[st + kPairThreads] = cur.w1;
     if (AD) x_rs = words_rsrc(item_ptr<float>(o.in[0], o.stride[0], item), kend * 4u);
-#pragma unroll
-    for (uint32_t i = 0; i < kPairBins / (4 * kPairThreads); ++i)
-      bins4[st + i * kPairThreads] = make_int4(0, 0, 0, 0);
-    __syncthreads();
-    if (tile == 0 && split == 0) sweep_books(AD ? bb : af, bb, 16 * G, o.status);
-    // largest |A book entry| (AD: largest |x|): 16 partial maxima, then every
-    // thread reads them
-    if (st < 16) {
-      float m = 0.0f;
-      if (AD) {
-        m = cur.a;
-      } else {
-#pragma unroll
-        for (int t = 0; t < G; t += 4) {
-          const float4 v = *reinterpret_cast<const float4*>(af + st * G + t);
-          m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        }
-      }
-      rmax[st] = m;
+    // largest |A book entry| (AD: largest |x|): every thread holds one book
+    // entry (zero past the book) or one of the 16 partial maxima; NaN counts
+    // as zero, as in a running fmaxf from zero
+    {
+      const float m = wave_max_nonneg(fmaxf(0.0f, AD ? cur.a : fabsf(cur.a)));
+      if (st % 64 == 0) rmax[st / 64] = m;
     }
     __syncthreads();
+    if (tile == 0 && split == 0) sweep_books(AD ? bb : af, bb, 16 * G, o.status);
     float amax = 0.0f;
 #pragma unroll
-    for (int t = 0; t < 16; t += 4) {
+    for (int t = 0; t < kPairWaves; t += 4) {
       const float4 v = *reinterpret_cast<const float4*>(rmax + t);
       amax = fmaxf(amax, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
     }
@@ -574,9 +641,9 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     nxt = setup_loads(next + zn < o.count ? next + zn : item);
     if (!SW) {
 #pragma unroll
-      for (int a = 0; a < kPairSH; ++a)
+      for (int a = 0; a < (SW ? 1 : kPairSH); ++a)
 #pragma unroll
-        for (int c = 0; c < kPairSL; ++c) acc[a][c] = 0.0f;
+        for (int c = 0; c < (SW ? 1 : kPairSL); ++c) acc[a][c] = 0.0f;
     }
 
     // ---- main loop: all but the last D batches refill from this instance ----
@@ -601,20 +668,28 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     float* pl = reinterpret_cast<float*>(smem);           // [HB][4][16 lo][32 q]
     float* ph = pl + kPairHB * 4 * 16 * kTileWords;       // [LB][4][16 hi][32 q]
     __syncthreads();  // every thread has flushed its bins
+    if (!SW) {
 #pragma unroll
-    for (int c = 0; c < kPairSL; ++c) {
-      float s = 0.0f;
+      for (int c = 0; c < kPairSL; ++c) {
+        float s = 0.0f;
 #pragma unroll
-      for (int a = 0; a < kPairSH; ++a) s += acc[a][c];
-      pl[((fh * 4 + fp) * 16 + fl * kPairSL + c) * kTileWords + fq] = s * unscale;
+        for (int a = 0; a < (SW ? 1 : kPairSH); ++a) s += acc[a][c];
+        csum[c] = s;
+      }
+#pragma unroll
+      for (int a = 0; a < kPairSH; ++a) {
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < (SW ? 1 : kPairSL); ++c) s += acc[a][c];
+        rsum[a] = s;
+      }
     }
 #pragma unroll
-    for (int a = 0; a < kPairSH; ++a) {
-      float s = 0.0f;
+    for (int c = 0; c < kPairSL; ++c)
+      pl[((fh * 4 + fp) * 16 + fl * kPairSL + c) * kTileWords + fq] = csum[c] * unscale;
 #pragma unroll
-      for (int c = 0; c < kPairSL; ++c) s += acc[a][c];
-      ph[((fl * 4 + fp) * 16 + fh * kPairSH + a) * kTileWords + fq] = s * unscale;
-    }
+    for (int a = 0; a < kPairSH; ++a)
+      ph[((fl * 4 + fp) * 16 + fh * kPairSH + a) * kTileWords + fq] = rsum[a] * unscale;
     __syncthreads();
     float sv[kSPer];
 #pragma unroll
@@ -634,13 +709,16 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       }
       sv[j] = v;
     }
-    float* ss = reinterpret_cast<float*>(sx);  // [e][n8][q]
+    // S as [e][n8][q ^ 4 n8]: the writes (lanes = word columns) and the output
+    // reads (a wave's 16 adjacent groups: 8 nibbles x 2 columns) each hit
+    // distinct banks
+    float* ss = reinterpret_cast<float*>(sx);
     if (gridDim.y == 1) {
 #pragma unroll
       for (int j = 0; j < kSPer; ++j) {
         const uint32_t s_ = ft + j * kPairThreads;
         const uint32_t qq = s_ % kTileWords, rest = s_ / kTileWords;
-        ss[((rest % 16) * 8 + rest / 16) * kTileWords + qq] = sv[j];
+        ss[((rest % 16) * 8 + rest / 16) * kTileWords + (qq ^ (4 * (rest / 16)))] = sv[j];
       }
     } else {
       // the finish kernel's [j][e] with j = 8 qq + n8
@@ -670,7 +748,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       bool bad = false;
       for (uint32_t e = ft; e < groups * (G / 4); e += kPairThreads) {
         const uint32_t j = e / (G / 4);
-        const float* sj = ss + (j % 8) * kTileWords + j / 8;
+        const float* sj = ss + (j % 8) * kTileWords + ((j / 8) ^ (4 * (j % 8)));
         float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (uint32_t c = 0; c < 16; ++c) {
@@ -690,6 +768,10 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       }
       if (__any(bad) && (ft % warpSize) == 0) atomicOr(o.status, 1u);
     }
+    // S lives in the staging area and pl/ph were read before the last barrier
+#pragma unroll
+    for (uint32_t i = 0; i < kPairBins / (4 * kPairThreads); ++i)
+      bins4[ft + i * kPairThreads] = make_int4(0, 0, 0, 0);
   }
 }
 
@@ -1131,17 +1213,25 @@ hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k
   zc = zc < o.count ? zc : o.count;
   const size_t shmem = pairs_shmem(G);
   const bool one_window = ks <= kPairWindow;
-  const void* fn = one_window ? reinterpret_cast<const void*>(&k_gemv_pairs<G, AD, true>)
-                              : reinterpret_cast<const void*>(&k_gemv_pairs<G, AD, false>);
+  // 16-byte loads need rows of whole tiles (then every chunk is 16-byte aligned)
+  const bool x4 = (n / (8 * G)) % kTileWords == 0;
+  const void* fn = one_window
+      ? (x4 ? reinterpret_cast<const void*>(&k_gemv_pairs<G, AD, true, true>)
+            : reinterpret_cast<const void*>(&k_gemv_pairs<G, AD, true, false>))
+      : (x4 ? reinterpret_cast<const void*>(&k_gemv_pairs<G, AD, false, true>)
+            : reinterpret_cast<const void*>(&k_gemv_pairs<G, AD, false, false>));
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
   if (e != hipSuccess) return e;
   dim3 grid(tiles, splits, zc);
-  if (one_window)
-    k_gemv_pairs<G, AD, true><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks,
-                                                                static_cast<float*>(workspace));
+  float* ws = static_cast<float*>(workspace);
+  if (one_window && x4)
+    k_gemv_pairs<G, AD, true, true><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws);
+  else if (one_window)
+    k_gemv_pairs<G, AD, true, false><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws);
+  else if (x4)
+    k_gemv_pairs<G, AD, false, true><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws);
   else
-    k_gemv_pairs<G, AD, false><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks,
-                                                                 static_cast<float*>(workspace));
+    k_gemv_pairs<G, AD, false, false><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || splits == 1) return err;
   dim3 fgrid(tiles * kFinishParts, 1, zc);
