@@ -285,7 +285,6 @@ constexpr int kPairThreads = 512;
 constexpr int kPairWaves = kPairThreads / 64;
 constexpr int kPairR = 16;                                          // rows per lane per batch
 constexpr int kPairD = 4;                                           // batches in the ring
-constexpr int kPairDX4 = 4;  // X4, one window: x takes 8 registers, and no accumulators
 constexpr uint32_t kPairBatchRows = kPairWaves * 2 * kPairR;        // 256 rows per batch
 constexpr uint32_t kPairBins = 256 * 4 * kTileWords;                // 32768
 constexpr uint32_t kPairXRows = 4096;                               // staged x rows (16 KiB)
@@ -313,6 +312,17 @@ struct PairLds {
 
 __device__ __forceinline__ uint32_t pair_dword(uint32_t v, uint32_t p, uint32_t q) {
   return (p >> 1) * 16384 + v * 64 + (p & 1) * 32 + q;
+}
+
+// Finalise partials pl/ph: [half][p][e][q ^ (2 (e & 3) + 8 p)]. The writes
+// (lanes = word columns q) and the product's reads (a wave's 16 groups x 4
+// codes: q's low bit, p and e & 3 vary) each spread over all 32 banks.
+constexpr uint32_t kPairPartWords = (kPairHB + kPairLB) * 4 * 16 * kTileWords;  // pl, ph: 8192
+constexpr uint32_t kPairTiles16 = kTileGroups / 16;               // 16-group product tiles
+static_assert(kPairHB == 2 && kPairLB == 2, "the product sums two partials per S entry");
+static_assert(kPairPartWords % (4 * kPairThreads) == 0 && kPairPartWords <= kPairBins, "pl/ph clears");
+__device__ __forceinline__ uint32_t pair_part(uint32_t half, uint32_t p, uint32_t e, uint32_t q) {
+  return ((half * 4 + p) * 16 + e) * kTileWords + (q ^ (2 * (e & 3u) + 8 * p));
 }
 
 // Largest of the wave's values, for values that are >= 0 and not NaN (their
@@ -354,7 +364,7 @@ template <int G, bool AD, bool SW, bool X4>
 __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint32_t n,
                                                                 uint32_t k, uint32_t ks,
                                                                 float* partial) {
-  constexpr uint32_t R = kPairR, D = (X4 && SW) ? kPairDX4 : kPairD, BR = kPairBatchRows;
+  constexpr uint32_t R = kPairR, D = kPairD, BR = kPairBatchRows;
   constexpr int kSPer = 16 * kTileGroups / kPairThreads;
   static_assert(16 * G <= kPairThreads, "one book entry per thread");
   static_assert(D % 2 == 0, "x buffers alternate by batch parity");
@@ -616,6 +626,10 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       if (st % 64 == 0) rmax[st / 64] = m;
     }
     __syncthreads();
+    // the previous instance's pl/ph (the first kPairPartWords bins) are read
+#pragma unroll
+    for (uint32_t i = 0; i < kPairPartWords / (4 * kPairThreads); ++i)
+      bins4[st + i * kPairThreads] = make_int4(0, 0, 0, 0);
     if (tile == 0 && split == 0) sweep_books(AD ? bb : af, bb, 16 * G, o.status);
     float amax = 0.0f;
 #pragma unroll
@@ -665,8 +679,8 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     const uint32_t fq = ft % kTileWords, fc = ft / kTileWords;
     const uint32_t fp = fc % 4, fs = fc / 4;
     const uint32_t fh = fs % kPairHB, fl = fs / kPairHB;
-    float* pl = reinterpret_cast<float*>(smem);           // [HB][4][16 lo][32 q]
-    float* ph = pl + kPairHB * 4 * 16 * kTileWords;       // [LB][4][16 hi][32 q]
+    float* pl = reinterpret_cast<float*>(smem);           // [HB][4][16 lo][32 q], swizzled
+    float* ph = pl + kPairHB * 4 * 16 * kTileWords;       // [LB][4][16 hi][32 q], swizzled
     __syncthreads();  // every thread has flushed its bins
     if (!SW) {
 #pragma unroll
@@ -686,91 +700,130 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     }
 #pragma unroll
     for (int c = 0; c < kPairSL; ++c)
-      pl[((fh * 4 + fp) * 16 + fl * kPairSL + c) * kTileWords + fq] = csum[c] * unscale;
+      pl[pair_part(fh, fp, fl * kPairSL + c, fq)] = csum[c] * unscale;
 #pragma unroll
     for (int a = 0; a < kPairSH; ++a)
-      ph[((fl * 4 + fp) * 16 + fh * kPairSH + a) * kTileWords + fq] = rsum[a] * unscale;
+      ph[pair_part(fl, fp, fh * kPairSH + a, fq)] = rsum[a] * unscale;
     __syncthreads();
-    float sv[kSPer];
+    const uint32_t groups = (rw - tile * kTileWords) < kTileWords ? (rw - tile * kTileWords) * 8
+                                                                 : kTileGroups;
+    float* out = item_ptr_mut<float>(o.out, o.stride[4], item) + tile * kTileGroups * G;
+    if (G == 16 && gridDim.y == 1) {
+      // y^T = C_B^T . S^T on v_mfma_f32_16x16x4f32, 16 groups per tile and
+      // 4 codes per step; S = the two partials of pl (even nibbles) or ph (odd
+      // nibbles), each its own product. Lane l: A = C_B[4 ks + l/16][l % 16],
+      // B = partial of group 16 tile + l % 16 at code 4 ks + l/16; it ends with
+      // y[16 tile + l % 16][4 (l/16) .. 4 (l/16) + 3].
+      const uint32_t lane16 = ft % 16, k4 = (ft % 64) / 16;
+      float bk[4];
 #pragma unroll
-    for (int j = 0; j < kSPer; ++j) {
-      // S entry (e, nibble n8 = 2 p + kind, word column qq)
-      const uint32_t s_ = ft + j * kPairThreads;
-      const uint32_t qq = s_ % kTileWords, rest = s_ / kTileWords;
-      const uint32_t e = rest % 16, n8 = rest / 16;
-      const uint32_t pp_ = n8 / 2;
-      float v = 0.0f;
-      if ((n8 & 1u) == 0) {
-#pragma unroll
-        for (int h = 0; h < kPairHB; ++h) v += pl[((h * 4 + pp_) * 16 + e) * kTileWords + qq];
-      } else {
-#pragma unroll
-        for (int l = 0; l < kPairLB; ++l) v += ph[((l * 4 + pp_) * 16 + e) * kTileWords + qq];
-      }
-      sv[j] = v;
-    }
-    // S as [e][n8][q ^ 4 n8]: the writes (lanes = word columns) and the output
-    // reads (a wave's 16 adjacent groups: 8 nibbles x 2 columns) each hit
-    // distinct banks
-    float* ss = reinterpret_cast<float*>(sx);
-    if (gridDim.y == 1) {
-#pragma unroll
-      for (int j = 0; j < kSPer; ++j) {
-        const uint32_t s_ = ft + j * kPairThreads;
-        const uint32_t qq = s_ % kTileWords, rest = s_ / kTileWords;
-        ss[((rest % 16) * 8 + rest / 16) * kTileWords + (qq ^ (4 * (rest / 16)))] = sv[j];
-      }
-    } else {
-      // the finish kernel's [j][e] with j = 8 qq + n8
-      float* pp = partial + ((uint64_t(item) * gridDim.x + tile) * gridDim.y + split) *
-                                (16 * kTileGroups);
-#pragma unroll
-      for (int j = 0; j < kSPer; ++j) {
-        const uint32_t s_ = ft + j * kPairThreads;
-        const uint32_t qq = s_ % kTileWords, rest = s_ / kTileWords;
-        pp[(qq * 8 + rest / 16) * 16 + rest % 16] = sv[j];
-      }
-    }
-    __syncthreads();
-    if (gridDim.y == 1) {
-      const uint32_t groups = (rw - tile * kTileWords) < kTileWords
-                                  ? (rw - tile * kTileWords) * 8
-                                  : kTileGroups;
-      // thread ft always takes columns 4 tc .. 4 tc + 3 (tc = ft % (G / 4)) of its
-      // groups: their 16 x 4 book entries stay in registers, and each S value
-      // read serves four outputs
-      const uint32_t tc = ft % (G / 4);
-      float4 cb[16];
-#pragma unroll
-      for (uint32_t c = 0; c < 16; ++c) cb[c] = *reinterpret_cast<const float4*>(bb + c * G + 4 * tc);
-      float* out = item_ptr_mut<float>(o.out, o.stride[4], item) + tile * kTileGroups * G;
-      const bool vec = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+      for (uint32_t ks = 0; ks < 4; ++ks) bk[ks] = bb[(4 * ks + k4) * 16 + lane16];
       bool bad = false;
-      for (uint32_t e = ft; e < groups * (G / 4); e += kPairThreads) {
-        const uint32_t j = e / (G / 4);
-        const float* sj = ss + (j % 8) * kTileWords + ((j / 8) ^ (4 * (j % 8)));
-        float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (uint32_t c = 0; c < 16; ++c) {
-          const float sv_ = sj[c * kTileGroups];
-          y.x = fmaf(cb[c].x, sv_, y.x);
-          y.y = fmaf(cb[c].y, sv_, y.y);
-          y.z = fmaf(cb[c].z, sv_, y.z);
-          y.w = fmaf(cb[c].w, sv_, y.w);
+      for (uint32_t tt = 0; tt < kPairTiles16 / kPairWaves; ++tt) {
+        const uint32_t tile16 = ft / 64 + tt * kPairWaves;
+        if (tile16 * 16 >= groups) break;  // wave-uniform
+        const uint32_t j = tile16 * 16 + lane16;
+        const uint32_t qq = j / 8, n8 = j % 8;
+        const float* part = (n8 & 1u) ? ph : pl;
+        typedef float float4v __attribute__((ext_vector_type(4)));
+        float4v d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (uint32_t h = 0; h < 2; ++h)
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(bk[ks], part[pair_part(h, n8 / 2, 4 * ks + k4, qq)],
+                                                     d, 0, 0, 0);
+        if (j < groups) {
+          float* oy = out + j * 16 + 4 * k4;
+          if ((reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
+            *reinterpret_cast<float4*>(oy) = make_float4(d[0], d[1], d[2], d[3]);
+          } else {
+            oy[0] = d[0]; oy[1] = d[1]; oy[2] = d[2]; oy[3] = d[3];
+          }
+          bad |= !finite_f32(d[0]) || !finite_f32(d[1]) || !finite_f32(d[2]) || !finite_f32(d[3]);
         }
-        float* oy = out + j * G + 4 * tc;
-        if (vec) {
-          *reinterpret_cast<float4*>(oy) = y;
-        } else {
-          oy[0] = y.x; oy[1] = y.y; oy[2] = y.z; oy[3] = y.w;
-        }
-        bad |= !finite_f32(y.x) || !finite_f32(y.y) || !finite_f32(y.z) || !finite_f32(y.w);
       }
       if (__any(bad) && (ft % warpSize) == 0) atomicOr(o.status, 1u);
-    }
-    // S lives in the staging area and pl/ph were read before the last barrier
+    } else {
+      float sv[kSPer];
 #pragma unroll
-    for (uint32_t i = 0; i < kPairBins / (4 * kPairThreads); ++i)
+      for (int j = 0; j < kSPer; ++j) {
+        // S entry (e, nibble n8 = 2 p + kind, word column qq)
+        const uint32_t s_ = ft + j * kPairThreads;
+        const uint32_t qq = s_ % kTileWords, rest = s_ / kTileWords;
+        const uint32_t e = rest % 16, n8 = rest / 16;
+        const uint32_t pp_ = n8 / 2;
+        float v = 0.0f;
+        if ((n8 & 1u) == 0) {
+#pragma unroll
+          for (int h = 0; h < kPairHB; ++h) v += pl[pair_part(h, pp_, e, qq)];
+        } else {
+#pragma unroll
+          for (int l = 0; l < kPairLB; ++l) v += ph[pair_part(l, pp_, e, qq)];
+        }
+        sv[j] = v;
+      }
+      // S as [e][n8][q ^ 4 n8]: the writes (lanes = word columns) and the output
+      // reads (a wave's 16 adjacent groups: 8 nibbles x 2 columns) each hit
+      // distinct banks
+      float* ss = reinterpret_cast<float*>(sx);
+      if (gridDim.y == 1) {
+#pragma unroll
+        for (int j = 0; j < kSPer; ++j) {
+          const uint32_t s_ = ft + j * kPairThreads;
+          const uint32_t qq = s_ % kTileWords, rest = s_ / kTileWords;
+          ss[((rest % 16) * 8 + rest / 16) * kTileWords + (qq ^ (4 * (rest / 16)))] = sv[j];
+        }
+      } else {
+        // the finish kernel's [j][e] with j = 8 qq + n8
+        float* pp = partial + ((uint64_t(item) * gridDim.x + tile) * gridDim.y + split) *
+                                  (16 * kTileGroups);
+#pragma unroll
+        for (int j = 0; j < kSPer; ++j) {
+          const uint32_t s_ = ft + j * kPairThreads;
+          const uint32_t qq = s_ % kTileWords, rest = s_ / kTileWords;
+          pp[(qq * 8 + rest / 16) * 16 + rest % 16] = sv[j];
+        }
+      }
+      __syncthreads();
+      if (gridDim.y == 1) {
+        // thread ft always takes columns 4 tc .. 4 tc + 3 (tc = ft % (G / 4)) of
+        // its groups: their 16 x 4 book entries stay in registers, and each S
+        // value read serves four outputs
+        const uint32_t tc = ft % (G / 4);
+        float4 cb[16];
+#pragma unroll
+        for (uint32_t c = 0; c < 16; ++c) cb[c] = *reinterpret_cast<const float4*>(bb + c * G + 4 * tc);
+        const bool vec = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+        bool bad = false;
+        for (uint32_t e = ft; e < groups * (G / 4); e += kPairThreads) {
+          const uint32_t j = e / (G / 4);
+          const float* sj = ss + (j % 8) * kTileWords + ((j / 8) ^ (4 * (j % 8)));
+          float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+          for (uint32_t c = 0; c < 16; ++c) {
+            const float sv_ = sj[c * kTileGroups];
+            y.x = fmaf(cb[c].x, sv_, y.x);
+            y.y = fmaf(cb[c].y, sv_, y.y);
+            y.z = fmaf(cb[c].z, sv_, y.z);
+            y.w = fmaf(cb[c].w, sv_, y.w);
+          }
+          float* oy = out + j * G + 4 * tc;
+          if (vec) {
+            *reinterpret_cast<float4*>(oy) = y;
+          } else {
+            oy[0] = y.x; oy[1] = y.y; oy[2] = y.z; oy[3] = y.w;
+          }
+          bad |= !finite_f32(y.x) || !finite_f32(y.y) || !finite_f32(y.z) || !finite_f32(y.w);
+        }
+        if (__any(bad) && (ft % warpSize) == 0) atomicOr(o.status, 1u);
+      }
+    }
+    // the bins past pl/ph are free now; pl/ph themselves are cleared after the
+    // next instance's first barrier, when every wave has read them
+#pragma unroll
+    for (uint32_t i = kPairPartWords / (4 * kPairThreads); i < kPairBins / (4 * kPairThreads); ++i)
       bins4[ft + i * kPairThreads] = make_int4(0, 0, 0, 0);
   }
 }
