@@ -236,6 +236,48 @@ def test_gemv_pairs_saturated_window(vqdev, sign):
         assert o.max_rel(out[i], ref) <= TOL
 
 
+@pytest.mark.parametrize("n,k", [(512, 4096), (4096, 512)])
+def test_gemv_pairs_four_instances_per_block(vqdev, oracle, n, k):
+    """1024 instances: each block walks four, and at group 16 the bins are
+    never cleared between them (each instance's sums are differences of
+    cumulative bins). n = 512 covers the one-word loads, n = 4096 the
+    16-byte loads of whole tiles."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(n + k)
+    m, group, count = 1, 16, 1024
+    items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
+    ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
+    say("gemv-pairs four per block", n, k, count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    for i in (0, 1, 255, 256, 511, 700, 1023):
+        ref, _ = oracle.matmul(*items[i], m, n, k, group, 0)
+        assert o.max_rel(out[i], ref) <= TOL
+        assert o.max_rel(out[i], _ref64(items[i], m, n, k, group, 0)) <= TOL
+
+
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_gemv_pairs_saturated_windows_in_sequence(vqdev, sign):
+    """The saturated window four times per block: the cumulative bins pass
+    2^31 several times, and each instance's difference must still be exact."""
+    from oracle import vq4_numpy as o
+    m, n, k, group = 1, 4096, 4096, 16
+    a_book = np.full((16, group), sign * np.nextafter(np.float32(1), np.float32(0)), np.float32)
+    a_codes = o.pack_indices(np.zeros(k // group, np.int64))
+    b_book = (np.arange(16 * group, dtype=np.float32).reshape(16, group) / 256.0).astype(np.float32)
+    b_codes = o.pack_indices(np.full(k * n // group, 0x5A % 16, np.int64))
+    one = (a_codes, a_book, b_codes, b_book)
+    count = 1024
+    ops = tuple(np.tile(a.reshape(-1), count) for a in one)
+    say("gemv-pairs saturated sequence", sign)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    ref = _ref64(one, m, n, k, group, 0)
+    for i in (0, 255, 256, 767, 1023):
+        assert o.max_rel(out[i], ref) <= TOL
+
+
 @pytest.mark.parametrize("m,k,group,flags", [(2, 20000, 8, 0), (8, 20000, 8, 0),
                                              (5, 12000, 16, 1), (6, 700, 32, 0)])
 def test_gemv_rows_split_slices(vqdev, m, k, group, flags):
