@@ -731,13 +731,16 @@ int32_t ack_vq_fit_codebook(const AckDevice* handle, const AckBuffer* values,
   const size_t sample_bytes = round_up(size_t(count) * group * 4);
   const size_t idx_bytes = round_up(count);
   const size_t gap_bytes = round_up(size_t(count) * 17 * 8);
-  if (int32_t rc = ensure_workspace(*dev, sample_bytes + idx_bytes + 256 + gap_bytes)) return rc;
+  const size_t book64_bytes = round_up(size_t(16) * group * 8);
+  if (int32_t rc = ensure_workspace(*dev, sample_bytes + idx_bytes + 256 + gap_bytes + book64_bytes))
+    return rc;
   char* ws = static_cast<char*>(dev->workspace);
   ackvq::FitArgs fit;
   fit.sample = reinterpret_cast<float*>(ws);
   fit.idx = reinterpret_cast<uint8_t*>(ws + sample_bytes);
   fit.flags = reinterpret_cast<uint32_t*>(ws + sample_bytes + idx_bytes);
   fit.gaps = reinterpret_cast<double*>(ws + sample_bytes + idx_bytes + 256);
+  fit.book64 = reinterpret_cast<double*>(ws + sample_bytes + idx_bytes + 256 + gap_bytes);
   fit.book = static_cast<float*>(bufs[2]->ptr);
   fit.count = count;
   fit.complete = complete;
@@ -812,13 +815,16 @@ int32_t ack_vq_adamw_step(const AckDevice* handle, const AckBuffer* b0, const Ac
   const size_t sample_bytes = round_up(size_t(3) * count * g * 4);
   const size_t idx_bytes = round_up(size_t(3) * count);
   const size_t gap_bytes = round_up(size_t(3) * count * 17 * 8);
-  if (int32_t rc = ensure_workspace(*dev, sample_bytes + idx_bytes + 256 + gap_bytes)) return rc;
+  const size_t book64_bytes = round_up(size_t(3) * 16 * g * 8);
+  if (int32_t rc = ensure_workspace(*dev, sample_bytes + idx_bytes + 256 + gap_bytes + book64_bytes))
+    return rc;
   char* ws = static_cast<char*>(dev->workspace);
   ackvq::FitArgs fit;
   fit.sample = reinterpret_cast<float*>(ws);
   fit.idx = reinterpret_cast<uint8_t*>(ws + sample_bytes);
   fit.flags = reinterpret_cast<uint32_t*>(ws + sample_bytes + idx_bytes);
   fit.gaps = reinterpret_cast<double*>(ws + sample_bytes + idx_bytes + 256);
+  fit.book64 = reinterpret_cast<double*>(ws + sample_bytes + idx_bytes + 256 + gap_bytes);
   fit.book = static_cast<float*>(bufs[4]->ptr);
   fit.count = count;
   fit.complete = complete;

@@ -53,5 +53,40 @@ __device__ __forceinline__ uint32_t nearest64(const double (&x)[G], const double
   return sel;
 }
 
+// One entry's float64 distance, in nearest64's order of operations.
+template <int G>
+__device__ __forceinline__ double dist64(const double (&x)[G], const double* c) {
+  double d = 0.0;
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    const double delta = x[j] - c[j];
+    const double sq = delta * delta;
+    d = d + sq;
+  }
+  return d;
+}
+
+// nearest64 with the book in global memory, read at wave-uniform addresses
+// (scalar loads, no LDS traffic), and a loop over the entries that no lane
+// leaves early: the first NaN distance still wins, through a flag.
+template <int G>
+__device__ __forceinline__ uint32_t nearest64_uniform(const double (&x)[G],
+                                                      const double* __restrict__ book) {
+  double best = 0.0;
+  uint32_t sel = 0;
+  bool done = false;
+#pragma unroll 2
+  for (uint32_t e = 0; e < 16; ++e) {
+    const double d = dist64<G>(x, book + e * G);
+    const bool nan = d != d;
+    if (!done && (e == 0 || nan || d < best)) {
+      best = d;
+      sel = e;
+    }
+    done = done || nan;
+  }
+  return sel;
+}
+
 }  // namespace fitdev
 }  // namespace ackvq

@@ -94,6 +94,7 @@ struct FitArgs {
   float* book = nullptr;
   uint32_t* flags = nullptr;
   double* gaps = nullptr;
+  double* book64 = nullptr;   // float64 copy of the books for the keep pass (problems x 16 x group)
   uint32_t count = 0;         // sample vectors per problem
   uint64_t complete = 0;      // complete vectors of the tensor being fitted
   uint32_t* status = nullptr;

@@ -339,17 +339,23 @@ __global__ __launch_bounds__(kThreads) void k_adamw_gather(AdamwInputs in, uint3
 }
 
 // The fit's keep pass over the recomputed states: for each state whose fit
-// set its keep-pass switch, the entries its complete vectors select under
-// the float64 rule. AdamW is evaluated once per element for all three.
+// set its keep-pass switch, which of its candidate entries (empty in the
+// sample, not duplicates; the only bits the update reads) its complete
+// vectors select under the float64 rule. AdamW is evaluated once per element
+// for all three.
 template <int G>
 __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs a) {
   const uint32_t active = (a.flags[2] ? 1u : 0u) | (a.flags[6] ? 2u : 0u) |
                           (a.flags[10] ? 4u : 0u);
   if (active == 0) return;
+  const double* __restrict__ book64 = a.book64;  // written by the decide kernel
+  const uint32_t cand[3] = {a.flags[3], a.flags[7], a.flags[11]};
   __shared__ double sbook[3 * 16 * G];
   __shared__ float sold[4 * 16 * G];
-  for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) sbook[i] = double(a.book[i]);
+  __shared__ uint32_t bused[3];
+  for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) sbook[i] = book64[i];
   for (uint32_t i = threadIdx.x; i < 4 * 16 * G; i += kThreads) sold[i] = in.books4[i];
+  if (threadIdx.x < 3) bused[threadIdx.x] = 0;
   __syncthreads();
   const Coeffs c = load_coeffs(in.coeffs);
   if (c.fail) return;  // the gather and encode passes report coefficient failures
@@ -370,14 +376,37 @@ __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs
       x[1][j] = double(r.m);
       x[2][j] = double(r.v);
     }
+    // Only the candidate entries' bits are read. The vector's current code
+    // e0 certifies most vectors at once: a candidate c with d_c > d_e0 is not
+    // the first minimum. Any other outcome (a tie, a closer candidate, a
+    // NaN) takes the full argmin.
 #pragma unroll
-    for (int st = 0; st < 3; ++st)
-      if (active & (1u << st)) used[st] |= 1u << fitdev::nearest64<G>(x[st], sbook + st * 16 * G);
+    for (int st = 0; st < 3; ++st) {
+      if (!(active & (1u << st))) continue;
+      const double* bk = book64 + st * 16 * G;
+      const double d0 = fitdev::dist64<G>(x[st], sbook + (st * 16 + code[st]) * G);
+      bool full = d0 != d0;
+      for (uint32_t bits = cand[st]; bits != 0; bits &= bits - 1) {
+        const double dc = fitdev::dist64<G>(x[st], bk + __builtin_ctz(bits) * G);
+        full |= !(dc > d0);
+      }
+      if (full) used[st] |= 1u << fitdev::nearest64_uniform<G>(x[st], bk);
+    }
   }
+  // One global atomic per block and state, and none when the bits are
+  // already set: every block reports, so atomics on the three words would
+  // otherwise serialise the whole pass.
 #pragma unroll
   for (int st = 0; st < 3; ++st) {
     for (int off = 1; off < warpSize; off <<= 1) used[st] |= __shfl_xor(used[st], off);
-    if (used[st] && (threadIdx.x % warpSize) == 0) atomicOr(&a.flags[st * 4 + 1], used[st]);
+    if (used[st] && (threadIdx.x % warpSize) == 0) atomicOr(&bused[st], used[st]);
+  }
+  __syncthreads();
+  if (threadIdx.x < 3) {
+    const uint32_t mine = bused[threadIdx.x];
+    uint32_t* word = &a.flags[threadIdx.x * 4 + 1];
+    const uint32_t seen = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (mine & ~seen) atomicOr(word, mine);
   }
 }
 
@@ -389,8 +418,10 @@ __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const
                                                            uint32_t* status) {
   __shared__ float sbook[3 * 16 * G];
   __shared__ float sold[4 * 16 * G];  // the op-3 input books; W's is the old weight book
+  __shared__ uint32_t bflags, bmoved;
   for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) sbook[i] = books3[i];
   for (uint32_t i = threadIdx.x; i < 4 * 16 * G; i += kThreads) sold[i] = in.books4[i];
+  if (threadIdx.x == 0) bflags = bmoved = 0;
   if (blockIdx.x == 0) sweep_book(books3, 3 * 16 * G, status);
   __syncthreads();
   const Coeffs c = load_coeffs(in.coeffs);
@@ -450,9 +481,15 @@ __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const
     flags |= __shfl_xor(flags, off);
     moved += __shfl_xor(moved, off);
   }
+  // one global atomic per block, not per wave (every block counts moves)
   if ((threadIdx.x % warpSize) == 0) {
-    if (flags) atomicOr(status, flags);
-    if (moved) atomicAdd(changed, moved);
+    if (flags) atomicOr(&bflags, flags);
+    if (moved) atomicAdd(&bmoved, moved);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (bflags) atomicOr(status, bflags);
+    if (bmoved) atomicAdd(changed, bmoved);
   }
 }
 

@@ -133,8 +133,14 @@ __global__ __launch_bounds__(64) void k_fit_decide(FitArgs a) {
     }
     candidate = !duplicate;
   }
-  const bool reachable = __any(candidate);
-  if (threadIdx.x == 0) a.flags[p * 4 + 2] = reachable ? 1u : 0u;
+  // lanes 0-15 are the entries; the keep pass needs only the candidates
+  const uint32_t candidates = uint32_t(__ballot(candidate) & 0xffffu);
+  if (threadIdx.x == 0) {
+    a.flags[p * 4 + 2] = candidates != 0 ? 1u : 0u;
+    a.flags[p * 4 + 3] = candidates;
+  }
+  // the keep pass reads the book as float64 from here
+  for (uint32_t i = threadIdx.x; i < 16 * G; i += blockDim.x) a.book64[p * 16 * G + i] = double(book[i]);
 }
 
 // The keep pass over a dense tensor (one problem): entries its complete
@@ -142,8 +148,9 @@ __global__ __launch_bounds__(64) void k_fit_decide(FitArgs a) {
 template <int G>
 __global__ __launch_bounds__(256) void k_fit_keep_dense(FitArgs a, const float* values) {
   if (a.flags[2] == 0) return;
-  __shared__ double sbook[16 * G];
-  load_book64<G>(a.book, sbook);
+  const double* __restrict__ book64 = a.book64;
+  __shared__ uint32_t bused;
+  if (threadIdx.x == 0) bused = 0;
   __syncthreads();
   uint32_t used = 0;
   for (uint64_t v = uint64_t(blockIdx.x) * 256 + threadIdx.x; v < a.complete;
@@ -151,10 +158,16 @@ __global__ __launch_bounds__(256) void k_fit_keep_dense(FitArgs a, const float* 
     double x[G];
 #pragma unroll
     for (int j = 0; j < G; ++j) x[j] = double(values[v * G + j]);
-    used |= 1u << nearest64<G>(x, sbook);
+    used |= 1u << fitdev::nearest64_uniform<G>(x, book64);
   }
+  // one global atomic per block, and none when its bits are already set
   for (int off = 1; off < warpSize; off <<= 1) used |= __shfl_xor(used, off);
-  if (used && (threadIdx.x % warpSize) == 0) atomicOr(&a.flags[1], used);
+  if (used && (threadIdx.x % warpSize) == 0) atomicOr(&bused, used);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t seen = __hip_atomic_load(&a.flags[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (bused & ~seen) atomicOr(&a.flags[1], bused);
+  }
 }
 
 // numpy's pairwise sum of the G >= 8 squared differences (G a multiple of
