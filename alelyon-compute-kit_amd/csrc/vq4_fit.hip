@@ -36,7 +36,8 @@ using fitdev::nearest64;
 
 constexpr uint32_t kAssignThreads = 256;
 constexpr uint32_t kUpdateThreads = 1024;  // 16 waves: wave e owns entry e
-constexpr uint32_t kStageBytes = 32768;     // sample rows staged per round in update
+constexpr uint32_t kStageBytes = 131072;    // sample rows staged per round in update (all of a
+                                             // 4,096-vector group-8 sample)
 
 __device__ __forceinline__ bool finite_f32(float x) { return fabsf(x) <= FLT_MAX; }
 
@@ -185,28 +186,46 @@ __device__ __forceinline__ double pairwise_gap(const float (&x)[G], const float*
   return ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
 }
 
-struct Far {
-  double gap;
-  uint32_t row;  // 0xffffffff: none
-  uint32_t nan;
-};
-
-// The argmax rule of vq.py:257 as a commutative choice: the first NaN if
-// any, else the largest gap, ties to the lower row.
-__device__ __forceinline__ Far farther(Far a, Far b) {
-  if (a.row == 0xffffffffu) return b;
-  if (b.row == 0xffffffffu) return a;
-  if (a.nan != b.nan) return a.nan ? a : b;
-  if (a.nan) return a.row < b.row ? a : b;
-  if (a.gap != b.gap) return a.gap > b.gap ? a : b;
-  return a.row < b.row ? a : b;
-}
-
 // The gap rule of vq.py:254-256 as a combination: a NaN distance wins, else
 // the smaller one. Gaps are sums of squares, never -0, so the result does not
 // depend on the order entries are combined in.
 __device__ __forceinline__ double nanmin(double a, double b) {
   return a != a ? a : (b != b ? b : (b < a ? b : a));
+}
+
+// The argmax rule of vq.py:257 (the first NaN if any, else the largest gap,
+// ties to the lower row) on integer keys: a gap is >= +0 (a sum of squares)
+// or NaN, so its bit pattern orders as the value, and NaN maps above every
+// gap; equal keys go to the lower row. "None" is key 0 with row 0xffffffff,
+// which any row beats.
+struct FarKey {
+  uint64_t key;
+  uint32_t row;
+};
+__device__ __forceinline__ uint64_t far_key(double gap) {
+  return gap != gap ? ~0ull : uint64_t(__double_as_longlong(gap));
+}
+__device__ __forceinline__ FarKey farther_key(FarKey a, FarKey b) {
+  return (a.key > b.key || (a.key == b.key && a.row < b.row)) ? a : b;
+}
+__device__ __forceinline__ FarKey shfl_xor_key(FarKey v, int off) {
+  FarKey o;
+  o.key = uint64_t(__shfl_xor(static_cast<unsigned long long>(v.key), off));
+  o.row = uint32_t(__shfl_xor(int(v.row), off));
+  return o;
+}
+// The block's farthest row: a butterfly within each wave, then one over the
+// 16 wave results; every thread returns the same row.
+__device__ __forceinline__ uint32_t block_farthest(FarKey best, FarKey* scratch) {
+  for (int off = 1; off < warpSize; off <<= 1) best = farther_key(best, shfl_xor_key(best, off));
+  const uint32_t lane = threadIdx.x % warpSize;
+  if (lane == 0) scratch[threadIdx.x / warpSize] = best;
+  __syncthreads();
+  constexpr uint32_t kWaves = kUpdateThreads / 64;
+  FarKey all = lane < kWaves ? scratch[lane] : FarKey{0, 0xffffffffu};
+  for (int off = 1; off < int(kWaves); off <<= 1) all = farther_key(all, shfl_xor_key(all, off));
+  __syncthreads();  // scratch is reused by the next reseed
+  return uint32_t(__shfl(int(all.row), 0));
 }
 
 // _reseed (vq.py:232-257) of entry e for the whole block: the sample row whose
@@ -222,8 +241,8 @@ __device__ __forceinline__ double nanmin(double a, double b) {
 template <int G>
 __device__ uint32_t reseed_row(const float* sample, uint32_t count, const float* cur,
                                uint32_t e, uint32_t done, bool first, double* near,
-                               double* suffix, Far* scratch) {
-  Far best{0.0, 0xffffffffu, 0};
+                               double* suffix, FarKey* scratch) {
+  FarKey best{0, 0xffffffffu};
   const double inf = __longlong_as_double(0x7ff0000000000000ll);
   for (uint32_t i = threadIdx.x; i < count; i += kUpdateThreads) {
     float x[G];
@@ -250,34 +269,80 @@ __device__ uint32_t reseed_row(const float* sample, uint32_t count, const float*
       hi = suffix[uint64_t(e) * count + i];
     }
     const double gap = nanmin(lo, hi);
-    best = farther(best, Far{gap, i, gap != gap ? 1u : 0u});
+    best = farther_key(best, FarKey{far_key(gap), i});
   }
-  for (int off = 1; off < warpSize; off <<= 1) {
-    Far o;
-    o.gap = __shfl_xor(best.gap, off);
-    o.row = __shfl_xor(best.row, off);
-    o.nan = __shfl_xor(best.nan, off);
-    best = farther(best, o);
+  return block_farthest(best, scratch);
+}
+
+// reseed_row for samples of at most kRegRows rows per thread: each thread
+// keeps near[] of its rows (t, t + kUpdateThreads, ...) in registers across
+// the iteration's reseeds, and a later reseed issues its suffix reads before
+// any gap arithmetic. Same rows, same values, same choice as reseed_row.
+constexpr uint32_t kRegRows = 4;
+template <int G>
+__device__ uint32_t reseed_row_regs(const float* sample, uint32_t count, const float* cur,
+                                    uint32_t e, uint32_t done, bool first,
+                                    double (&near_r)[kRegRows], double* suffix, FarKey* scratch) {
+  static_assert(G == 8, "four rows of a wider group do not fit in registers");
+  FarKey best{0, 0xffffffffu};
+  const double inf = __longlong_as_double(0x7ff0000000000000ll);
+  double hi_r[kRegRows];
+  if (!first) {
+#pragma unroll
+    for (uint32_t r = 0; r < kRegRows; ++r) {
+      const uint32_t i = threadIdx.x + r * kUpdateThreads;
+      hi_r[r] = i < count ? suffix[uint64_t(e) * count + i] : inf;
+    }
   }
-  const uint32_t wave = threadIdx.x / warpSize;
-  if (threadIdx.x % warpSize == 0) scratch[wave] = best;
-  __syncthreads();
-  Far all = scratch[0];
-  for (uint32_t w = 1; w < kUpdateThreads / warpSize; ++w) all = farther(all, scratch[w]);
-  __syncthreads();  // scratch is reused by the next reseed
-  return all.row;
+#pragma unroll
+  for (uint32_t r = 0; r < kRegRows; ++r) {
+    const uint32_t i = threadIdx.x + r * kUpdateThreads;
+    if (i >= count) break;
+    float x[G];
+    const float4* row = reinterpret_cast<const float4*>(sample + uint64_t(i) * G);
+#pragma unroll
+    for (int q = 0; q < G / 4; ++q) {
+      const float4 v = row[q];
+      x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+    }
+    double lo = first ? inf : near_r[r];
+#pragma unroll 1
+    for (uint32_t ee = first ? 0 : done; ee < e; ++ee)
+      lo = nanmin(lo, pairwise_gap<G>(x, cur + ee * G));
+    near_r[r] = lo;
+    double hi;
+    if (first) {
+      hi = inf;
+#pragma unroll 1
+      for (uint32_t ee = 16; ee-- > e;) {
+        hi = nanmin(pairwise_gap<G>(x, cur + ee * G), hi);
+        if (ee > e) suffix[uint64_t(ee) * count + i] = hi;
+      }
+    } else {
+      hi = hi_r[r];
+    }
+    const double gap = nanmin(lo, hi);
+    best = farther_key(best, FarKey{far_key(gap), i});
+  }
+  return block_farthest(best, scratch);
 }
 
 // Means and reseeds of one iteration (vq.py:223-229). One block per problem.
 template <int G>
 __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
   constexpr uint32_t kRows = kStageBytes / (4 * G);  // rows per staged round
+  constexpr uint32_t kBlocks = kRows / 64;            // 64-row blocks per staged round
+  static_assert(kRows % 64 == 0 && kBlocks <= 64, "one lane per block in the offset scan");
   __shared__ float4 xs4[kStageBytes / 16];
   __shared__ uint8_t ids[kRows];
+  __shared__ uint16_t order[kRows];                   // the round's rows, grouped by entry
+  __shared__ uint16_t bcount[kBlocks * 16];           // members of entry e in block b
+  __shared__ uint16_t bstart[kBlocks * 16];           // where they go in `order`
+  __shared__ uint32_t etotal[16];
   __shared__ float cur[16 * G];
   __shared__ float mean[16 * G];
   __shared__ uint32_t members[16];
-  __shared__ Far scratch[kUpdateThreads / 64];
+  __shared__ FarKey scratch[kUpdateThreads / 64];
 
   const uint32_t p = blockIdx.x;
   const uint32_t t = threadIdx.x;
@@ -302,32 +367,75 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
     for (uint32_t q = t; q < rows * G / 4; q += kUpdateThreads) xs4[q] = src[q];
     for (uint32_t q = t; q < rows; q += kUpdateThreads) ids[q] = idx[c0 + q];
     __syncthreads();
-    for (uint32_t sb = 0; sb < rows; sb += 64) {
-      const uint32_t r = sb + lane;
-      uint64_t bits = __ballot(r < rows && ids[r] == wave);
-      n += __popcll(bits);
-      const float* block = xs + sb * G;
-      const uint32_t j = lane < G ? lane : 0;
-      while (bits) {
-        const uint32_t b0 = __builtin_ctzll(bits);
-        bits &= bits - 1;
-        const bool h1 = bits != 0;
-        const uint32_t b1 = h1 ? __builtin_ctzll(bits) : b0;
-        bits &= bits - 1;
-        const bool h2 = bits != 0;
-        const uint32_t b2 = h2 ? __builtin_ctzll(bits) : b0;
-        bits &= bits - 1;
-        const bool h3 = bits != 0;
-        const uint32_t b3 = h3 ? __builtin_ctzll(bits) : b0;
-        bits &= bits - 1;
-        const float x0 = block[b0 * G + j], x1 = block[b1 * G + j];
-        const float x2 = block[b2 * G + j], x3 = block[b3 * G + j];
-        sum = sum + double(x0);
-        sum = sum + (h1 ? double(x1) : 0.0);
-        sum = sum + (h2 ? double(x2) : 0.0);
-        sum = sum + (h3 ? double(x3) : 0.0);
+    // A stable counting sort of the round's rows by entry, then wave e adds
+    // its members' values in sample order, 16 per round trip.
+    const uint32_t nblk = (rows + 63) / 64;
+    for (uint32_t b = wave; b < nblk; b += 16) {  // counts: one wave per block
+      const uint32_t r = b * 64 + lane;
+      const uint32_t id = r < rows ? ids[r] : 16u;
+      uint32_t mine = 0;
+#pragma unroll
+      for (uint32_t e = 0; e < 16; ++e) {
+        const uint32_t c = __popcll(__ballot(id == e));
+        mine = lane == e ? c : mine;
       }
+      if (lane < 16) bcount[b * 16 + lane] = uint16_t(mine);
     }
+    __syncthreads();
+    uint32_t before = 0;  // wave e: members of entry e in the blocks before lane's
+    {
+      const uint32_t c = lane < nblk ? bcount[lane * 16 + wave] : 0u;
+      uint32_t incl = c;
+#pragma unroll
+      for (uint32_t off = 1; off < 64; off <<= 1) {
+        const uint32_t o = uint32_t(__shfl_up(int(incl), off));
+        incl += lane >= off ? o : 0u;
+      }
+      before = incl - c;
+      if (lane == 63) etotal[wave] = incl;
+    }
+    __syncthreads();
+    uint32_t estart = 0;
+    for (uint32_t e = 0; e < wave; ++e) estart += etotal[e];
+    const uint32_t ecount = etotal[wave];
+    if (lane < nblk) bstart[lane * 16 + wave] = uint16_t(estart + before);
+    __syncthreads();
+    for (uint32_t b = wave; b < nblk; b += 16) {  // scatter, in row order within an entry
+      const uint32_t r = b * 64 + lane;
+      const uint32_t id = r < rows ? ids[r] : 16u;
+      uint32_t pos = 0;
+#pragma unroll
+      for (uint32_t e = 0; e < 16; ++e) {
+        const uint64_t bal = __ballot(id == e);
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi(uint32_t(bal >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u));
+        pos = id == e ? rank : pos;
+      }
+      if (id < 16) order[bstart[b * 16 + id] + pos] = uint16_t(r);
+    }
+    __syncthreads();
+    n += ecount;
+    const uint32_t j = lane < G ? lane : 0;
+    // whole batches of 16: the next batch's rows are read before this batch's
+    // additions, which then run unconditionally
+    const uint32_t whole = ecount / 16 * 16;
+    uint32_t rowv[16];
+    if (whole > 0) {
+#pragma unroll
+      for (uint32_t q = 0; q < 16; ++q) rowv[q] = order[estart + q];
+    }
+    for (uint32_t k0 = 0; k0 < whole; k0 += 16) {
+      float xv[16];
+#pragma unroll
+      for (uint32_t q = 0; q < 16; ++q) xv[q] = xs[rowv[q] * G + j];
+      if (k0 + 16 < whole) {
+#pragma unroll
+        for (uint32_t q = 0; q < 16; ++q) rowv[q] = order[estart + k0 + 16 + q];
+      }
+#pragma unroll
+      for (uint32_t q = 0; q < 16; ++q) sum = sum + double(xv[q]);
+    }
+    for (uint32_t k = whole; k < ecount; ++k) sum = sum + double(xs[uint32_t(order[estart + k]) * G + j]);
   }
   if (lane < G && n > 0) mean[wave * G + lane] = float(sum / double(n));
   if (lane == 0) members[wave] = n;
@@ -337,6 +445,7 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
   const uint32_t kept = flags[1];
   double* near = a.gaps + uint64_t(p) * count * 17;
   double* suffix = near + count;
+  double near_r[G == 8 ? kRegRows : 1];
   bool first = true;
   uint32_t done = 0;
   for (uint32_t e = 0; e < 16; ++e) {
@@ -346,8 +455,17 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
     }
     if (kept & (1u << e)) continue;
     __syncthreads();
-    const uint32_t row = reseed_row<G>(sample, count, cur, e, done, first, near, suffix, scratch);
-    if (t < G) cur[e * G + t] = sample[uint64_t(row) * G + t];
+    // the staged rows when they are the whole sample (one staging round)
+    const float* rows_src = count <= kRows ? xs : sample;
+    uint32_t row;
+    if constexpr (G == 8) {  // wider rows do not fit four per thread in registers
+      row = count <= kRegRows * kUpdateThreads
+                ? reseed_row_regs<G>(rows_src, count, cur, e, done, first, near_r, suffix, scratch)
+                : reseed_row<G>(rows_src, count, cur, e, done, first, near, suffix, scratch);
+    } else {
+      row = reseed_row<G>(rows_src, count, cur, e, done, first, near, suffix, scratch);
+    }
+    if (t < G) cur[e * G + t] = rows_src[uint64_t(row) * G + t];
     first = false;
     done = e;
   }
