@@ -339,6 +339,11 @@ __device__ __forceinline__ float wave_max_nonneg(float m) {
   return __int_as_float(r);
 }
 
+// Cache policy of the loads that stream B's codes: non-temporal (the `nt`
+// bit), since every code word is read once. It measured ~7 % faster on the
+// config-3 GEMV than the default policy.
+constexpr int kStreamLoad = 2;
+
 // Buffer descriptor over the first `bytes` of an array: raw buffer loads past
 // it return zero, which is how rows past a slice (or a missing instance) read.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t words_rsrc(const void* base, uint32_t bytes) {
@@ -452,13 +457,13 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     if (X4) {
 #pragma unroll
       for (uint32_t u = 0; u < RX; ++u) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + u * rw * 4u, 0, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + u * rw * 4u, 0, kStreamLoad);
         w[4 * u] = v[0]; w[4 * u + 1] = v[1]; w[4 * u + 2] = v[2]; w[4 * u + 3] = v[3];
       }
     } else {
 #pragma unroll
       for (uint32_t u = 0; u < R; ++u)
-        w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, off + u * rw * 4u, 0, 0));
+        w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, off + u * rw * 4u, 0, kStreamLoad));
     }
   };
 
@@ -993,7 +998,7 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
     asm volatile("" : "+v"(off));
 #pragma unroll
     for (uint32_t u = 0; u < R; ++u)
-      w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, off + u * rw * 4u, 0, 0));
+      w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, off + u * rw * 4u, 0, kStreamLoad));
   };
 
   uint32_t buf[D][R];
