@@ -65,14 +65,17 @@ def test_warm_fit_with_the_keep_pass_equals_the_host_fit(vqdev, group):
 
 
 @pytest.mark.parametrize("group", [8, 16, 32])
-def test_identical_rows_reseed_every_empty_entry(vqdev, group):
+@pytest.mark.parametrize("sample", [4096, 30000])
+def test_identical_rows_reseed_every_empty_entry(vqdev, group, sample):
     """A book of identical rows sends the whole sample to entry 0 and empties
-    the other fifteen, which are reseeded one after another."""
+    the other fifteen, which are reseeded one after another: one 4,096-term
+    in-order mean, then fifteen farthest-row searches. A 30,000-row sample
+    takes several staging rounds and keeps the reseed gaps in memory."""
     rng = np.random.default_rng(100 + group)
     values = (rng.standard_normal(30000 * group) * 0.1).astype(np.float32)
     zero = np.zeros((16, group), np.float32)
-    say("zero-book fit", group)
-    host, dev = _both(vqdev, values, group=group, init=zero)
+    say("zero-book fit", group, sample)
+    host, dev = _both(vqdev, values, group=group, init=zero, sample_vectors=sample)
     np.testing.assert_array_equal(dev, host)
     assert len(np.unique(dev, axis=0)) == 16
 
