@@ -230,6 +230,19 @@ __device__ __forceinline__ AdamwOut adamw_value(float weight, float moment, floa
   return r;
 }
 
+// adamw_value's M' and V' only (the same expressions, so the same bits): they
+// need none of the divisions and the square root behind W'.
+__device__ __forceinline__ void adamw_moments(float weight, float moment, float variance,
+                                              float gradient, const Coeffs& c, float& m, float& v) {
+  const bool inputs_finite =
+      finite_f32(weight) & finite_f32(moment) & finite_f32(variance) & finite_f32(gradient);
+  const float next_m = c.beta1 * moment + (1.0f - c.beta1) * gradient;
+  const float next_v = c.beta2 * variance + (1.0f - c.beta2) * (gradient * gradient);
+  const bool write = inputs_finite & !(variance < 0.0f);
+  m = write ? next_m : 0.0f;
+  v = write ? next_v : 0.0f;
+}
+
 // unpack_state (vq4.comp:74-78) then adamw_value for element i.
 template <int G>
 __device__ __forceinline__ AdamwOut adamw_element(const uint32_t* codes4, const float* books4,
@@ -355,12 +368,25 @@ __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs
   if (active == 0) return;
   const double* __restrict__ book64 = a.book64;  // written by the decide kernel
   const uint32_t cand[3] = {a.flags[3], a.flags[7], a.flags[11]};
-  __shared__ double sbook[3 * 16 * G];
+  // rows padded to G + 1 doubles, so per-lane row gathers spread over the banks
+  constexpr uint32_t RS = G + 1;
+  __shared__ double sbook[3 * 16 * RS];
+  __shared__ double sgap[3 * 16 * 16];  // ||c - e|| between the entries of each state's book
   __shared__ float sold[4 * 16 * G];
   __shared__ uint32_t bused[3];
-  for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) sbook[i] = book64[i];
+  for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) sbook[(i / G) * RS + i % G] = book64[i];
   for (uint32_t i = threadIdx.x; i < 4 * 16 * G; i += kThreads) sold[i] = in.books4[i];
   if (threadIdx.x < 3) bused[threadIdx.x] = 0;
+  for (uint32_t i = threadIdx.x; i < 3 * 16 * 16; i += kThreads) {
+    const double* b = book64 + (i / 256) * 16 * G;
+    double d = 0.0;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const double t = b[((i / 16) % 16) * G + j] - b[(i % 16) * G + j];
+      d = d + t * t;
+    }
+    sgap[i] = sqrt(d);
+  }
   __syncthreads();
   const Coeffs c = load_coeffs(in.coeffs);
   if (c.fail) return;  // the gather and encode passes report coefficient failures
@@ -372,27 +398,60 @@ __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs
 #pragma unroll
     for (int st = 0; st < 4; ++st) code[st] = nibble(in.codes4 + st * words, v);
     double x[3][G];
+    if (active & 1u) {
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-      const AdamwOut r = adamw_value(sold[code[0] * G + j], sold[(16 + code[1]) * G + j],
-                                     sold[(32 + code[2]) * G + j], sold[(48 + code[3]) * G + j],
-                                     c);
-      x[0][j] = double(r.w);
-      x[1][j] = double(r.m);
-      x[2][j] = double(r.v);
+      for (int j = 0; j < G; ++j) {
+        const AdamwOut r = adamw_value(sold[code[0] * G + j], sold[(16 + code[1]) * G + j],
+                                       sold[(32 + code[2]) * G + j], sold[(48 + code[3]) * G + j],
+                                       c);
+        x[0][j] = double(r.w);
+        x[1][j] = double(r.m);
+        x[2][j] = double(r.v);
+      }
+    } else {  // W's fit needs no pass: skip W' and its divisions
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        float m, v;
+        adamw_moments(sold[code[0] * G + j], sold[(16 + code[1]) * G + j],
+                      sold[(32 + code[2]) * G + j], sold[(48 + code[3]) * G + j], c, m, v);
+        x[0][j] = 0.0;
+        x[1][j] = double(m);
+        x[2][j] = double(v);
+      }
     }
     // Only the candidate entries' bits are read. The vector's current code
     // e0 certifies most vectors at once: a candidate c with d_c > d_e0 is not
-    // the first minimum. Any other outcome (a tie, a closer candidate, a
-    // NaN) takes the full argmin.
+    // the first minimum. ||c - e0|| > 2 ||x - e0|| proves it without d_c
+    // (triangle inequality; the 2e-6 margin dwarfs the float64 rounding of
+    // every distance involved); otherwise d_c is computed. Any other outcome
+    // (a tie, a closer candidate, a non-finite distance) takes the full
+    // argmin.
 #pragma unroll
     for (int st = 0; st < 3; ++st) {
       if (!(active & (1u << st))) continue;
       const double* bk = book64 + st * 16 * G;
-      const double d0 = fitdev::dist64<G>(x[st], sbook + (st * 16 + code[st]) * G);
-      bool full = d0 != d0;
+      // the current code, or, when it is a candidate itself (as for a state
+      // whose codes were all zero), the nearest entry by the first two
+      // components: any entry closer than c certifies it
+      uint32_t e0 = code[st];
+      if (cand[st] & (1u << e0)) {
+        float best = __int_as_float(0x7f800000);
+        for (uint32_t e = 0; e < 16; ++e) {
+          if (cand[st] & (1u << e)) continue;  // wave-uniform
+          const float t0 = float(x[st][0]) - float(sbook[(st * 16 + e) * RS]);
+          const float t1 = float(x[st][1]) - float(sbook[(st * 16 + e) * RS + 1]);
+          const float dd = t0 * t0 + t1 * t1;
+          if (dd < best) { best = dd; e0 = e; }
+        }
+      }
+      const double d0 = fitdev::dist64<G>(x[st], sbook + (st * 16 + e0) * RS);
+      bool full = !(d0 <= 1.7976931348623157e308);  // NaN or infinite
+      const double reach = 2.000002 * sqrt(d0);
+      const double* gap_e0 = sgap + (st * 16) * 16 + e0;
       for (uint32_t bits = cand[st]; bits != 0; bits &= bits - 1) {
-        const double dc = fitdev::dist64<G>(x[st], bk + __builtin_ctz(bits) * G);
+        const uint32_t cidx = __builtin_ctz(bits);
+        if (gap_e0[cidx * 16] > reach) continue;
+        const double dc = fitdev::dist64<G>(x[st], bk + cidx * G);
         full |= !(dc > d0);
       }
       if (full) used[st] |= 1u << fitdev::nearest64_uniform<G>(x[st], bk);
@@ -549,7 +608,11 @@ hipError_t launch_adamw_gather(hipStream_t s, const AdamwInputs& in, uint32_t co
 }
 
 hipError_t launch_adamw_keep(hipStream_t s, const AdamwInputs& in, const FitArgs& a) {
-  dim3 grid(grid_for(in.m / in.group, kThreads));
+  // eight blocks per compute unit, each walking many vectors: the per-block
+  // set-up (books, the entry-gap table) is paid 2,048 times, not once per
+  // 512 vectors
+  const uint32_t blocks = grid_for(in.m / in.group, kThreads);
+  dim3 grid(blocks < 2048u ? blocks : 2048u);
   if (in.group == 8) k_adamw_keep<8><<<grid, kThreads, 0, s>>>(in, a);
   else if (in.group == 16) k_adamw_keep<16><<<grid, kThreads, 0, s>>>(in, a);
   else k_adamw_keep<32><<<grid, kThreads, 0, s>>>(in, a);
