@@ -209,16 +209,21 @@ class ExpertHarness:
         self._residents[(layer, expert)] = res
         return res
 
-    def _device_image(self, values: np.ndarray, group: int, buf, status):
+    def _device_image(self, values: np.ndarray, group: int, buf, status, on_device=None):
         """fit_codebook and encode on the device: the image ``_encode`` makes
-        (the same tiny-batch padding for the fit), left in device buffers."""
+        (the same tiny-batch padding for the fit), left in device buffers.
+        ``on_device``, a buffer already holding ``values`` as float32, saves
+        the upload (tensors of at least one vector need no padding)."""
         flat = values.reshape(-1)
-        sample = flat if flat.size >= group else np.pad(flat, (0, group - flat.size))
-        sample = np.ascontiguousarray(sample, dtype=np.float32)
-        vals = buf(sample.nbytes)
-        vals.upload(sample)
+        if on_device is not None and flat.size >= group:
+            vals, size = on_device, flat.size
+        else:
+            sample = flat if flat.size >= group else np.pad(flat, (0, group - flat.size))
+            sample = np.ascontiguousarray(sample, dtype=np.float32)
+            vals, size = buf(sample.nbytes), sample.size
+            vals.upload(sample)
         book = buf(vq.ENTRIES * group * 4)
-        self.backend.fit_resident(vals, sample.size, book, status, group=group)
+        self.backend.fit_resident(vals, size, book, status, group=group)
         codes = buf(vq.storage_layout(values.shape, group)["code_bytes"])
         self.backend.run((0, flat.size, 1, 1, group, vq.ENTRIES, 0, 0), [vals, book], codes,
                          status)
@@ -288,7 +293,9 @@ class ExpertHarness:
                 raise HarnessError("expert gradient norm is nonfinite")
             scale = min(1.0, max_grad_norm / (norm + 1e-6))
             gradient *= np.float32(scale)
-            gc, gb = self._device_image(gradient, group, buf, status)
+            # unclipped, the device copy is already the gradient to encode
+            gc, gb = self._device_image(gradient, group, buf, status,
+                                        on_device=grad if scale == 1.0 else None)
             res.codes4.copy_from(gc, res.words * 4, offset=3 * res.words * 4)
             res.books4.copy_from(gb, res.book * 4, offset=3 * res.book * 4)
             try:
