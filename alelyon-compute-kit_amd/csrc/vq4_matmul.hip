@@ -297,13 +297,29 @@ static_assert(kPairSH * kPairSL * kPairThreads == int(kPairBins), "every bin flu
 static_assert(kPairThreads / kTileWords == 4 * kPairHB * kPairLB, "thread roles");
 static_assert(kPairXRows >= 16 * kTileGroups, "S reuses the x staging area");
 
+// Cumulative finalise (one window per instance, g <= 16): the bins are never
+// cleared between instances. Each thread keeps the int32 row and column sums
+// its sub-block had at the previous instance's end, and this instance's sums
+// are the differences, exact modulo 2^32 (every window sum is below 2^31 in
+// magnitude). The partials then live past the bins, in the x staging area and
+// the words after it: two halves of the even-nibble sums, then the complete
+// odd-nibble sums (the two row halves meet inside the wave), all int32.
+constexpr uint32_t kCumHalfWords = 4 * 16 * kTileWords;            // [p][e][q ^ swizzle]
+constexpr uint32_t kCumHiBase = 2 * kCumHalfWords + 4;             // bank bit 2 off the halves
+constexpr uint32_t kCumWords = kCumHiBase + kCumHalfWords + 12;    // 6,160 (16-byte multiple)
+static_assert(kCumWords >= kPairXRows && kCumWords % 4 == 0, "the x staging area grows");
+__device__ __forceinline__ uint32_t cum_part(uint32_t p, uint32_t e, uint32_t q) {
+  return (p * 16 + e) * kTileWords + (q ^ (2 * (e & 3u) + 8 * p));
+}
+
 // LDS layout (bytes): bins | staged x (later S) | A book | B book x 2 | A words | row maxima.
 // The B book alternates between two copies by instance, so an instance's
 // set-up need not wait for the previous output phase, the book's only reader.
 template <int G>
 struct PairLds {
+  static constexpr bool cum = G <= 16;  // room for the cumulative partials
   static constexpr uint32_t xs = kPairBins * 4;
-  static constexpr uint32_t af = xs + kPairXRows * 4;
+  static constexpr uint32_t af = xs + (cum ? kCumWords : kPairXRows) * 4;
   static constexpr uint32_t bb = af + 16 * G * 4;
   static constexpr uint32_t aw = bb + 2 * 16 * G * 4;
   static constexpr uint32_t rmax = aw + kPairMaxAWords * 4;
@@ -473,6 +489,12 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   // column sums, formed as the bins are read (the same sums in the same order)
   float acc[SW ? 1 : kPairSH][SW ? 1 : kPairSL];
   float rsum[kPairSH], csum[kPairSL];
+  // cumulative bins: this flush's int32 row and column sums, and the
+  // previous instance's (rows 0..7, columns 8..15)
+  constexpr bool CUM = SW && L::cum;
+  uint32_t rsi[CUM ? kPairSH : 1], csi[CUM ? kPairSL : 1], prv[CUM ? 16 : 1];
+#pragma unroll
+  for (int i = 0; i < (CUM ? 16 : 1); ++i) prv[i] = 0;
   int shift = 0;
   uint32_t xbase = k0;
   __amdgpu_buffer_rsrc_t x_rs = words_rsrc(nullptr, 0u);  // AD: this instance's x[0, kend)
@@ -519,6 +541,21 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   // this thread's sub-block: word column fq, byte position fp, sub-block (fh, fl)
   auto flush = [&](bool clear) __attribute__((always_inline)) {
     const uint32_t ft = opaque(tid);
+    if (CUM) {
+      // half-wave = column half fl, wave = (fp, fh): the two column halves of
+      // a row half are lanes l and l + 32 of one wave
+      const uint32_t cq = ft % kTileWords, cl = (ft / kTileWords) % 2, cw = ft / 64;
+      const uint32_t cp = cw % 4, ch = cw / 4;
+#pragma unroll
+      for (int a = 0; a < kPairSH; ++a)
+#pragma unroll
+        for (int c = 0; c < kPairSL; ++c) {
+          const uint32_t v = uint32_t(bins[pair_dword(16 * (ch * kPairSH + a) + cl * kPairSL + c, cp, cq)]);
+          csi[c] = a == 0 ? v : csi[c] + v;
+          rsi[a] = c == 0 ? v : rsi[a] + v;
+        }
+      return;
+    }
     const uint32_t fq = ft % kTileWords, fc = ft / kTileWords;
     const uint32_t fp = fc % 4, fs = fc / 4;
     const uint32_t fh = fs % kPairHB, fl = fs / kPairHB;
@@ -632,9 +669,11 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     }
     __syncthreads();
     // the previous instance's pl/ph (the first kPairPartWords bins) are read
+    if (!CUM) {
 #pragma unroll
-    for (uint32_t i = 0; i < kPairPartWords / (4 * kPairThreads); ++i)
-      bins4[st + i * kPairThreads] = make_int4(0, 0, 0, 0);
+      for (uint32_t i = 0; i < kPairPartWords / (4 * kPairThreads); ++i)
+        bins4[st + i * kPairThreads] = make_int4(0, 0, 0, 0);
+    }
     if (tile == 0 && split == 0) sweep_books(AD ? bb : af, bb, 16 * G, o.status);
     float amax = 0.0f;
 #pragma unroll
@@ -686,7 +725,34 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     const uint32_t fh = fs % kPairHB, fl = fs / kPairHB;
     float* pl = reinterpret_cast<float*>(smem);           // [HB][4][16 lo][32 q], swizzled
     float* ph = pl + kPairHB * 4 * 16 * kTileWords;       // [LB][4][16 hi][32 q], swizzled
-    __syncthreads();  // every thread has flushed its bins
+    uint32_t* cpt = reinterpret_cast<uint32_t*>(sx);      // cumulative partials
+    if (CUM) {
+      // the flush's mapping: column half cl = half-wave, wave = (cp, ch)
+      const uint32_t cq = ft % kTileWords, cl = (ft / kTileWords) % 2, cw = ft / 64;
+      const uint32_t cp = cw % 4, ch = cw / 4;
+#pragma unroll
+      for (int i = 0; i < kPairSH; ++i) {
+        uint32_t t = rsi[i];
+        rsi[i] = t - prv[i];
+        prv[i] = t;
+        t = csi[i];
+        csi[i] = t - prv[8 + i];
+        prv[8 + i] = t;
+      }
+      // even nibbles: this row half's partial of 8 codes
+#pragma unroll
+      for (int c = 0; c < kPairSL; ++c) cpt[ch * kCumHalfWords + cum_part(cp, cl * 8 + c, cq)] = csi[c];
+      // odd nibbles: v_permlane32_swap trades lanes 32..63 of its first operand
+      // for lanes 0..31 of its second, so lane l (cl = 0) ends with both halves
+      // of row a = i and lane l + 32 (cl = 1) with both of row a = 4 + i
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const auto r = __builtin_amdgcn_permlane32_swap(rsi[i], rsi[4 + i], false, false);
+        cpt[kCumHiBase + cum_part(cp, ch * 8 + cl * 4 + i, cq)] = r[0] + r[1];
+      }
+    } else {
+      __syncthreads();  // every thread has flushed its bins
+    }
     if (!SW) {
 #pragma unroll
       for (int c = 0; c < kPairSL; ++c) {
@@ -703,13 +769,22 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
         rsum[a] = s;
       }
     }
+    if (!CUM) {
 #pragma unroll
-    for (int c = 0; c < kPairSL; ++c)
-      pl[pair_part(fh, fp, fl * kPairSL + c, fq)] = csum[c] * unscale;
+      for (int c = 0; c < kPairSL; ++c)
+        pl[pair_part(fh, fp, fl * kPairSL + c, fq)] = csum[c] * unscale;
 #pragma unroll
-    for (int a = 0; a < kPairSH; ++a)
-      ph[pair_part(fl, fp, fh * kPairSH + a, fq)] = rsum[a] * unscale;
+      for (int a = 0; a < kPairSH; ++a)
+        ph[pair_part(fl, fp, fh * kPairSH + a, fq)] = rsum[a] * unscale;
+    }
     __syncthreads();
+    // S entry (p, e, q) of nibble 2 p + odd, from the cumulative partials
+    auto cum_s = [&](uint32_t p, uint32_t e, uint32_t qq, bool odd) __attribute__((always_inline)) {
+      const uint32_t at = cum_part(p, e, qq);
+      const uint32_t v0 = cpt[(odd ? kCumHiBase : 0u) + at];
+      const uint32_t v1 = cpt[kCumHalfWords + at];  // odd nibbles: read, unused
+      return float(int32_t(odd ? v0 : v0 + v1)) * unscale;
+    };
     const uint32_t groups = (rw - tile * kTileWords) < kTileWords ? (rw - tile * kTileWords) * 8
                                                                  : kTileGroups;
     float* out = item_ptr_mut<float>(o.out, o.stride[4], item) + tile * kTileGroups * G;
@@ -733,12 +808,22 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
         const float* part = (n8 & 1u) ? ph : pl;
         typedef float float4v __attribute__((ext_vector_type(4)));
         float4v d = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (CUM) {
+          // cumulative partials: S itself, one product per code step
+          float sb[4];
 #pragma unroll
-        for (uint32_t ks = 0; ks < 4; ++ks)
+          for (uint32_t ks = 0; ks < 4; ++ks) sb[ks] = cum_s(n8 / 2, 4 * ks + k4, qq, (n8 & 1u) != 0);
 #pragma unroll
-          for (uint32_t h = 0; h < 2; ++h)
-            d = __builtin_amdgcn_mfma_f32_16x16x4f32(bk[ks], part[pair_part(h, n8 / 2, 4 * ks + k4, qq)],
-                                                     d, 0, 0, 0);
+          for (uint32_t ks = 0; ks < 4; ++ks)
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(bk[ks], sb[ks], d, 0, 0, 0);
+        } else {
+#pragma unroll
+          for (uint32_t ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (uint32_t h = 0; h < 2; ++h)
+              d = __builtin_amdgcn_mfma_f32_16x16x4f32(bk[ks], part[pair_part(h, n8 / 2, 4 * ks + k4, qq)],
+                                                       d, 0, 0, 0);
+        }
         if (j < groups) {
           float* oy = out + j * 16 + 4 * k4;
           if ((reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
@@ -760,7 +845,9 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
         const uint32_t e = rest % 16, n8 = rest / 16;
         const uint32_t pp_ = n8 / 2;
         float v = 0.0f;
-        if ((n8 & 1u) == 0) {
+        if (CUM) {
+          v = cum_s(pp_, e, qq, (n8 & 1u) != 0);
+        } else if ((n8 & 1u) == 0) {
 #pragma unroll
           for (int h = 0; h < kPairHB; ++h) v += pl[pair_part(h, pp_, e, qq)];
         } else {
@@ -774,6 +861,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       // distinct banks
       float* ss = reinterpret_cast<float*>(sx);
       if (gridDim.y == 1) {
+        if (CUM) __syncthreads();  // S overwrites the cumulative partials
 #pragma unroll
         for (int j = 0; j < kSPer; ++j) {
           const uint32_t s_ = ft + j * kPairThreads;
@@ -827,9 +915,11 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     }
     // the bins past pl/ph are free now; pl/ph themselves are cleared after the
     // next instance's first barrier, when every wave has read them
+    if (!CUM) {
 #pragma unroll
-    for (uint32_t i = kPairPartWords / (4 * kPairThreads); i < kPairBins / (4 * kPairThreads); ++i)
-      bins4[ft + i * kPairThreads] = make_int4(0, 0, 0, 0);
+      for (uint32_t i = kPairPartWords / (4 * kPairThreads); i < kPairBins / (4 * kPairThreads); ++i)
+        bins4[ft + i * kPairThreads] = make_int4(0, 0, 0, 0);
+    }
   }
 }
 
