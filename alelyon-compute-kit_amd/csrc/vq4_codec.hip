@@ -80,6 +80,80 @@ __device__ __forceinline__ uint32_t argmin32(const float (&x)[G], uint32_t valid
   return selected;
 }
 
+// Screen in front of argmin32 for whole vectors: it ranks the codes by
+// A_c = |c|^2 - 2 x.c, one FMA per component from -2c and |c|^2 prepared in
+// LDS, and proves when its best code is also the shader's. With X = |x|^2 and
+// u = 2^-24, the shader's computed distance d_c lies within (G + 2) u D_c of
+// the exact D_c <= 2 (X + |c|^2), and A_c within G u (X + 3.01 |c|^2) of
+// D_c - X, so |A_c + X - d_c| <= 5.01 (G + 2) u (X + |c|^2). E below takes
+// 8 (G + 2) u (xn + cmax), where xn and cmax (the largest |c|^2) are the FP32
+// sums (relative error G u), which also covers the rounding of E and of the
+// gap; 2^-140 bounds the absolute error that subnormal results add (2^-150
+// per operation). If the runner-up's A exceeds the best's by more than 2E,
+// then d(best) < d(c) for every other code: the best is the shader's strict
+// argmin. The screen applies while the book is finite and xn, cmax < 2^120
+// (then every d_c is finite, so no status bit is due); otherwise, or on a
+// narrower gap, the caller runs argmin32.
+struct Screen {
+  const float* m2;  // -2 c, [16][G]
+  const float* cn;  // |c|^2 per code, +inf where the entry is not finite
+  float base;       // 2 E's part from the book: 16 (G + 2) u cmax + 2^-139
+  bool on;
+};
+
+// -2 c and |c|^2 of `books` consecutive 16-entry books; then a barrier.
+template <int G>
+__device__ __forceinline__ void screen_prepare(const float* sbook, float* m2, float* cn,
+                                               uint32_t books) {
+  for (uint32_t i = threadIdx.x; i < books * 16 * G; i += blockDim.x) m2[i] = -2.0f * sbook[i];
+  for (uint32_t t = threadIdx.x; t < books * 16; t += blockDim.x) {
+    float n = 0.0f;
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const float c = sbook[t * G + j];
+      ok &= finite_f32(c);
+      n = fmaf(c, c, n);
+    }
+    cn[t] = ok ? n : __int_as_float(0x7f800000);
+  }
+}
+
+template <int G>
+__device__ __forceinline__ Screen screen_load(const float* m2, const float* cn) {
+  float cmax = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 16; ++t) cmax = fmaxf(cmax, cn[t]);
+  constexpr float k2 = float(16 * (G + 2)) * 0x1p-24f;
+  return Screen{m2, cn, fmaf(k2, cmax, 0x1p-139f), cmax < 0x1p120f};
+}
+
+// The screened code of a whole vector, or kNoScreen when argmin32 must decide.
+constexpr uint32_t kNoScreen = 16;
+template <int G>
+__device__ __forceinline__ uint32_t argmin_screen(const float (&x)[G], const Screen& s) {
+  constexpr float k2 = float(16 * (G + 2)) * 0x1p-24f;
+  float xn = 0.0f;
+#pragma unroll
+  for (int j = 0; j < G; ++j) xn = fmaf(x[j], x[j], xn);
+  float b1 = __int_as_float(0x7f800000), b2 = b1;
+  uint32_t i1 = 0;
+  // 32 book values in flight per step at any G (more spills the fused step's kernel)
+#pragma unroll(32 / G)
+  for (uint32_t code = 0; code < 16; ++code) {
+    const float* c = s.m2 + code * G;
+    float r = s.cn[code];
+#pragma unroll
+    for (int j = 0; j < G; ++j) r = fmaf(x[j], c[j], r);
+    const bool lt = r < b1;
+    b2 = __builtin_amdgcn_fmed3f(b1, b2, r);  // the runner-up (b1 <= b2)
+    b1 = lt ? r : b1;
+    i1 = lt ? code : i1;
+  }
+  const bool proven = s.on && xn < 0x1p120f && (b2 - b1) > fmaf(k2, xn, s.base);
+  return proven ? i1 : kNoScreen;
+}
+
 // OR the nibbles of 8 consecutive lanes into lane (v % 8 == 0)'s word.
 __device__ __forceinline__ uint32_t gather_word(uint32_t part) {
   part |= __shfl_xor(part, 1);
@@ -100,9 +174,14 @@ __global__ __launch_bounds__(kThreads) void k_encode(Operands o, uint32_t m) {
   const float* book = item_ptr<float>(o.in[1], o.stride[1], item);
   uint32_t* out = item_ptr_mut<uint32_t>(o.out, o.stride[4], item);
   __shared__ float sbook[16 * G];
+  __shared__ float sm2[16 * G];
+  __shared__ float scn[16];
   for (uint32_t i = threadIdx.x; i < 16 * G; i += kThreads) sbook[i] = book[i];
   if (blockIdx.x == 0) sweep_book(book, 16 * G, o.status);
   __syncthreads();
+  screen_prepare<G>(sbook, sm2, scn, 1);
+  __syncthreads();
+  const Screen screen = screen_load<G>(sm2, scn);
 
   const uint32_t vectors = m / G + (m % G != 0);
   const uint32_t words = vectors / 8 + (vectors % 8 != 0);
@@ -128,7 +207,8 @@ __global__ __launch_bounds__(kThreads) void k_encode(Operands o, uint32_t m) {
         }
 #pragma unroll
         for (int j = 0; j < G; ++j) bad |= !finite_f32(xv[j]);
-        code = argmin32<G, true>(xv, G, sbook, bad);
+        code = argmin_screen<G>(xv, screen);
+        if (code == kNoScreen) code = argmin32<G, true>(xv, G, sbook, bad);
       } else {
 #pragma unroll
         for (int j = 0; j < G; ++j) {
@@ -482,12 +562,19 @@ __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const
                                                            uint32_t* status) {
   __shared__ float sbook[3 * 16 * G];
   __shared__ float sold[4 * 16 * G];  // the op-3 input books; W's is the old weight book
+  __shared__ float sm2[3 * 16 * G];
+  __shared__ float scn[3 * 16];
   __shared__ uint32_t bflags, bmoved;
   for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) sbook[i] = books3[i];
   for (uint32_t i = threadIdx.x; i < 4 * 16 * G; i += kThreads) sold[i] = in.books4[i];
   if (threadIdx.x == 0) bflags = bmoved = 0;
   if (blockIdx.x == 0) sweep_book(books3, 3 * 16 * G, status);
   __syncthreads();
+  screen_prepare<G>(sbook, sm2, scn, 3);
+  __syncthreads();
+  Screen screen[3];
+#pragma unroll
+  for (int st = 0; st < 3; ++st) screen[st] = screen_load<G>(sm2 + st * 16 * G, scn + st * 16);
   const Coeffs c = load_coeffs(in.coeffs);
   if (c.fail) {
     if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(status, c.fail);
@@ -523,8 +610,10 @@ __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const
       }
       if (valid == G) {
 #pragma unroll
-        for (int st = 0; st < 3; ++st)
-          code[st] = argmin32<G, true>(xs[st], G, sbook + st * 16 * G, bad);
+        for (int st = 0; st < 3; ++st) {
+          code[st] = argmin_screen<G>(xs[st], screen[st]);
+          if (code[st] == kNoScreen) code[st] = argmin32<G, true>(xs[st], G, sbook + st * 16 * G, bad);
+        }
       } else {
 #pragma unroll
         for (int st = 0; st < 3; ++st)

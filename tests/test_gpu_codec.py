@@ -85,6 +85,47 @@ def test_encode_near_ties_and_duplicates(vqdev, oracle, group):
     np.testing.assert_array_equal(out, ref)
 
 
+@pytest.mark.parametrize("group", GROUPS)
+def test_encode_screen_margins(vqdev, oracle, group):
+    """The kernel ranks codes by |c|^2 - 2 x.c and keeps that ranking only
+    when a rounding bound proves it equals the shader's FP32 argmin. Vectors
+    placed at offsets from 1e-9 to 1e-2 on either side of a boundary between
+    two codes, at scales from subnormal squares to just past the 2^120 cut,
+    and a book too large for the screen must all encode bit-exactly."""
+    rng = np.random.default_rng(300 + group)
+    base = rng.standard_normal((16, group)).astype(np.float32)
+    offsets = np.concatenate([-np.logspace(-9, -2, 29), [0.0], np.logspace(-9, -2, 29)])
+    pairs = [(a, b) for a in range(16) for b in range(16) if a < b][::7]
+    for scale in (2.0 ** -70, 2.0 ** -60, 2.0 ** -20, 1.0, 2.0 ** 40, 2.0 ** 57, 2.0 ** 58, 2.0 ** 59):
+        book = (base * np.float32(scale)).astype(np.float32)
+        rows = []
+        for a, b in pairs:
+            mid = (book[a].astype(np.float64) + book[b]) / 2
+            step = book[a].astype(np.float64) - book[b]
+            rows.append(mid[None, :] + offsets[:, None] * step[None, :])
+        x = np.concatenate(rows).astype(np.float32).reshape(-1)
+        # random vectors at the same scale fill out the waves
+        x = np.concatenate([x, (rng.standard_normal(64 * group) * scale).astype(np.float32)])
+        say("encode screen", group, scale)
+        words = -(-(x.size // group) // 8)
+        out, status = run_plan(vqdev, (0, x.size, 1, 1, group, 16, 0, 0), (x, book), 4 * words,
+                               np.uint32)
+        ref, ref_status = oracle.encode(x, book, group)
+        np.testing.assert_array_equal(out, ref)
+        assert status == ref_status
+    # one entry with |c|^2 >= 2^120 turns the screen off for the whole book
+    book = base.copy()
+    book[7] = np.float32(2.0 ** 61)
+    x = rng.standard_normal(200 * group).astype(np.float32)
+    say("encode screen off", group)
+    words = -(-(x.size // group) // 8)
+    out, status = run_plan(vqdev, (0, x.size, 1, 1, group, 16, 0, 0), (x, book), 4 * words,
+                           np.uint32)
+    ref, ref_status = oracle.encode(x, book, group)
+    np.testing.assert_array_equal(out, ref)
+    assert status == ref_status
+
+
 def test_encode_status_bits(vqdev, oracle):
     book = np.zeros((16, 8), np.float32)
     for name, x in (("nan", np.array([1, 2, np.nan, 4, 5, 6, 7, 8, 9], np.float32)),
