@@ -295,6 +295,31 @@ def test_gemv_rows_split_slices(vqdev, m, k, group, flags):
     assert o.max_rel(out, _ref64(ops, m, n, k, group, flags)) <= TOL
 
 
+@pytest.mark.parametrize("m,n,k,group,flags,count", [
+    (4, 4096, 512, 16, 0, 64),      # one tile
+    (3, 2560, 384, 8, 0, 40),       # two tiles, the second 8 words wide
+    (8, 4096, 1024, 32, 0, 70),     # a 16-word tile
+    (2, 4096, 4224, 16, 0, 64),     # one row pair; two windows, restaged activations
+    (4, 4096, 512, 16, 1, 64),      # A transposed
+    (5, 12288, 256, 16, 0, 24),     # three tiles
+])
+def test_gemv_rows_batched_shapes(vqdev, oracle, m, n, k, group, flags, count):
+    """The 2..8-row product over many instances: several tiles and partial
+    ones, every group, two windows, A transposed, and instance counts that are
+    not a multiple of the blocks per instance group."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(m * 1000 + n + k + group + flags)
+    items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
+    ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
+    say("gemv rows batched", m, n, k, group, flags, count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, flags, count=count)
+    assert status == 0
+    for i in sorted({0, 1, count // 2, count - 1}):
+        ref, _ = oracle.matmul(*items[i], m, n, k, group, flags)
+        assert o.max_rel(out[i], ref) <= TOL
+        assert o.max_rel(out[i], _ref64(items[i], m, n, k, group, flags)) <= TOL
+
+
 @pytest.mark.parametrize("sign", [1.0, -1.0])
 def test_gemv_rows_saturated_window(vqdev, sign):
     """Both rows of a 64-bit bin pair at the largest activation over a full
