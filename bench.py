@@ -463,8 +463,9 @@ def main(argv=None) -> int:
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
-              "(the vq4 path runs on one device; sharding it would split the batched "
-              "instances or a weight's columns across GPUs, with no collective on the path)",
+              "(the vq4 path runs on one device; sharding would split a weight's output "
+              "columns or the batched instances across GPUs, and the optimizer refit would "
+              "all-gather its calibration sample)",
               file=sys.stderr)
         return 2
     if args.copy_calibration:
