@@ -1002,7 +1002,14 @@ struct RowAhead {
 // AD: A is dense FP32 in in[0]; in[1] holds the partial maxima of |x|.
 // The launch bins rows r0 .. r0 + m - 1 of A's `mall` rows (outputs are
 // written from o.out, which the caller offsets to row r0).
-template <int G, int MP, bool AD>
+// X4 (rows of whole 32-word tiles): each lane loads 4 adjacent words of R/4
+// rows with 16-byte loads and reads each row's x once for its 4 words. Within
+// a half-wave, lane = 16 chunk_hi + 4 slot + chunk_lo (chunk = 4 chunk_hi +
+// chunk_lo of 8 four-word chunks, slot = row of 4), and a lane rotates its 4
+// words by its slot, so at every atomic each 16-lane group covers 16 word
+// columns of distinct residue mod 16: distinct 8-byte bank pairs, as the
+// one-word-per-lane layout has.
+template <int G, int MP, bool AD, bool X4 = false>
 __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32_t m, uint32_t n,
                                                               uint32_t k, uint32_t flags,
                                                               uint32_t ks, float* partial,
@@ -1037,9 +1044,18 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
   const uint32_t nbp = (nb + D - 1) / D * D;
   const uint32_t lane = tid % 64, wave = tid / 64;
   const uint32_t q = lane % 32, half = lane / 32;
-  const uint32_t lane_row = (wave * 2 + half) * R;
-  const uint32_t col = (tile * kTileWords + q < rw) ? tile * kTileWords + q : rw - 1;
+  constexpr uint32_t RX = X4 ? R / 4 : R;  // rows per lane per batch
+  static_assert(RX % 2 == 0, "x pairs alternate by row parity");
+  const uint32_t chunk = (q / 16) * 4 + q % 4, slot = half * 4 + (q / 4) % 4;
+  const uint32_t lane_row = X4 ? wave * (2 * R) + slot * RX : (wave * 2 + half) * R;
+  const uint32_t col = X4 ? tile * kTileWords + 4 * chunk
+                          : ((tile * kTileWords + q < rw) ? tile * kTileWords + q : rw - 1);
   const uint32_t q8 = q * 8;
+  // X4: word t of the rotated row is word (t + slot) % 4 of the chunk
+  uint32_t lq8[X4 ? 4 : 1];
+#pragma unroll
+  for (uint32_t t = 0; t < (X4 ? 4u : 1u); ++t) lq8[t] = X4 ? (4 * chunk + ((t + slot) & 3u)) * 8 : q8;
+  const bool rot1 = (slot & 1u) != 0, rot2 = (slot & 2u) != 0;
   const RowAWords awn = row_a_words(m, mall, ks, G, flags);
   const uint32_t a_vec_elems = mall * k;  // A's flat extent
 
@@ -1086,9 +1102,17 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
   auto load_batch = [&](__amdgpu_buffer_rsrc_t rs, uint32_t b, uint32_t (&w)[R]) {
     uint32_t off = voff_lane + (k0 + b * BR) * rw * 4u;
     asm volatile("" : "+v"(off));
+    if (X4) {
 #pragma unroll
-    for (uint32_t u = 0; u < R; ++u)
-      w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, off + u * rw * 4u, 0, kStreamLoad));
+      for (uint32_t u = 0; u < RX; ++u) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + u * rw * 4u, 0, kStreamLoad);
+        w[4 * u] = v[0]; w[4 * u + 1] = v[1]; w[4 * u + 2] = v[2]; w[4 * u + 3] = v[3];
+      }
+    } else {
+#pragma unroll
+      for (uint32_t u = 0; u < R; ++u)
+        w[u] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(rs, off + u * rw * 4u, 0, kStreamLoad));
+    }
   };
 
   uint32_t buf[D][R];
@@ -1153,23 +1177,36 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
     if (b < nb) {  // padding batches (past the slice) bin nothing
       const uint32_t first = k0 + b * BR + lane_row;
 #pragma unroll
-      for (uint32_t u = 0; u < R; ++u) {
+      for (uint32_t u = 0; u < RX; ++u) {
         int2 (&cur)[MP] = (u & 1u) ? xb : xa;
         int2 (&nxt)[MP] = (u & 1u) ? xa : xb;
         // the next row's x is read ahead of this row's atomics (LDS operations
         // complete in order)
-        if (u + 1 < R) read_row(first + u + 1, nxt);
+        if (u + 1 < RX) read_row(first + u + 1, nxt);
         else if (b + 1 < nb && !restage) read_row(first + BR, nxt);
-        const uint32_t ww = w[u];
         int64_t add[MP];
 #pragma unroll
         for (int rp = 0; rp < MP; ++rp)
           add[rp] = int64_t((uint64_t(uint32_t(cur[rp].y)) << 32) | uint32_t(cur[rp].x));
+        uint32_t r[X4 ? 4 : 1];
+        if (X4) {
+          const uint32_t a0 = rot1 ? w[4 * u + 1] : w[4 * u];
+          const uint32_t a1 = rot1 ? w[4 * u + 2] : w[4 * u + 1];
+          const uint32_t a2 = rot1 ? w[4 * u + 3] : w[4 * u + 2];
+          const uint32_t a3 = rot1 ? w[4 * u] : w[4 * u + 3];
+          r[0] = rot2 ? a2 : a0; r[X4 ? 1 : 0] = rot2 ? a3 : a1;
+          r[X4 ? 2 : 0] = rot2 ? a0 : a2; r[X4 ? 3 : 0] = rot2 ? a1 : a3;
+        } else {
+          r[0] = w[u];
+        }
 #pragma unroll
-        for (uint32_t n8 = 0; n8 < 8; ++n8) {
-          const uint32_t base = __builtin_amdgcn_ubfe(ww, 4 * n8, 4) * (2048u * MP) + q8;
+        for (uint32_t t = 0; t < (X4 ? 4u : 1u); ++t) {
 #pragma unroll
-          for (int rp = 0; rp < MP; ++rp) lds_add64(base + (n8 * MP + rp) * 256, add[rp]);
+          for (uint32_t n8 = 0; n8 < 8; ++n8) {
+            const uint32_t base = __builtin_amdgcn_ubfe(r[t], 4 * n8, 4) * (2048u * MP) + lq8[t];
+#pragma unroll
+            for (int rp = 0; rp < MP; ++rp) lds_add64(base + (n8 * MP + rp) * 256, add[rp]);
+          }
         }
       }
     }
@@ -1411,15 +1448,20 @@ hipError_t launch_rows_mp(hipStream_t s, const Operands& o, uint32_t m, uint32_t
   uint32_t zc = per_z >= 256 ? 1u : 256u / per_z;
   zc = zc < o.count ? zc : o.count;
   const size_t shmem = RowLds<G, MP>::total;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_rows<G, MP, AD>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
+  // 16-byte loads need rows of whole tiles (then every chunk is 16-byte aligned)
+  const bool x4 = (n / (8 * G)) % kTileWords == 0;
+  const void* fn = x4 ? reinterpret_cast<const void*>(&k_gemv_rows<G, MP, AD, true>)
+                      : reinterpret_cast<const void*>(&k_gemv_rows<G, MP, AD, false>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(shmem));
   if (e != hipSuccess) return e;
   Operands oc = o;  // this chunk's outputs start at row r0
   oc.out = static_cast<char*>(o.out) + uint64_t(r0) * n * sizeof(float);
   dim3 grid(tiles, splits, zc);
-  k_gemv_rows<G, MP, AD><<<grid, kRowThreads, shmem, s>>>(oc, m, n, k, flags, ks,
-                                                          static_cast<float*>(workspace), r0,
-                                                          mall);
+  float* ws = static_cast<float*>(workspace);
+  if (x4)
+    k_gemv_rows<G, MP, AD, true><<<grid, kRowThreads, shmem, s>>>(oc, m, n, k, flags, ks, ws, r0, mall);
+  else
+    k_gemv_rows<G, MP, AD, false><<<grid, kRowThreads, shmem, s>>>(oc, m, n, k, flags, ks, ws, r0, mall);
   e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   dim3 fgrid(tiles * kFinishParts, 1, zc);
