@@ -364,8 +364,32 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
     const uint32_t rows = count - c0 < kRows ? count - c0 : kRows;
     __syncthreads();
     const float4* src = reinterpret_cast<const float4*>(sample + uint64_t(c0) * G);
-    for (uint32_t q = t; q < rows * G / 4; q += kUpdateThreads) xs4[q] = src[q];
-    for (uint32_t q = t; q < rows; q += kUpdateThreads) ids[q] = idx[c0 + q];
+    {
+      // every load of the round first, then the LDS writes: one round trip
+      // to memory instead of one per loop step
+      constexpr uint32_t kQ = kStageBytes / 16 / kUpdateThreads, kI = kRows / kUpdateThreads;
+      static_assert(kQ * kUpdateThreads * 16 == kStageBytes && kI * kUpdateThreads == kRows,
+                    "whole staging steps per thread");
+      const uint32_t nq = rows * G / 4;
+      float4 v[kQ];
+      uint32_t iv[kI];
+#pragma unroll
+      for (uint32_t i = 0; i < kQ; ++i) {
+        const uint32_t q = t + i * kUpdateThreads;
+        v[i] = q < nq ? src[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+#pragma unroll
+      for (uint32_t i = 0; i < kI; ++i) {
+        const uint32_t q = t + i * kUpdateThreads;
+        iv[i] = q < rows ? idx[c0 + q] : 0u;
+      }
+#pragma unroll
+      for (uint32_t i = 0; i < kQ; ++i)
+        if (t + i * kUpdateThreads < nq) xs4[t + i * kUpdateThreads] = v[i];
+#pragma unroll
+      for (uint32_t i = 0; i < kI; ++i)
+        if (t + i * kUpdateThreads < rows) ids[t + i * kUpdateThreads] = uint8_t(iv[i]);
+    }
     __syncthreads();
     // A stable counting sort of the round's rows by entry, then wave e adds
     // its members' values in sample order, 16 per round trip.
