@@ -203,45 +203,61 @@ __global__ __launch_bounds__(256) void k_dense_amax(Operands o, uint32_t values,
 }
 
 // Sum the split-k bins in split order (one thread per bin), then apply the B
-// codebook. grid: (n tiles * kFinishParts, 1, instances); each block owns
-// kTileGroups / kFinishParts groups of one tile.
+// codebook. grid: (n tiles * kFinishParts, M, instances); each block owns
+// kTileGroups / kFinishParts groups of one tile in one row (blockIdx.y). A
+// thread sums one bin over the splits in split order, with the loads of four
+// splits issued before their adds: more blocks and loads in flight than one
+// block per group range walking every row, and the same sums bit for bit.
 constexpr uint32_t kFinishParts = 16;
 constexpr uint32_t kFinishGroups = kTileGroups / kFinishParts;  // 16 groups, 256 bins
+static_assert(kFinishGroups * 16 == 256, "one bin per thread of a 256-thread block");
 
 template <int G, int M>
 __global__ __launch_bounds__(256) void k_gemv_finish(Operands o, uint32_t n, uint32_t splits,
                                                           uint32_t tiles, const float* partial) {
   __shared__ float sb_book[16 * G];
-  __shared__ float ssum[M][kFinishGroups * 16];
+  __shared__ float ssum[kFinishGroups * 16];
   const uint32_t tile = blockIdx.x / kFinishParts, part = blockIdx.x % kFinishParts;
+  const uint32_t r = blockIdx.y;
   const uint32_t row_words = n / (8 * G);
   const uint32_t groups = (row_words - tile * kTileWords) < kTileWords
                               ? (row_words - tile * kTileWords) * 8
                               : kTileGroups;
   const uint32_t j0 = part * kFinishGroups;
-  if (j0 >= groups) return;
+  if (j0 >= groups || r >= uint32_t(M)) return;
   const uint32_t jn = (groups - j0) < kFinishGroups ? (groups - j0) : kFinishGroups;
+  constexpr uint64_t kSplitStride = uint64_t(M) * 16 * kTileGroups;
   for (uint32_t item = blockIdx.z; item < o.count; item += gridDim.z) {
     const float* b_book = item_ptr<float>(o.in[3], o.stride[3], item);
     float* out = item_ptr_mut<float>(o.out, o.stride[4], item);
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < 16 * G; i += blockDim.x) sb_book[i] = b_book[i];
-    const float* base = partial + (uint64_t(item) * tiles + tile) * splits * (M * 16 * kTileGroups);
-    for (uint32_t e = threadIdx.x; e < M * jn * 16; e += blockDim.x) {
-      const uint32_t r = e / (jn * 16), je = e % (jn * 16);
+    const float* base = partial + (uint64_t(item) * tiles + tile) * splits * kSplitStride;
+    const uint32_t je = threadIdx.x;
+    if (je < jn * 16) {
       const float* p = base + r * 16 * kTileGroups + j0 * 16 + je;
       float s = 0.0f;
-      for (uint32_t sp = 0; sp < splits; ++sp) s += p[uint64_t(sp) * (M * 16 * kTileGroups)];
-      ssum[r][je] = s;
+      uint32_t sp = 0;
+      for (; sp + 4 <= splits; sp += 4) {
+        const float v0 = p[uint64_t(sp) * kSplitStride];
+        const float v1 = p[uint64_t(sp + 1) * kSplitStride];
+        const float v2 = p[uint64_t(sp + 2) * kSplitStride];
+        const float v3 = p[uint64_t(sp + 3) * kSplitStride];
+        s += v0;
+        s += v1;
+        s += v2;
+        s += v3;
+      }
+      for (; sp < splits; ++sp) s += p[uint64_t(sp) * kSplitStride];
+      ssum[je] = s;
     }
     __syncthreads();
     bool bad = false;
-    for (uint32_t e = threadIdx.x; e < M * jn * G; e += blockDim.x) {
-      const uint32_t r = e / (jn * G), jt = e % (jn * G);
+    for (uint32_t jt = threadIdx.x; jt < jn * G; jt += blockDim.x) {
       const uint32_t j = jt / G, t = jt % G;
       float y = 0.0f;
 #pragma unroll
-      for (int c = 0; c < 16; ++c) y = fmaf(sb_book[c * G + t], ssum[r][j * 16 + c], y);
+      for (int c = 0; c < 16; ++c) y = fmaf(sb_book[c * G + t], ssum[j * 16 + c], y);
       out[uint64_t(r) * n + (tile * kTileGroups + j0) * G + jt] = y;
       bad |= !finite_f32(y);
     }
@@ -1419,7 +1435,7 @@ hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k
     k_gemv_pairs<G, AD, false, false><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || splits == 1) return err;
-  dim3 fgrid(tiles * kFinishParts, 1, zc);
+  dim3 fgrid(tiles * kFinishParts, 1, zc);  // one row
   k_gemv_finish<G, 1><<<fgrid, 256, 0, s>>>(o, n, splits, tiles,
                                                  static_cast<const float*>(workspace));
   return hipGetLastError();
@@ -1464,7 +1480,7 @@ hipError_t launch_rows_mp(hipStream_t s, const Operands& o, uint32_t m, uint32_t
     k_gemv_rows<G, MP, AD, false><<<grid, kRowThreads, shmem, s>>>(oc, m, n, k, flags, ks, ws, r0, mall);
   e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
-  dim3 fgrid(tiles * kFinishParts, 1, zc);
+  dim3 fgrid(tiles * kFinishParts, m, zc);  // a block row per row of A
   const float* part = static_cast<const float*>(workspace);
   switch (m) {
     case 1: k_gemv_finish<G, 1><<<fgrid, 256, 0, s>>>(oc, n, splits, tiles, part); break;
