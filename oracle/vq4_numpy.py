@@ -12,14 +12,40 @@ Two halves:
   ``ExpertBank.initialize_expert`` (_kit/python/expert_bank.py:357-390) and
   the harness's gradient clip (src/alelyon_compute_kit/harness.py:196-200).
 
-Pins: the plan and ABI known-answer tests of the reference's Rust tests; the
-README's 3,128-byte image; golden vectors written from the reference's own
-Python (tests/golden/make_golden.py) for encode, fit_codebook and the seeded
-payloads; closed forms (decode is a gather; matmul against a float64 GEMM of
-the decoded operands; AdamW against float64 arithmetic); brute force on tiny
-inputs. The shader's driver-precision division and square root are not
-pinned by anything in the reference: AdamW parity against the reference
-itself is "parity unpinned" beyond the stated FP32 tolerance.
+Pins, function by function (each test also plants a mistake that must fail):
+
+* ShaderOracle.decode -- a gather, bitwise, NaN payloads kept
+  (tests/test_oracle.py test_decode_is_a_bit_exact_gather).
+* ShaderOracle.encode -- a numpy float32 brute force, bitwise; the reference's
+  float64 CPU encode except at near-ties; planted nonfinite values for the
+  status bits (test_encode_*).
+* ShaderOracle.matmul -- the sequential FP32 sum by brute force on straddling
+  groups in all four layouts, bitwise; a float64 GEMM within 1e-5; planted
+  overflow (test_matmul_*). ShaderOracle.matmul_dense -- op 2 with A
+  decoded first, bitwise (test_dense_matmul_reduces_to_op2_on_decoded_activations).
+* ShaderOracle.adamw, adamw_coefficients, adamw64 -- numpy float32 step by
+  step, bitwise; float64 within 1e-6; the status bits (test_adamw_*); the
+  reference's VQAdamW orchestration on recorded steps
+  (tests/test_host_calibration.py test_vqadamw_steps_match_the_reference_with_a_host_backend).
+* image_bytes, pack_indices, unpack_indices, words_for -- the README's
+  3,128-byte image and the config-1 image written by the reference, byte for
+  byte (tests/test_format.py).
+* encode64 -- the reference's CPU encode on recorded vectors
+  (test_oracle_encode_matches_reference_vectors).
+* fit_codebook, reseed, linspace_index -- the reference's fit on recorded
+  vectors, and numpy's linspace (test_oracle_fit_matches_reference_vectors,
+  test_linspace_sampling_matches_numpy).
+* expert_payload -- the payloads the reference's ExpertBank.initialize_expert
+  wrote (test_expert_payload_equals_the_reference_initializer).
+* clip_scale -- closed forms on gradients of known norm, and the clip the
+  reference harness applied on recorded steps
+  (test_clip_scale_closed_forms, test_clip_scale_equals_the_reference_harness).
+* matmul64, max_rel -- textbook float64 product and the north star's metric;
+  checked against the brute-force sums above.
+
+The shader's driver-precision division and square root are not pinned by
+anything in the reference: AdamW parity against the reference itself is
+"parity unpinned" beyond the stated FP32 tolerance.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
 import this module.

@@ -5,12 +5,17 @@ Run in the build container only, where the reference is mounted:
     PYTHONPATH=/root/reference/src python tests/golden/make_golden.py
 
 It imports the reference's CPU functions -- ``encode``, ``fit_codebook``,
-``VQArray``, ``VQAdamW`` (src/alelyon_compute_kit/_kit/python/vq.py) and
+``VQArray``, ``VQAdamW`` (src/alelyon_compute_kit/_kit/python/vq.py),
 ``ExpertBank`` (_kit/python/expert_bank.py:148-430: ``initialize_expert``
-payloads and the files a short sequence of commits leaves on disk) -- the
+payloads and the files a short sequence of commits leaves on disk) and the
+harness's gradient clip (src/alelyon_compute_kit/harness.py:196-200, observed
+through ``VulkanExpertHarness.train_step`` with a host backend) -- the
 functions no closed form or known-answer test pins bit for bit, and records
 their inputs and outputs as .npz fixtures (no pickles). Nothing under
 /root/reference is needed, read or copied at test time.
+
+With fixture names as arguments (``clip_scale``, ``bank_files``, ...) only
+those files are written; the default writes all of them.
 """
 from __future__ import annotations
 
@@ -24,6 +29,7 @@ import numpy as np
 OUT = Path(__file__).resolve().parent
 
 try:
+    from alelyon_compute_kit import harness as ref_harness
     from alelyon_compute_kit._kit.python import expert_bank as ref_bank
     from alelyon_compute_kit._kit.python import vq as ref_vq
 except ImportError as exc:  # pragma: no cover - build container only
@@ -226,15 +232,78 @@ def bank_files() -> dict:
             "stats": np.frombuffer(stats, dtype=np.uint8)}
 
 
-def main() -> int:
-    np.savez_compressed(OUT / "encode_cpu.npz", **encode_cases())
-    np.savez_compressed(OUT / "fit_codebook.npz", **fit_cases())
-    np.savez_compressed(OUT / "config1.npz", **config1())
-    np.savez_compressed(OUT / "expert_payloads.npz", **expert_payloads())
-    np.savez_compressed(OUT / "vqadamw_steps.npz", **vqadamw_steps())
-    np.savez_compressed(OUT / "bank_files.npz", **bank_files())
-    for p in sorted(OUT.glob("*.npz")):
-        print(p.name, p.stat().st_size)
+class _ClipRecorder:
+    """A host backend for the reference harness that keeps the dense gradient
+    it returns from the transposed product. The harness scales that array in
+    place by its clip factor (harness.py:196-200) before encoding it, so after
+    ``train_step`` the kept array holds the clipped gradient exactly as the
+    reference computed it; a copy taken before returning holds the unclipped
+    one."""
+
+    def __init__(self):
+        self.before = None
+        self.after = None
+
+    def encode(self, values, codebook, *, group):
+        return ref_vq.encode(values, codebook, group=group)
+
+    def decode(self, value):
+        return value.decode()
+
+    def matmul(self, left, right, *, transpose_a=False, transpose_b=False):
+        a, b = left.decode(), right.decode()
+        out = ((a.T if transpose_a else a) @ (b.T if transpose_b else b)).astype(np.float32)
+        if transpose_a:
+            self.before, self.after = out.copy(), out
+        return out
+
+    def adamw(self, weight, momentum, variance, gradient, *, lr, beta1, beta2, eps,
+              weight_decay, step):
+        return _Float32Backend().adamw(weight, momentum, variance, gradient, lr=lr, beta1=beta1,
+                                       beta2=beta2, eps=eps, weight_decay=weight_decay, step=step)
+
+
+def clip_cases() -> dict:
+    """The reference harness's clip on real steps: per case the unclipped
+    gradient, the clipped one, the norm it reported and whether it clipped."""
+    rng = np.random.default_rng(77)
+    out = {}
+    cases = [((4, 3), 8, 2, 0.01), ((4, 3), 8, 2, 1e6), ((64, 48), 16, 32, 1.0),
+             ((64, 48), 16, 32, 0.05), ((40, 40), 8, 5, 3.0)]
+    with tempfile.TemporaryDirectory() as tmp:
+        for i, (shape, group, rows, max_norm) in enumerate(cases):
+            bank = ref_bank.ExpertBank.create(Path(tmp) / f"b{i}",
+                                              ref_bank.BankConfig(1, 1, (shape,) * 3, group))
+            bank.initialize_expert(0, 0, seed=i, zero_optimizer_state=True)
+            rec = _ClipRecorder()
+            runner = ref_harness.VulkanExpertHarness(bank, backend=rec)
+            x = rng.standard_normal((rows, shape[0])).astype(np.float32)
+            y = rng.standard_normal((rows, shape[1])).astype(np.float32)
+            step = runner.train_step(x, y, max_grad_norm=max_norm)
+            out[f"c{i}_max_norm"] = np.array(max_norm, np.float64)
+            out[f"c{i}_before"], out[f"c{i}_after"] = rec.before, rec.after
+            out[f"c{i}_norm"] = np.array(step.gradient_norm_before_clip, np.float64)
+            out[f"c{i}_clipped"] = np.array(step.clipped)
+    out["count"] = np.array(len(cases))
+    return out
+
+
+FIXTURES = {
+    "encode_cpu": encode_cases,
+    "fit_codebook": fit_cases,
+    "config1": config1,
+    "expert_payloads": expert_payloads,
+    "vqadamw_steps": vqadamw_steps,
+    "bank_files": bank_files,
+    "clip_scale": clip_cases,
+}
+
+
+def main(argv=None) -> int:
+    names = list(sys.argv[1:] if argv is None else argv) or list(FIXTURES)
+    for name in names:
+        np.savez_compressed(OUT / f"{name}.npz", **FIXTURES[name]())
+        print(f"{name}.npz", (OUT / f"{name}.npz").stat().st_size)
     return 0
 
 

@@ -241,3 +241,64 @@ def test_adamw_status_bits(oracle):
     assert status == 4 and np.isnan(out).all()        # nothing written
     codes4, books4, _ = _adamw_inputs(rng, 64, 8, variance_sign=-1.0)
     assert oracle.adamw(codes4, books4, good, 64, 8)[1] & 4
+
+
+# ---- caller-side helpers of the oracle: seeded payloads and the gradient clip ----
+
+def test_expert_payload_equals_the_reference_initializer():
+    """oracle expert_payload (restating expert_bank.py:357-390) against the
+    payloads the reference's ExpertBank.initialize_expert wrote
+    (tests/golden/expert_payloads.npz): config 2's three seed-7 matrices and
+    the weight of a zero-optimizer-state bank; bit for bit."""
+    from oracle import vq4_numpy as o
+    g = golden("expert_payloads.npz")
+    for i in range(3):
+        codes, book = o.expert_payload((128, 128), 16, 7, 0, 0, i)
+        np.testing.assert_array_equal(codes, g[f"c2_{i}_codes"])
+        np.testing.assert_array_equal(book.view(np.uint32), g[f"c2_{i}_book"].view(np.uint32))
+    codes, book = o.expert_payload((4, 3), 8, 4, 0, 0, 0)
+    np.testing.assert_array_equal(codes, g["h_0_codes"])          # tail nibbles masked
+    np.testing.assert_array_equal(book.view(np.uint32), g["h_0_book"].view(np.uint32))
+    # planted mistakes: another stream index, or a scale by the column count
+    assert not np.array_equal(o.expert_payload((128, 128), 16, 7, 0, 0, 1)[0], g["c2_0_codes"])
+    wrong = o.expert_payload((4, 3), 8, 4, 0, 0, 0)[1] * np.float32(np.sqrt(4) / np.sqrt(3))
+    assert not np.array_equal(wrong, g["h_0_book"])
+
+
+def test_clip_scale_closed_forms():
+    """clip_scale = min(1, max_norm / (||g||_2 + 1e-6)) on gradients of known
+    norm: (3, 4) has norm 5 exactly; a gradient inside the ball is not scaled;
+    a zero gradient divides by 1e-6 alone."""
+    from oracle import vq4_numpy as o
+    g = np.array([[3.0, 4.0]], np.float32)
+    assert o.clip_scale(g, 1.0) == 1.0 / (5.0 + 1e-6)
+    assert o.clip_scale(g, 10.0) == 1.0
+    assert o.clip_scale(np.zeros((2, 2), np.float32), 1e-9) == min(1.0, 1e-9 / 1e-6)
+    # 12 x 12 of 0.25: sum of squares 9, norm 3 exactly
+    assert o.clip_scale(np.full((12, 12), 0.25, np.float32), 0.3) == 0.3 / (3.0 + 1e-6)
+    # planted mistake: the squared norm in place of the norm fails the first case
+    assert 1.0 / (25.0 + 1e-6) != o.clip_scale(g, 1.0)
+
+
+def test_clip_scale_equals_the_reference_harness():
+    """clip_scale against the clip the reference harness applied on real
+    steps (tests/golden/clip_scale.npz, recorded through
+    VulkanExpertHarness.train_step with a host backend): the same norm, and
+    the gradient times float32(scale) equal bit for bit to the clipped
+    gradient it encoded; the same clipped/unclipped verdict."""
+    from oracle import vq4_numpy as o
+    g = golden("clip_scale.npz")
+    for i in range(int(g["count"])):
+        before, after = g[f"c{i}_before"], g[f"c{i}_after"]
+        max_norm = float(g[f"c{i}_max_norm"])
+        scale = o.clip_scale(before, max_norm)
+        assert float(np.linalg.norm(before.astype(np.float64))) == float(g[f"c{i}_norm"])
+        assert (scale < 1.0) == bool(g[f"c{i}_clipped"])
+        clipped = before * np.float32(scale)
+        np.testing.assert_array_equal(clipped.view(np.uint32), after.view(np.uint32))
+    # planted mistake: without the 1e-6 the clipped cases differ in their last bits
+    i = next(i for i in range(int(g["count"])) if bool(g[f"c{i}_clipped"]))
+    before, after = g[f"c{i}_before"], g[f"c{i}_after"]
+    norm = float(np.linalg.norm(before.astype(np.float64)))
+    wrong = before * np.float32(float(g[f"c{i}_max_norm"]) / norm)
+    assert not np.array_equal(wrong.view(np.uint32), after.view(np.uint32))
