@@ -1,26 +1,35 @@
-"""ctypes binding of libackvq.so: device, buffers, transfers and errors.
+"""ctypes binding of libackvq.so: the device, its buffers, transfers, errors.
 
-The vq binding needs only the device/buffer/transfer part of the reference's
-``ack`` module (src/alelyon_compute_kit/_kit/python/ack.py:599-1160): the same
-error classes, the same ``Device``/``Buffer`` lifecycle (explicit ``free``,
-``close`` refused while buffers live, every call serialised under the
-device's ``RLock``) and the same return codes. The reference's ABI-14
-handshake over every operator family does not apply: this library carries
-the vq4/v1 extension only, and ``VQDevice`` checks its schema itself.
+The vq4 path needs the device/buffer/transfer part of the reference's
+``ack`` module (src/alelyon_compute_kit/_kit/python/ack.py:599-1160). What
+callers can observe is kept: the error classes, the return codes, a
+``Device`` that refuses to close while its buffers live, ``Buffer`` objects
+with ``upload``/``download``/``free``, every call on a device serialised.
+The reference's ABI-14 handshake over every operator family does not apply
+to a library that carries the vq4/v1 extension only; ``VQDevice`` checks the
+extension's schema itself.
 
-Loading the library never touches the GPU; ``Device()`` opens it.
+Design here: one ``Library`` object holds the loaded shared library with
+every entry point declared from a table; return codes map to exception
+classes in one place (``Library.check``); a device keeps a registry of its
+live buffer handles; a buffer dropped without ``free()`` is released by a
+``weakref.finalize`` hook that reports any refusal as a ResourceWarning.
+
+Loading the library never touches the GPU; ``Device()`` opens one.
 """
 from __future__ import annotations
 
 import ctypes
-import operator
+import numbers
 import os
 import threading
 import warnings
+import weakref
 from pathlib import Path
 
 import numpy as np
 
+# Return codes of the C ABI (include/ack_vq.h; the reference's ffi.rs codes).
 ACK_OK = 0
 ACK_ERR_NULL = -1
 ACK_ERR_DEVICE = -2          # the reference's ACK_ERR_VULKAN: the device runtime failed
@@ -35,10 +44,8 @@ ACK_ERR_ABI = -9
 ACK_ERR_POISONED = -10
 ACK_ERR_UNSUPPORTED_OP = -11
 
-_MAX_NBYTES = 1 << 40
-_POD_SIZES = {"b": (1,), "i": (1, 2, 4, 8), "u": (1, 2, 4, 8), "f": (2, 4, 8)}
-_HERE = Path(__file__).resolve().parent
 LIBRARY_NAME = "libackvq.so"
+MAX_BUFFER_BYTES = 1 << 40
 
 
 class AckError(RuntimeError):
@@ -50,7 +57,7 @@ class AckUnavailable(AckError):
 
 
 class AckShapeError(AckError):
-    """The request's geometry is refused."""
+    """The library refused the request's geometry (ACK_ERR_SHAPE)."""
 
 
 class AckPoisoned(AckError):
@@ -58,296 +65,289 @@ class AckPoisoned(AckError):
     later call on it refuses; close it and start a new process."""
 
 
-def _kit_error(what: str, rc: int, message: str) -> AckError:
-    cls = AckPoisoned if rc == ACK_ERR_POISONED else AckError
-    return cls(f"{what}: {message}")
+_EXCEPTION_FOR_CODE = {ACK_ERR_POISONED: AckPoisoned, ACK_ERR_SHAPE: AckShapeError}
 
+# (kind, itemsize) of the element types a transfer accepts: plain
+# fixed-width numbers and bool, never objects, records or sub-arrays.
+_TRANSFER_TYPES = frozenset([("b", 1)] + [(k, s) for k in "iu" for s in (1, 2, 4, 8)]
+                            + [("f", s) for s in (2, 4, 8)])
 
-def _is_bool(value) -> bool:
-    return isinstance(value, (bool, np.bool_))
-
-
-def _checked_nbytes(nbytes: int) -> int:
-    if _is_bool(nbytes):
-        raise AckError("nbytes must be a positive integer, not a boolean")
-    try:
-        count = operator.index(nbytes)
-    except TypeError as exc:
-        raise AckError("nbytes must be a positive integer") from exc
-    if not 0 < count <= _MAX_NBYTES:
-        raise AckError(f"nbytes must be in 1..{_MAX_NBYTES}")
-    return count
-
-
-def _pod_dtype(dtype) -> np.dtype:
-    try:
-        result = np.dtype(dtype)
-    except (TypeError, ValueError) as exc:
-        raise AckError("unsupported buffer dtype") from exc
-    if (result.hasobject or result.fields is not None or result.subdtype is not None
-            or result.itemsize not in _POD_SIZES.get(result.kind, ())):
-        raise AckError(f"unsupported buffer dtype {result} is refused; use a plain "
-                       "fixed-width numeric or bool dtype")
-    return result
-
-
-def library_path() -> Path | None:
-    """``ACK_LIBRARY`` if set, else the library built into this package."""
-    candidates = []
-    if os.environ.get("ACK_LIBRARY"):
-        candidates.append(Path(os.environ["ACK_LIBRARY"]))
-    candidates.append(_HERE / "_lib" / LIBRARY_NAME)
-    for candidate in candidates:
-        if candidate.is_file():
-            return candidate
-    return None
-
-
-_c = ctypes
-_SIGNATURES = {
-    "ack_vq_schema": ([], _c.c_uint32),
-    "ack_vq": ([_c.c_void_p] * 7 + [_c.c_void_p, _c.c_size_t], _c.c_int32),
-    "ack_vq_batch": ([_c.c_void_p] * 7 + [_c.c_void_p, _c.c_size_t, _c.c_uint32], _c.c_int32),
-    "ack_open": ([], _c.c_void_p),
-    "ack_close": ([_c.c_void_p], _c.c_int32),
-    "ack_device_name": ([_c.c_void_p, _c.c_char_p, _c.c_size_t], _c.c_int32),
-    "ack_last_error": ([_c.c_char_p, _c.c_size_t], _c.c_int32),
-    "ack_buffer_alloc": ([_c.c_void_p, _c.c_uint64], _c.c_void_p),
-    "ack_buffer_free": ([_c.c_void_p, _c.c_void_p], _c.c_int32),
-    "ack_upload": ([_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_size_t], _c.c_int32),
-    "ack_download": ([_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_size_t], _c.c_int32),
-    "ack_vq_plan_query": ([_c.c_void_p, _c.c_size_t, _c.c_uint32, _c.c_void_p, _c.c_void_p,
-                           _c.c_void_p], _c.c_int32),
-    "ack_vq_plan_check_buffers": ([_c.c_void_p, _c.c_size_t, _c.c_void_p, _c.c_void_p],
-                                  _c.c_int32),
-    "ack_vq_adamw_step": ([_c.c_void_p] * 8 + [_c.c_void_p, _c.c_size_t, _c.c_uint32,
-                                               _c.c_uint32], _c.c_int32),
-    "ack_stream_timer": ([_c.c_void_p, _c.c_uint32, _c.POINTER(_c.c_float)], _c.c_int32),
-    "ack_sync": ([_c.c_void_p], _c.c_int32),
-    "ack_vq_path_name": ([_c.c_void_p, _c.c_size_t, _c.c_char_p, _c.c_size_t], _c.c_int32),
-    "ack_vq_set_policy": ([_c.c_void_p, _c.c_uint32], _c.c_int32),
-    "ack_vq_host_encode": ([_c.c_void_p, _c.c_uint64, _c.c_void_p, _c.c_uint32, _c.c_void_p],
-                           _c.c_int32),
-    "ack_vq_host_fit_codebook": ([_c.c_void_p, _c.c_uint64, _c.c_uint32, _c.c_uint32,
-                                  _c.c_uint32, _c.c_void_p, _c.c_void_p], _c.c_int32),
-    "ack_vq_fit_codebook": ([_c.c_void_p] * 5 + [_c.c_uint64, _c.c_uint32, _c.c_uint32,
-                                                 _c.c_uint32], _c.c_int32),
-    "ack_vq_matmul_dense": ([_c.c_void_p] * 6 + [_c.c_void_p, _c.c_size_t], _c.c_int32),
-    "ack_vq_dense_path_name": ([_c.c_void_p, _c.c_size_t, _c.c_char_p, _c.c_size_t], _c.c_int32),
-    "ack_buffer_copy": ([_c.c_void_p, _c.c_void_p, _c.c_uint64, _c.c_void_p, _c.c_uint64,
-                         _c.c_uint64], _c.c_int32),
+_P, _U32, _U64, _I32, _SZ = (ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32,
+                             ctypes.c_size_t)
+# name: (argument types, result type), as include/ack_vq.h declares them
+_ENTRY_POINTS = {
+    "ack_vq_schema": ((), _U32),
+    "ack_vq": ((_P,) * 8 + (_SZ,), _I32),
+    "ack_vq_batch": ((_P,) * 8 + (_SZ, _U32), _I32),
+    "ack_open": ((), _P),
+    "ack_close": ((_P,), _I32),
+    "ack_device_name": ((_P, ctypes.c_char_p, _SZ), _I32),
+    "ack_last_error": ((ctypes.c_char_p, _SZ), _I32),
+    "ack_buffer_alloc": ((_P, _U64), _P),
+    "ack_buffer_free": ((_P, _P), _I32),
+    "ack_upload": ((_P, _P, _P, _SZ), _I32),
+    "ack_download": ((_P, _P, _P, _SZ), _I32),
+    "ack_buffer_copy": ((_P, _P, _U64, _P, _U64, _U64), _I32),
+    "ack_sync": ((_P,), _I32),
+    "ack_stream_timer": ((_P, _U32, ctypes.POINTER(ctypes.c_float)), _I32),
+    "ack_vq_plan_query": ((_P, _SZ, _U32, _P, _P, _P), _I32),
+    "ack_vq_plan_check_buffers": ((_P, _SZ, _P, _P), _I32),
+    "ack_vq_path_name": ((_P, _SZ, ctypes.c_char_p, _SZ), _I32),
+    "ack_vq_dense_path_name": ((_P, _SZ, ctypes.c_char_p, _SZ), _I32),
+    "ack_vq_set_policy": ((_P, _U32), _I32),
+    "ack_vq_host_encode": ((_P, _U64, _P, _U32, _P), _I32),
+    "ack_vq_host_fit_codebook": ((_P, _U64, _U32, _U32, _U32, _P, _P), _I32),
+    "ack_vq_fit_codebook": ((_P,) * 5 + (_U64, _U32, _U32, _U32), _I32),
+    "ack_vq_matmul_dense": ((_P,) * 7 + (_SZ,), _I32),
+    "ack_vq_adamw_step": ((_P,) * 9 + (_SZ, _U32, _U32), _I32),
 }
 
 
-class _Lib:
-    """The loaded library with every entry point declared."""
+def library_path() -> Path | None:
+    """``ACK_LIBRARY`` if it names a file, else the library built into this
+    package, else None."""
+    here = Path(__file__).resolve().parent / "_lib" / LIBRARY_NAME
+    for candidate in (os.environ.get("ACK_LIBRARY"), here):
+        if candidate and Path(candidate).is_file():
+            return Path(candidate)
+    return None
+
+
+class Library:
+    """libackvq.so loaded once per process, every entry point declared."""
 
     def __init__(self, path: Path) -> None:
-        self.path = path
-        self.cdll = ctypes.CDLL(str(path))
-        for name, (argtypes, restype) in _SIGNATURES.items():
-            try:
-                fn = getattr(self.cdll, name)
-            except AttributeError as exc:
-                raise AckUnavailable(f"{path} lacks {name}") from exc
-            fn.argtypes, fn.restype = argtypes, restype
+        self.path = Path(path)
+        self.cdll = ctypes.CDLL(str(self.path))
+        missing = [name for name in _ENTRY_POINTS if not hasattr(self.cdll, name)]
+        if missing:
+            raise AckUnavailable(f"{self.path} lacks {', '.join(missing)}; rebuild it")
+        for name, (args, result) in _ENTRY_POINTS.items():
+            entry = getattr(self.cdll, name)
+            entry.argtypes, entry.restype = list(args), result
 
     def last_error(self) -> str:
-        buf = ctypes.create_string_buffer(1024)
-        self.cdll.ack_last_error(buf, len(buf))
-        return buf.value.decode("utf-8", errors="replace")
+        """This thread's last error message from the library."""
+        text = ctypes.create_string_buffer(1024)
+        self.cdll.ack_last_error(text, len(text))
+        return text.value.decode("utf-8", errors="replace")
+
+    def check(self, rc: int, context: str) -> None:
+        """Raise the exception of a nonzero return code, with the message."""
+        if rc != ACK_OK:
+            raise _EXCEPTION_FOR_CODE.get(rc, AckError)(f"{context}: {self.last_error()}")
 
 
-_LIB: _Lib | None = None
-_LIB_LOCK = threading.Lock()
+_loaded: Library | None = None
+_load_guard = threading.Lock()
 
 
-def _lib() -> _Lib:
-    global _LIB
-    with _LIB_LOCK:
-        if _LIB is None:
+def library() -> Library:
+    """The process's Library; AckUnavailable when nothing is built."""
+    global _loaded
+    with _load_guard:
+        if _loaded is None:
             path = library_path()
             if path is None:
                 raise AckUnavailable(
                     f"{LIBRARY_NAME} is not built; run alelyon-compute-kit_amd/build.py")
-            _LIB = _Lib(path)
-        return _LIB
+            _loaded = Library(path)
+        return _loaded
+
+
+_lib = library  # the name the tests' fixtures use
+
+
+def _byte_count(nbytes) -> int:
+    if isinstance(nbytes, (bool, np.bool_)):
+        raise AckError("nbytes must be a positive integer, not a boolean")
+    if not isinstance(nbytes, numbers.Integral):
+        raise AckError("nbytes must be a positive integer")
+    count = int(nbytes)
+    if count < 1 or count > MAX_BUFFER_BYTES:
+        raise AckError(f"nbytes must be in 1..{MAX_BUFFER_BYTES}")
+    return count
+
+
+def _transfer_dtype(dtype) -> np.dtype:
+    try:
+        dt = np.dtype(dtype)
+    except (TypeError, ValueError) as exc:
+        raise AckError("unsupported buffer dtype") from exc
+    plain = dt.fields is None and dt.subdtype is None and not dt.hasobject
+    if not plain or (dt.kind, dt.itemsize) not in _TRANSFER_TYPES:
+        raise AckError(f"unsupported buffer dtype {dt} is refused; use a plain "
+                       "fixed-width numeric or bool dtype")
+    return dt
+
+
+def _release_dropped(device: "Device", handle: int) -> None:
+    """Finaliser of a Buffer that was never freed."""
+    try:
+        device._release(handle)
+    except AckError as exc:
+        warnings.warn(f"ack.Buffer finaliser: {exc}", ResourceWarning, stacklevel=2)
+
+
+class Device:
+    """One HIP device. Free its buffers before close(); calls are serialised
+    under the device's re-entrant lock."""
+
+    def __init__(self) -> None:
+        self.lib = library()
+        self.lock = threading.RLock()
+        self._live: set[int] = set()
+        self._handle = self.lib.cdll.ack_open()
+        if not self._handle:
+            raise AckUnavailable(f"ack_open: {self.lib.last_error()}")
+        try:
+            label = ctypes.create_string_buffer(256)
+            self.lib.check(self.lib.cdll.ack_device_name(self._handle, label, len(label)),
+                           "device name")
+            self.name = label.value.decode("utf-8", errors="replace")
+        except BaseException:
+            self.close()
+            raise
+
+    # -- the handle every entry point takes ---------------------------------
+    @property
+    def handle(self) -> int:
+        """The open device's handle; AckError once closed."""
+        if not self._handle:
+            raise AckError("device is closed")
+        return self._handle
+
+    def call(self, entry: str, *args, context: str | None = None) -> None:
+        """Call a status-returning entry point on this device under its lock
+        and raise on a nonzero code."""
+        with self.lock:
+            rc = getattr(self.lib.cdll, entry)(self.handle, *args)
+            self.lib.check(rc, context or entry)
+
+    # -- buffers -----------------------------------------------------------------
+    def buffer(self, nbytes: int) -> "Buffer":
+        return Buffer(self, nbytes)
+
+    def _allocate(self, nbytes: int) -> int:
+        with self.lock:
+            handle = self.lib.cdll.ack_buffer_alloc(self.handle, nbytes)
+            if not handle:
+                raise AckError(f"buffer alloc: {self.lib.last_error()}")
+            self._live.add(handle)
+            return handle
+
+    def _release(self, handle: int) -> None:
+        with self.lock:
+            if handle not in self._live:
+                return
+            self._live.discard(handle)  # whatever the library answers, it is gone here
+            self.lib.check(self.lib.cdll.ack_buffer_free(self.handle, handle), "free")
+
+    # -- lifetime ------------------------------------------------------------
+    def close(self) -> None:
+        """Free the device only on ACK_OK; a refusal keeps the handle valid,
+        except when the library already considers it closed."""
+        with self.lock:
+            if not self._handle:
+                return
+            if self._live:
+                raise AckError("device has live buffers still allocated; free them before close")
+            rc = self.lib.cdll.ack_close(self._handle)
+            if rc in (ACK_OK, ACK_ERR_CLOSED):
+                self._handle = None
+            if rc != ACK_OK:
+                raise AckError(f"close: {self.lib.last_error()}")
+
+    def __enter__(self) -> "Device":
+        self.handle  # refuses a closed device
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
+    # -- stream control and diagnostics ----------------------------------------
+    def capability_record(self) -> dict:
+        """What this device and library declare, JSON-serialisable."""
+        with self.lock:
+            self.handle
+            return {"device": self.name, "library": str(self.lib.path),
+                    "vq_schema": int(self.lib.cdll.ack_vq_schema())}
+
+    def synchronize(self) -> None:
+        self.call("ack_sync", context="sync")
+
+    def timer_start(self) -> None:
+        """Record a start event on the device stream (benchmarks)."""
+        self.call("ack_stream_timer", 0, None, context="timer")
+
+    def timer_stop(self) -> float:
+        """Record a stop event, wait for it, return milliseconds since start."""
+        elapsed = ctypes.c_float()
+        self.call("ack_stream_timer", 1, ctypes.byref(elapsed), context="timer")
+        return float(elapsed.value)
+
+    def set_policy(self, policy: int) -> None:
+        """0: automatic kernel choice; 1: the general matmul kernel only;
+        2: factorised paths at any size (tests of small shapes)."""
+        self.call("ack_vq_set_policy", policy, context="policy")
 
 
 class Buffer:
-    """A device buffer; explicit free() releases it."""
+    """A device buffer of ``nbytes``; ``free()`` releases it explicitly."""
 
-    def __init__(self, device: "Device", nbytes: int) -> None:
+    def __init__(self, device: Device, nbytes: int) -> None:
+        size = _byte_count(nbytes)
         self._device = device
-        self._handle = None
-        self._nbytes = _checked_nbytes(nbytes)
-        with device._lock:
-            device._require_open()
-            handle = device._lib.cdll.ack_buffer_alloc(device._handle, self._nbytes)
-            if not handle:
-                raise AckError(f"buffer alloc: {device._lib.last_error()}")
-            device._buffers.add(handle)
-            self._handle = handle
+        self._nbytes = size
+        self._handle = device._allocate(size)
+        self._finalizer = weakref.finalize(self, _release_dropped, device, self._handle)
 
     @property
     def nbytes(self) -> int:
         return self._nbytes
 
-    def _require_live(self) -> None:
+    @property
+    def handle(self) -> int:
+        """The live buffer's handle; AckError once freed or its device closed."""
         if not self._handle:
             raise AckError("buffer has been freed")
-        self._device._require_open()
+        self._device.handle
+        return self._handle
 
     def upload(self, data) -> None:
-        with self._device._lock:
-            self._require_live()
-            array = np.asarray(data)
-            _pod_dtype(array.dtype)
-            if array.nbytes != self.nbytes:
-                raise AckError(f"upload of {array.nbytes} bytes into a {self.nbytes}-byte buffer")
-            raw = np.ascontiguousarray(array)
-            lib = self._device._lib
-            rc = lib.cdll.ack_upload(self._device._handle, self._handle, raw.ctypes.data,
-                                     raw.nbytes)
-            if rc != ACK_OK:
-                raise _kit_error("upload", rc, lib.last_error())
+        """Copy a host array of exactly ``nbytes`` into the buffer."""
+        host = np.asarray(data)
+        _transfer_dtype(host.dtype)
+        if host.nbytes != self._nbytes:
+            raise AckError(f"upload of {host.nbytes} bytes into a {self._nbytes}-byte buffer")
+        host = np.ascontiguousarray(host)
+        self._device.call("ack_upload", self.handle, host.ctypes.data, host.nbytes,
+                          context="upload")
 
     def download(self, dtype) -> np.ndarray:
-        with self._device._lock:
-            self._require_live()
-            dtype = _pod_dtype(dtype)
-            if self.nbytes % dtype.itemsize:
-                raise AckError(f"buffer size {self.nbytes} is not divisible by dtype itemsize "
-                               f"{dtype.itemsize}; a transfer requires a whole number of elements")
-            out = np.empty(self.nbytes // dtype.itemsize, dtype=dtype)
-            lib = self._device._lib
-            rc = lib.cdll.ack_download(self._device._handle, self._handle, out.ctypes.data,
-                                       out.nbytes)
-            if rc != ACK_OK:
-                raise _kit_error("download", rc, lib.last_error())
-            return out
+        """The buffer's bytes as a new 1-D host array of ``dtype`` (waits for
+        the device stream)."""
+        dt = _transfer_dtype(dtype)
+        count, rest = divmod(self._nbytes, dt.itemsize)
+        if rest:
+            raise AckError(f"buffer size {self._nbytes} is not divisible by dtype itemsize "
+                           f"{dt.itemsize}; a transfer requires a whole number of elements")
+        host = np.empty(count, dtype=dt)
+        self._device.call("ack_download", self.handle, host.ctypes.data, host.nbytes,
+                          context="download")
+        return host
 
     def copy_from(self, src: "Buffer", nbytes: int, *, offset: int = 0,
                   src_offset: int = 0) -> None:
         """Enqueue a device-to-device copy of ``nbytes`` from ``src``."""
-        with self._device._lock:
-            self._require_live()
-            src._require_live()
-            lib = self._device._lib
-            rc = lib.cdll.ack_buffer_copy(self._device._handle, self._handle, offset,
-                                          src._handle, src_offset, nbytes)
-            if rc != ACK_OK:
-                raise _kit_error("copy", rc, lib.last_error())
+        self._device.call("ack_buffer_copy", self.handle, offset, src.handle, src_offset, nbytes,
+                          context="copy")
 
     def free(self) -> None:
-        with self._device._lock:
-            if self._handle:
-                self._device._require_open()
-                lib = self._device._lib
-                rc = lib.cdll.ack_buffer_free(self._device._handle, self._handle)
-                self._device._buffers.discard(self._handle)
-                self._handle = None
-                if rc != ACK_OK:
-                    raise _kit_error("free", rc, lib.last_error())
-
-    def __del__(self) -> None:
-        try:
-            self.free()
-        except AckError as exc:
-            try:
-                warnings.warn(f"ack.Buffer finaliser: {exc}", ResourceWarning, stacklevel=2)
-            except Exception:
-                pass
-        except Exception:
-            pass
-
-
-class Device:
-    """One HIP device. Free its buffers before close(); calls are serialised."""
-
-    def __init__(self) -> None:
-        self._lock = threading.RLock()
-        self._buffers: set[int] = set()
-        self._handle = None
-        self._lib = lib = _lib()
-        self._handle = lib.cdll.ack_open()
+        """Release the buffer; a second call does nothing."""
         if not self._handle:
-            raise AckUnavailable(f"ack_open: {lib.last_error()}")
-        try:
-            buf = ctypes.create_string_buffer(256)
-            rc = lib.cdll.ack_device_name(self._handle, buf, len(buf))
-            if rc != ACK_OK:
-                raise AckError(f"device name: {lib.last_error()}")
-            self.name = buf.value.decode("utf-8", errors="replace")
-        except BaseException:
-            self.close()
-            raise
-
-    def capability_record(self) -> dict:
-        """What this device and library declare, JSON-serialisable."""
-        with self._lock:
-            self._require_open()
-            return {"device": self.name, "library": str(self._lib.path),
-                    "vq_schema": int(self._lib.cdll.ack_vq_schema())}
-
-    def _require_open(self) -> None:
-        if not self._handle:
-            raise AckError("device is closed")
-
-    def close(self) -> None:
-        """Free the device only on ACK_OK; a refusal keeps the handle valid."""
-        with self._lock:
-            if self._handle:
-                if self._buffers:
-                    raise AckError("device has live buffers still allocated; free them before close")
-                rc = self._lib.cdll.ack_close(self._handle)
-                if rc == ACK_ERR_CLOSED:
-                    self._handle = None
-                    raise AckError(f"close: {self._lib.last_error()}")
-                if rc != ACK_OK:
-                    raise AckError(f"close: {self._lib.last_error()}")
-                self._handle = None
-
-    def __enter__(self) -> "Device":
-        with self._lock:
-            self._require_open()
-            return self
-
-    def __exit__(self, *exc) -> None:
-        self.close()
-
-    def buffer(self, nbytes: int) -> Buffer:
-        return Buffer(self, nbytes)
-
-    def synchronize(self) -> None:
-        with self._lock:
-            self._require_open()
-            rc = self._lib.cdll.ack_sync(self._handle)
-            if rc != ACK_OK:
-                raise _kit_error("sync", rc, self._lib.last_error())
-
-    def timer_start(self) -> None:
-        """Record a start event on the device stream (benchmarks)."""
-        with self._lock:
-            self._require_open()
-            rc = self._lib.cdll.ack_stream_timer(self._handle, 0, None)
-            if rc != ACK_OK:
-                raise _kit_error("timer", rc, self._lib.last_error())
-
-    def timer_stop(self) -> float:
-        """Record a stop event, wait for it, return milliseconds since start."""
-        with self._lock:
-            self._require_open()
-            ms = ctypes.c_float()
-            rc = self._lib.cdll.ack_stream_timer(self._handle, 1, ctypes.byref(ms))
-            if rc != ACK_OK:
-                raise _kit_error("timer", rc, self._lib.last_error())
-            return float(ms.value)
-
-    def set_policy(self, policy: int) -> None:
-        """0: automatic kernel choice; 1: the general matmul kernel only."""
-        with self._lock:
-            self._require_open()
-            rc = self._lib.cdll.ack_vq_set_policy(self._handle, policy)
-            if rc != ACK_OK:
-                raise _kit_error("policy", rc, self._lib.last_error())
+            return
+        self._device.handle  # freeing through a closed device is refused
+        handle, self._handle = self._handle, None
+        self._finalizer.detach()
+        self._device._release(handle)

@@ -533,8 +533,8 @@ int32_t ack_stream_timer(const AckDevice* handle, uint32_t phase, float* ms_out)
 }
 
 int32_t ack_vq_set_policy(const AckDevice* handle, uint32_t policy) {
-  if (policy > 1) {
-    set_error("ack_vq_set_policy: policy must be 0 (automatic) or 1 (general)");
+  if (policy > 2) {
+    set_error("ack_vq_set_policy: policy must be 0 (automatic), 1 (general) or 2 (any size)");
     return ACK_ERR_SHAPE;
   }
   std::shared_ptr<Device> dev;

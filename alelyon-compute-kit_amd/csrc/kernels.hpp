@@ -33,11 +33,13 @@ enum class MatmulPath : int {
 
 const char* matmul_path_name(MatmulPath p);
 
-// Chooses the path for a product; `policy` 1 forces General.
+// Chooses the path for a product; `policy` 1 forces General, 2 takes a
+// factorised path wherever its shape applies, whatever the size (tests).
 MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                               uint32_t count, uint32_t policy);
 
-bool gram_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
+bool gram_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                  bool any_size);
 hipError_t launch_gram(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t group);
 
@@ -62,7 +64,7 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
 
 // The dense-activation product: op 2's geometry and flags with A a dense FP32
 // array in in[0] (in[1] unused). Paths: row-bins (m >= 64), the GEMV paths
-// (m <= 8, after a pass that takes max |x|), else General.
+// (m <= 8; each window's fixed-point scale comes from x itself), else General.
 MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                              uint32_t count, uint32_t policy);
 size_t dense_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,

@@ -11,10 +11,11 @@
 //   C = P . Q,  P[r][(j,e)] = [a(r,j) == e],  Q[(j,e)][c] = Gram[e][b(c,j)],
 // and it runs on v_mfma_f32_32x32x16_f16 with one 16-step of K per group j:
 // P is a one-hot row (exact in fp16), and Q is Gram scaled by a power of two
-// and split into fp16 hi + lo (22 significant bits; relative error below
-// 2^-21 of the largest Gram entry), so each j costs two MFMAs per 32 x 32
+// and split into three fp16 terms hi + mid + lo (33 significant bits: every
+// FP32 Gram entry within 2^-40 of the largest one is carried exactly, the
+// rest to 2^-40 of the largest), so each j costs three MFMAs per 32 x 32
 // output block and the accumulation is FP32. Neither operand is decoded:
-// P is built in registers from A's nibbles, Q is read from a 1 KiB LDS
+// P is built in registers from A's nibbles, Q is read from a 1.5 KiB LDS
 // table addressed by B's nibble.
 //
 // The sum order differs from the shader's sequential one; results agree to
@@ -67,12 +68,14 @@ __device__ __forceinline__ half8 one_hot(uint32_t d) {
   return __builtin_bit_cast(half8, v);
 }
 
+constexpr int kGramTerms = 3;  // fp16 terms of each scaled Gram entry
+
 struct GramTile {
   f32x16 acc[2][2];
 };
 
-// One group j: two one-hot A fragments (rows), hi and lo B fragments for two
-// column blocks from the LDS table, eight MFMAs.
+// One group j: two one-hot A fragments (rows), hi, mid and lo B fragments for
+// two column blocks from the LDS table, twelve MFMAs.
 // dead0/dead1 are OR-ed into the one-hot selectors of rows past the matrix.
 __device__ __forceinline__ void gram_step(GramTile& t, uint32_t aw0, uint32_t aw1, uint32_t bw0,
                                           uint32_t bw1, uint32_t jj, uint32_t h8, uint32_t dead0,
@@ -80,15 +83,16 @@ __device__ __forceinline__ void gram_step(GramTile& t, uint32_t aw0, uint32_t aw
   half8 af[2];
   af[0] = one_hot((__builtin_amdgcn_ubfe(aw0, 4 * jj, 4) - h8) | dead0);
   af[1] = one_hot((__builtin_amdgcn_ubfe(aw1, 4 * jj, 4) - h8) | dead1);
-  half8 bf[2][2];
+  half8 bf[2][kGramTerms];
   const char* p0 = tab_lane + 32 * __builtin_amdgcn_ubfe(bw0, 4 * jj, 4);
   const char* p1 = tab_lane + 32 * __builtin_amdgcn_ubfe(bw1, 4 * jj, 4);
-  bf[0][0] = *reinterpret_cast<const half8*>(p0);
-  bf[0][1] = *reinterpret_cast<const half8*>(p0 + 512);
-  bf[1][0] = *reinterpret_cast<const half8*>(p1);
-  bf[1][1] = *reinterpret_cast<const half8*>(p1 + 512);
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
+  for (int s = 0; s < kGramTerms; ++s) {
+    bf[0][s] = *reinterpret_cast<const half8*>(p0 + 512 * s);
+    bf[1][s] = *reinterpret_cast<const half8*>(p1 + 512 * s);
+  }
+#pragma unroll
+  for (int s = 0; s < kGramTerms; ++s)
 #pragma unroll
     for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -102,7 +106,7 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
                                                                uint32_t k) {
   __shared__ float sa[16 * G];
   __shared__ float sb[16 * G];
-  __shared__ __align__(16) _Float16 tab[2][16][16];  // [hi/lo][B code][A code], scaled Gram
+  __shared__ __align__(16) _Float16 tab[kGramTerms][16][16];  // [term][B code][A code], scaled Gram
   __shared__ float sred[kGramThreads / 64];
   const uint32_t J = k / G;
   const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
@@ -131,7 +135,9 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
     float* out = reinterpret_cast<float*>(static_cast<char*>(o.out) + o.stride[4] * item);
 
     // ---- Gram table: entry (e, f) per thread, in float64, then scaled so
-    // the largest magnitude is below 2^15 and split into fp16 hi + lo.
+    // the largest magnitude is below 2^15 and split into fp16 hi + mid + lo
+    // (each term the fp16 rounding of what the previous ones leave; the
+    // differences are exact in FP32).
     __syncthreads();  // the previous instance's table is no longer read
     for (uint32_t i = tid; i < 16 * G; i += kGramThreads) {
       sa[i] = a_book[i];
@@ -162,8 +168,11 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
     }
     const float scaled = ldexpf(gv, shift);
     const _Float16 hi = _Float16(scaled);
+    const float r1 = scaled - float(hi);
+    const _Float16 mid = _Float16(r1);
     tab[0][f][e] = hi;
-    tab[1][f][e] = _Float16(scaled - float(hi));
+    tab[1][f][e] = mid;
+    tab[2][f][e] = _Float16(r1 - float(mid));
     const float unscale = ldexpf(1.0f, -shift);
     __syncthreads();
 
@@ -216,10 +225,13 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
 
 }  // namespace
 
-bool gram_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags) {
-  (void)m;
-  (void)n;
-  return flags == 2 && k % group == 0;
+// Below kGramMinMacs the general kernel, bit-identical to the shader, is
+// fast enough; `any_size` (the test policy) lifts the bound.
+constexpr uint64_t kGramMinMacs = 1ull << 22;
+
+bool gram_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                  bool any_size) {
+  return flags == 2 && k % group == 0 && (any_size || uint64_t(m) * n * k >= kGramMinMacs);
 }
 
 hipError_t launch_gram(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,

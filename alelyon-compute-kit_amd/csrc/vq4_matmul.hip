@@ -145,11 +145,20 @@ __global__ __launch_bounds__(kGThreads) void k_matmul_general(Operands o, uint32
 
 // ---- shared by the GEMV paths ------------------------------------------------
 // A tile is kTileWords words of each B row (8 * kTileWords output groups);
-// the bins are 32-bit (or paired 64-bit) fixed point in LDS: x is scaled by
-// 2^s from the A codebook's largest magnitude and rounded once, and integer
-// LDS atomics -- exact, and on gfx950 about fifty times the rate of FP32 LDS
-// atomics -- accumulate it; windows of rows are flushed into FP32 registers
-// before an int32 sum could overflow.
+// the bins are 32-bit (or paired 64-bit) fixed point in LDS: each activation
+// x is scaled by 2^s and rounded once, and integer LDS atomics -- exact, and
+// on gfx950 about fifty times the rate of FP32 LDS atomics -- accumulate it.
+// Rows of k are binned in windows; at a window's end its bins are flushed into
+// FP32 registers, scaled back by 2^-s.
+//
+// The scale of a window comes from L1 = sum |x| over its rows (per row of A):
+// a bin holds the sum over a subset of those rows, so every bin, and every
+// sum of bins taken later, is at most 2^s L1 + rows/2 in magnitude. Choosing
+// 2^s L1 (1 + 2^-8) < 2^31 keeps all of them inside int32 whatever the codes
+// (the margin covers the FP32 rounding of the L1 sum itself, ~20 ulps), and
+// makes the rounding step 2^-s at most 2^-30 (1 + 2^-8) L1. So each x is
+// rounded by at most 2^-31 (1 + 2^-8) L1 absolutely: an outlier raises L1 by
+// its own magnitude only, not the step of every other value to its scale.
 constexpr int kTileWords = 32;
 constexpr int kTileGroups = kTileWords * 8;
 constexpr uint32_t kGemvMaxM = 8;    // rows of A one GEMV launch bins
@@ -164,6 +173,41 @@ bool rows_apply(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t fla
   return m <= kGemvMaxM || (m <= kRowsMaxM && uint64_t(n) * k >= kRowsChunkMinWeight);
 }
 
+// A window's fixed-point scale: x -> rint(x 2^shift), from the window's L1.
+__device__ __forceinline__ int window_shift(float l1) {
+  if (!(l1 > 0.0f && l1 <= FLT_MAX)) return 0;  // zero, NaN or Inf (status bit 1 covers the last two)
+  float t = l1 * (1.0f + 0x1p-8f);
+  t = t <= FLT_MAX ? t : FLT_MAX;
+  int ex;
+  frexpf(t, &ex);  // t < 2^ex, so 2^shift * l1 * (1 + 2^-8) < 2^31
+  return 31 - ex;
+}
+
+// S 2^-shift in two power-of-two steps, so that a shift above 126
+// (activations summing below 2^-96) needs no clamp: the first product is
+// exact, the second rounds once, as S 2^-shift itself would.
+__device__ __forceinline__ float unscale(float v, int shift) {
+  const int s1 = shift < 126 ? shift : 126;
+  return ldexpf(ldexpf(v, -s1), s1 - shift);
+}
+
+// 2^31 - 128, the largest float below 2^31: finite activations never reach it
+// (|x| 2^shift < 2^31 (1 - 2^-9)); NaN and Inf, which status bit 1 reports,
+// are clamped so that the integer conversion stays defined.
+constexpr float kQuantMax = 2147483520.0f;
+
+__device__ __forceinline__ int32_t quantize(float x, int shift) {
+  const float v = rintf(ldexpf(x, shift));
+  return int32_t(fminf(fmaxf(v, -kQuantMax), kQuantMax));
+}
+
+// Sum over the 64 lanes of a wave by xor butterfly: every lane ends with the
+// same value (each step adds the same two operands on both sides).
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
 typedef __attribute__((address_space(3))) int32_t lds_i32;
 
 // Integer add into LDS at an absolute byte address. The bins sit at LDS
@@ -172,34 +216,6 @@ typedef __attribute__((address_space(3))) int32_t lds_i32;
 __device__ __forceinline__ void lds_add(uint32_t byte_addr, int32_t v) {
   __hip_atomic_fetch_add(reinterpret_cast<lds_i32*>(static_cast<size_t>(byte_addr)), v,
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-// Dense A (the dense-activation product): the largest |x| of each instance's
-// m x k values sets the fixed-point scale of the GEMV bins. kAmaxParts blocks
-// per instance each write the maximum of their share; the GEMV set-up takes
-// the maximum of the parts. A nonfinite value sets status bit 1.
-constexpr uint32_t kAmaxParts = 16;
-
-__global__ __launch_bounds__(256) void k_dense_amax(Operands o, uint32_t values, float* parts) {
-  __shared__ float wmax[4];
-  for (uint32_t item = blockIdx.y; item < o.count; item += gridDim.y) {
-    const float* x = item_ptr<float>(o.in[0], o.stride[0], item);
-    float mx = 0.0f;
-    bool bad = false;
-    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < values; i += kAmaxParts * 256) {
-      const float v = x[i];
-      bad |= !finite_f32(v);
-      mx = fmaxf(mx, fabsf(v));
-    }
-    for (int off = 1; off < warpSize; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    __syncthreads();  // the previous instance's maxima are read
-    if (threadIdx.x % warpSize == 0) wmax[threadIdx.x / warpSize] = mx;
-    if (__any(bad) && (threadIdx.x % warpSize) == 0) atomicOr(o.status, 1u);
-    __syncthreads();
-    if (threadIdx.x == 0)
-      parts[uint64_t(item) * kAmaxParts + blockIdx.x] =
-          fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  }
 }
 
 // Sum the split-k bins in split order (one thread per bin), then apply the B
@@ -288,10 +304,9 @@ __global__ __launch_bounds__(256) void k_gemv_finish(Operands o, uint32_t n, uin
 // read before the current batch's atomics (LDS ops complete in order, so a
 // read issued after them would wait for them).
 //
-// Integer windows are kPairWindow rows: x is scaled so that max|x| * 2^shift
-// < 2^19 and rounded values are capped at 2^19 - 1, so a window's sums stay
-// inside int32 (|sum| <= 4096 * 2^19 = 2^31 only for negative sums). The
-// quantisation step is at most 2^-19 of max|x|.
+// Windows are kPairWindow rows, the same rows one staging of x covers: the
+// staging takes the window's L1 norm and every read of x quantises it with
+// the window's scale (window_scale), so no sum of the window can leave int32.
 //
 // Finalisation: each thread flushes one 8 x 8 (or SH x SL) sub-block of the
 // 16 x 16 pair-bin matrix of one (p, q), conflict-free (lanes are word
@@ -328,7 +343,7 @@ __device__ __forceinline__ uint32_t cum_part(uint32_t p, uint32_t e, uint32_t q)
   return (p * 16 + e) * kTileWords + (q ^ (2 * (e & 3u) + 8 * p));
 }
 
-// LDS layout (bytes): bins | staged x (later S) | A book | B book x 2 | A words | row maxima.
+// LDS layout (bytes): bins | staged x (later S) | A book | B book x 2 | A words | wave L1 sums.
 // The B book alternates between two copies by instance, so an instance's
 // set-up need not wait for the previous output phase, the book's only reader.
 template <int G>
@@ -338,8 +353,8 @@ struct PairLds {
   static constexpr uint32_t af = xs + (cum ? kCumWords : kPairXRows) * 4;
   static constexpr uint32_t bb = af + 16 * G * 4;
   static constexpr uint32_t aw = bb + 2 * 16 * G * 4;
-  static constexpr uint32_t rmax = aw + kPairMaxAWords * 4;
-  static constexpr uint32_t total = rmax + 16 * 4;
+  static constexpr uint32_t wl1 = aw + kPairMaxAWords * 4;
+  static constexpr uint32_t total = wl1 + 16 * 4;
 };
 
 __device__ __forceinline__ uint32_t pair_dword(uint32_t v, uint32_t p, uint32_t q) {
@@ -388,8 +403,8 @@ struct PairAhead {
 };
 
 // grid: (n tiles, k splits, z); block z serves instances z, z + gridDim.z, ...
-// ks is a multiple of kPairBatchRows. AD: x is dense FP32 in in[0] and in[1]
-// holds the kAmaxParts partial maxima of |x| per instance (k_dense_amax).
+// ks is a multiple of kPairBatchRows. AD: x is dense FP32 in in[0] (in[1] is
+// not read); a nonfinite x sets status bit 1.
 // SW: the slice is one window (ks <= kPairWindow), so the bins are read out
 // once, at the end, and no FP32 accumulator lives through the main loop.
 // X4 (rows of whole 32-word tiles): each lane loads 4 adjacent words of 4 rows
@@ -410,11 +425,11 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   char* lds = reinterpret_cast<char*>(smem);
   int32_t* bins = smem;
   int4* bins4 = reinterpret_cast<int4*>(smem);
-  int32_t* sx = reinterpret_cast<int32_t*>(lds + L::xs);
+  float* sx = reinterpret_cast<float*>(lds + L::xs);    // the window's x, FP32
   float* af = reinterpret_cast<float*>(lds + L::af);
   float* const bb0 = reinterpret_cast<float*>(lds + L::bb);
   uint32_t* aw = reinterpret_cast<uint32_t*>(lds + L::aw);
-  float* rmax = reinterpret_cast<float*>(lds + L::rmax);
+  float* wl1 = reinterpret_cast<float*>(lds + L::wl1);  // per-wave L1 of the staged x
   // Defensive: the perm-built bin addresses assume the bins start at LDS 0.
   if (static_cast<uint32_t>(reinterpret_cast<size_t>((lds_i32*)smem)) != 0) {
     if (threadIdx.x == 0) atomicOr(o.status, 2u);
@@ -463,12 +478,11 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     const uint32_t lt = opaque(tid);
     const __amdgpu_buffer_rsrc_t ars =
         words_rsrc(item_ptr<uint32_t>(o.in[0], o.stride[0], item) + a_w0, a_words * 4u);
-    const __amdgpu_buffer_rsrc_t abk = words_rsrc(item_ptr<float>(o.in[1], o.stride[1], item),
-                                                  AD ? kAmaxParts * 4u : 64u * G);
+    const __amdgpu_buffer_rsrc_t abk =
+        words_rsrc(AD ? nullptr : item_ptr<float>(o.in[1], o.stride[1], item), AD ? 0u : 64u * G);
     const __amdgpu_buffer_rsrc_t bbk = words_rsrc(item_ptr<float>(o.in[3], o.stride[3], item), 64u * G);
     PairAhead h;
-    h.a = __uint_as_float(uint32_t(
-        __builtin_amdgcn_raw_buffer_load_b32(abk, (AD ? lt % kAmaxParts : lt) * 4u, 0, 0)));
+    h.a = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(abk, lt * 4u, 0, 0)));
     h.b = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(bbk, lt * 4u, 0, 0)));
     h.w0 = h.w1 = 0;
     if (!AD) {
@@ -500,7 +514,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   };
 
   uint32_t buf[D][R];
-  int32_t xa[RX], xb[RX];
+  float xa[RX], xb[RX];  // x of the lane's next rows as staged; quantised where binned
   // multi-window: the sub-block's FP32 accumulators; one window: its row and
   // column sums, formed as the bins are read (the same sums in the same order)
   float acc[SW ? 1 : kPairSH][SW ? 1 : kPairSL];
@@ -511,46 +525,60 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   uint32_t rsi[CUM ? kPairSH : 1], csi[CUM ? kPairSL : 1], prv[CUM ? 16 : 1];
 #pragma unroll
   for (int i = 0; i < (CUM ? 16 : 1); ++i) prv[i] = 0;
-  int shift = 0;
+  int shift = 0;  // the current window's fixed-point scale
   uint32_t xbase = k0;
   __amdgpu_buffer_rsrc_t x_rs = words_rsrc(nullptr, 0u);  // AD: this instance's x[0, kend)
 
-  // rows [xb0, xb0 + kPairXRows) of A's single row, quantised; zero past kend
+  // Rows [xb0, xb0 + kPairXRows) of A's single row as FP32, zero past kend,
+  // and each wave's share of their L1 norm in wl1. The caller's barrier
+  // publishes both; take_scale() then sets the window's scale.
   auto stage_x = [&](uint32_t xb0) __attribute__((always_inline)) {
+    float l1 = 0.0f;
+    bool bad = false;
     for (uint32_t r4 = opaque(tid) * 4; r4 < kPairXRows; r4 += 4 * kPairThreads) {
       const uint32_t row = xb0 + r4;
-      int4 v = make_int4(0, 0, 0, 0);
+      float4 f = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       if (AD) {
-        const float lim = 524287.0f;  // 2^19 - 1; reads past kend return zero
-        auto quant = [&](uint32_t rr) {
-          const float f = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(x_rs, rr * 4u, 0, 0)));
-          return int32_t(fminf(rintf(ldexpf(f, shift)), lim));
+        auto ld = [&](uint32_t rr) {  // reads past kend return zero
+          return __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(x_rs, rr * 4u, 0, 0)));
         };
-        v = make_int4(quant(row), quant(row + 1), quant(row + 2), quant(row + 3));
+        f = make_float4(ld(row), ld(row + 1), ld(row + 2), ld(row + 3));
+        bad |= !finite_f32(f.x) || !finite_f32(f.y) || !finite_f32(f.z) || !finite_f32(f.w);
       } else if (row < kend) {
         const uint32_t u = row / G;
         const uint32_t code = (aw[(u >> 3) - a_w0] >> ((u & 7u) * 4u)) & 15u;
-        const float4 f = *reinterpret_cast<const float4*>(af + code * G + row % G);
-        const float lim = 524287.0f;  // 2^19 - 1
-        v.x = int32_t(fminf(rintf(ldexpf(f.x, shift)), lim));
-        v.y = row + 1 < kend ? int32_t(fminf(rintf(ldexpf(f.y, shift)), lim)) : 0;
-        v.z = row + 2 < kend ? int32_t(fminf(rintf(ldexpf(f.z, shift)), lim)) : 0;
-        v.w = row + 3 < kend ? int32_t(fminf(rintf(ldexpf(f.w, shift)), lim)) : 0;
+        f = *reinterpret_cast<const float4*>(af + code * G + row % G);
+        if (row + 1 >= kend) f.y = 0.0f;
+        if (row + 2 >= kend) f.z = 0.0f;
+        if (row + 3 >= kend) f.w = 0.0f;
       }
-      *reinterpret_cast<int4*>(sx + r4) = v;
+      l1 += fabsf(f.x);
+      l1 += fabsf(f.y);
+      l1 += fabsf(f.z);
+      l1 += fabsf(f.w);
+      *reinterpret_cast<float4*>(sx + r4) = f;
     }
+    l1 = wave_sum(l1);
+    if (lane == 0) wl1[wave] = l1;
+    if (AD && tile == 0 && __any(bad) && lane == 0) atomicOr(o.status, 1u);
   };
-  auto read_x = [&](uint32_t b, int32_t (&xs)[RX]) __attribute__((always_inline)) {
+  auto take_scale = [&]() __attribute__((always_inline)) {
+    float l1 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kPairWaves; ++w) l1 += wl1[w];
+    shift = window_shift(l1);
+  };
+  auto read_x = [&](uint32_t b, float (&xs)[RX]) __attribute__((always_inline)) {
     asm volatile("" : "+s"(b));
     if (k0 + b * BR >= kend) {  // a padding batch: nothing staged for it
 #pragma unroll
-      for (uint32_t u = 0; u < RX; ++u) xs[u] = 0;
+      for (uint32_t u = 0; u < RX; ++u) xs[u] = 0.0f;
       return;
     }
-    const int4* xr = reinterpret_cast<const int4*>(sx + (k0 + b * BR + lane_row - xbase));
+    const float4* xr = reinterpret_cast<const float4*>(sx + (k0 + b * BR + lane_row - xbase));
 #pragma unroll
     for (uint32_t c4 = 0; c4 < RX / 4; ++c4) {
-      const int4 v = xr[c4];
+      const float4 v = xr[c4];
       xs[4 * c4] = v.x; xs[4 * c4 + 1] = v.y; xs[4 * c4 + 2] = v.z; xs[4 * c4 + 3] = v.w;
     }
   };
@@ -585,13 +613,13 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
           csum[c] = a == 0 ? v : csum[c] + v;
           rsum[a] = c == 0 ? v : rsum[a] + v;
         } else {
-          acc[a][c] += float(bins[d]);
+          acc[a][c] += unscale(float(bins[d]), shift);
           if (clear) bins[d] = 0;
         }
       }
   };
   // `tail`: a batch of the peeled last D, the only ones that can be the last
-  auto stage = [&](uint32_t (&w)[R], uint32_t b, int32_t (&xs)[RX], int32_t (&xn)[RX],
+  auto stage = [&](uint32_t (&w)[R], uint32_t b, float (&xs)[RX], float (&xn)[RX],
                    __amdgpu_buffer_rsrc_t rs_refill, uint32_t b_refill, bool tail)
                    __attribute__((always_inline)) {
     asm volatile("" : "+s"(b));  // row arithmetic is redone per batch, not strength-reduced
@@ -610,7 +638,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
           const uint32_t a2 = rot1 ? w[4 * u + 3] : w[4 * u + 2];
           const uint32_t a3 = rot1 ? w[4 * u] : w[4 * u + 3];
           const uint32_t r[4] = {rot2 ? a2 : a0, rot2 ? a3 : a1, rot2 ? a0 : a2, rot2 ? a1 : a3};
-          const int32_t xv = xs[u];
+          const int32_t xv = quantize(xs[u], shift);
 #pragma unroll
           for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -620,7 +648,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
 #pragma unroll
         for (uint32_t u = 0; u < R; ++u) {
           const uint32_t ww = w[u];
-          const int32_t xv = xs[u];
+          const int32_t xv = quantize(xs[u], shift);
 #pragma unroll
           for (int p = 0; p < 4; ++p) lds_add(__builtin_amdgcn_perm(ww, lcs[0], kSel[p]), xv);
         }
@@ -638,6 +666,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       xbase = k0 + done;
       stage_x(xbase);
       __syncthreads();
+      take_scale();  // the flush above used the previous window's
       read_x(b + 1, xn);
       // settle here, so at the join the common path's x (read a batch
       // earlier) needs no wait behind this batch's atomics
@@ -676,13 +705,6 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     if (!AD && st < a_words) aw[st] = cur.w0;
     if (!AD && st + kPairThreads < a_words) aw[st + kPairThreads] = cur.w1;
     if (AD) x_rs = words_rsrc(item_ptr<float>(o.in[0], o.stride[0], item), kend * 4u);
-    // largest |A book entry| (AD: largest |x|): every thread holds one book
-    // entry (zero past the book) or one of the 16 partial maxima; NaN counts
-    // as zero, as in a running fmaxf from zero
-    {
-      const float m = wave_max_nonneg(fmaxf(0.0f, AD ? cur.a : fabsf(cur.a)));
-      if (st % 64 == 0) rmax[st / 64] = m;
-    }
     __syncthreads();
     // the previous instance's pl/ph (the first kPairPartWords bins) are read
     if (!CUM) {
@@ -691,23 +713,10 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
         bins4[st + i * kPairThreads] = make_int4(0, 0, 0, 0);
     }
     if (tile == 0 && split == 0) sweep_books(AD ? bb : af, bb, 16 * G, o.status);
-    float amax = 0.0f;
-#pragma unroll
-    for (int t = 0; t < kPairWaves; t += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(rmax + t);
-      amax = fmaxf(amax, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
-    }
-    shift = 0;
-    if (amax > 0.0f) {
-      int ex;
-      frexpf(amax, &ex);  // amax < 2^ex: max|x| * 2^shift < 2^19
-      shift = 31 - (ex + 12);
-      shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
-    }
-    const float unscale = ldexpf(1.0f, -shift);
     xbase = k0;
     stage_x(xbase);
     __syncthreads();
+    take_scale();
     read_x(0, xa);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // settle the first x before the loop
     // the next instance's set-up data moves up; the one after is requested now
@@ -788,10 +797,10 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     if (!CUM) {
 #pragma unroll
       for (int c = 0; c < kPairSL; ++c)
-        pl[pair_part(fh, fp, fl * kPairSL + c, fq)] = csum[c] * unscale;
+        pl[pair_part(fh, fp, fl * kPairSL + c, fq)] = SW ? unscale(csum[c], shift) : csum[c];
 #pragma unroll
       for (int a = 0; a < kPairSH; ++a)
-        ph[pair_part(fl, fp, fh * kPairSH + a, fq)] = rsum[a] * unscale;
+        ph[pair_part(fl, fp, fh * kPairSH + a, fq)] = SW ? unscale(rsum[a], shift) : rsum[a];
     }
     __syncthreads();
     // S entry (p, e, q) of nibble 2 p + odd, from the cumulative partials
@@ -799,7 +808,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       const uint32_t at = cum_part(p, e, qq);
       const uint32_t v0 = cpt[(odd ? kCumHiBase : 0u) + at];
       const uint32_t v1 = cpt[kCumHalfWords + at];  // odd nibbles: read, unused
-      return float(int32_t(odd ? v0 : v0 + v1)) * unscale;
+      return unscale(float(int32_t(odd ? v0 : v0 + v1)), shift);
     };
     const uint32_t groups = (rw - tile * kTileWords) < kTileWords ? (rw - tile * kTileWords) * 8
                                                                  : kTileGroups;
@@ -939,8 +948,6 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   }
 }
 
-static_assert(kAmaxParts == 16, "the GEMV set-up reduces 16 partial maxima");
-
 size_t pairs_shmem(uint32_t g) {
   return g == 8 ? PairLds<8>::total : (g == 16 ? PairLds<16>::total : PairLds<32>::total);
 }
@@ -971,9 +978,12 @@ constexpr uint32_t kRowWindow = 4096;
 constexpr uint32_t kRowXBytes = 16384;
 constexpr uint32_t kRowAWords = 2048;                              // A words of a slice
 
-// Rows of x per staged chunk for MP row pairs: whole batches.
+// Rows of x per staged chunk for MP row pairs: a power of two, so that the
+// chunks tile every window (a window's rows share one scale per row of A).
 __host__ __device__ constexpr uint32_t row_x_rows(uint32_t mp) {
-  return kRowXBytes / (8 * mp) / kRowBatchRows * kRowBatchRows;
+  uint32_t rows = kRowWindow;
+  while (rows * 8 * mp > kRowXBytes) rows /= 2;
+  return rows;
 }
 
 template <int G, int MP>
@@ -984,8 +994,9 @@ struct RowLds {
   static constexpr uint32_t af = xs + xr * MP * 8;
   static constexpr uint32_t bb = af + 16 * G * 4;
   static constexpr uint32_t aw = bb + 16 * G * 4;
-  static constexpr uint32_t rmax = aw + kRowAWords * 4;
-  static constexpr uint32_t total = rmax + 16 * 4;
+  static constexpr uint32_t wl1 = aw + kRowAWords * 4;       // [wave][row] L1 partials
+  static constexpr uint32_t wsh = wl1 + (kRowThreads / 64) * 8 * 4;  // [row] window shifts
+  static constexpr uint32_t total = wsh + 8 * 4;
 };
 
 typedef __attribute__((address_space(3))) int64_t lds_i64;
@@ -1015,7 +1026,10 @@ struct RowAhead {
   float a, b;      // entry tid of the A and B books
 };
 
-// AD: A is dense FP32 in in[0]; in[1] holds the partial maxima of |x|.
+// AD: A is dense FP32 in in[0] (in[1] is not read); a nonfinite x sets status
+// bit 1. Each row of A has its own scale per window (window_scale of the
+// row's L1 over the window's rows), so rows of very different magnitudes
+// each keep their full precision.
 // The launch bins rows r0 .. r0 + m - 1 of A's `mall` rows (outputs are
 // written from o.out, which the caller offsets to row r0).
 // X4 (rows of whole 32-word tiles): each lane loads 4 adjacent words of R/4
@@ -1038,7 +1052,7 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
   static_assert(kRowAWords <= 4 * kRowThreads, "A words per thread");
   using L = RowLds<G, MP>;
   constexpr uint32_t XR = L::xr;
-  static_assert(XR >= BR && kRowWindow % BR == 0, "staging");
+  static_assert(XR >= BR && kRowWindow % XR == 0 && XR % BR == 0, "staging chunks tile windows");
   extern __shared__ int32_t smem[];
   char* lds = reinterpret_cast<char*>(smem);
   int64_t* bins = reinterpret_cast<int64_t*>(smem);
@@ -1046,7 +1060,8 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
   float* af = reinterpret_cast<float*>(lds + L::af);
   float* bb = reinterpret_cast<float*>(lds + L::bb);
   uint32_t* aw = reinterpret_cast<uint32_t*>(lds + L::aw);
-  float* rmax = reinterpret_cast<float*>(lds + L::rmax);
+  float* wl1 = reinterpret_cast<float*>(lds + L::wl1);
+  int32_t* wsh = reinterpret_cast<int32_t*>(lds + L::wsh);
   if (static_cast<uint32_t>(reinterpret_cast<size_t>((lds_i32*)smem)) != 0) {
     if (threadIdx.x == 0) atomicOr(o.status, 2u);
     return;
@@ -1088,12 +1103,11 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
     const uint32_t a_words_all = ((a_vec_elems + G - 1) / G + 7) / 8;
     const __amdgpu_buffer_rsrc_t ars =
         words_rsrc(item_ptr<uint32_t>(o.in[0], o.stride[0], item), a_words_all * 4u);
-    const __amdgpu_buffer_rsrc_t abk = words_rsrc(item_ptr<float>(o.in[1], o.stride[1], item),
-                                                  AD ? kAmaxParts * 4u : 64u * G);
+    const __amdgpu_buffer_rsrc_t abk =
+        words_rsrc(AD ? nullptr : item_ptr<float>(o.in[1], o.stride[1], item), AD ? 0u : 64u * G);
     const __amdgpu_buffer_rsrc_t bbk = words_rsrc(item_ptr<float>(o.in[3], o.stride[3], item), 64u * G);
     RowAhead h;
-    h.a = __uint_as_float(uint32_t(
-        __builtin_amdgcn_raw_buffer_load_b32(abk, (AD ? lt % kAmaxParts : lt) * 4u, 0, 0)));
+    h.a = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(abk, lt * 4u, 0, 0)));
     h.b = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(bbk, lt * 4u, 0, 0)));
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1133,31 +1147,65 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
 
   uint32_t buf[D][R];
   float acc[kPer][2];
-  int shift = 0;
   uint32_t xbase = k0;
   __amdgpu_buffer_rsrc_t x_rs = words_rsrc(nullptr, 0u);  // AD: this instance's m x k values
 
-  // one quantised activation of A
-  auto x_of = [&](uint32_t r, uint32_t kk) -> int32_t {
+  // one activation of A, as FP32
+  auto x_val = [&](uint32_t r, uint32_t kk) -> float {
     const uint32_t flat = (flags & 1u) ? kk * mall + r0 + r : (r0 + r) * k + kk;
-    if (AD) {
-      const float f = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(x_rs, flat * 4u, 0, 0)));
-      return int32_t(fminf(rintf(ldexpf(f, shift)), 524287.0f));
-    }
+    if (AD)
+      return __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(x_rs, flat * 4u, 0, 0)));
     const uint32_t v = flat / G;
     const uint32_t slot = (flags & 1u) ? (v >> 3) - a_base(0) : r * awn.per_row + (v >> 3) - a_base(r);
     const uint32_t code = (aw[slot] >> ((v & 7u) * 4u)) & 15u;
-    const float lim = 524287.0f;  // 2^19 - 1: a 4096-row window of sums fits int32
-    return int32_t(fminf(rintf(ldexpf(af[code * G + flat % G], shift)), lim));
+    return af[code * G + flat % G];
   };
-  // rows [xb0, xb0 + XR): per row and row pair, the 64-bit addend's two halves
+  // Per-row L1 of x over the window of rows [w0, min(w0 + kRowWindow, kend)),
+  // then each row's shift for that window in wsh (LDS: nothing of it lives
+  // in registers through the main loop). Two barriers; flags a nonfinite x.
+  auto window_scales = [&](uint32_t w0) __attribute__((always_inline)) {
+    constexpr int kPerWin = kRowWindow / kRowThreads;
+    const uint32_t w1 = (w0 + kRowWindow) < kend ? (w0 + kRowWindow) : kend;
+    const uint32_t t = opaque(tid);
+    bool bad = false;
+#pragma unroll 1
+    for (uint32_t r = 0; r < 2 * MP; ++r) {
+      float l1 = 0.0f;
+      if (r < m) {
+        float v[kPerWin];
+#pragma unroll
+        for (int j = 0; j < kPerWin; ++j) {
+          const uint32_t kk = w0 + t + j * kRowThreads;
+          v[j] = kk < w1 ? x_val(r, kk) : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kPerWin; ++j) {
+          bad |= !finite_f32(v[j]);
+          l1 += fabsf(v[j]);
+        }
+      }
+      l1 = wave_sum(l1);
+      if (lane == 0) wl1[wave * 8 + r] = l1;
+    }
+    if (AD && tile == 0 && __any(bad) && lane == 0) atomicOr(o.status, 1u);
+    __syncthreads();
+    if (t < 2 * MP) {
+      float l1 = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kRowThreads / 64; ++w) l1 += wl1[w * 8 + t];
+      wsh[t] = window_shift(l1);
+    }
+    __syncthreads();
+  };
+  // rows [xb0, xb0 + XR): per row and row pair, the 64-bit addend's two
+  // halves, each quantised with its own row's scale
   auto stage_x = [&](uint32_t xb0) __attribute__((always_inline)) {
     for (uint32_t idx = opaque(tid); idx < XR * MP; idx += kRowThreads) {
       const uint32_t kk = xb0 + idx / MP, rp = idx % MP;
       int32_t lo = 0, hi = 0;
       if (kk < kend) {
-        if (2 * rp < m) lo = x_of(2 * rp, kk);
-        if (2 * rp + 1 < m) hi = x_of(2 * rp + 1, kk);
+        if (2 * rp < m) lo = quantize(x_val(2 * rp, kk), wsh[2 * rp]);
+        if (2 * rp + 1 < m) hi = quantize(x_val(2 * rp + 1, kk), wsh[2 * rp + 1]);
       }
       sx[idx] = make_int2(lo, hi + (lo >> 31));
     }
@@ -1173,10 +1221,11 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const uint32_t bi = ft + i * kRowThreads;
+      const uint32_t rp = (bi / kTileWords) % MP;  // bin (e, n8, rp, q)
       const int64_t v = bins[bi];
       const uint32_t lo = uint32_t(uint64_t(v)), hi = uint32_t(uint64_t(v) >> 32);
-      acc[i][0] += float(int32_t(lo));
-      acc[i][1] += float(int32_t(hi + (lo >> 31)));
+      acc[i][0] += unscale(float(int32_t(lo)), wsh[2 * rp]);
+      acc[i][1] += unscale(float(int32_t(hi + (lo >> 31))), wsh[2 * rp + 1]);
       if (clear) bins[bi] = 0;
     }
   };
@@ -1235,6 +1284,8 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
     }
     if (restage) {
       if (!wend) __syncthreads();
+      // a new window starts: its scales (the flush above used the old ones)
+      if (done % kRowWindow == 0) window_scales(k0 + done);
       xbase = k0 + done;
       stage_x(xbase);
       __syncthreads();
@@ -1273,34 +1324,7 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
     for (int i = 0; i < kPer; ++i) bins[st + i * kRowThreads] = 0;
     __syncthreads();
     if (tile == 0 && split == 0) sweep_books(AD ? bb : af, bb, 16 * G, o.status);
-    if (st < 16) {
-      float mx = 0.0f;
-      if (AD) {
-        mx = cur.a;
-      } else {
-#pragma unroll
-        for (int t = 0; t < G; t += 4) {
-          const float4 v = *reinterpret_cast<const float4*>(af + st * G + t);
-          mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        }
-      }
-      rmax[st] = mx;
-    }
-    __syncthreads();
-    float amax = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 16; t += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(rmax + t);
-      amax = fmaxf(amax, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
-    }
-    shift = 0;
-    if (amax > 0.0f) {
-      int ex;
-      frexpf(amax, &ex);  // max|x| * 2^shift < 2^19
-      shift = 31 - (ex + 12);
-      shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
-    }
-    const float unscale = ldexpf(1.0f, -shift);
+    window_scales(k0);
     xbase = k0;
     stage_x(xbase);
     __syncthreads();
@@ -1331,7 +1355,7 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
 #pragma unroll
       for (uint32_t h = 0; h < 2; ++h) {
         const uint32_t r = 2 * rp + h;
-        const float s = acc[i][h] * unscale;
+        const float s = acc[i][h];  // scaled back at each flush
         if (gridDim.y == 1) {
           ss[((r * 16 + e) * 8 + n8) * kTileWords + qq] = s;
         } else if (r < m) {
@@ -1547,7 +1571,7 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
                               uint32_t count, uint32_t policy) {
   if (policy == 1) return MatmulPath::General;
   if (count == 1 && rowbins_applies(m, n, k, group, flags)) return MatmulPath::RowBins;
-  if (gram_applies(m, n, k, group, flags)) return MatmulPath::GramMfma;
+  if (gram_applies(m, n, k, group, flags, policy == 2)) return MatmulPath::GramMfma;
   if (rows_apply(m, n, k, group, flags))
     return m == 1 ? MatmulPath::GemvPairs : MatmulPath::GemvRows;
   return MatmulPath::General;
@@ -1601,13 +1625,11 @@ MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group,
   return MatmulPath::General;
 }
 
-// The factorised paths' split-k partials, then (256-byte aligned) the
-// partial maxima of |x|.
+// The factorised paths' split-k partials (the GEMV kernels take each window's
+// scale from x themselves, so the dense product needs nothing more).
 size_t dense_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                              uint32_t flags, uint32_t count) {
-  const size_t base = matmul_workspace_bytes(p, m, n, k, group, flags, count);
-  if (p != MatmulPath::GemvRows && p != MatmulPath::GemvPairs) return base;
-  return (base + 255) / 256 * 256 + size_t(count) * kAmaxParts * sizeof(float);
+  return matmul_workspace_bytes(p, m, n, k, group, flags, count);
 }
 
 hipError_t launch_matmul_dense(hipStream_t s, const Operands& o, uint32_t m, uint32_t n,
@@ -1615,18 +1637,8 @@ hipError_t launch_matmul_dense(hipStream_t s, const Operands& o, uint32_t m, uin
                                void* workspace, size_t workspace_bytes) {
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins_dense(s, o, m, n, k, group, workspace);
-  if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows) {
-    const size_t base = matmul_workspace_bytes(path, m, n, k, group, flags, o.count);
-    float* parts = reinterpret_cast<float*>(static_cast<char*>(workspace) + (base + 255) / 256 * 256);
-    Operands od = o;
-    od.in[1] = parts;
-    od.stride[1] = kAmaxParts * sizeof(float);
-    const uint32_t zc = o.count < 65535 ? o.count : 65535;
-    k_dense_amax<<<dim3(kAmaxParts, zc), 256, 0, s>>>(od, m * k, parts);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    return launch_factorised<true>(s, od, m, n, k, group, flags, path, workspace);
-  }
+  if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows)
+    return launch_factorised<true>(s, o, m, n, k, group, flags, path, workspace);
   const uint32_t zc = o.count < 65535 ? o.count : 65535;
   dim3 grid((n + kGT - 1) / kGT, (m + kGT - 1) / kGT, zc);
   if (group == 8) k_matmul_general<8, true><<<grid, kGThreads, 0, s>>>(o, m, n, k, flags);

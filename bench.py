@@ -291,7 +291,7 @@ def bench_config5(device, dev, steps, warmup):
     del grad
     opt = vq.VQAdamW(dev, w_img, lr=1e-3, betas=(0.9, 0.999))
     # op-3 AdamW to dense scratch, resident
-    count, c4, b4, coeff = vq.VQDevice._adamw_inputs(
+    count, c4, b4, coeff = vq.VQDevice.op3_inputs(
         opt.weight, opt.momentum, opt.variance, g_img, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1)
     bufs = [device.buffer(a.nbytes) for a in (c4, b4, coeff)]
     scratch = device.buffer(3 * count * 4)

@@ -33,7 +33,7 @@ class OracleBackend:
         return out.reshape(value.shape)
 
     def matmul(self, a, b, *, transpose_a=False, transpose_b=False):
-        m, n, k, flags = vq.VQDevice._matmul_geometry(a, b, transpose_a, transpose_b)
+        m, n, k, flags = vq.VQDevice.matmul_geometry(a, b, transpose_a, transpose_b)
         out, status = self.oracle.matmul(a.codes, a.codebook, b.codes, b.codebook,
                                          m, n, k, a.group, flags)
         self._ok(status, "matmul")
@@ -41,7 +41,7 @@ class OracleBackend:
 
     def adamw(self, weight, momentum, variance, gradient, *, lr, beta1, beta2, eps,
               weight_decay, step):
-        count, codes, books, coefficients = vq.VQDevice._adamw_inputs(
+        count, codes, books, coefficients = vq.VQDevice.op3_inputs(
             weight, momentum, variance, gradient, lr, beta1, beta2, eps, weight_decay, step)
         out, status = self.oracle.adamw(codes, books, coefficients, count, weight.group)
         self._ok(status, "adamw")

@@ -22,7 +22,7 @@ def _weight(rng, shape, group, scale=0.02):
 def _check(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol=1e-5):
     from alelyon_compute_kit import vq
     from oracle import vq4_numpy as o
-    m, n, k, flags = vq.VQDevice._dense_geometry(x, w, transpose_a, transpose_b)
+    m, n, k, flags = vq.VQDevice.dense_geometry(x, w, transpose_a, transpose_b)
     words = (2, m, n, k, w.group, 16, flags, 0)
     assert vqdev.dense_path_name(words) == path
     say("dense matmul", path, m, n, k, w.group, flags)
@@ -64,16 +64,65 @@ def test_dense_gemv_transposed_activations(vqdev, oracle):
     _check(vqdev, oracle, x, w, True, False, "gemv-rows")
 
 
+def _rows_within(y, exact, tol=1e-5):
+    """Each row against its own largest magnitude."""
+    from oracle import vq4_numpy as o
+    for r in range(exact.shape[0]):
+        if np.any(exact[r]):
+            assert o.max_rel(y[r], exact[r]) <= tol, f"row {r}"
+        else:
+            assert not np.any(y[r]), f"row {r}"
+
+
 def test_dense_gemv_outliers_and_zero_rows(vqdev, oracle):
     rng = np.random.default_rng(6)
     w = _weight(rng, (2048, 8 * 16 * 32), 16)
     x = rng.standard_normal((4, 2048)).astype(np.float32)
     x[1] = 0.0                                              # an all-zero row
-    x[2, 7] = 30.0                                          # one outlier sets the scale
-    _check(vqdev, oracle, x, w, False, False, "gemv-rows", tol=2e-5)
+    x[2, 7] = 30.0                                          # one outlier in a N(0,1) row
+    y = _check(vqdev, oracle, x, w, False, False, "gemv-rows")
+    _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
     zero = np.zeros((1, 2048), np.float32)
     y = vqdev.matmul_dense(zero, w)
     assert not np.any(y)
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("k", [4096, 14336])
+def test_dense_gemv_outlier_per_row(vqdev, oracle, m, k):
+    """N(0,1) rows with one activation of 30 each, at config 3's k and at
+    config 4's 14336 (several integer windows)."""
+    rng = np.random.default_rng(k + m)
+    w = _weight(rng, (k, 2048), 16)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[np.arange(m), rng.integers(0, k, m)] = 30.0
+    y = _check(vqdev, oracle, x, w, False, False, "gemv-pairs" if m == 1 else "gemv-rows")
+    _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
+
+
+def test_dense_gemv_rows_of_very_different_magnitude(vqdev, oracle):
+    """Rows 1e-6, 1, 30 and 1e-30 in scale in one product: each row has its
+    own fixed-point scale, so each keeps the 1e-5 bar against its own
+    largest output (one scale from the largest row would zero the others)."""
+    rng = np.random.default_rng(61)
+    w = _weight(rng, (4096, 4096), 16)
+    x = rng.standard_normal((4, 4096)).astype(np.float32)
+    x *= np.array([[1e-6], [1.0], [30.0], [1e-30]], np.float32)
+    y = _check(vqdev, oracle, x, w, False, False, "gemv-rows")
+    _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_dense_gemv_tiny_activations(vqdev, oracle, m):
+    """Activations summing to far below 2^-96 per window (the fixed-point
+    shift passes 126; the scale back is taken in two exact steps): the
+    results are those of the float64 product, not zero."""
+    rng = np.random.default_rng(62 + m)
+    w = _weight(rng, (2048, 4096), 16, scale=1.0)
+    x = (rng.standard_normal((m, 2048)) * 1e-33).astype(np.float32)
+    y = _check(vqdev, oracle, x, w, False, False, "gemv-pairs" if m == 1 else "gemv-rows")
+    assert np.abs(y).max() > 0
+    _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
 
 
 @pytest.mark.parametrize("group", [8, 16, 32])

@@ -49,6 +49,15 @@ def general(device):
     device.set_policy(0)
 
 
+@pytest.fixture
+def any_size(device):
+    """Factorised paths wherever their shape applies, also below the sizes
+    at which the automatic choice keeps the general kernel."""
+    device.set_policy(2)
+    yield
+    device.set_policy(0)
+
+
 GENERAL_SHAPES = [(3, 5, 7, 8), (37, 53, 96, 16), (64, 64, 64, 32), (1, 256, 256, 16),
                   (130, 70, 33, 8)]
 
@@ -412,9 +421,10 @@ def test_row_bins_within_tolerance(vqdev, oracle, m, n, k, group):
     assert o.max_rel(out, _ref64(ops, m, n, k, group, 0)) <= TOL
 
 
-def test_config4_forward_rows_against_float64(vqdev):
+def test_config4_forward_against_float64(vqdev):
     """BASELINE config 4 forward at full size: X 2048x4096 . W 4096x14336 at
-    group 32; 16 rows checked against float64, all rows finite."""
+    group 32; every output against the float64 product of the decoded
+    operands, over the whole matrix and row by row."""
     from alelyon_compute_kit import vq
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(4)
@@ -425,10 +435,10 @@ def test_config4_forward_rows_against_float64(vqdev):
     assert vqdev.path_name((2, 2048, 14336, 4096, 32, 16, 0, 0)) == "row-bins"
     say("config4 forward")
     y = vqdev.matmul(x_img, w_img)
-    rows = np.r_[0:8, 2040:2048]
-    ref = x_img.decode()[rows].astype(np.float64) @ w_img.decode().astype(np.float64)
-    assert o.max_rel(y[rows], ref) <= TOL
-    assert np.isfinite(y).all()
+    ref = x_img.decode().astype(np.float64) @ w_img.decode().astype(np.float64)
+    assert o.max_rel(y, ref) <= TOL
+    row_err = np.abs(y - ref).max(axis=1) / np.abs(ref).max(axis=1)
+    assert row_err.max() <= TOL, f"row {int(row_err.argmax())}"
 
 
 # (m, n, k, group): k / group of 12, 17 and 33 start rows mid-word
@@ -437,13 +447,15 @@ GRAM_SHAPES = [(1, 256, 256, 16), (37, 53, 96, 8), (64, 96, 128, 32), (130, 200,
 
 
 @pytest.mark.parametrize("m,n,k,group", GRAM_SHAPES)
-def test_gram_mfma_within_tolerance(vqdev, oracle, m, n, k, group):
+def test_gram_mfma_within_tolerance(vqdev, oracle, any_size, m, n, k, group):
     """B stored (n, k) with both operands grouped along k: one-hot A times the
-    codebooks' Gram table on fp16 MFMA (hi + lo split)."""
+    codebooks' Gram table on fp16 MFMA (hi + mid + lo split). Products below
+    2^22 multiply-adds take the general kernel by default; the test policy
+    sends them through the Gram kernel."""
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(m * 7 + n + k)
     words = (2, m, n, k, group, 16, 2, 0)
-    assert vqdev.path_name(words) == "gram-mfma"
+    assert vqdev.path_name(words) == ("gram-mfma" if m * n * k >= 1 << 22 else "general")
     say("gram-mfma", m, n, k, group)
     ops = _operands(rng, m, n, k, group, 0.1, 0.02)
     out, status = _gpu(vqdev, ops, m, n, k, group, 2)
@@ -453,7 +465,7 @@ def test_gram_mfma_within_tolerance(vqdev, oracle, m, n, k, group):
     assert o.max_rel(out, _ref64(ops, m, n, k, group, 2)) <= TOL
 
 
-def test_gram_mfma_batched(vqdev, oracle):
+def test_gram_mfma_batched(vqdev, oracle, any_size):
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(123)
     m, n, k, group, count = 70, 96, 160, 16, 5
@@ -467,7 +479,7 @@ def test_gram_mfma_batched(vqdev, oracle):
         assert o.max_rel(out[i], ref) <= TOL
 
 
-def test_gram_mfma_status_on_overflow(vqdev, oracle):
+def test_gram_mfma_status_on_overflow(vqdev, oracle, any_size):
     from oracle import vq4_numpy as o
     codes = o.pack_indices(np.zeros(4, np.int64))
     book = np.full((16, 8), 3e19, np.float32)
@@ -476,10 +488,11 @@ def test_gram_mfma_status_on_overflow(vqdev, oracle):
     assert status == oracle.matmul(codes, book, codes, book, 4, 4, 8, 8, 2)[1] == 1
 
 
-def test_config4_backward_rows_against_float64(vqdev):
+def test_config4_backward_against_float64(vqdev):
     """BASELINE config 4 backward at full size: dY 2048x14336 ~ N(0, 1e-2) .
-    W^T with W 4096x14336 stored (n, k) at group 32; 16 rows checked against
-    float64, all rows finite."""
+    W^T with W 4096x14336 stored (n, k) at group 32; every output against the
+    float64 product of the decoded operands, over the whole matrix and row by
+    row."""
     from alelyon_compute_kit import vq
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(5)
@@ -491,10 +504,10 @@ def test_config4_backward_rows_against_float64(vqdev):
     say("config4 backward")
     y = vqdev.matmul(dy_img, w_img, transpose_b=True)
     assert y.shape == (2048, 4096)
-    rows = np.r_[0:8, 2040:2048]
-    ref = dy_img.decode()[rows].astype(np.float64) @ w_img.decode().astype(np.float64).T
-    assert o.max_rel(y[rows], ref) <= TOL
-    assert np.isfinite(y).all()
+    ref = dy_img.decode().astype(np.float64) @ w_img.decode().astype(np.float64).T
+    assert o.max_rel(y, ref) <= TOL
+    row_err = np.abs(y - ref).max(axis=1) / np.abs(ref).max(axis=1)
+    assert row_err.max() <= TOL, f"row {int(row_err.argmax())}"
 
 
 @pytest.mark.parametrize("m,flags", [(1, 0), (6, 2), (48, 1), (200, 0)])
@@ -520,3 +533,142 @@ def test_matmul_batch_method_matches_each_instance(vqdev, m, flags):
     with pytest.raises(ValueError, match="share shapes"):
         vqdev.matmul_batch(a[:2], [b[0], vq.encode(b_vals[1].T.copy(), b[1].codebook,
                                                     group=group)])
+
+
+# ---- activations with outliers, rows of different magnitudes ------------------
+def _outlier_a(rng, m, k, group, *, tiny_rows=False):
+    """A (m x k, groups along k) whose codebook has one outlier entry, 7 =
+    30.0 in every component, that each row uses exactly once; the other
+    vectors draw from entries 4..15 ~ N(0,1). With tiny_rows the even rows use
+    only entries 0..3, ~ 1e-6 N(0,1): rows 2^20 below their neighbours."""
+    from oracle import vq4_numpy as o
+    book = rng.standard_normal((16, group)).astype(np.float32)
+    book[:4] *= np.float32(1e-6)
+    book[7] = np.float32(30.0)
+    per_row = k // group
+    idx = rng.choice(np.r_[4:7, 8:16], size=(m, per_row))
+    idx[np.arange(m), rng.integers(0, per_row, m)] = 7
+    if tiny_rows:
+        idx[0::2] = rng.integers(0, 4, size=idx[0::2].shape)
+    return o.pack_indices(idx.reshape(-1)), book
+
+
+def _check_rows(out, ref, tol=TOL):
+    """max_rel over the whole output and row by row, each row against its own
+    largest magnitude."""
+    from oracle import vq4_numpy as o
+    assert o.max_rel(out, ref) <= tol
+    for r in range(ref.shape[0]):
+        assert o.max_rel(out[r], ref[r]) <= tol, f"row {r}"
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("k,n", [(4096, 4096), (14336, 2048)])
+@pytest.mark.parametrize("count", [1, 256])
+def test_gemv_outlier_codebook_entry(vqdev, oracle, m, k, n, count):
+    """One activation of 30 per row among N(0,1) ones: the fixed-point step
+    follows the window's L1 norm, so the outlier costs no precision elsewhere.
+    count = 1 splits k over blocks (finish kernel); 256 instances run whole
+    slices of one window per block, the config-3 path."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(k + m + count)
+    group = 16
+    a_codes, a_book = _outlier_a(rng, m, k, group)
+    b_codes, b_book = image(rng, k * n, group, 0.02)
+    one = (a_codes, a_book, b_codes, b_book)
+    ops = tuple(np.tile(a.reshape(-1), count) for a in one)
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == ("gemv-pairs" if m == 1 else "gemv-rows")
+    say("gemv outlier entry", m, k, n, count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    out = out.reshape(count, m, n)
+    ref, ref_status = oracle.matmul(*one, m, n, k, group, 0)
+    assert ref_status == 0
+    exact = _ref64(one, m, n, k, group, 0)
+    for i in sorted({0, count // 2, count - 1}):
+        _check_rows(out[i], ref.reshape(m, n))
+        _check_rows(out[i], exact)
+    # every instance holds the same operands: the same bits
+    assert (out.view(np.uint32) == out[0].view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("m", [2, 5, 8])
+@pytest.mark.parametrize("count", [1, 256])
+def test_gemv_rows_each_row_its_own_scale(vqdev, oracle, m, count):
+    """Rows of A 2^20 apart in magnitude in one launch (even rows ~1e-6,
+    odd rows ~1 with an outlier of 30): every row, checked against its own
+    largest output, keeps the 1e-5 bar; a shared scale would round the small
+    rows to zero."""
+    rng = np.random.default_rng(300 + m + count)
+    k, n, group = 4096, 4096, 16
+    a_codes, a_book = _outlier_a(rng, m, k, group, tiny_rows=True)
+    b_codes, b_book = image(rng, k * n, group, 0.02)
+    one = (a_codes, a_book, b_codes, b_book)
+    ops = tuple(np.tile(a.reshape(-1), count) for a in one)
+    say("gemv-rows own scale", m, count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    out = out.reshape(count, m, n)
+    exact = _ref64(one, m, n, k, group, 0)
+    assert np.abs(exact[0]).max() < 1e-3 < np.abs(exact[1]).max()
+    for i in sorted({0, count - 1}):
+        _check_rows(out[i], exact)
+
+
+# ---- status word on the reordered paths ----------------------------------------
+# path, m, n, k, group, flags: shapes each path takes
+STATUS_PATHS = [("gemv-pairs", 1, 512, 512, 16, 0), ("gemv-rows", 4, 512, 512, 16, 0),
+                ("gemv-rows", 7, 384, 1024, 8, 1), ("row-bins", 128, 512, 256, 16, 0),
+                ("gram-mfma", 64, 96, 1024, 16, 2)]
+
+
+def _status_case(rng, case, m, n, k, group):
+    """Operands of one status case: a NaN in A's book, an Inf in B's, a
+    product that overflows (3e19 * 3e19), or clean operands."""
+    ops = list(_operands(rng, m, n, k, group, 1.0, 0.02))
+    if case == "nan_a":
+        ops[1] = ops[1].copy()
+        ops[1][11, 3] = np.nan                 # an entry no code need select
+    elif case == "inf_b":
+        ops[3] = ops[3].copy()
+        ops[3][2, 0] = np.inf
+    elif case == "overflow":
+        ops[1] = np.full_like(ops[1], 3e19)
+        ops[3] = np.full_like(ops[3], 3e19)
+    return tuple(ops)
+
+
+@pytest.mark.parametrize("path,m,n,k,group,flags", STATUS_PATHS)
+@pytest.mark.parametrize("case", ["clean", "nan_a", "inf_b", "overflow"])
+def test_status_equals_the_shader_on_reordered_paths(vqdev, oracle, path, m, n, k, group,
+                                                     flags, case):
+    """Status bit 1 (vq4.comp:149-158 book sweep, :173 nonfinite product or
+    total) of the reordered paths equals the shader's: nonfinite book
+    entries, used or not, and an overflowing product set it; clean operands
+    do not."""
+    rng = np.random.default_rng([m, n, k, flags, ["clean", "nan_a", "inf_b", "overflow"].index(case)])
+    assert vqdev.path_name((2, m, n, k, group, 16, flags, 0)) == path
+    ops = _status_case(rng, case, m, n, k, group)
+    say("status", path, m, n, k, group, flags, case)
+    _, status = _gpu(vqdev, ops, m, n, k, group, flags)
+    _, ref_status = oracle.matmul(*ops, m, n, k, group, flags)
+    assert status == ref_status == (0 if case == "clean" else 1)
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_status_of_batched_gemv_flags_the_bad_instance_only_once(vqdev, oracle, m):
+    """ack_vq_batch shares one status word: one instance with a NaN in its
+    B book among clean ones sets bit 1; all clean instances leave it 0."""
+    rng = np.random.default_rng(40 + m)
+    k, n, group, count = 4096, 4096, 16, 256
+    items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(4)]
+    clean = [items[i % 4] for i in range(count)]
+    ops = tuple(np.concatenate([it[s].reshape(-1) for it in clean]) for s in range(4))
+    say("status batch clean", m)
+    _, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    bad_book = ops[3].copy()
+    bad_book[(count - 3) * 16 * group + 5] = np.nan
+    say("status batch one bad", m)
+    _, status = _gpu(vqdev, (ops[0], ops[1], ops[2], bad_book), m, n, k, group, 0, count=count)
+    assert status == 1
