@@ -79,6 +79,7 @@ _ENTRY_POINTS = {
     "ack_vq_schema": ((), _U32),
     "ack_vq": ((_P,) * 8 + (_SZ,), _I32),
     "ack_vq_batch": ((_P,) * 8 + (_SZ, _U32), _I32),
+    "ack_vq_noalloc": ((_P,) * 8 + (_SZ,), _I32),
     "ack_open": ((), _P),
     "ack_close": ((_P,), _I32),
     "ack_device_name": ((_P, ctypes.c_char_p, _SZ), _I32),

@@ -56,6 +56,7 @@ struct Device {
   std::string name;
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
+  void* scratch = nullptr;  // this GPU's copy of `scratch` (ack_vq_noalloc), or null
 };
 
 struct Registry {
@@ -155,6 +156,34 @@ int32_t parse_plan(const uint8_t* plan, size_t plan_len, ackvq::Bounds bounds, a
 
 size_t round_up(size_t bytes) { return (bytes + 255) / 256 * 256; }
 
+// ---- the allocation-free entry's scratch ----------------------------------------
+// ack_vq_noalloc takes the workspace of the paths that need one (the GEMV's
+// split-k partials, row-bins' transposed code words) from this array instead
+// of allocating it. Every GPU the library runs on holds its own copy until
+// the process ends. In host code `scratch` names a host-side stand-in, never
+// a device address: the address is resolved per GPU with
+// hipGetSymbolAddress (scratch_address) and only that pointer is passed on.
+constexpr size_t kScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxGpus = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxGpus] = {};
+bool g_scratch_done[kMaxGpus] = {};
+
+// This GPU's `scratch`, resolved once per GPU with that GPU current (the
+// caller has selected it). Null when resolution failed.
+void* scratch_address(int hip_device) {
+  if (hip_device < 0 || hip_device >= kMaxGpus) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_done[hip_device]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess) g_scratch_ptr[hip_device] = ptr;
+    g_scratch_done[hip_device] = true;
+  }
+  return g_scratch_ptr[hip_device];
+}
+
 int32_t ensure_workspace(Device& dev, size_t bytes) {
   if (bytes <= dev.workspace_bytes) return ACK_OK;
   if (dev.workspace) {
@@ -173,9 +202,11 @@ int32_t ensure_workspace(Device& dev, size_t bytes) {
   return ACK_OK;
 }
 
-// Steps 4-7 then the launch, shared by ack_vq and ack_vq_batch.
+// Steps 4-7 then the launch, shared by ack_vq, ack_vq_batch and
+// ack_vq_noalloc (no_alloc: the workspace is the GPU's `scratch`, and a plan
+// needing more than kScratchBytes of it is refused).
 int32_t run_vq(const AckDevice* handle, const AckBuffer* const slots[6], const uint8_t* plan_bytes,
-               size_t plan_len, uint32_t count) {
+               size_t plan_len, uint32_t count, bool no_alloc = false) {
   ackvq::Plan plan;
   if (int32_t rc = parse_plan(plan_bytes, plan_len, ackvq::Bounds::Library, &plan)) return rc;
   std::shared_ptr<Device> dev;
@@ -236,9 +267,27 @@ int32_t run_vq(const AckDevice* handle, const AckBuffer* const slots[6], const u
       const ackvq::MatmulPath path =
           ackvq::choose_matmul_path(m, n, k, g, plan.flags(), count, dev->policy);
       const size_t ws = ackvq::matmul_workspace_bytes(path, m, n, k, g, plan.flags(), count);
-      if (int32_t rc = ensure_workspace(*dev, ws)) return rc;
-      he = ackvq::launch_matmul(dev->stream, o, m, n, k, g, plan.flags(), path, dev->workspace,
-                                dev->workspace_bytes);
+      void* work = nullptr;
+      size_t work_bytes = 0;
+      if (no_alloc) {
+        if (ws > kScratchBytes) {
+          set_error("vq noalloc: the product needs " + std::to_string(ws) +
+                    " bytes of workspace, more than the " + std::to_string(kScratchBytes) +
+                    "-byte scratch; use ack_vq");
+          return ACK_ERR_SIZE;
+        }
+        if (dev->scratch == nullptr) {
+          set_error("vq noalloc: the device address of the scratch array is unknown");
+          return ACK_ERR_DEVICE;
+        }
+        work = dev->scratch;
+        work_bytes = kScratchBytes;
+      } else {
+        if (int32_t rc = ensure_workspace(*dev, ws)) return rc;
+        work = dev->workspace;
+        work_bytes = dev->workspace_bytes;
+      }
+      he = ackvq::launch_matmul(dev->stream, o, m, n, k, g, plan.flags(), path, work, work_bytes);
       break;
     }
   }
@@ -289,6 +338,13 @@ int32_t ack_vq_batch(const AckDevice* dev, const AckBuffer* b0, const AckBuffer*
   return run_vq(dev, slots, plan, plan_len, count);
 }
 
+int32_t ack_vq_noalloc(const AckDevice* dev, const AckBuffer* b0, const AckBuffer* b1,
+                       const AckBuffer* b2, const AckBuffer* b3, const AckBuffer* out,
+                       const AckBuffer* status, const uint8_t* plan, size_t plan_len) {
+  const AckBuffer* slots[6] = {b0, b1, b2, b3, out, status};
+  return run_vq(dev, slots, plan, plan_len, 1, true);
+}
+
 AckDevice* ack_open(void) {
   int count = 0;
   hipError_t e = hipGetDeviceCount(&count);
@@ -329,6 +385,7 @@ AckDevice* ack_open(void) {
   else
     dev->name = "HIP device " + std::to_string(index);
   if (have_prop) dev->name += std::string(" (") + prop.gcnArchName + ")";
+  dev->scratch = scratch_address(index);  // `index` is current (hipSetDevice above)
   dev->id = g_next_device.fetch_add(1);
   Registry& r = registry();
   std::lock_guard<std::mutex> lock(r.mu);

@@ -124,6 +124,20 @@ int32_t ack_vq_batch(const AckDevice* dev, const AckBuffer* b0, const AckBuffer*
                      const AckBuffer* status, const uint8_t* plan, size_t plan_len,
                      uint32_t count);
 
+/* ack_vq that allocates nothing. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same arguments,
+ * check order, codes and results as ack_vq; the workspace some product paths
+ * need (split-k partials of the GEMV kernels, the transposed code words of
+ * row-bins) comes from a fixed 8 MiB device array that each GPU holds until
+ * the process ends, in place of memory ack_vq would allocate. A plan needing
+ * more than 8 MiB of it is refused with ACK_ERR_SIZE. Calls share their GPU's
+ * array: calls on one device handle are ordered on its stream, but calls
+ * that overlap on one GPU through different device handles race on it. */
+int32_t ack_vq_noalloc(const AckDevice* dev, const AckBuffer* b0, const AckBuffer* b1,
+                       const AckBuffer* b2, const AckBuffer* b3, const AckBuffer* out,
+                       const AckBuffer* status, const uint8_t* plan, size_t plan_len);
+
 /* One fused VQAdamW step for VQAdamW.step on this library (vq.py:388-410):
  * the op-3 inputs (b0 = codes of W, M, V, G back to back; b1 = their four
  * books; b2 = seven FP32 coefficients; plan = the op-3 plan) are decoded and

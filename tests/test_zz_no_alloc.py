@@ -1,0 +1,108 @@
+"""ack_vq_noalloc, the entry point that allocates nothing: through the C ABI
+its results equal ack_vq's bit for bit (the same kernels, with their
+workspace in the library's fixed scratch array instead of allocated memory),
+on consecutive calls whose second input is smaller than the first, for
+every path that uses a workspace; a plan needing more workspace than the
+array holds is refused before anything is enqueued."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gpu_util import image, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _operands(rng, m, n, k, group, flags=0):
+    a_codes, a_book = image(rng, m * k, group, 1.0)
+    b_codes, b_book = image(rng, k * n, group, 0.02)
+    return a_codes, a_book, b_codes, b_book
+
+
+def _call(vqdev, entry, words, arrays, out_bytes):
+    """Run `entry` (ack_vq or ack_vq_noalloc) through the C ABI on fresh
+    buffers; returns (rc, output bytes as uint32, status word)."""
+    device = vqdev.device
+    held = []
+    try:
+        for a in arrays:
+            b = device.buffer(a.nbytes)
+            b.upload(a)
+            held.append(b)
+        out = device.buffer(out_bytes)
+        out.upload(np.full(out_bytes, 0xA5, np.uint8))     # unwritten outputs are visible
+        status = device.buffer(4)
+        status.upload(np.zeros(1, np.uint32))
+        held += [out, status]
+        slots = held[:len(arrays)] + [held[0]] * (4 - len(arrays))
+        plan = np.asarray(words, dtype="<u4").tobytes()
+        with device.lock:
+            rc = getattr(device.lib.cdll, entry)(device.handle, *(b.handle for b in slots),
+                                                 out.handle, status.handle, plan, len(plan))
+        if rc != 0:
+            return rc, None, None
+        return rc, out.download(np.uint32), int(status.download(np.uint32)[0])
+    finally:
+        for b in held:
+            b.free()
+
+
+# (m, n, k, group, flags, path): every path whose launch takes a workspace,
+# the larger product first in each pair
+PAIRS = [
+    [(1, 4096, 4096, 16, 0, "gemv-pairs"), (1, 2048, 1024, 16, 0, "gemv-pairs")],
+    [(8, 4096, 4096, 16, 0, "gemv-rows"), (3, 1024, 2048, 8, 0, "gemv-rows")],
+    [(24, 2048, 8192, 16, 0, "gemv-rows"), (12, 1024, 4096, 16, 1, "gemv-rows")],
+    [(256, 4096, 4096, 32, 0, "row-bins"), (64, 1024, 1024, 16, 0, "row-bins")],
+]
+
+
+@pytest.mark.parametrize("pair", PAIRS, ids=[p[0][5] + str(i) for i, p in enumerate(PAIRS)])
+def test_noalloc_equals_ack_vq_on_consecutive_calls(vqdev, pair):
+    rng = np.random.default_rng(len(pair[0]) + pair[0][0] + pair[0][1])
+    for m, n, k, group, flags, path in pair:
+        words = (2, m, n, k, group, 16, flags, 0)
+        assert vqdev.path_name(words) == path
+        ops = _operands(rng, m, n, k, group, flags)
+        say("noalloc", path, m, n, k, group, flags)
+        rc, got, status = _call(vqdev, "ack_vq_noalloc", words, ops, 4 * m * n)
+        assert rc == 0 and status == 0
+        rc, want, ref_status = _call(vqdev, "ack_vq", words, ops, 4 * m * n)
+        assert rc == 0 and ref_status == 0
+        np.testing.assert_array_equal(got, want)
+
+
+def test_noalloc_other_ops_and_status(vqdev, oracle):
+    """Ops without a workspace run unchanged; status bits still come back."""
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(4096).astype(np.float32)
+    book = rng.standard_normal((16, 16)).astype(np.float32)
+    words = (0, x.size, 1, 1, 16, 16, 0, 0)
+    say("noalloc encode")
+    rc, codes, status = _call(vqdev, "ack_vq_noalloc", words, (x, book), x.size // 16 // 2)
+    assert rc == 0 and status == 0
+    np.testing.assert_array_equal(codes, oracle.encode(x, book, 16)[0])
+    ops = list(_operands(rng, 1, 2048, 2048, 16))
+    ops[3] = ops[3].copy()
+    ops[3][4, 2] = np.nan
+    say("noalloc status")
+    rc, _, status = _call(vqdev, "ack_vq_noalloc", (2, 1, 2048, 2048, 16, 16, 0, 0), ops, 4 * 2048)
+    assert rc == 0 and status == 1
+
+
+def test_noalloc_refuses_a_workspace_past_the_scratch(vqdev):
+    """8 activation rows over a 16384 x 16384 weight at group 16, one
+    product: k splits 64 ways over 4 column tiles, 32 MiB of split-k
+    partials. Refused with ACK_ERR_SIZE and a message naming the scratch;
+    ack_vq would allocate them."""
+    from alelyon_compute_kit import ack
+    m, n, k, group = 8, 16384, 16384, 16
+    words = (2, m, n, k, group, 16, 0, 0)
+    assert vqdev.path_name(words) == "gemv-rows"
+    rng = np.random.default_rng(8)
+    ops = _operands(rng, m, n, k, group)
+    say("noalloc refusal")
+    rc, _, _ = _call(vqdev, "ack_vq_noalloc", words, ops, 4 * m * n)
+    assert rc == ack.ACK_ERR_SIZE
+    assert "scratch" in vqdev.device.lib.last_error()
