@@ -35,6 +35,26 @@ def _weight(rng, shape, group, scale=0.05):
     return vq.encode(w, vq.fit_codebook(w, group=group), group=group)
 
 
+def _check_report(fused, plain, opt, grad, step):
+    """The report of the fused step carries the reference's keys with the
+    reference's meanings (vq.py:405-410): the same values as the unfused
+    sequence's, native_update_output_bytes the dense [W'|M'|V'] update's size
+    (the fused step evaluates it without storing it); only the calibration
+    text says where the fit ran."""
+    keys = {"step", "changed_weight_values", "persistent_state_bytes", "gradient_bytes",
+            "native_update_output_bytes", "calibration", "model_quality_validated"}
+    assert set(fused) == set(plain) == keys
+    elements = opt.weight.layout["elements"]
+    assert fused["step"] == step and fused["native_update_output_bytes"] == 12 * elements
+    assert fused["gradient_bytes"] == grad.layout["serialized_bytes"]
+    assert fused["persistent_state_bytes"] == sum(
+        s.layout["serialized_bytes"] for s in (opt.weight, opt.momentum, opt.variance))
+    assert fused["model_quality_validated"] is False
+    assert fused["calibration"].startswith("device") and plain["calibration"].startswith("native")
+    for key in keys - {"calibration"}:
+        assert fused[key] == plain[key], key
+
+
 @pytest.mark.parametrize("shape,group", [((64, 48), 16), ((40, 40), 8), ((3000, 32), 32),
                                          ((512, 512), 8), ((1000, 77), 16)])
 def test_fused_step_equals_the_unfused_sequence(vqdev, shape, group):
@@ -49,7 +69,7 @@ def test_fused_step_equals_the_unfused_sequence(vqdev, shape, group):
         say("adamw step", shape, group, step)
         r1 = fused.step(grad)
         r2 = plain.step(grad)
-        assert r1["changed_weight_values"] == r2["changed_weight_values"]
+        _check_report(r1, r2, fused, grad, step + 1)
         for a, b in ((fused.weight, plain.weight), (fused.momentum, plain.momentum),
                      (fused.variance, plain.variance)):
             np.testing.assert_array_equal(a.codebook, b.codebook)

@@ -404,7 +404,7 @@ def test_forward_batch_is_one_launch_over_many_experts(tmp_path, vqdev, m):
     for x, (layer, e), y in zip(xs, experts, got):
         one = h.forward(x, layer=layer, expert=e)
         assert o.max_rel(y, one) <= 1e-5
-        x_img = h._encode(x, 16)
+        x_img = h.encode_activations(x, 16)
         exact = o.matmul64(x_img.decode(), bank.read_expert(layer, e)[0].decode())
         assert o.max_rel(y, exact) <= 1e-5
 
@@ -419,3 +419,69 @@ def test_forward_batch_refuses_a_wrong_width(tmp_path):
     with pytest.raises(harness.HarnessError, match="width"):
         h.forward_batch([x[:, :8]], [(0, 0)])
     assert h.forward_batch([x, x], [(0, 0), (1, 0)]).shape == (2, 2, 24)
+
+
+# ---- command line and its files ------------------------------------------------------
+def test_cli_file_helpers(tmp_path):
+    """.npy inputs only (no archives, no symlinks, no pickles), checked as
+    matrices; outputs never overwritten without --force, written whole."""
+    good = tmp_path / "x.npy"
+    np.save(good, np.ones((2, 3), np.float32))
+    np.testing.assert_array_equal(harness._read_matrix(good, "input"), np.ones((2, 3)))
+    archive = tmp_path / "x.npz"
+    np.savez(archive, a=np.ones((2, 3), np.float32))
+    with pytest.raises(harness.HarnessError, match="archive"):
+        harness._read_matrix(archive, "input")
+    link = tmp_path / "link.npy"
+    link.symlink_to(good)
+    with pytest.raises(harness.HarnessError, match="regular file"):
+        harness._read_matrix(link, "input")
+    junk = tmp_path / "junk.npy"
+    junk.write_bytes(b"not an array")
+    with pytest.raises(harness.HarnessError, match="readable NumPy"):
+        harness._read_matrix(junk, "input")
+    pickled = tmp_path / "obj.npy"
+    np.save(pickled, np.array([{"a": 1}], dtype=object), allow_pickle=True)
+    with pytest.raises(harness.HarnessError, match="readable NumPy"):
+        harness._read_matrix(pickled, "input")
+    wide = tmp_path / "f64.npy"
+    np.save(wide, np.ones((2, 3)))
+    with pytest.raises(harness.HarnessError, match="rank-2 float32"):
+        harness._read_matrix(wide, "input")
+    out = tmp_path / "sub" / "y.npy"
+    harness._write_matrix(out, np.arange(6, dtype=np.float32).reshape(2, 3), force=False)
+    with pytest.raises(harness.HarnessError, match="overwrite"):
+        harness._write_matrix(out, np.zeros((2, 3), np.float32), force=False)
+    harness._write_matrix(out, np.zeros((2, 3), np.float32), force=True)
+    assert not np.load(out).any()
+    assert sorted(p.name for p in out.parent.iterdir()) == ["y.npy"]   # no temporaries left
+
+
+def test_cli_requires_the_device_flag(tmp_path, capsys):
+    with pytest.raises(SystemExit):
+        harness.main(["--bank", str(tmp_path), "--input", "x", "--output", "y"])
+    assert "--device is required" in capsys.readouterr().err
+
+
+@pytest.mark.gpu
+def test_cli_forward_and_train_on_the_gpu(tmp_path, capsys):
+    """The command line over a bank: a forward, then two training steps and
+    the forward after them, each reported as JSON."""
+    from gpu_util import say
+    bank = _small_bank(tmp_path)
+    x, t = tmp_path / "x.npy", tmp_path / "t.npy"
+    np.save(x, np.ones((2, 4), np.float32))
+    np.save(t, np.zeros((2, 3), np.float32))
+    say("cli forward")
+    assert harness.main(["--device", "--bank", str(bank.root), "--input", str(x),
+                         "--output", str(tmp_path / "y.npy")]) == 0
+    report = json.loads(capsys.readouterr().out.strip().splitlines()[-1])
+    assert report["mode"] == "forward" and report["shape"] == [2, 3]
+    assert np.load(tmp_path / "y.npy").shape == (2, 3)
+    say("cli train")
+    assert harness.main(["--device", "--bank", str(bank.root), "--input", str(x), "--target",
+                         str(t), "--steps", "2", "--output", str(tmp_path / "y.npy"),
+                         "--force"]) == 0
+    report = json.loads(capsys.readouterr().out.strip().splitlines()[-1])
+    assert report["mode"] == "train" and [s["optimizer_step"] for s in report["steps"]] == [1, 2]
+    assert bank.read_expert_state(0, 0).revision == 3
