@@ -56,6 +56,10 @@ size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, 
                               uint32_t flags, uint32_t count);
 
 hipError_t launch_encode(hipStream_t s, const Operands& o, uint32_t m, uint32_t group);
+
+// One streaming read of `bytes` (< 2^31) at `data` with the GEMV's loads,
+// nothing written (benchmarks' HBM read ceiling; hbm_probe.hip).
+hipError_t launch_read_probe(hipStream_t s, const void* data, uint64_t bytes, uint32_t* sink);
 hipError_t launch_decode(hipStream_t s, const Operands& o, uint32_t m, uint32_t group);
 hipError_t launch_adamw(hipStream_t s, const Operands& o, uint32_t m, uint32_t group);
 hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
