@@ -208,6 +208,29 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF,
+                                                    0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;  // quad_perm 1,0,3,2
+constexpr int kDppXor2 = 0x4E;  // quad_perm 2,3,0,1
+
+// Sum of the wave's values by DPP within each row of 16 lanes, then the four
+// row sums read out (wave-uniform). Any wave given the same values returns the
+// same sum: the order of additions is fixed.
+__device__ __forceinline__ float wave_sum_rows(float v) {
+  v += dpp_f32<kDppXor1>(v);
+  v += dpp_f32<kDppXor2>(v);
+  v += dpp_f32<0x141>(v);  // row_half_mirror: lanes 0-3 meet lanes 4-7
+  v += dpp_f32<0x140>(v);  // row_mirror: lanes 0-7 meet lanes 8-15
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 typedef __attribute__((address_space(3))) int32_t lds_i32;
 
 // Integer add into LDS at an absolute byte address. The bins sit at LDS
@@ -398,8 +421,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t words_rsrc(const void* base, u
 }
 
 struct PairAhead {
-  uint32_t w0, w1;  // A words tid and tid + kPairThreads of the slice
+  uint32_t w0, w1;  // A words tid and tid + kPairThreads of the slice (PK: w0 = word `lane`)
   float a, b;       // entry tid of the A and B books
+  float4 a4;        // PK: A book values 4 lane .. 4 lane + 3
 };
 
 // grid: (n tiles, k splits, z); block z serves instances z, z + gridDim.z, ...
@@ -412,6 +436,17 @@ struct PairAhead {
 // row, so the 32 lanes of a half-wave hold 4 rows; a lane rotates its 4 words
 // by its row slot so that at every atomic the half-wave still covers the 32
 // word columns once (32 distinct banks).
+//
+// PK (packed x, one window, cumulative bins: the batched decode shape): x is
+// never staged. A wave's 32 rows of a batch lie in one A word, so each lane
+// keeps one A word of the slice in a register (lane l: word l) and read_x
+// decodes its rows from that word (v_readlane) and the A book in LDS. The A
+// book alternates between two LDS copies by instance and the next instance's
+// copy is written one instance ahead, so an instance's set-up writes LDS only
+// where no wave can still be reading. The window's L1 norm is a code
+// histogram against the book's row norms, which every wave forms alike from
+// registers (so all waves hold the same scale without exchanging it). An
+// instance then has two barriers: before the flush and before the product.
 template <int G, bool AD, bool SW, bool X4>
 __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint32_t n,
                                                                 uint32_t k, uint32_t ks,
@@ -421,6 +456,11 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   static_assert(16 * G <= kPairThreads, "one book entry per thread");
   static_assert(D % 2 == 0, "x buffers alternate by batch parity");
   using L = PairLds<G>;
+  constexpr bool PK = SW && !AD && L::cum;
+  // PK: one A word per lane covers a window (kPairWindow rows), one float4 per
+  // lane covers the A book, and the A book's second copy fits the words' area
+  static_assert(!PK || (kPairWindow / (8 * G) <= 64 && 16 * G <= 4 * 64 &&
+                        16 * G <= kPairMaxAWords), "PK registers and LDS");
   extern __shared__ int32_t smem[];
   char* lds = reinterpret_cast<char*>(smem);
   int32_t* bins = smem;
@@ -430,6 +470,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   float* const bb0 = reinterpret_cast<float*>(lds + L::bb);
   uint32_t* aw = reinterpret_cast<uint32_t*>(lds + L::aw);
   float* wl1 = reinterpret_cast<float*>(lds + L::wl1);  // per-wave L1 of the staged x
+  float* const afx = reinterpret_cast<float*>(lds + L::aw);  // PK: the A book's second copy
   // Defensive: the perm-built bin addresses assume the bins start at LDS 0.
   if (static_cast<uint32_t>(reinterpret_cast<size_t>((lds_i32*)smem)) != 0) {
     if (threadIdx.x == 0) atomicOr(o.status, 2u);
@@ -482,10 +523,18 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
         words_rsrc(AD ? nullptr : item_ptr<float>(o.in[1], o.stride[1], item), AD ? 0u : 64u * G);
     const __amdgpu_buffer_rsrc_t bbk = words_rsrc(item_ptr<float>(o.in[3], o.stride[3], item), 64u * G);
     PairAhead h;
-    h.a = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(abk, lt * 4u, 0, 0)));
     h.b = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(bbk, lt * 4u, 0, 0)));
     h.w0 = h.w1 = 0;
-    if (!AD) {
+    h.a = 0.0f;
+    h.a4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (PK) {  // words and book values past the slice and the book read as zero
+      const uint32_t ll = lt % 64;
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(abk, ll * 16u, 0, 0);
+      h.a4 = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                         __uint_as_float(v[3]));
+      h.w0 = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(ars, ll * 4u, 0, 0));
+    } else if (!AD) {
+      h.a = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(abk, lt * 4u, 0, 0)));
       h.w0 = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(ars, lt * 4u, 0, 0));
       h.w1 = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(ars, (lt + kPairThreads) * 4u, 0, 0));
     }
@@ -527,6 +576,11 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   for (int i = 0; i < (CUM ? 16 : 1); ++i) prv[i] = 0;
   int shift = 0;  // the current window's fixed-point scale
   uint32_t xbase = k0;
+  // PK: this instance's copy of the A book, and the lane's A word of the slice
+  const float* af_cur = af;
+  uint32_t wreg = 0;
+  PairAhead cur{}, nxt{};  // set-up data of this instance and the next
+  static_assert(!PK || (8 * G) % (2 * R) == 0, "a wave's rows of a batch lie in one A word");
   __amdgpu_buffer_rsrc_t x_rs = words_rsrc(nullptr, 0u);  // AD: this instance's x[0, kend)
 
   // Rows [xb0, xb0 + kPairXRows) of A's single row as FP32, zero past kend,
@@ -575,6 +629,25 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       for (uint32_t u = 0; u < RX; ++u) xs[u] = 0.0f;
       return;
     }
+    if (PK) {
+      // the wave's 2 R rows of the batch (slice rows b BR + 2 R wave ..) lie in
+      // word (b BR + 2 R wave) / (8 G) of the slice, held by that lane
+      const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+      const uint32_t word =
+          uint32_t(__builtin_amdgcn_readlane(int(wreg), int((b * BR + 2 * R * wv) / (8 * G))));
+      const uint32_t len = kend - k0;
+#pragma unroll
+      for (uint32_t c4 = 0; c4 < RX / 4; ++c4) {
+        const uint32_t row = b * BR + lane_row + 4 * c4;  // of the slice
+        const uint32_t code = (word >> (((row / G) % 8u) * 4u)) & 15u;
+        const float4 v = *reinterpret_cast<const float4*>(af_cur + code * G + row % G);
+        xs[4 * c4] = row < len ? v.x : 0.0f;  // rows past the slice bin nothing
+        xs[4 * c4 + 1] = row + 1 < len ? v.y : 0.0f;
+        xs[4 * c4 + 2] = row + 2 < len ? v.z : 0.0f;
+        xs[4 * c4 + 3] = row + 3 < len ? v.w : 0.0f;
+      }
+      return;
+    }
     const float4* xr = reinterpret_cast<const float4*>(sx + (k0 + b * BR + lane_row - xbase));
 #pragma unroll
     for (uint32_t c4 = 0; c4 < RX / 4; ++c4) {
@@ -582,6 +655,120 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       xs[4 * c4] = v.x; xs[4 * c4 + 1] = v.y; xs[4 * c4 + 2] = v.z; xs[4 * c4 + 3] = v.w;
     }
   };
+  // PK: the window's scale from an instance's set-up registers. The book's row
+  // norms (entry e = its G / 4 lanes' sums) meet the slice's codes (lane l:
+  // word l); every lane of every wave forms the same sums in the same order.
+  auto pk_shift = [&](const PairAhead& h) __attribute__((always_inline)) {
+    float part = fabsf(h.a4.x);
+    part += fabsf(h.a4.y);
+    part += fabsf(h.a4.z);
+    part += fabsf(h.a4.w);
+    part += dpp_f32<kDppXor1>(part);  // entry e's G / 4 lanes (aligned, 2 or 4)
+    if (G / 4 == 4) part += dpp_f32<kDppXor2>(part);
+    const uint32_t groups = (kend - k0 + G - 1) / G;
+    float l1 = 0.0f;
+#pragma unroll
+    for (uint32_t c = 0; c < 8; ++c) {
+      const uint32_t code = (h.w0 >> (4 * c)) & 15u;
+      const float r = __shfl(part, int(code * (G / 4)));
+      if (lane * 8 + c < groups) l1 += r;
+    }
+    return __builtin_amdgcn_readfirstlane(window_shift(wave_sum_rows(l1)));
+  };
+  static_assert(!PK || G == 8 || G == 16, "book row norms over 2 or 4 lanes");
+  // CUM at G = 16 with one k slice: y^T = C_B^T . S^T on v_mfma_f32_16x16x4f32,
+  // S read from an instance's cumulative partials, 16 groups per product tile
+  // and 4 codes per step. Lane l: A = C_B[4 ks + l/16][l % 16], B = S of group
+  // 16 tile + l % 16 at code 4 ks + l/16; it ends with y[16 tile + l % 16]
+  // [4 (l/16) .. 4 (l/16) + 3]. A wave reads both its tiles' partials before
+  // its first product.
+  //
+  // Kept outputs: a global store counts in the same in-order counter as the
+  // code loads, so a wait for any load issued after it also waits for the
+  // store's acknowledgement, which queues behind every read in flight (tens
+  // of MiB, microseconds). A deferred product therefore keeps its outputs in
+  // registers until the next instance's last batch has refilled, and stores
+  // them there: the first load issued after them is waited for four batches
+  // and a finalisation later, when they have long been acknowledged.
+  constexpr uint32_t TT = kPairTiles16 / kPairWaves;
+  static_assert(kPairTiles16 % kPairWaves == 0, "whole tiles per wave");
+  float4 kept[TT];
+  uint32_t kept_item = 0;
+  bool has_kept = false;
+  const uint32_t groups_tile = (rw - tile * kTileWords) < kTileWords ? (rw - tile * kTileWords) * 8
+                                                                     : kTileGroups;
+  auto store_out = [&](uint32_t pitem, const float4 (&y)[TT]) __attribute__((always_inline)) {
+    const uint32_t ft = opaque(tid);
+    const uint32_t lane16 = ft % 16, k4 = (ft % 64) / 16;
+    float* out = item_ptr_mut<float>(o.out, o.stride[4], pitem) + tile * kTileGroups * G;
+    const bool vec = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+#pragma unroll
+    for (uint32_t tt = 0; tt < TT; ++tt) {
+      const uint32_t j = (ft / 64 + tt * kPairWaves) * 16 + lane16;
+      if (j < groups_tile) {
+        float* oy = out + j * 16 + 4 * k4;
+        if (vec) {
+          *reinterpret_cast<float4*>(oy) = y[tt];
+        } else {
+          oy[0] = y[tt].x; oy[1] = y[tt].y; oy[2] = y[tt].z; oy[3] = y[tt].w;
+        }
+      }
+    }
+  };
+  auto mfma_product = [&](uint32_t pitem, int pshift, const float* pbb, bool keep)
+                          __attribute__((always_inline)) {
+    const uint32_t ft = opaque(tid);
+    const uint32_t* cpt = reinterpret_cast<const uint32_t*>(sx);
+    const uint32_t lane16 = ft % 16, k4 = (ft % 64) / 16;
+    const uint32_t groups = groups_tile;
+    float bk[4];
+#pragma unroll
+    for (uint32_t ks = 0; ks < 4; ++ks) bk[ks] = pbb[(4 * ks + k4) * 16 + lane16];
+    float sb[TT][4];
+#pragma unroll
+    for (uint32_t tt = 0; tt < TT; ++tt) {
+      const uint32_t j = (ft / 64 + tt * kPairWaves) * 16 + lane16;
+      const uint32_t qq = j / 8, n8 = j % 8;
+      const bool odd = (n8 & 1u) != 0;
+#pragma unroll
+      for (uint32_t ks = 0; ks < 4; ++ks) {
+        const uint32_t at = cum_part(n8 / 2, 4 * ks + k4, qq);
+        const uint32_t v0 = cpt[(odd ? kCumHiBase : 0u) + at];
+        const uint32_t v1 = cpt[kCumHalfWords + at];  // odd nibbles: read, unused
+        sb[tt][ks] = unscale(float(int32_t(odd ? v0 : v0 + v1)), pshift);
+      }
+    }
+    bool bad = false;
+    float4 y[TT];
+#pragma unroll
+    for (uint32_t tt = 0; tt < TT; ++tt) {
+      const uint32_t j = (ft / 64 + tt * kPairWaves) * 16 + lane16;
+      typedef float float4v __attribute__((ext_vector_type(4)));
+      float4v d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (uint32_t ks = 0; ks < 4; ++ks) d = __builtin_amdgcn_mfma_f32_16x16x4f32(bk[ks], sb[tt][ks], d, 0, 0, 0);
+      y[tt] = make_float4(d[0], d[1], d[2], d[3]);
+      if (j < groups)
+        bad |= !finite_f32(d[0]) || !finite_f32(d[1]) || !finite_f32(d[2]) || !finite_f32(d[3]);
+    }
+    if (__any(bad) && (ft % warpSize) == 0) atomicOr(o.status, 1u);
+    if (!keep || has_kept) {  // (a kept instance is stored before the next product)
+      store_out(pitem, y);
+      return;
+    }
+    kept_item = pitem;
+#pragma unroll
+    for (uint32_t tt = 0; tt < TT; ++tt) kept[tt] = y[tt];
+    has_kept = true;
+  };
+  // PK at G = 16 with one k slice: an instance's product waits until the next
+  // instance's first refill is in flight (its partials and B book copy stay
+  // untouched until the next flush barrier)
+  const bool defer = PK && G == 16 && gridDim.y == 1;
+  bool pending = false;
+  uint32_t p_item = 0;
+  int p_shift = 0;
+  const float* p_bb = bb0;
   // this thread's sub-block: word column fq, byte position fp, sub-block (fh, fl)
   auto flush = [&](bool clear) __attribute__((always_inline)) {
     const uint32_t ft = opaque(tid);
@@ -619,8 +806,9 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       }
   };
   // `tail`: a batch of the peeled last D, the only ones that can be the last
+  // `first`: may be the instance's batch 0, where a deferred product runs
   auto stage = [&](uint32_t (&w)[R], uint32_t b, float (&xs)[RX], float (&xn)[RX],
-                   __amdgpu_buffer_rsrc_t rs_refill, uint32_t b_refill, bool tail)
+                   __amdgpu_buffer_rsrc_t rs_refill, uint32_t b_refill, bool tail, bool first)
                    __attribute__((always_inline)) {
     asm volatile("" : "+s"(b));  // row arithmetic is redone per batch, not strength-reduced
     const uint32_t done = (b + 1) * BR;
@@ -656,6 +844,15 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     }
     load_batch(rs_refill, b_refill, w);
     __builtin_amdgcn_sched_barrier(0);
+    if (first && pending) {  // every thread has written the previous instance's partials
+      __syncthreads();
+      mfma_product(p_item, p_shift, p_bb, true);
+      pending = false;
+    }
+    if (last && has_kept) {
+      store_out(kept_item, kept);
+      has_kept = false;
+    }
     if (wend) {
       __syncthreads();
       flush(!last);
@@ -675,7 +872,6 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   };
 
   uint32_t item = blockIdx.z;
-  PairAhead cur{}, nxt{};
   if (item < o.count) {
     cur = setup_loads(item);
     nxt = setup_loads(item + zn < o.count ? item + zn : item);
@@ -688,6 +884,10 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
 #pragma unroll
   for (uint32_t i = 0; i < kPairBins / (4 * kPairThreads); ++i)
     bins4[tid + i * kPairThreads] = make_int4(0, 0, 0, 0);
+  if (PK) {  // the first instance's A book; instances alternate copies from here
+    if (4 * tid < 16 * G) *reinterpret_cast<float4*>(af + 4 * tid) = cur.a4;
+    __syncthreads();
+  }
   for (; item < o.count; item += zn) {
     const uint32_t next = item + zn;
     const __amdgpu_buffer_rsrc_t cur_rs = batch_rsrc(item);
@@ -697,27 +897,47 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     // and the other copy of the B book, and its bin clears precede this
     // instance's atomics by the barriers below.
     const uint32_t st = opaque(tid);
-    float* bb = bb0 + (((item - blockIdx.z) / zn) & 1u) * (16 * G);
-    if (st < 16 * G) {
-      if (!AD) af[st] = cur.a;
-      bb[st] = cur.b;
-    }
-    if (!AD && st < a_words) aw[st] = cur.w0;
-    if (!AD && st + kPairThreads < a_words) aw[st + kPairThreads] = cur.w1;
-    if (AD) x_rs = words_rsrc(item_ptr<float>(o.in[0], o.stride[0], item), kend * 4u);
-    __syncthreads();
-    // the previous instance's pl/ph (the first kPairPartWords bins) are read
-    if (!CUM) {
+    const uint32_t par = ((item - blockIdx.z) / zn) & 1u;
+    float* bb = bb0 + par * (16 * G);
+    if (PK) {
+      // No barrier: the B book copy written here was last read by the product
+      // two instances back, and the A book copy written here (the next
+      // instance's) by the previous instance's loop; every wave has passed
+      // the previous instance's flush barrier, which follows both.
+      if (st < 16 * G) bb[st] = cur.b;
+      if (4 * st < 16 * G) *reinterpret_cast<float4*>((par ? af : afx) + 4 * st) = nxt.a4;
+      if (tile == 0 && split == 0) {  // nonfinite book values, from the set-up registers
+        const bool bad = (4 * st < 16 * G && (!finite_f32(cur.a4.x) || !finite_f32(cur.a4.y) ||
+                                              !finite_f32(cur.a4.z) || !finite_f32(cur.a4.w))) ||
+                         (st < 16 * G && !finite_f32(cur.b));
+        if (__any(bad) && lane == 0) atomicOr(o.status, 1u);
+      }
+      af_cur = par ? afx : af;
+      wreg = cur.w0;
+      shift = pk_shift(cur);
+      read_x(0, xa);
+    } else {
+      if (st < 16 * G) {
+        if (!AD) af[st] = cur.a;
+        bb[st] = cur.b;
+      }
+      if (!AD && st < a_words) aw[st] = cur.w0;
+      if (!AD && st + kPairThreads < a_words) aw[st + kPairThreads] = cur.w1;
+      if (AD) x_rs = words_rsrc(item_ptr<float>(o.in[0], o.stride[0], item), kend * 4u);
+      __syncthreads();
+      // the previous instance's pl/ph (the first kPairPartWords bins) are read
+      if (!CUM) {
 #pragma unroll
-      for (uint32_t i = 0; i < kPairPartWords / (4 * kPairThreads); ++i)
-        bins4[st + i * kPairThreads] = make_int4(0, 0, 0, 0);
+        for (uint32_t i = 0; i < kPairPartWords / (4 * kPairThreads); ++i)
+          bins4[st + i * kPairThreads] = make_int4(0, 0, 0, 0);
+      }
+      if (tile == 0 && split == 0) sweep_books(AD ? bb : af, bb, 16 * G, o.status);
+      xbase = k0;
+      stage_x(xbase);
+      __syncthreads();
+      take_scale();
+      read_x(0, xa);
     }
-    if (tile == 0 && split == 0) sweep_books(AD ? bb : af, bb, 16 * G, o.status);
-    xbase = k0;
-    stage_x(xbase);
-    __syncthreads();
-    take_scale();
-    read_x(0, xa);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // settle the first x before the loop
     // the next instance's set-up data moves up; the one after is requested now
     cur = nxt;
@@ -733,14 +953,14 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     for (uint32_t b0 = 0; b0 + D < nbp; b0 += D) {
 #pragma unroll
       for (uint32_t d = 0; d < D; d += 2) {
-        stage(buf[d], b0 + d, xa, xb, cur_rs, b0 + d + D, false);
-        stage(buf[d + 1], b0 + d + 1, xb, xa, cur_rs, b0 + d + 1 + D, false);
+        stage(buf[d], b0 + d, xa, xb, cur_rs, b0 + d + D, false, d == 0 && b0 == 0);
+        stage(buf[d + 1], b0 + d + 1, xb, xa, cur_rs, b0 + d + 1 + D, false, false);
       }
     }
 #pragma unroll
     for (uint32_t d = 0; d < D; d += 2) {
-      stage(buf[d], nbp - D + d, xa, xb, next_rs, d, true);
-      stage(buf[d + 1], nbp - D + d + 1, xb, xa, next_rs, d + 1, true);
+      stage(buf[d], nbp - D + d, xa, xb, next_rs, d, true, d == 0 && nbp == D);
+      stage(buf[d + 1], nbp - D + d + 1, xb, xa, next_rs, d + 1, true, false);
     }
 
     // ---- finalise: sub-block row/column sums, one exchange, S, outputs ----
@@ -774,6 +994,13 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       for (int i = 0; i < 4; ++i) {
         const auto r = __builtin_amdgcn_permlane32_swap(rsi[i], rsi[4 + i], false, false);
         cpt[kCumHiBase + cum_part(cp, ch * 8 + cl * 4 + i, cq)] = r[0] + r[1];
+      }
+      if (defer) {
+        pending = true;
+        p_item = item;
+        p_shift = shift;
+        p_bb = bb;
+        continue;
       }
     } else {
       __syncthreads();  // every thread has flushed its bins
@@ -813,7 +1040,9 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     const uint32_t groups = (rw - tile * kTileWords) < kTileWords ? (rw - tile * kTileWords) * 8
                                                                  : kTileGroups;
     float* out = item_ptr_mut<float>(o.out, o.stride[4], item) + tile * kTileGroups * G;
-    if (G == 16 && gridDim.y == 1) {
+    if (CUM && G == 16 && gridDim.y == 1) {
+      mfma_product(item, shift, bb, false);
+    } else if (G == 16 && gridDim.y == 1) {
       // y^T = C_B^T . S^T on v_mfma_f32_16x16x4f32, 16 groups per tile and
       // 4 codes per step; S = the two partials of pl (even nibbles) or ph (odd
       // nibbles), each its own product. Lane l: A = C_B[4 ks + l/16][l % 16],
@@ -833,22 +1062,12 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
         const float* part = (n8 & 1u) ? ph : pl;
         typedef float float4v __attribute__((ext_vector_type(4)));
         float4v d = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (CUM) {
-          // cumulative partials: S itself, one product per code step
-          float sb[4];
 #pragma unroll
-          for (uint32_t ks = 0; ks < 4; ++ks) sb[ks] = cum_s(n8 / 2, 4 * ks + k4, qq, (n8 & 1u) != 0);
+        for (uint32_t ks = 0; ks < 4; ++ks)
 #pragma unroll
-          for (uint32_t ks = 0; ks < 4; ++ks)
-            d = __builtin_amdgcn_mfma_f32_16x16x4f32(bk[ks], sb[ks], d, 0, 0, 0);
-        } else {
-#pragma unroll
-          for (uint32_t ks = 0; ks < 4; ++ks)
-#pragma unroll
-            for (uint32_t h = 0; h < 2; ++h)
-              d = __builtin_amdgcn_mfma_f32_16x16x4f32(bk[ks], part[pair_part(h, n8 / 2, 4 * ks + k4, qq)],
-                                                       d, 0, 0, 0);
-        }
+          for (uint32_t h = 0; h < 2; ++h)
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(bk[ks], part[pair_part(h, n8 / 2, 4 * ks + k4, qq)],
+                                                     d, 0, 0, 0);
         if (j < groups) {
           float* oy = out + j * 16 + 4 * k4;
           if ((reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
@@ -946,6 +1165,11 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
         bins4[ft + i * kPairThreads] = make_int4(0, 0, 0, 0);
     }
   }
+  if (pending) {  // the block's last instance
+    __syncthreads();
+    mfma_product(p_item, p_shift, p_bb, true);
+  }
+  if (has_kept) store_out(kept_item, kept);
 }
 
 size_t pairs_shmem(uint32_t g) {

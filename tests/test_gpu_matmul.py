@@ -266,6 +266,27 @@ def test_gemv_pairs_four_instances_per_block(vqdev, oracle, n, k):
         assert o.max_rel(out[i], _ref64(items[i], m, n, k, group, 0)) <= TOL
 
 
+@pytest.mark.parametrize("count", [257, 1536])
+def test_gemv_pairs_kept_outputs_across_instances(vqdev, oracle, count):
+    """Blocks walking one to six instances: the batched decode path keeps an
+    instance's outputs in registers and stores them during the next
+    instance (or when the block ends). Neighbouring instances of a block use
+    different operands, so an output stored for the wrong item fails."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(count)
+    m, n, k, group = 1, 512, 4096, 16
+    sets = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(7)]
+    pick = [(i + i // 256) % 7 for i in range(count)]
+    ops = tuple(np.concatenate([sets[p][s].reshape(-1) for p in pick]) for s in range(4))
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
+    say("gemv-pairs kept outputs", count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    refs = [oracle.matmul(*st, m, n, k, group, 0)[0] for st in sets]
+    for i in range(count):
+        assert o.max_rel(out[i], refs[pick[i]]) <= TOL, i
+
+
 @pytest.mark.parametrize("sign", [1.0, -1.0])
 def test_gemv_pairs_saturated_windows_in_sequence(vqdev, sign):
     """The saturated window four times per block: the cumulative bins pass
