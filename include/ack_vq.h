@@ -211,7 +211,8 @@ int32_t ack_buffer_copy(const AckDevice* dev, const AckBuffer* dst, uint64_t dst
 int32_t ack_sync(const AckDevice* dev);
 
 /* Enqueue one streaming read of the whole buffer (16 bytes to 2 GiB) with
- * the loads the GEMV kernels stream their codes with, writing nothing. No
+ * the loads and per-block contiguous streams the GEMV kernels read their
+ * codes with (one block per compute unit), writing nothing. No
  * counterpart in the reference: for benchmarks, which time it with
  * ack_stream_timer to state the HBM read rate the GEMV is measured against. */
 int32_t ack_hbm_read_probe(const AckDevice* dev, const AckBuffer* buffer);
