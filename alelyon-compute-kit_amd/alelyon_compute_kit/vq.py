@@ -665,7 +665,7 @@ class VQAdamW:
             calibration = "device float64 fit of the update; no dense scratch written"
         else:
             images, moved = self._stepwise(gradient, hyper)
-            calibration = "native float64 fit of FP32 scratch"
+            calibration = "CPU float32/float64 temporary arrays"  # the reference's text
         self.weight, self.momentum, self.variance = images
         self.steps = upcoming
         elements = _Geometry(self.weight.shape, self.weight.group).elements
