@@ -95,6 +95,7 @@ _ENTRY_POINTS = {
     "ack_vq_plan_query": ((_P, _SZ, _U32, _P, _P, _P), _I32),
     "ack_vq_plan_check_buffers": ((_P, _SZ, _P, _P), _I32),
     "ack_vq_path_name": ((_P, _SZ, ctypes.c_char_p, _SZ), _I32),
+    "ack_vq_batch_path_name": ((_P, _SZ, ctypes.c_uint32, ctypes.c_char_p, _SZ), _I32),
     "ack_vq_dense_path_name": ((_P, _SZ, ctypes.c_char_p, _SZ), _I32),
     "ack_vq_set_policy": ((_P, _U32), _I32),
     "ack_vq_host_encode": ((_P, _U64, _P, _U32, _P), _I32),

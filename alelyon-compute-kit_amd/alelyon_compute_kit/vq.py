@@ -443,9 +443,15 @@ class VQDevice:
         lib.check(getattr(lib.cdll, entry)(plan, len(plan), name, len(name)), "vq")
         return name.value.decode()
 
-    def path_name(self, words) -> str:
-        """The kernel path ack_vq takes for a plan (automatic policy)."""
-        return self._path("ack_vq_path_name", words)
+    def path_name(self, words, count: int = 1) -> str:
+        """The kernel path ack_vq (count 1) or ack_vq_batch takes for a plan
+        (automatic policy)."""
+        name = ctypes.create_string_buffer(64)
+        plan = _plan(words)
+        lib = self.device.lib
+        count = _bounded_int(count, "count", 1, 2**31)
+        lib.check(lib.cdll.ack_vq_batch_path_name(plan, len(plan), count, name, len(name)), "vq")
+        return name.value.decode()
 
     def dense_path_name(self, words) -> str:
         """The kernel path the dense-activation product takes for an op-2 plan."""

@@ -647,8 +647,13 @@ int32_t ack_vq_plan_check_buffers(const uint8_t* plan, size_t plan_len,
   return ACK_OK;
 }
 
-int32_t ack_vq_path_name(const uint8_t* plan, size_t plan_len, char* out, size_t len) {
+int32_t ack_vq_batch_path_name(const uint8_t* plan, size_t plan_len, uint32_t count, char* out,
+                               size_t len) {
   if (out == nullptr || len == 0) return ACK_ERR_NULL;
+  if (count == 0) {
+    set_error("vq path name: count must be at least 1");
+    return ACK_ERR_SHAPE;
+  }
   ackvq::Plan p;
   if (int32_t rc = parse_plan(plan, plan_len, ackvq::Bounds::Library, &p)) return rc;
   const char* name = "encode";
@@ -656,11 +661,15 @@ int32_t ack_vq_path_name(const uint8_t* plan, size_t plan_len, char* out, size_t
   if (p.op == ackvq::Op::AdamW) name = "adamw";
   if (p.op == ackvq::Op::Matmul)
     name = ackvq::matmul_path_name(
-        ackvq::choose_matmul_path(p.m(), p.n(), p.k(), p.group(), p.flags(), 1, 0));
+        ackvq::choose_matmul_path(p.m(), p.n(), p.k(), p.group(), p.flags(), count, 0));
   const size_t n = std::strlen(name) < len - 1 ? std::strlen(name) : len - 1;
   std::memcpy(out, name, n);
   out[n] = '\0';
   return ACK_OK;
+}
+
+int32_t ack_vq_path_name(const uint8_t* plan, size_t plan_len, char* out, size_t len) {
+  return ack_vq_batch_path_name(plan, plan_len, 1, out, len);
 }
 
 int32_t ack_vq_host_encode(const float* values, uint64_t m, const float* book, uint32_t group,

@@ -29,6 +29,8 @@ enum class MatmulPath : int {
   GramMfma = 3,   // both operands grouped along k: one-hot x Gram table on fp16 MFMA
   RowBins = 4,    // large m, B groups along n: wave-uniform codes, bins in VGPRs
   GemvPairs = 5,  // m = 1, B groups along n: one atomic per byte into 256-way pair bins
+  GemvRowPairs = 6,  // 2 <= m <= 8 (row-major A, batches that fill the chip): each row of A
+                     // a GemvPairs instance, the rows of one product on one XCD
 };
 
 const char* matmul_path_name(MatmulPath p);

@@ -173,6 +173,18 @@ bool rows_apply(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t fla
   return m <= kGemvMaxM || (m <= kRowsMaxM && uint64_t(n) * k >= kRowsChunkMinWeight);
 }
 
+// "gemv-row-pairs": 2 <= m <= 8 rows of a row-major A, each its own instance of
+// the m = 1 pair-bin kernel, when the row instances alone fill the chip (256
+// blocks or more without splitting k). Packed A rows must start on whole code
+// words (k a multiple of 8 g); dense rows may start anywhere.
+bool row_pairs_apply(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                     uint32_t count, bool dense) {
+  if (m < 2 || m > kGemvMaxM || flags != 0 || n % (8 * group) != 0) return false;
+  if (!dense && k % (8 * group) != 0) return false;
+  const uint64_t tiles = (n / (8 * group) + kTileWords - 1) / kTileWords;
+  return tiles * count * m >= 256;
+}
+
 // A window's fixed-point scale: x -> rint(x 2^shift), from the window's L1.
 __device__ __forceinline__ int window_shift(float l1) {
   if (!(l1 > 0.0f && l1 <= FLT_MAX)) return 0;  // zero, NaN or Inf (status bit 1 covers the last two)
@@ -447,10 +459,17 @@ struct PairAhead {
 // histogram against the book's row norms, which every wave forms alike from
 // registers (so all waves hold the same scale without exchanging it). An
 // instance then has two barriers: before the flush and before the product.
+//
+// Row instances (mrows > 1: "gemv-row-pairs", 2 <= m <= 8 with A row-major):
+// each row of A is an instance of its own, instance i = (item i / mrows, row
+// i % mrows), binning that row against the item's B. A block's instance
+// sequence starts at an XCD-aware position, so the mrows instances of one item
+// run at the same time on blocks of one XCD and read B's codes through its L2
+// once from HBM. The caller guarantees one k slice (no split).
 template <int G, bool AD, bool SW, bool X4>
 __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint32_t n,
                                                                 uint32_t k, uint32_t ks,
-                                                                float* partial) {
+                                                                float* partial, uint32_t mrows) {
   constexpr uint32_t R = kPairR, D = kPairD, BR = kPairBatchRows;
   constexpr int kSPer = 16 * kTileGroups / kPairThreads;
   static_assert(16 * G <= kPairThreads, "one book entry per thread");
@@ -515,13 +534,28 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     asm volatile("" : "+v"(v));
     return v;
   };
+  // instance i: item i / mrows, row i % mrows of A (one instance per item when mrows = 1)
+  const uint32_t ninst = o.count * mrows;
+  auto src_item = [&](uint32_t i) { return mrows == 1 ? i : i / mrows; };
+  auto src_row = [&](uint32_t i) { return mrows == 1 ? 0u : i % mrows; };
+  // A's row of instance i: packed rows start on whole words (k a multiple of 8 G)
+  auto a_row_words = [&](uint32_t i) {
+    return item_ptr<uint32_t>(o.in[0], o.stride[0], src_item(i)) + src_row(i) * (k / (8 * G));
+  };
+  auto x_row = [&](uint32_t i) {
+    return item_ptr<float>(o.in[0], o.stride[0], src_item(i)) + uint64_t(src_row(i)) * k;
+  };
+  auto out_row = [&](uint32_t i) {
+    return item_ptr_mut<float>(o.out, o.stride[4], src_item(i)) + uint64_t(src_row(i)) * n +
+           tile * kTileGroups * G;
+  };
   auto setup_loads = [&](uint32_t item) {
     const uint32_t lt = opaque(tid);
-    const __amdgpu_buffer_rsrc_t ars =
-        words_rsrc(item_ptr<uint32_t>(o.in[0], o.stride[0], item) + a_w0, a_words * 4u);
-    const __amdgpu_buffer_rsrc_t abk =
-        words_rsrc(AD ? nullptr : item_ptr<float>(o.in[1], o.stride[1], item), AD ? 0u : 64u * G);
-    const __amdgpu_buffer_rsrc_t bbk = words_rsrc(item_ptr<float>(o.in[3], o.stride[3], item), 64u * G);
+    const __amdgpu_buffer_rsrc_t ars = words_rsrc(a_row_words(item) + a_w0, a_words * 4u);
+    const __amdgpu_buffer_rsrc_t abk = words_rsrc(
+        AD ? nullptr : item_ptr<float>(o.in[1], o.stride[1], src_item(item)), AD ? 0u : 64u * G);
+    const __amdgpu_buffer_rsrc_t bbk =
+        words_rsrc(item_ptr<float>(o.in[3], o.stride[3], src_item(item)), 64u * G);
     PairAhead h;
     h.b = __uint_as_float(uint32_t(__builtin_amdgcn_raw_buffer_load_b32(bbk, lt * 4u, 0, 0)));
     h.w0 = h.w1 = 0;
@@ -541,8 +575,8 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     return h;
   };
   auto batch_rsrc = [&](uint32_t item) {
-    const bool real = item < o.count;
-    return words_rsrc(item_ptr<uint32_t>(o.in[2], o.stride[2], real ? item : 0),
+    const bool real = item < ninst;
+    return words_rsrc(item_ptr<uint32_t>(o.in[2], o.stride[2], real ? src_item(item) : 0),
                       real ? kend * rw * 4u : 0u);
   };
   const uint32_t voff_lane = (lane_row * rw + col) * 4u;
@@ -700,7 +734,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   auto store_out = [&](uint32_t pitem, const float4 (&y)[TT]) __attribute__((always_inline)) {
     const uint32_t ft = opaque(tid);
     const uint32_t lane16 = ft % 16, k4 = (ft % 64) / 16;
-    float* out = item_ptr_mut<float>(o.out, o.stride[4], pitem) + tile * kTileGroups * G;
+    float* out = out_row(pitem);
     const bool vec = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
 #pragma unroll
     for (uint32_t tt = 0; tt < TT; ++tt) {
@@ -871,10 +905,14 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     }
   };
 
-  uint32_t item = blockIdx.z;
-  if (item < o.count) {
+  // the block's first instance; with row instances, blocks z, z + 8, z + 16, ...
+  // (one XCD) take consecutive instances, the rows of one item
+  const uint32_t first_inst =
+      (mrows > 1 && zn % 8 == 0) ? (blockIdx.z % 8) * (zn / 8) + blockIdx.z / 8 : blockIdx.z;
+  uint32_t item = first_inst;
+  if (item < ninst) {
     cur = setup_loads(item);
-    nxt = setup_loads(item + zn < o.count ? item + zn : item);
+    nxt = setup_loads(item + zn < ninst ? item + zn : item);
     const __amdgpu_buffer_rsrc_t r0 = batch_rsrc(item);
 #pragma unroll
     for (uint32_t d = 0; d < D; ++d) load_batch(r0, d, buf[d]);
@@ -888,7 +926,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     if (4 * tid < 16 * G) *reinterpret_cast<float4*>(af + 4 * tid) = cur.a4;
     __syncthreads();
   }
-  for (; item < o.count; item += zn) {
+  for (; item < ninst; item += zn) {
     const uint32_t next = item + zn;
     const __amdgpu_buffer_rsrc_t cur_rs = batch_rsrc(item);
     const __amdgpu_buffer_rsrc_t next_rs = batch_rsrc(next);
@@ -897,7 +935,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     // and the other copy of the B book, and its bin clears precede this
     // instance's atomics by the barriers below.
     const uint32_t st = opaque(tid);
-    const uint32_t par = ((item - blockIdx.z) / zn) & 1u;
+    const uint32_t par = ((item - first_inst) / zn) & 1u;
     float* bb = bb0 + par * (16 * G);
     if (PK) {
       // No barrier: the B book copy written here was last read by the product
@@ -923,7 +961,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       }
       if (!AD && st < a_words) aw[st] = cur.w0;
       if (!AD && st + kPairThreads < a_words) aw[st + kPairThreads] = cur.w1;
-      if (AD) x_rs = words_rsrc(item_ptr<float>(o.in[0], o.stride[0], item), kend * 4u);
+      if (AD) x_rs = words_rsrc(x_row(item), kend * 4u);
       __syncthreads();
       // the previous instance's pl/ph (the first kPairPartWords bins) are read
       if (!CUM) {
@@ -941,7 +979,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     __builtin_amdgcn_s_waitcnt(0xc07f);  // settle the first x before the loop
     // the next instance's set-up data moves up; the one after is requested now
     cur = nxt;
-    nxt = setup_loads(next + zn < o.count ? next + zn : item);
+    nxt = setup_loads(next + zn < ninst ? next + zn : item);
     if (!SW) {
 #pragma unroll
       for (int a = 0; a < (SW ? 1 : kPairSH); ++a)
@@ -1039,7 +1077,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     };
     const uint32_t groups = (rw - tile * kTileWords) < kTileWords ? (rw - tile * kTileWords) * 8
                                                                  : kTileGroups;
-    float* out = item_ptr_mut<float>(o.out, o.stride[4], item) + tile * kTileGroups * G;
+    float* out = out_row(item);
     if (CUM && G == 16 && gridDim.y == 1) {
       mfma_product(item, shift, bb, false);
     } else if (G == 16 && gridDim.y == 1) {
@@ -1648,18 +1686,22 @@ void pairs_slices(uint32_t n, uint32_t k, uint32_t group, uint32_t count, uint32
   *splits = (k + *ks - 1) / *ks;
 }
 
+// mrows > 1: the row instances of "gemv-row-pairs" (row_pairs_apply holds, so
+// the instances fill the chip without splitting k).
 template <int G, bool AD>
 hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k, uint32_t flags,
-                        void* workspace) {
-  (void)flags;  // m = 1: A's flat index is the inner index either way
+                        void* workspace, uint32_t mrows) {
+  (void)flags;  // m = 1: A's flat index is the inner index either way; row instances: row-major A
   const uint32_t tiles = (n / (8 * G) + kTileWords - 1) / kTileWords;
+  const uint32_t ninst = o.count * mrows;
   uint32_t ks, splits;
-  pairs_slices(n, k, G, o.count, &ks, &splits);
+  pairs_slices(n, k, G, ninst, &ks, &splits);
+  if (mrows > 1 && splits > 1) return hipErrorInvalidValue;  // excluded by row_pairs_apply
   // about one block per compute unit; each block walks its instances with the
   // next instance's first batches and set-up data already in flight
   const uint32_t per_z = tiles * splits;
   uint32_t zc = per_z >= 256 ? 1u : 256u / per_z;
-  zc = zc < o.count ? zc : o.count;
+  zc = zc < ninst ? zc : ninst;
   const size_t shmem = pairs_shmem(G);
   const bool one_window = ks <= kPairWindow;
   // 16-byte loads need rows of whole tiles (then every chunk is 16-byte aligned)
@@ -1674,13 +1716,13 @@ hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k
   dim3 grid(tiles, splits, zc);
   float* ws = static_cast<float*>(workspace);
   if (one_window && x4)
-    k_gemv_pairs<G, AD, true, true><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws);
+    k_gemv_pairs<G, AD, true, true><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws, mrows);
   else if (one_window)
-    k_gemv_pairs<G, AD, true, false><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws);
+    k_gemv_pairs<G, AD, true, false><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws, mrows);
   else if (x4)
-    k_gemv_pairs<G, AD, false, true><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws);
+    k_gemv_pairs<G, AD, false, true><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws, mrows);
   else
-    k_gemv_pairs<G, AD, false, false><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws);
+    k_gemv_pairs<G, AD, false, false><<<grid, kPairThreads, shmem, s>>>(o, n, k, ks, ws, mrows);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || splits == 1) return err;
   dim3 fgrid(tiles * kFinishParts, 1, zc);  // one row
@@ -1767,10 +1809,11 @@ hipError_t launch_rows(hipStream_t s, const Operands& o, uint32_t m, uint32_t n,
 template <bool AD>
 hipError_t launch_factorised(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                              uint32_t group, uint32_t flags, MatmulPath path, void* workspace) {
-  if (path == MatmulPath::GemvPairs) {
-    if (group == 8) return launch_pairs<8, AD>(s, o, n, k, flags, workspace);
-    if (group == 16) return launch_pairs<16, AD>(s, o, n, k, flags, workspace);
-    return launch_pairs<32, AD>(s, o, n, k, flags, workspace);
+  if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRowPairs) {
+    const uint32_t mrows = path == MatmulPath::GemvPairs ? 1u : m;
+    if (group == 8) return launch_pairs<8, AD>(s, o, n, k, flags, workspace, mrows);
+    if (group == 16) return launch_pairs<16, AD>(s, o, n, k, flags, workspace, mrows);
+    return launch_pairs<32, AD>(s, o, n, k, flags, workspace, mrows);
   }
   if (group == 8) return launch_rows<8, AD>(s, o, m, n, k, flags, workspace);
   if (group == 16) return launch_rows<16, AD>(s, o, m, n, k, flags, workspace);
@@ -1784,6 +1827,7 @@ const char* matmul_path_name(MatmulPath p) {
     case MatmulPath::General: return "general";
     case MatmulPath::GemvRows: return "gemv-rows";
     case MatmulPath::GemvPairs: return "gemv-pairs";
+    case MatmulPath::GemvRowPairs: return "gemv-row-pairs";
     case MatmulPath::GemvTable: return "gemv-table";
     case MatmulPath::GramMfma: return "gram-mfma";
     case MatmulPath::RowBins: return "row-bins";
@@ -1796,6 +1840,7 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
   if (policy == 1) return MatmulPath::General;
   if (count == 1 && rowbins_applies(m, n, k, group, flags)) return MatmulPath::RowBins;
   if (gram_applies(m, n, k, group, flags, policy == 2)) return MatmulPath::GramMfma;
+  if (row_pairs_apply(m, n, k, group, flags, count, false)) return MatmulPath::GemvRowPairs;
   if (rows_apply(m, n, k, group, flags))
     return m == 1 ? MatmulPath::GemvPairs : MatmulPath::GemvRows;
   return MatmulPath::General;
@@ -1830,7 +1875,8 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins(s, o, m, n, k, group, workspace);
   if (path == MatmulPath::GramMfma) return launch_gram(s, o, m, n, k, group);
-  if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows)
+  if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows ||
+      path == MatmulPath::GemvRowPairs)
     return launch_factorised<false>(s, o, m, n, k, group, flags, path, workspace);
   const uint32_t zc = o.count < 65535 ? o.count : 65535;
   dim3 grid((n + kGT - 1) / kGT, (m + kGT - 1) / kGT, zc);
@@ -1844,6 +1890,7 @@ MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                              uint32_t count, uint32_t policy) {
   if (policy == 1) return MatmulPath::General;
   if (count == 1 && rowbins_applies_dense(m, n, k, group, flags)) return MatmulPath::RowBins;
+  if (row_pairs_apply(m, n, k, group, flags, count, true)) return MatmulPath::GemvRowPairs;
   if (rows_apply(m, n, k, group, flags))
     return m == 1 ? MatmulPath::GemvPairs : MatmulPath::GemvRows;
   return MatmulPath::General;
@@ -1861,7 +1908,8 @@ hipError_t launch_matmul_dense(hipStream_t s, const Operands& o, uint32_t m, uin
                                void* workspace, size_t workspace_bytes) {
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins_dense(s, o, m, n, k, group, workspace);
-  if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows)
+  if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows ||
+      path == MatmulPath::GemvRowPairs)
     return launch_factorised<true>(s, o, m, n, k, group, flags, path, workspace);
   const uint32_t zc = o.count < 65535 ? o.count : 65535;
   dim3 grid((n + kGT - 1) / kGT, (m + kGT - 1) / kGT, zc);

@@ -107,7 +107,7 @@ def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
     status = device.buffer(4)
     status.upload(np.zeros(1, np.uint32))
     words = (2, m, 4096, 4096, 16, 16, 0, 0)
-    path = dev.path_name(words)
+    path = dev.path_name(words, count=items)
     single_ms = None
     sustained_ms = None
     dense = None

@@ -221,6 +221,13 @@ int32_t ack_hbm_read_probe(const AckDevice* dev, const AckBuffer* buffer);
  * (for tests that must know a fast path ran). */
 int32_t ack_vq_path_name(const uint8_t* plan, size_t plan_len, char* out, size_t len);
 
+/* The same for `count` instances launched together by ack_vq_batch (a batch
+ * whose row instances fill the chip can take a path a single product does
+ * not). No counterpart in the reference: for tests and benchmarks that must
+ * know which kernel served a batched launch. */
+int32_t ack_vq_batch_path_name(const uint8_t* plan, size_t plan_len, uint32_t count, char* out,
+                               size_t len);
+
 /* Path policy for one device: 0 = automatic, 1 = the general tiled kernel
  * for every matmul (a second implementation to cross-check fast paths),
  * 2 = a factorised path wherever its shape applies, below the size at which

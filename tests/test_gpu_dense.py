@@ -174,3 +174,24 @@ def test_dense_refusals_and_status(vqdev):
     finally:
         for b in (x, codes, book, out, status):
             b.free()
+
+
+@pytest.mark.parametrize("m,k", [(8, 136), (8, 264)])
+def test_dense_gemv_row_pairs(vqdev, oracle, m, k):
+    """A dense product wide enough that its rows alone fill the chip runs each
+    row of x as a pair-bin instance (k need not be a multiple of 8 g: dense
+    rows start anywhere); every row keeps the 1e-5 bar against its own
+    largest output."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(900 + m)
+    group = 8
+    n = 8 * group * 32 * (256 // m)            # 256 row instances of whole 32-word tiles
+    # (at m = 8, g = 8: n = 65536, the largest dimension a product admits)
+    w = _weight(rng, (k, n), group)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[1] *= 1e-6                               # rows of very different magnitude
+    y = _check(vqdev, oracle, x, w, False, False, "gemv-row-pairs")
+    exact = o.matmul64(x, w.decode(), False, False)
+    for r in range(m):
+        assert o.max_rel(y[r], exact[r]) <= 1e-5, r
+

@@ -636,6 +636,51 @@ def test_gemv_rows_each_row_its_own_scale(vqdev, oracle, m, count):
         _check_rows(out[i], exact)
 
 
+
+ROW_PAIR_SHAPES = [
+    # m, n, k, group, count
+    (2, 4096, 512, 16, 128),     # two rows, cumulative bins, MFMA output product
+    (3, 4096, 512, 16, 90),      # 3 rows: an item's rows straddle the XCD groups of 32
+    (7, 2048, 512, 8, 40),       # 7 rows at g = 8 (cumulative bins, scalar output product)
+    (8, 4096, 1024, 32, 40),     # g = 32, a 16-word tile: one-word loads, bins cleared
+    (4, 1024, 8192, 16, 64),     # two windows per row: x restaged, FP32 window sums
+    (8, 65536, 512, 8, 1),       # one product whose rows alone fill the chip
+]
+
+
+@pytest.mark.parametrize("m,n,k,group,count", ROW_PAIR_SHAPES)
+def test_gemv_row_pairs(vqdev, oracle, m, n, k, group, count):
+    """2..8 rows of a row-major A over a batch (or a product wide enough)
+    whose row instances fill the chip: each row runs as an m = 1 pair-bin
+    instance, the rows of one product on one XCD. Every checked row is held
+    to the 1e-5 bar against its own largest output; neighbouring instances
+    have different operands, so a row or item mix-up fails."""
+    rng = np.random.default_rng(m * 7 + n + k + group + count)
+    words = (2, m, n, k, group, 16, 0, 0)
+    assert vqdev.path_name(words, count=count) == "gemv-row-pairs"
+    b_sets = [image(rng, k * n, group, 0.02) for _ in range(min(count, 3))]
+    items = [image(rng, m * k, group, 1.0) + b_sets[i % len(b_sets)] for i in range(count)]
+    ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
+    say("gemv-row-pairs", m, n, k, group, count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    out = out.reshape(count, m, n)
+    for i in sorted({0, 1 % count, count // 2, count - 1}):
+        _check_rows(out[i], _ref64(items[i], m, n, k, group, 0))
+    if m * n * k <= 1 << 24:
+        ref, _ = oracle.matmul(*items[0], m, n, k, group, 0)
+        _check_rows(out[0], ref.reshape(m, n))
+
+
+def test_gemv_row_pairs_not_taken_where_rows_cannot_be_instances(vqdev):
+    """A transposed, k not a multiple of 8 g, or too few row instances keep
+    the row-pair-atomic kernel."""
+    assert vqdev.path_name((2, 4, 4096, 512, 16, 16, 1, 0), count=64) == "gemv-rows"
+    assert vqdev.path_name((2, 4, 4096, 520, 8, 16, 0, 0), count=64) == "gemv-rows"
+    assert vqdev.path_name((2, 4, 4096, 512, 16, 16, 0, 0), count=63) == "gemv-rows"
+    assert vqdev.path_name((2, 4, 4096, 512, 16, 16, 0, 0), count=64) == "gemv-row-pairs"
+    assert vqdev.path_name((2, 4, 4096, 512, 16, 16, 0, 0)) == "gemv-rows"
+
 # ---- status word on the reordered paths ----------------------------------------
 # path, m, n, k, group, flags: shapes each path takes
 STATUS_PATHS = [("gemv-pairs", 1, 512, 512, 16, 0), ("gemv-rows", 4, 512, 512, 16, 0),
