@@ -7,7 +7,8 @@ Run in the build container only, where the reference is mounted:
 It imports the reference's CPU functions -- ``encode``, ``fit_codebook``,
 ``VQArray``, ``VQAdamW`` (src/alelyon_compute_kit/_kit/python/vq.py),
 ``ExpertBank`` (_kit/python/expert_bank.py:148-430: ``initialize_expert``
-payloads and the files a short sequence of commits leaves on disk) and the
+payloads and the files a short sequence of commits leaves on disk, at 10x13
+and at 4096x4096) and the
 harness's gradient clip (src/alelyon_compute_kit/harness.py:196-200, observed
 through ``VulkanExpertHarness.train_step`` with a host backend) -- the
 functions no closed form or known-answer test pins bit for bit, and records
@@ -232,6 +233,43 @@ def bank_files() -> dict:
             "stats": np.frombuffer(stats, dtype=np.uint8)}
 
 
+def bank_scale() -> dict:
+    """A bank of full-size experts (three 4096x4096 group-16 matrices): two
+    seeded experts (one with zeroed optimizer state) and a committed update of
+    expert (0, 0) carrying expert (0, 1)'s payload. There are nine 525 KB shards,
+    so the fixture keeps each file's name, size and SHA-256, and the pointer
+    and bank JSON texts in full (generation ids as recorded)."""
+    import hashlib
+    with tempfile.TemporaryDirectory() as tmp:
+        root = Path(tmp) / "bank"
+        config = ref_bank.BankConfig(1, 2, ((4096, 4096),) * 3, 16)
+        bank = ref_bank.ExpertBank.create(root, config)
+        history = []
+
+        def generation():
+            text = (root / "expert-0-0.json").read_text()
+            return text.split('"generation":"')[1].split('"')[0]
+
+        bank.initialize_expert(0, 0, seed=11)
+        history.append(generation())
+        bank.initialize_expert(0, 1, seed=12, zero_optimizer_state=True)
+        bank.write_expert(0, 0, bank.read_expert(0, 1), updated_count=4096, optimizer_step=2)
+        history.append(generation())
+        stats = ref_bank._json(bank.stats())
+        names = sorted(p.name for p in root.iterdir())
+        sizes = [(root / n).stat().st_size for n in names]
+        digests = [hashlib.sha256((root / n).read_bytes()).hexdigest() for n in names]
+        texts = {n: (root / n).read_bytes() for n in names if n.endswith(".json")}
+    text_names = sorted(texts)
+    offsets = np.cumsum([0] + [len(texts[n]) for n in text_names]).astype(np.int64)
+    return {"names": np.array(names), "sizes": np.array(sizes, np.int64),
+            "sha256": np.array(digests), "json_names": np.array(text_names),
+            "json_offsets": offsets,
+            "json_blob": np.frombuffer(b"".join(texts[n] for n in text_names), dtype=np.uint8),
+            "history_0_0": np.array(history),
+            "stats": np.frombuffer(stats, dtype=np.uint8)}
+
+
 class _ClipRecorder:
     """A host backend for the reference harness that keeps the dense gradient
     it returns from the transposed product. The harness scales that array in
@@ -295,6 +333,7 @@ FIXTURES = {
     "expert_payloads": expert_payloads,
     "vqadamw_steps": vqadamw_steps,
     "bank_files": bank_files,
+    "bank_scale": bank_scale,
     "clip_scale": clip_cases,
 }
 

@@ -183,6 +183,49 @@ def test_this_writer_leaves_the_reference_files(tmp_path):
     assert expert_bank.canonical_json(bank.stats()) == stats
 
 
+def test_this_writer_leaves_the_reference_files_at_full_size(tmp_path):
+    """Full-size experts (three 4096x4096 group-16 matrices): the same seeded
+    experts and committed update leave files of the same names (generation
+    ids mapped), sizes and SHA-256 as the reference writer's, the same pointer
+    and bank JSON, and the same stats (tests/golden/bank_scale.npz)."""
+    import hashlib
+    g = golden("bank_scale.npz")
+    ref = {str(n): (int(sz), str(h)) for n, sz, h in zip(g["names"], g["sizes"], g["sha256"])}
+    blob, off = g["json_blob"].tobytes(), g["json_offsets"]
+    ref_json = {str(n): blob[off[i]:off[i + 1]] for i, n in enumerate(g["json_names"])}
+    history = [str(h) for h in g["history_0_0"]]
+    root = tmp_path / "scale"
+    bank = expert_bank.ExpertBank.create(
+        root, expert_bank.BankConfig(1, 2, ((4096, 4096),) * 3, 16))
+
+    def generation(base):
+        return json.loads((root / f"{base}.json").read_text())["generation"]
+
+    ours = []
+    bank.initialize_expert(0, 0, seed=11)
+    ours.append(generation("expert-0-0"))
+    bank.initialize_expert(0, 1, seed=12, zero_optimizer_state=True)
+    bank.write_expert(0, 0, bank.read_expert(0, 1), updated_count=4096, optimizer_step=2)
+    ours.append(generation("expert-0-0"))
+    rename = dict(zip(ours, history))
+    rename[generation("expert-0-1")] = json.loads(ref_json["expert-0-1.json"])["generation"]
+
+    def mapped(text: str) -> str:
+        for mine, theirs in rename.items():
+            text = text.replace(mine, theirs)
+        return text
+
+    written = {mapped(p.name): p for p in root.iterdir()}
+    assert sorted(written) == sorted(ref)
+    for name, path in written.items():
+        data = path.read_bytes()
+        if name.endswith(".json"):
+            data = mapped(data.decode()).encode()
+            assert data == ref_json[name], name
+        assert (len(data), hashlib.sha256(data).hexdigest()) == ref[name], name
+    assert expert_bank.canonical_json(bank.stats()) == g["stats"].tobytes()
+
+
 def test_a_changed_shard_is_refused(tmp_path):
     bank = _small_bank(tmp_path)
     pointer = json.loads((bank.root / "expert-0-0.json").read_bytes())
