@@ -171,7 +171,8 @@ int32_t ack_vq_adamw_step(const AckDevice* dev, const AckBuffer* b0, const AckBu
  * bit-identical to the op-2 loop with A read from X; the factorised paths
  * (m <= 8, m >= 64) agree within FP32 rounding. Enqueued like ack_vq. The
  * output and status must be distinct and alias no input. No counterpart in
- * the reference: the next step its survey names for this path. */
+ * the reference: for callers whose activations are dense float32, which the
+ * reference harness must first encode, lossily, to call op 2. */
 int32_t ack_vq_matmul_dense(const AckDevice* dev, const AckBuffer* x, const AckBuffer* b_codes,
                             const AckBuffer* b_book, const AckBuffer* out, const AckBuffer* status,
                             const uint8_t* plan, size_t plan_len);
