@@ -245,19 +245,22 @@ def test_gemv_pairs_saturated_window(vqdev, sign):
         assert o.max_rel(out[i], ref) <= TOL
 
 
-@pytest.mark.parametrize("n,k", [(512, 4096), (4096, 512)])
-def test_gemv_pairs_four_instances_per_block(vqdev, oracle, n, k):
-    """1024 instances: each block walks four, and at group 16 the bins are
-    never cleared between them (each instance's sums are differences of
-    cumulative bins). n = 512 covers the one-word loads, n = 4096 the
-    16-byte loads of whole tiles."""
+@pytest.mark.parametrize("n,k,group", [(512, 4096, 16), (4096, 512, 16), (4096, 512, 8),
+                                       (1024, 1024, 8)])
+def test_gemv_pairs_four_instances_per_block(vqdev, oracle, n, k, group):
+    """1024 instances: each block walks four, and at groups 8 and 16 the bins
+    are never cleared between them (each instance's sums are differences of
+    cumulative bins). n = 512 (g16) and 1024 (g8) cover the one-word loads,
+    n = 4096 the 16-byte loads of whole tiles (two tiles at g8); group 16
+    takes the MFMA output product with deferred products and kept outputs,
+    group 8 the S table."""
     from oracle import vq4_numpy as o
-    rng = np.random.default_rng(n + k)
-    m, group, count = 1, 16, 1024
+    rng = np.random.default_rng(n + k + group)
+    m, count = 1, 1024
     items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
     ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
     assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
-    say("gemv-pairs four per block", n, k, count)
+    say("gemv-pairs four per block", n, k, group, count)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
     for i in (0, 1, 255, 256, 511, 700, 1023):
