@@ -84,8 +84,8 @@ __device__ __forceinline__ void gram_step(GramTile& t, uint32_t aw0, uint32_t aw
   af[0] = one_hot((__builtin_amdgcn_ubfe(aw0, 4 * jj, 4) - h8) | dead0);
   af[1] = one_hot((__builtin_amdgcn_ubfe(aw1, 4 * jj, 4) - h8) | dead1);
   half8 bf[2][kGramTerms];
-  const char* p0 = tab_lane + 32 * __builtin_amdgcn_ubfe(bw0, 4 * jj, 4);
-  const char* p1 = tab_lane + 32 * __builtin_amdgcn_ubfe(bw1, 4 * jj, 4);
+  const char* p0 = tab_lane + 16 * __builtin_amdgcn_ubfe(bw0, 4 * jj, 4);
+  const char* p1 = tab_lane + 16 * __builtin_amdgcn_ubfe(bw1, 4 * jj, 4);
 #pragma unroll
   for (int s = 0; s < kGramTerms; ++s) {
     bf[0][s] = *reinterpret_cast<const half8*>(p0 + 512 * s);
@@ -106,7 +106,11 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
                                                                uint32_t k) {
   __shared__ float sa[16 * G];
   __shared__ float sb[16 * G];
-  __shared__ __align__(16) _Float16 tab[kGramTerms][16][16];  // [term][B code][A code], scaled Gram
+  // [term][A code / 8][B code][A code % 8], scaled Gram: a lane reads the 8
+  // entries of its half (h = A code / 8) for its column's B code, and for one
+  // half the 16 B codes' 16-byte rows fill the 64 banks once, so the 16 lanes
+  // of a pass (one h) never conflict (equal codes broadcast)
+  __shared__ __align__(16) _Float16 tab[kGramTerms][2][16][8];
   __shared__ float sred[kGramThreads / 64];
   const uint32_t J = k / G;
   const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
@@ -170,9 +174,9 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
     const _Float16 hi = _Float16(scaled);
     const float r1 = scaled - float(hi);
     const _Float16 mid = _Float16(r1);
-    tab[0][f][e] = hi;
-    tab[1][f][e] = mid;
-    tab[2][f][e] = _Float16(r1 - float(mid));
+    tab[0][e / 8][f][e % 8] = hi;
+    tab[1][e / 8][f][e % 8] = mid;
+    tab[2][e / 8][f][e % 8] = _Float16(r1 - float(mid));
     const float unscale = ldexpf(1.0f, -shift);
     __syncthreads();
 
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
     for (int x = 0; x < 2; ++x)
 #pragma unroll
       for (int y = 0; y < 2; ++y) tile.acc[x][y] = (f32x16)0.0f;
-    const char* tab_lane = reinterpret_cast<const char*>(&tab[0][0][0]) + 16 * h;
+    const char* tab_lane = reinterpret_cast<const char*>(&tab[0][0][0][0]) + 256 * h;
     const uint32_t h8 = 8 * h;
     uint32_t an0 = nibbles8(a_codes, av[0], a_last), an1 = nibbles8(a_codes, av[1], a_last);
     uint32_t bn0 = nibbles8(b_codes, bv[0], b_last), bn1 = nibbles8(b_codes, bv[1], b_last);
