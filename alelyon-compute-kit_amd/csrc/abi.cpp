@@ -57,6 +57,7 @@ struct Device {
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
   void* scratch = nullptr;  // this GPU's copy of `scratch` (ack_vq_noalloc), or null
+  uint32_t* arrivals = nullptr;  // gemv-direct's counters, zeroed at open (Operands::arrivals)
 };
 
 struct Registry {
@@ -250,6 +251,7 @@ int32_t run_vq(const AckDevice* handle, const AckBuffer* const slots[6], const u
   if (he != hipSuccess) return hip_failure(*dev, "vq: device selection", he, false);
 
   ackvq::Operands o;
+  o.arrivals = dev->arrivals;
   for (int i = 0; i < 4; ++i) {
     o.in[i] = bufs[i]->ptr;
     o.stride[i] = count > 1 ? plan.required_bytes[i] : 0;
@@ -373,8 +375,17 @@ AckDevice* ack_open(void) {
   if ((e = hipSetDevice(index)) != hipSuccess ||
       (e = hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking)) != hipSuccess ||
       (e = hipEventCreate(&dev->timer_start)) != hipSuccess ||
-      (e = hipEventCreate(&dev->timer_stop)) != hipSuccess) {
+      (e = hipEventCreate(&dev->timer_stop)) != hipSuccess ||
+      (e = hipMalloc(reinterpret_cast<void**>(&dev->arrivals),
+                     ackvq::kDirectCounters * sizeof(uint32_t))) != hipSuccess ||
+      (e = hipMemset(dev->arrivals, 0, ackvq::kDirectCounters * sizeof(uint32_t))) !=
+          hipSuccess ||
+      (e = hipDeviceSynchronize()) != hipSuccess) {
     set_error(std::string("device open: ") + hipGetErrorString(e));
+    if (dev->arrivals) (void)hipFree(dev->arrivals);
+    if (dev->timer_stop) (void)hipEventDestroy(dev->timer_stop);
+    if (dev->timer_start) (void)hipEventDestroy(dev->timer_start);
+    if (dev->stream) (void)hipStreamDestroy(dev->stream);
     return nullptr;
   }
   char name[256] = {0};
@@ -414,11 +425,13 @@ int32_t ack_close(AckDevice* handle) {
         set_error(std::string("close waited for enqueued work and it failed: ") +
                   hipGetErrorString(e));
       if (dev->workspace) (void)hipFree(dev->workspace);
+      if (dev->arrivals) (void)hipFree(dev->arrivals);
       (void)hipEventDestroy(dev->timer_start);
       (void)hipEventDestroy(dev->timer_stop);
       (void)hipStreamDestroy(dev->stream);
     }
     dev->workspace = nullptr;
+    dev->arrivals = nullptr;
   }
   Registry& r = registry();
   std::lock_guard<std::mutex> lock(r.mu);
@@ -740,6 +753,7 @@ int32_t ack_vq_matmul_dense(const AckDevice* handle, const AckBuffer* x, const A
     return plan_code(e);
   }
   ackvq::Operands o;
+  o.arrivals = dev->arrivals;
   for (int i = 0; i < 4; ++i) o.in[i] = bufs[i]->ptr;
   o.out = bufs[4]->ptr;
   o.status = static_cast<uint32_t*>(bufs[5]->ptr);

@@ -19,7 +19,12 @@ struct Operands {
   uint32_t* status = nullptr;
   uint64_t stride[5] = {0, 0, 0, 0, 0};  // slots 0..3, then out
   uint32_t count = 1;
+  // gemv-direct's arrival counters: kDirectCounters words, zero between
+  // launches, one array per device handle (its launches share one stream)
+  uint32_t* arrivals = nullptr;
 };
+
+constexpr uint32_t kDirectCounters = 1u << 16;
 
 // Which implementation serves an op-2 product.
 enum class MatmulPath : int {
@@ -31,12 +36,15 @@ enum class MatmulPath : int {
   GemvPairs = 5,  // m = 1, B groups along n: one atomic per byte into 256-way pair bins
   GemvRowPairs = 6,  // 2 <= m <= 8 (row-major A, batches that fill the chip): each row of A
                      // a GemvPairs instance, the rows of one product on one XCD
+  GemvDirect = 7,    // m = 1, few weights (kDirectMaxWeights): decode and FMA per output,
+                     // split k reduced by the last block of each tile, one launch
 };
 
 const char* matmul_path_name(MatmulPath p);
 
 // Chooses the path for a product; `policy` 1 forces General, 2 takes a
-// factorised path wherever its shape applies, whatever the size (tests).
+// factorised path wherever its shape applies, whatever the size (tests; it
+// never takes gemv-direct, which only the automatic choice does).
 MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                               uint32_t count, uint32_t policy);
 
@@ -44,6 +52,15 @@ bool gram_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t f
                   bool any_size);
 hipError_t launch_gram(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t group);
+
+// gemv-direct (vq4_direct.hip): the automatic choice for m = 1 products of at
+// most this many weights in all (n k count); above it the pair bins are faster.
+constexpr uint64_t kDirectMaxWeights = uint64_t(1) << 25;
+bool direct_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                    uint32_t count);
+size_t direct_workspace_bytes(uint32_t n, uint32_t k, uint32_t group, uint32_t count);
+hipError_t launch_direct(hipStream_t s, const Operands& o, uint32_t n, uint32_t k, uint32_t group,
+                         bool dense, void* workspace);
 
 bool rowbins_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
 bool rowbins_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);

@@ -1831,6 +1831,7 @@ const char* matmul_path_name(MatmulPath p) {
     case MatmulPath::GemvTable: return "gemv-table";
     case MatmulPath::GramMfma: return "gram-mfma";
     case MatmulPath::RowBins: return "row-bins";
+    case MatmulPath::GemvDirect: return "gemv-direct";
   }
   return "unknown";
 }
@@ -1840,6 +1841,7 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
   if (policy == 1) return MatmulPath::General;
   if (count == 1 && rowbins_applies(m, n, k, group, flags)) return MatmulPath::RowBins;
   if (gram_applies(m, n, k, group, flags, policy == 2)) return MatmulPath::GramMfma;
+  if (policy == 0 && direct_applies(m, n, k, group, flags, count)) return MatmulPath::GemvDirect;
   if (row_pairs_apply(m, n, k, group, flags, count, false)) return MatmulPath::GemvRowPairs;
   if (rows_apply(m, n, k, group, flags))
     return m == 1 ? MatmulPath::GemvPairs : MatmulPath::GemvRows;
@@ -1849,6 +1851,7 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
 size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                               uint32_t flags, uint32_t count) {
   if (p == MatmulPath::RowBins) return rowbins_workspace_bytes(n, k, group);
+  if (p == MatmulPath::GemvDirect) return direct_workspace_bytes(n, k, group, count);
   if (p != MatmulPath::GemvRows && p != MatmulPath::GemvPairs) return 0;
   uint32_t ks, splits;
   // the largest chunk of rows one launch bins; chunks reuse the partials
@@ -1874,6 +1877,7 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
                          size_t workspace_bytes) {
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins(s, o, m, n, k, group, workspace);
+  if (path == MatmulPath::GemvDirect) return launch_direct(s, o, n, k, group, false, workspace);
   if (path == MatmulPath::GramMfma) return launch_gram(s, o, m, n, k, group);
   if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows ||
       path == MatmulPath::GemvRowPairs)
@@ -1890,6 +1894,7 @@ MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                              uint32_t count, uint32_t policy) {
   if (policy == 1) return MatmulPath::General;
   if (count == 1 && rowbins_applies_dense(m, n, k, group, flags)) return MatmulPath::RowBins;
+  if (policy == 0 && direct_applies(m, n, k, group, flags, count)) return MatmulPath::GemvDirect;
   if (row_pairs_apply(m, n, k, group, flags, count, true)) return MatmulPath::GemvRowPairs;
   if (rows_apply(m, n, k, group, flags))
     return m == 1 ? MatmulPath::GemvPairs : MatmulPath::GemvRows;
@@ -1908,6 +1913,7 @@ hipError_t launch_matmul_dense(hipStream_t s, const Operands& o, uint32_t m, uin
                                void* workspace, size_t workspace_bytes) {
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins_dense(s, o, m, n, k, group, workspace);
+  if (path == MatmulPath::GemvDirect) return launch_direct(s, o, n, k, group, true, workspace);
   if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows ||
       path == MatmulPath::GemvRowPairs)
     return launch_factorised<true>(s, o, m, n, k, group, flags, path, workspace);

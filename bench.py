@@ -108,7 +108,7 @@ def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
     status.upload(np.zeros(1, np.uint32))
     words = (2, m, 4096, 4096, 16, 16, 0, 0)
     path = dev.path_name(words, count=items)
-    single_ms = None
+    single_ms = single_path = y_single = None
     dense = None
     try:
         def launch():
@@ -125,6 +125,8 @@ def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
                 b.upload(a)
             s_out = device.buffer(m * 4096 * 4)
             single_ms = timed(device, lambda: dev.run(words, s_bufs, s_out, status), 50, 5)
+            single_path = dev.path_name(words)
+            y_single = s_out.download(np.float32).reshape(m, 4096)
             # the dense-activation product on the same weight: x as float32
             d_x = device.buffer(x.nbytes)
             d_x.upload(x)
@@ -147,7 +149,9 @@ def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
     if dense is not None:
         exact = x.astype(np.float64) @ w_img.decode().astype(np.float64)
         dense["max_rel_vs_float64"] = max_rel(y_dense, exact)
-    return {"ms": ms, "single_ms": single_ms, "path": path,
+    single_err = None if y_single is None else max_rel(y_single, ref)
+    return {"ms": ms, "single_ms": single_ms, "single_path": single_path, "single_err": single_err,
+            "path": path,
             "max_rel": err, "dense": dense,
             "gbs": items * W_BYTES / (ms * 1e-3) / 1e9, "x_img": x_img, "w_img": w_img}
 
@@ -609,6 +613,8 @@ def main(argv=None) -> int:
                    "items": args.items, "m": 1, "n": 4096, "k": 4096, "group": 16,
                    "path": gemv["path"], "hbm_fraction": round(gbs / HBM_PEAK_GBS, 4),
                    "single_matrix_us": round(gemv["single_ms"] * 1e3, 3),
+                   "single_matrix_path": gemv["single_path"],
+                   "single_matrix_max_rel": gemv["single_err"],
                    "sustained_gbs": round(args.items * W_BYTES / (sustained_ms * 1e-3) / 1e9, 2),
                    "sustained_launches": SUSTAINED_LAUNCHES,
                    "max_rel_vs_oracle": gemv["max_rel"]},

@@ -52,3 +52,14 @@ def image(rng, m, group, scale=1.0):
         words[:part.size] |= part << np.uint32(4 * lane)
     book = (rng.standard_normal((16, group)) * scale).astype(np.float32)
     return words, book
+
+
+# The automatic choice for m = 1 products of B grouped along n: gemv-direct up
+# to this many weights in all (n k count; kDirectMaxWeights in
+# alelyon-compute-kit_amd/csrc/kernels.hpp), gemv-pairs above it. The test
+# policy (2) always takes gemv-pairs.
+DIRECT_MAX_WEIGHTS = 1 << 25
+
+
+def m1_auto_path(n, k, count=1):
+    return "gemv-direct" if n * k * count <= DIRECT_MAX_WEIGHTS else "gemv-pairs"

@@ -8,7 +8,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from gpu_util import say
+from gpu_util import m1_auto_path, say
 
 pytestmark = pytest.mark.gpu
 
@@ -20,12 +20,30 @@ def _weight(rng, shape, group, scale=0.02):
 
 
 def _check(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol=1e-5):
+    """`path` is the automatic choice; "m1" stands for m = 1's (gemv-direct up
+    to 2^25 weights, else gemv-pairs), and where that is gemv-direct the
+    product is also checked on gemv-pairs under the test policy."""
     from alelyon_compute_kit import vq
-    from oracle import vq4_numpy as o
     m, n, k, flags = vq.VQDevice.dense_geometry(x, w, transpose_a, transpose_b)
+    if path == "m1":
+        path = m1_auto_path(n, k)
+        if path == "gemv-direct":
+            vqdev.device.set_policy(2)
+            try:
+                say("dense matmul", "gemv-pairs (test policy)", m, n, k, w.group, flags)
+                _check_run(vqdev, oracle, x, w, transpose_a, transpose_b, "gemv-pairs", tol)
+            finally:
+                vqdev.device.set_policy(0)
     words = (2, m, n, k, w.group, 16, flags, 0)
     assert vqdev.dense_path_name(words) == path
     say("dense matmul", path, m, n, k, w.group, flags)
+    return _check_run(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol)
+
+
+def _check_run(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol):
+    from alelyon_compute_kit import vq
+    from oracle import vq4_numpy as o
+    m, n, k, flags = vq.VQDevice.dense_geometry(x, w, transpose_a, transpose_b)
     y = vqdev.matmul_dense(x, w, transpose_a=transpose_a, transpose_b=transpose_b)
     ref, status = oracle.matmul_dense(x, w.codes, w.codebook, m, n, k, w.group, flags)
     assert status == 0
@@ -44,7 +62,7 @@ def test_dense_gemv_paths(vqdev, oracle, group, m):
     k, n = 1536, 8 * group * 40            # 40 word columns: one full tile and a ragged one
     w = _weight(rng, (k, n), group)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    _check(vqdev, oracle, x, w, False, False, "gemv-pairs" if m == 1 else "gemv-rows")
+    _check(vqdev, oracle, x, w, False, False, "m1" if m == 1 else "gemv-rows")
 
 
 @pytest.mark.parametrize("m,k,group", [(1, 20000, 16), (4, 20000, 8), (3, 700, 32),
@@ -54,7 +72,7 @@ def test_dense_gemv_split_and_ragged_k(vqdev, oracle, m, k, group):
     n = 8 * group * 32
     w = _weight(rng, (k, n), group)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    _check(vqdev, oracle, x, w, False, False, "gemv-pairs" if m == 1 else "gemv-rows")
+    _check(vqdev, oracle, x, w, False, False, "m1" if m == 1 else "gemv-rows")
 
 
 def test_dense_gemv_transposed_activations(vqdev, oracle):
@@ -96,7 +114,7 @@ def test_dense_gemv_outlier_per_row(vqdev, oracle, m, k):
     w = _weight(rng, (k, 2048), 16)
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[np.arange(m), rng.integers(0, k, m)] = 30.0
-    y = _check(vqdev, oracle, x, w, False, False, "gemv-pairs" if m == 1 else "gemv-rows")
+    y = _check(vqdev, oracle, x, w, False, False, "m1" if m == 1 else "gemv-rows")
     _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
 
 
@@ -120,7 +138,7 @@ def test_dense_gemv_tiny_activations(vqdev, oracle, m):
     rng = np.random.default_rng(62 + m)
     w = _weight(rng, (2048, 4096), 16, scale=1.0)
     x = (rng.standard_normal((m, 2048)) * 1e-33).astype(np.float32)
-    y = _check(vqdev, oracle, x, w, False, False, "gemv-pairs" if m == 1 else "gemv-rows")
+    y = _check(vqdev, oracle, x, w, False, False, "m1" if m == 1 else "gemv-rows")
     assert np.abs(y).max() > 0
     _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
 

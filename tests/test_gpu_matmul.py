@@ -7,10 +7,12 @@ lie within the north star's FP32 tolerance: max|y - y_ref| / max|y_ref| <=
 """
 from __future__ import annotations
 
+import itertools
+
 import numpy as np
 import pytest
 
-from gpu_util import image, run_plan, say
+from gpu_util import image, m1_auto_path, run_plan, say
 
 pytestmark = pytest.mark.gpu
 
@@ -91,17 +93,126 @@ GEMV_SHAPES = [(256, 256, 16), (4096, 4096, 16), (512, 1024, 8), (1024, 768, 32)
 def test_gemv_within_tolerance(vqdev, oracle, m):
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(50 + m)
-    for k, n, group in GEMV_SHAPES:
+    for (k, n, group), policy in itertools.product(GEMV_SHAPES, (0, 2) if m == 1 else (0,)):
         words = (2, m, n, k, group, 16, 0, 0)
-        assert vqdev.path_name(words) == ("gemv-pairs" if m == 1 else "gemv-rows")
-        say("gemv", m, k, n, group)
+        auto = m1_auto_path(n, k) if m == 1 else "gemv-rows"
+        assert vqdev.path_name(words) == auto
+        say("gemv", m, k, n, group, auto if policy == 0 else "gemv-pairs")
         ops = _operands(rng, m, n, k, group, 1.0, 0.02)
-        out, status = _gpu(vqdev, ops, m, n, k, group, 0)
+        vqdev.device.set_policy(policy)   # 2: gemv-pairs for m = 1
+        try:
+            out, status = _gpu(vqdev, ops, m, n, k, group, 0)
+        finally:
+            vqdev.device.set_policy(0)
         assert status == 0
         if m * n * k <= 1 << 24:
             ref, _ = oracle.matmul(*ops, m, n, k, group, 0)
             assert o.max_rel(out, ref) <= TOL
         assert o.max_rel(out, _ref64(ops, m, n, k, group, 0)) <= TOL
+
+
+# n, k, group, count: whole and ragged tiles of 256 columns (640 at g 16, 320
+# at g 8), k below one group, k with a tail of rows, several slices and
+# instances, and the size limit itself (2^25 weights)
+DIRECT_SHAPES = [(4096, 4096, 16, 1), (4096, 4096, 16, 2), (1024, 1024, 8, 1),
+                 (640, 1000, 16, 3), (320, 1000, 8, 1), (64, 4, 8, 1), (2048, 63, 16, 5),
+                 (256, 8192, 16, 4), (8192, 4096, 8, 1), (512, 2048, 32, 2)]
+
+
+@pytest.mark.parametrize("n,k,group,count", DIRECT_SHAPES)
+def test_gemv_direct(vqdev, oracle, n, k, group, count):
+    """m = 1 products of at most 2^25 weights in all take gemv-direct (decode
+    per output, one launch): within 1e-5 of the oracle and of the float64
+    product for every instance."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(n + k + group + count)
+    m = 1
+    items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
+    ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0), count=count) == "gemv-direct"
+    say("gemv-direct", n, k, group, count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+    assert status == 0
+    out = out.reshape(count, m, n)
+    for i in range(count):
+        ref, _ = oracle.matmul(*items[i], m, n, k, group, 0)
+        assert o.max_rel(out[i], ref) <= TOL
+        assert o.max_rel(out[i], _ref64(items[i], m, n, k, group, 0)) <= TOL
+
+
+def test_gemv_direct_repeats_bit_for_bit(vqdev):
+    """The slices' partial sums are added by the last block of each tile in
+    slice order, counted through arrival counters that block resets: 64 calls
+    in a row, alternating two shapes with different tile and slice counts,
+    give the same bits every time."""
+    rng = np.random.default_rng(77)
+    device = vqdev.device
+    shapes = [(4096, 4096, 16), (1280, 3000, 8)]
+    runs = []
+    try:
+        for n, k, group in shapes:
+            ops = _operands(rng, 1, n, k, group, 1.0, 0.02)
+            bufs = [device.buffer(a.nbytes) for a in ops]
+            for b, a in zip(bufs, ops):
+                b.upload(a)
+            out, status = device.buffer(4 * n), device.buffer(4)
+            status.upload(np.zeros(1, np.uint32))
+            words = (2, 1, n, k, group, 16, 0, 0)
+            assert vqdev.path_name(words) == "gemv-direct"
+            runs.append((words, bufs, out, status))
+        first = []
+        for words, bufs, out, status in runs:
+            vqdev.run(words, bufs, out, status)
+            first.append(out.download(np.uint32).copy())
+        say("gemv-direct repeats", 64)
+        for i in range(64):
+            words, bufs, out, status = runs[i % 2]
+            vqdev.run(words, bufs, out, status)
+            if i % 8 < 2:   # download now and then; the other calls queue back to back
+                assert np.array_equal(out.download(np.uint32), first[i % 2]), i
+        for (words, bufs, out, status), ref in zip(runs, first):
+            assert np.array_equal(out.download(np.uint32), ref)
+            assert int(status.download(np.uint32)[0]) == 0
+    finally:
+        for _, bufs, out, status in runs:
+            for b in bufs + [out, status]:
+                b.free()
+
+
+def test_gemv_direct_on_two_handles_of_one_gpu(vqdev):
+    """Each device handle has its own stream and its own arrival counters:
+    products enqueued alternately on two handles of the same GPU, without
+    waiting in between, each equal that handle's first result."""
+    from alelyon_compute_kit import ack, vq
+    rng = np.random.default_rng(78)
+    n, k, group = 2048, 4096, 16
+    ops = _operands(rng, 1, n, k, group, 1.0, 0.02)
+    words = (2, 1, n, k, group, 16, 0, 0)
+    with ack.Device() as other:
+        devs = [vqdev, vq.VQDevice(other)]
+        held = []
+        try:
+            runs = []
+            for d in devs:
+                bufs = [d.device.buffer(a.nbytes) for a in ops]
+                for b, a in zip(bufs, ops):
+                    b.upload(a)
+                out, status = d.device.buffer(4 * n), d.device.buffer(4)
+                status.upload(np.zeros(1, np.uint32))
+                held.append((d, bufs + [out, status]))
+                runs.append((d, bufs, out, status))
+            say("gemv-direct two handles", 32)
+            for i in range(32):
+                d, bufs, out, status = runs[i % 2]
+                d.run(words, bufs, out, status)
+            first = runs[0][2].download(np.uint32)
+            assert np.array_equal(runs[1][2].download(np.uint32), first)
+            for d, bufs, out, status in runs:
+                assert int(status.download(np.uint32)[0]) == 0
+        finally:
+            for d, bs in held:
+                for b in bs:
+                    b.free()
 
 
 @pytest.mark.parametrize("m,flags", [(9, 0), (16, 0), (17, 1), (32, 0), (40, 1), (63, 0)])
@@ -192,7 +303,7 @@ def test_gemv_pairs_restaged_activations(vqdev, oracle):
     m, k, n, group, count = 1, 9000, 256, 16, 256
     items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
     ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
-    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0), count=count) == "gemv-pairs"
     say("gemv-pairs restaged", count)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
@@ -203,7 +314,7 @@ def test_gemv_pairs_restaged_activations(vqdev, oracle):
 
 
 @pytest.mark.parametrize("k,group", [(300, 16), (4352, 8), (7936, 32), (12500, 16)])
-def test_gemv_pairs_padding_batches(vqdev, oracle, k, group):
+def test_gemv_pairs_padding_batches(vqdev, oracle, any_size, k, group):
     """m = 1 with slice lengths that are not a whole number of ring turns:
     the last turn carries padding batches past the slice, which must add
     nothing (and, past a restage, read no stale activations)."""
@@ -212,7 +323,8 @@ def test_gemv_pairs_padding_batches(vqdev, oracle, k, group):
     m, n, count = 1, 256, 256
     items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
     ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
-    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
+    # automatic choice: gemv-direct for the smallest batch; the test policy runs gemv-pairs
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0), count=count) == m1_auto_path(n, k, count)
     say("gemv-pairs padding", k, group, count)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
@@ -236,7 +348,7 @@ def test_gemv_pairs_saturated_window(vqdev, sign):
     one = (a_codes, a_book, b_codes, b_book)
     count = 256  # enough instances that no block splits k: one slice holds the window
     ops = tuple(np.tile(a.reshape(-1), count) for a in one)
-    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0), count=count) == "gemv-pairs"
     say("gemv-pairs saturated", sign)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
@@ -259,7 +371,7 @@ def test_gemv_pairs_four_instances_per_block(vqdev, oracle, n, k, group):
     m, count = 1, 1024
     items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
     ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
-    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0), count=count) == "gemv-pairs"
     say("gemv-pairs four per block", n, k, group, count)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
@@ -281,7 +393,7 @@ def test_gemv_pairs_kept_outputs_across_instances(vqdev, oracle, count):
     sets = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(7)]
     pick = [(i + i // 256) % 7 for i in range(count)]
     ops = tuple(np.concatenate([sets[p][s].reshape(-1) for p in pick]) for s in range(4))
-    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-pairs"
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0), count=count) == "gemv-pairs"
     say("gemv-pairs kept outputs", count)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
@@ -592,8 +704,9 @@ def _check_rows(out, ref, tol=TOL):
 def test_gemv_outlier_codebook_entry(vqdev, oracle, m, k, n, count):
     """One activation of 30 per row among N(0,1) ones: the fixed-point step
     follows the window's L1 norm, so the outlier costs no precision elsewhere.
-    count = 1 splits k over blocks (finish kernel); 256 instances run whole
-    slices of one window per block, the config-3 path."""
+    m = 1, count = 1 takes gemv-direct by default and, under the test policy,
+    the pair bins with k split over blocks (finish kernel); 256 instances run
+    whole slices of one window per block, the config-3 path."""
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(k + m + count)
     group = 16
@@ -601,10 +714,24 @@ def test_gemv_outlier_codebook_entry(vqdev, oracle, m, k, n, count):
     b_codes, b_book = image(rng, k * n, group, 0.02)
     one = (a_codes, a_book, b_codes, b_book)
     ops = tuple(np.tile(a.reshape(-1), count) for a in one)
-    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == ("gemv-pairs" if m == 1 else "gemv-rows")
-    say("gemv outlier entry", m, k, n, count)
+    if m == 1:
+        auto = m1_auto_path(n, k, count)
+        assert vqdev.path_name((2, m, n, k, group, 16, 0, 0), count=count) == auto
+    else:   # one product's path (the batch of 256 takes the row instances)
+        auto = "gemv-rows"
+        assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == auto
+    say("gemv outlier entry", m, k, n, count, auto)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
+    if auto == "gemv-direct":   # the fixed-point pair bins too, under the test policy
+        vqdev.device.set_policy(2)
+        try:
+            pairs, pairs_status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+        finally:
+            vqdev.device.set_policy(0)
+        assert pairs_status == 0
+        pairs = pairs.reshape(count, m, n)
+        _check_rows(pairs[0], _ref64(one, m, n, k, group, 0))
     out = out.reshape(count, m, n)
     ref, ref_status = oracle.matmul(*one, m, n, k, group, 0)
     assert ref_status == 0
@@ -686,7 +813,8 @@ def test_gemv_row_pairs_not_taken_where_rows_cannot_be_instances(vqdev):
 
 # ---- status word on the reordered paths ----------------------------------------
 # path, m, n, k, group, flags: shapes each path takes
-STATUS_PATHS = [("gemv-pairs", 1, 512, 512, 16, 0), ("gemv-rows", 4, 512, 512, 16, 0),
+STATUS_PATHS = [("gemv-direct", 1, 512, 512, 16, 0), ("gemv-pairs", 1, 8192, 4160, 16, 0),
+                ("gemv-rows", 4, 512, 512, 16, 0),
                 ("gemv-rows", 7, 384, 1024, 8, 1), ("row-bins", 128, 512, 256, 16, 0),
                 ("gram-mfma", 64, 96, 1024, 16, 2)]
 
