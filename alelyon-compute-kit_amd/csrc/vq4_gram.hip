@@ -15,8 +15,8 @@
 // FP32 Gram entry within 2^-40 of the largest one is carried exactly, the
 // rest to 2^-40 of the largest), so each j costs three MFMAs per 32 x 32
 // output block and the accumulation is FP32. Neither operand is decoded:
-// P is built in registers from A's nibbles, Q is read from a 1.5 KiB LDS
-// table addressed by B's nibble.
+// P's fragments are read from a 768-byte LDS table of the one-hot rows
+// addressed by A's nibble, Q's from a 1.5 KiB LDS table addressed by B's.
 //
 // The sum order differs from the shader's sequential one; results agree to
 // FP32 rounding (k/G FP32 accumulations of exact Gram entries).
@@ -74,15 +74,16 @@ struct GramTile {
   f32x16 acc[2][2];
 };
 
-// One group j: two one-hot A fragments (rows), hi, mid and lo B fragments for
-// two column blocks from the LDS table, twelve MFMAs.
-// dead0/dead1 are OR-ed into the one-hot selectors of rows past the matrix.
+// One group j: two one-hot A fragments (rows) and hi, mid and lo B fragments
+// for two column blocks, all from LDS tables, then twelve MFMAs. sel0/sel1 are
+// the lanes' one-hot table bases (16 h for the lane's half h of K, 32 for a
+// row past the matrix, whose entries are empty), OR-ed with the A nibble.
 __device__ __forceinline__ void gram_step(GramTile& t, uint32_t aw0, uint32_t aw1, uint32_t bw0,
-                                          uint32_t bw1, uint32_t jj, uint32_t h8, uint32_t dead0,
-                                          uint32_t dead1, const char* tab_lane) {
+                                          uint32_t bw1, uint32_t jj, uint32_t sel0, uint32_t sel1,
+                                          const char* tab_lane, const char* lut) {
   half8 af[2];
-  af[0] = one_hot((__builtin_amdgcn_ubfe(aw0, 4 * jj, 4) - h8) | dead0);
-  af[1] = one_hot((__builtin_amdgcn_ubfe(aw1, 4 * jj, 4) - h8) | dead1);
+  af[0] = *reinterpret_cast<const half8*>(lut + 16 * (__builtin_amdgcn_ubfe(aw0, 4 * jj, 4) | sel0));
+  af[1] = *reinterpret_cast<const half8*>(lut + 16 * (__builtin_amdgcn_ubfe(aw1, 4 * jj, 4) | sel1));
   half8 bf[2][kGramTerms];
   const char* p0 = tab_lane + 16 * __builtin_amdgcn_ubfe(bw0, 4 * jj, 4);
   const char* p1 = tab_lane + 16 * __builtin_amdgcn_ubfe(bw1, 4 * jj, 4);
@@ -112,6 +113,9 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
   // of a pass (one h) never conflict (equal codes broadcast)
   __shared__ __align__(16) _Float16 tab[kGramTerms][2][16][8];
   __shared__ float sred[kGramThreads / 64];
+  // one-hot A fragments: entry 16 h + code holds one_hot(code - 8 h), entries
+  // 32..47 (dead rows) are empty
+  __shared__ __align__(16) u32x4 ohlut[48];
   const uint32_t J = k / G;
   const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const uint32_t i32 = lane % 32, h = lane / 32;
@@ -122,14 +126,17 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
   // Rows and columns past the matrix read the last row's (column's) codes;
   // a dead row's one-hot is forced empty, a dead column is never stored.
   uint64_t av[2], bv[2];
-  uint32_t dead[2];
+  uint32_t sel[2];
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
     const uint32_t r = row0 + 32 * x + i32, c = col0 + 32 * x + i32;
     av[x] = uint64_t(r < m ? r : m - 1) * J;
     bv[x] = uint64_t(c < n ? c : n - 1) * J;
-    dead[x] = r < m ? 0u : 0xFFFFFFF0u;  // OR-ed into a selector: no entry 0..7 matches
+    sel[x] = r < m ? 16u * h : 32u;  // the lane's one-hot table base
   }
+  if (tid < 48)
+    ohlut[tid] = tid < 32 ? __builtin_bit_cast(u32x4, one_hot((tid % 16) - 8u * (tid / 16)))
+                          : u32x4{0u, 0u, 0u, 0u};
 
   for (uint32_t item = blockIdx.z; item < o.count; item += gridDim.z) {
     const uint32_t* a_codes = item_ptr<uint32_t>(o.in[0], o.stride[0], item);
@@ -187,7 +194,6 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
 #pragma unroll
       for (int y = 0; y < 2; ++y) tile.acc[x][y] = (f32x16)0.0f;
     const char* tab_lane = reinterpret_cast<const char*>(&tab[0][0][0][0]) + 256 * h;
-    const uint32_t h8 = 8 * h;
     uint32_t an0 = nibbles8(a_codes, av[0], a_last), an1 = nibbles8(a_codes, av[1], a_last);
     uint32_t bn0 = nibbles8(b_codes, bv[0], b_last), bn1 = nibbles8(b_codes, bv[1], b_last);
     const uint32_t full = J / 8 * 8;
@@ -202,10 +208,12 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
       }
 #pragma unroll
       for (uint32_t jj = 0; jj < 8; ++jj)
-        gram_step(tile, aw0, aw1, bw0, bw1, jj, h8, dead[0], dead[1], tab_lane);
+        gram_step(tile, aw0, aw1, bw0, bw1, jj, sel[0], sel[1], tab_lane,
+                  reinterpret_cast<const char*>(ohlut));
     }
     for (uint32_t jj = 0; j0 + jj < J; ++jj)
-      gram_step(tile, an0, an1, bn0, bn1, jj, h8, dead[0], dead[1], tab_lane);
+      gram_step(tile, an0, an1, bn0, bn1, jj, sel[0], sel[1], tab_lane,
+                reinterpret_cast<const char*>(ohlut));
 
     // ---- store: lane (column i32, half h), item t holds row (t%4) + 4h + 8(t/4)
 #pragma unroll
