@@ -36,7 +36,7 @@ enum class MatmulPath : int {
   GemvPairs = 5,  // m = 1, B groups along n: one atomic per byte into 256-way pair bins
   GemvRowPairs = 6,  // 2 <= m <= 8 (row-major A, batches that fill the chip): each row of A
                      // a GemvPairs instance, the rows of one product on one XCD
-  GemvDirect = 7,    // m = 1, few weights (kDirectMaxWeights): decode and FMA per output,
+  GemvDirect = 7,    // m <= 8, few weights (kDirectMaxWeights): decode and FMA per output,
                      // split k reduced by the last block of each tile, one launch
 };
 
@@ -53,14 +53,17 @@ bool gram_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t f
 hipError_t launch_gram(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t group);
 
-// gemv-direct (vq4_direct.hip): the automatic choice for m = 1 products of at
-// most this many weights in all (n k count); above it the pair bins are faster.
+// gemv-direct (vq4_direct.hip): the automatic choice for products of at most
+// kDirectMaxRows rows of A and at most kDirectMaxWeights weights in all
+// (n k count); above them the bin kernels are faster.
+constexpr uint32_t kDirectMaxRows = 8;
 constexpr uint64_t kDirectMaxWeights = uint64_t(1) << 25;
 bool direct_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                     uint32_t count);
-size_t direct_workspace_bytes(uint32_t n, uint32_t k, uint32_t group, uint32_t count);
-hipError_t launch_direct(hipStream_t s, const Operands& o, uint32_t n, uint32_t k, uint32_t group,
-                         bool dense, void* workspace);
+size_t direct_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t group,
+                              uint32_t count);
+hipError_t launch_direct(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                         uint32_t group, uint32_t flags, bool dense, void* workspace);
 
 bool rowbins_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
 bool rowbins_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);

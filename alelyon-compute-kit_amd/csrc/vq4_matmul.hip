@@ -1851,7 +1851,7 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
 size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                               uint32_t flags, uint32_t count) {
   if (p == MatmulPath::RowBins) return rowbins_workspace_bytes(n, k, group);
-  if (p == MatmulPath::GemvDirect) return direct_workspace_bytes(n, k, group, count);
+  if (p == MatmulPath::GemvDirect) return direct_workspace_bytes(m, n, k, group, count);
   if (p != MatmulPath::GemvRows && p != MatmulPath::GemvPairs) return 0;
   uint32_t ks, splits;
   // the largest chunk of rows one launch bins; chunks reuse the partials
@@ -1877,7 +1877,8 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
                          size_t workspace_bytes) {
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins(s, o, m, n, k, group, workspace);
-  if (path == MatmulPath::GemvDirect) return launch_direct(s, o, n, k, group, false, workspace);
+  if (path == MatmulPath::GemvDirect)
+    return launch_direct(s, o, m, n, k, group, flags, false, workspace);
   if (path == MatmulPath::GramMfma) return launch_gram(s, o, m, n, k, group);
   if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows ||
       path == MatmulPath::GemvRowPairs)
@@ -1913,7 +1914,8 @@ hipError_t launch_matmul_dense(hipStream_t s, const Operands& o, uint32_t m, uin
                                void* workspace, size_t workspace_bytes) {
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins_dense(s, o, m, n, k, group, workspace);
-  if (path == MatmulPath::GemvDirect) return launch_direct(s, o, n, k, group, true, workspace);
+  if (path == MatmulPath::GemvDirect)
+    return launch_direct(s, o, m, n, k, group, flags, true, workspace);
   if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows ||
       path == MatmulPath::GemvRowPairs)
     return launch_factorised<true>(s, o, m, n, k, group, flags, path, workspace);

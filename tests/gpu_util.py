@@ -54,12 +54,26 @@ def image(rng, m, group, scale=1.0):
     return words, book
 
 
-# The automatic choice for m = 1 products of B grouped along n: gemv-direct up
-# to this many weights in all (n k count; kDirectMaxWeights in
-# alelyon-compute-kit_amd/csrc/kernels.hpp), gemv-pairs above it. The test
-# policy (2) always takes gemv-pairs.
+# The automatic choice for m <= 8 rows of A against B grouped along n (flags
+# bit 1 clear): gemv-direct up to this many weights in all (n k count;
+# kDirectMaxWeights and kDirectMaxRows in alelyon-compute-kit_amd/csrc/kernels.hpp),
+# the bin kernels above it. The test policy (2) never takes gemv-direct.
 DIRECT_MAX_WEIGHTS = 1 << 25
 
 
+def small_auto_path(m, n, k, count=1):
+    """gemv-direct where it applies, else gemv-pairs (m = 1) or gemv-rows; a
+    batch filling the chip with row instances is gemv-row-pairs, which this
+    helper does not model (callers pass count 1 there)."""
+    if m <= 8 and n * k * count <= DIRECT_MAX_WEIGHTS:
+        return "gemv-direct"
+    return "gemv-pairs" if m == 1 else "gemv-rows"
+
+
+def binned_path(m):
+    """The path the test policy takes for m <= 8 (B grouped along n)."""
+    return "gemv-pairs" if m == 1 else "gemv-rows"
+
+
 def m1_auto_path(n, k, count=1):
-    return "gemv-direct" if n * k * count <= DIRECT_MAX_WEIGHTS else "gemv-pairs"
+    return small_auto_path(1, n, k, count)

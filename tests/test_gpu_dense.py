@@ -8,7 +8,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from gpu_util import m1_auto_path, say
+from gpu_util import binned_path, say, small_auto_path
 
 pytestmark = pytest.mark.gpu
 
@@ -19,21 +19,23 @@ def _weight(rng, shape, group, scale=0.02):
     return vq.encode(w, vq.fit_codebook(w, group=group), group=group)
 
 
-def _check(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol=1e-5):
-    """`path` is the automatic choice; "m1" stands for m = 1's (gemv-direct up
-    to 2^25 weights, else gemv-pairs), and where that is gemv-direct the
-    product is also checked on gemv-pairs under the test policy."""
+def _check(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol=1e-5, binned=None):
+    """`path` is the automatic choice; "small" stands for that of up to 8 rows
+    (gemv-direct up to 2^25 weights, else the bin kernels). Where the choice is
+    gemv-direct the product is also checked under the test policy, on the bin
+    kernel `binned` names (by default gemv-pairs for m = 1, else gemv-rows)."""
     from alelyon_compute_kit import vq
     m, n, k, flags = vq.VQDevice.dense_geometry(x, w, transpose_a, transpose_b)
-    if path == "m1":
-        path = m1_auto_path(n, k)
-        if path == "gemv-direct":
-            vqdev.device.set_policy(2)
-            try:
-                say("dense matmul", "gemv-pairs (test policy)", m, n, k, w.group, flags)
-                _check_run(vqdev, oracle, x, w, transpose_a, transpose_b, "gemv-pairs", tol)
-            finally:
-                vqdev.device.set_policy(0)
+    if path == "small":
+        path = small_auto_path(m, n, k)
+    if path == "gemv-direct":
+        vqdev.device.set_policy(2)
+        try:
+            label = binned or binned_path(m)
+            say("dense matmul", label, "(test policy)", m, n, k, w.group, flags)
+            _check_run(vqdev, oracle, x, w, transpose_a, transpose_b, label, tol)
+        finally:
+            vqdev.device.set_policy(0)
     words = (2, m, n, k, w.group, 16, flags, 0)
     assert vqdev.dense_path_name(words) == path
     say("dense matmul", path, m, n, k, w.group, flags)
@@ -62,7 +64,7 @@ def test_dense_gemv_paths(vqdev, oracle, group, m):
     k, n = 1536, 8 * group * 40            # 40 word columns: one full tile and a ragged one
     w = _weight(rng, (k, n), group)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    _check(vqdev, oracle, x, w, False, False, "m1" if m == 1 else "gemv-rows")
+    _check(vqdev, oracle, x, w, False, False, "small")
 
 
 @pytest.mark.parametrize("m,k,group", [(1, 20000, 16), (4, 20000, 8), (3, 700, 32),
@@ -72,14 +74,14 @@ def test_dense_gemv_split_and_ragged_k(vqdev, oracle, m, k, group):
     n = 8 * group * 32
     w = _weight(rng, (k, n), group)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    _check(vqdev, oracle, x, w, False, False, "m1" if m == 1 else "gemv-rows")
+    _check(vqdev, oracle, x, w, False, False, "small")
 
 
 def test_dense_gemv_transposed_activations(vqdev, oracle):
     rng = np.random.default_rng(5)
     w = _weight(rng, (1024, 8 * 16 * 32), 16)
     x = rng.standard_normal((1024, 6)).astype(np.float32)     # stored k x m
-    _check(vqdev, oracle, x, w, True, False, "gemv-rows")
+    _check(vqdev, oracle, x, w, True, False, "small")
 
 
 def _rows_within(y, exact, tol=1e-5):
@@ -98,7 +100,7 @@ def test_dense_gemv_outliers_and_zero_rows(vqdev, oracle):
     x = rng.standard_normal((4, 2048)).astype(np.float32)
     x[1] = 0.0                                              # an all-zero row
     x[2, 7] = 30.0                                          # one outlier in a N(0,1) row
-    y = _check(vqdev, oracle, x, w, False, False, "gemv-rows")
+    y = _check(vqdev, oracle, x, w, False, False, "small")
     _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
     zero = np.zeros((1, 2048), np.float32)
     y = vqdev.matmul_dense(zero, w)
@@ -114,7 +116,7 @@ def test_dense_gemv_outlier_per_row(vqdev, oracle, m, k):
     w = _weight(rng, (k, 2048), 16)
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[np.arange(m), rng.integers(0, k, m)] = 30.0
-    y = _check(vqdev, oracle, x, w, False, False, "m1" if m == 1 else "gemv-rows")
+    y = _check(vqdev, oracle, x, w, False, False, "small")
     _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
 
 
@@ -126,7 +128,7 @@ def test_dense_gemv_rows_of_very_different_magnitude(vqdev, oracle):
     w = _weight(rng, (4096, 4096), 16)
     x = rng.standard_normal((4, 4096)).astype(np.float32)
     x *= np.array([[1e-6], [1.0], [30.0], [1e-30]], np.float32)
-    y = _check(vqdev, oracle, x, w, False, False, "gemv-rows")
+    y = _check(vqdev, oracle, x, w, False, False, "small")
     _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
 
 
@@ -138,7 +140,7 @@ def test_dense_gemv_tiny_activations(vqdev, oracle, m):
     rng = np.random.default_rng(62 + m)
     w = _weight(rng, (2048, 4096), 16, scale=1.0)
     x = (rng.standard_normal((m, 2048)) * 1e-33).astype(np.float32)
-    y = _check(vqdev, oracle, x, w, False, False, "m1" if m == 1 else "gemv-rows")
+    y = _check(vqdev, oracle, x, w, False, False, "small")
     assert np.abs(y).max() > 0
     _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
 
@@ -196,10 +198,11 @@ def test_dense_refusals_and_status(vqdev):
 
 @pytest.mark.parametrize("m,k", [(8, 136), (8, 264)])
 def test_dense_gemv_row_pairs(vqdev, oracle, m, k):
-    """A dense product wide enough that its rows alone fill the chip runs each
-    row of x as a pair-bin instance (k need not be a multiple of 8 g: dense
-    rows start anywhere); every row keeps the 1e-5 bar against its own
-    largest output."""
+    """A dense product wide enough that its rows alone fill the chip runs, under
+    the test policy, each row of x as a pair-bin instance (k need not be a
+    multiple of 8 g: dense rows start anywhere), and by default gemv-direct
+    (n k at most 2^25); every row keeps the 1e-5 bar against its own largest
+    output."""
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(900 + m)
     group = 8
@@ -208,7 +211,7 @@ def test_dense_gemv_row_pairs(vqdev, oracle, m, k):
     w = _weight(rng, (k, n), group)
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[1] *= 1e-6                               # rows of very different magnitude
-    y = _check(vqdev, oracle, x, w, False, False, "gemv-row-pairs")
+    y = _check(vqdev, oracle, x, w, False, False, "small", binned="gemv-row-pairs")
     exact = o.matmul64(x, w.decode(), False, False)
     for r in range(m):
         assert o.max_rel(y[r], exact[r]) <= 1e-5, r

@@ -12,7 +12,7 @@ import itertools
 import numpy as np
 import pytest
 
-from gpu_util import image, m1_auto_path, run_plan, say
+from gpu_util import binned_path, image, m1_auto_path, run_plan, say, small_auto_path
 
 pytestmark = pytest.mark.gpu
 
@@ -93,13 +93,13 @@ GEMV_SHAPES = [(256, 256, 16), (4096, 4096, 16), (512, 1024, 8), (1024, 768, 32)
 def test_gemv_within_tolerance(vqdev, oracle, m):
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(50 + m)
-    for (k, n, group), policy in itertools.product(GEMV_SHAPES, (0, 2) if m == 1 else (0,)):
+    for (k, n, group), policy in itertools.product(GEMV_SHAPES, (0, 2)):
         words = (2, m, n, k, group, 16, 0, 0)
-        auto = m1_auto_path(n, k) if m == 1 else "gemv-rows"
+        auto = small_auto_path(m, n, k)
         assert vqdev.path_name(words) == auto
-        say("gemv", m, k, n, group, auto if policy == 0 else "gemv-pairs")
+        say("gemv", m, k, n, group, auto if policy == 0 else binned_path(m))
         ops = _operands(rng, m, n, k, group, 1.0, 0.02)
-        vqdev.device.set_policy(policy)   # 2: gemv-pairs for m = 1
+        vqdev.device.set_policy(policy)   # 2: the bin kernels
         try:
             out, status = _gpu(vqdev, ops, m, n, k, group, 0)
         finally:
@@ -140,36 +140,65 @@ def test_gemv_direct(vqdev, oracle, n, k, group, count):
         assert o.max_rel(out[i], _ref64(items[i], m, n, k, group, 0)) <= TOL
 
 
+# m, n, k, group, flags (bit 0: A stored k x m), count
+DIRECT_ROW_SHAPES = [(2, 4096, 4096, 16, 0, 1), (3, 1024, 1000, 8, 1, 1),
+                     (4, 2048, 2048, 32, 0, 2), (5, 640, 1000, 16, 1, 3),
+                     (6, 256, 63, 8, 0, 4), (7, 4096, 1024, 16, 1, 1),
+                     (8, 4096, 4096, 16, 0, 1), (8, 2048, 2048, 8, 1, 2), (8, 64, 4, 8, 0, 1)]
+
+
+@pytest.mark.parametrize("m,n,k,group,flags,count", DIRECT_ROW_SHAPES)
+def test_gemv_direct_rows(vqdev, oracle, m, n, k, group, flags, count):
+    """2..8 rows of A, row-major or stored k x m, over products of at most
+    2^25 weights in all: one gemv-direct launch, each block holding 1, 2, 4
+    or 8 rows; within 1e-5 of the oracle and of the float64 product, row by
+    row, for every instance."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(m * 31 + n + k + group + flags + count)
+    items = [_operands(rng, m, n, k, group, 1.0, 0.02) for _ in range(count)]
+    ops = tuple(np.concatenate([it[s].reshape(-1) for it in items]) for s in range(4))
+    words = (2, m, n, k, group, 16, flags, 0)
+    assert vqdev.path_name(words, count=count) == "gemv-direct"
+    say("gemv-direct rows", m, n, k, group, flags, count)
+    out, status = _gpu(vqdev, ops, m, n, k, group, flags, count=count)
+    assert status == 0
+    out = out.reshape(count, m, n)
+    for i in range(count):
+        ref, _ = oracle.matmul(*items[i], m, n, k, group, flags)
+        assert o.max_rel(out[i], ref) <= TOL
+        _check_rows(out[i], _ref64(items[i], m, n, k, group, flags))
+
+
 def test_gemv_direct_repeats_bit_for_bit(vqdev):
     """The slices' partial sums are added by the last block of each tile in
-    slice order, counted through arrival counters that block resets: 64 calls
-    in a row, alternating two shapes with different tile and slice counts,
-    give the same bits every time."""
+    slice order, counted through arrival counters that block resets: 96 calls
+    in a row, cycling through three shapes with different row, tile and slice
+    counts, give the same bits every time."""
     rng = np.random.default_rng(77)
     device = vqdev.device
-    shapes = [(4096, 4096, 16), (1280, 3000, 8)]
+    shapes = [(1, 4096, 4096, 16, 0), (1, 1280, 3000, 8, 0), (5, 1024, 2000, 8, 1)]
     runs = []
     try:
-        for n, k, group in shapes:
-            ops = _operands(rng, 1, n, k, group, 1.0, 0.02)
+        for m, n, k, group, flags in shapes:
+            ops = _operands(rng, m, n, k, group, 1.0, 0.02)
             bufs = [device.buffer(a.nbytes) for a in ops]
             for b, a in zip(bufs, ops):
                 b.upload(a)
-            out, status = device.buffer(4 * n), device.buffer(4)
+            out, status = device.buffer(4 * m * n), device.buffer(4)
             status.upload(np.zeros(1, np.uint32))
-            words = (2, 1, n, k, group, 16, 0, 0)
+            words = (2, m, n, k, group, 16, flags, 0)
             assert vqdev.path_name(words) == "gemv-direct"
             runs.append((words, bufs, out, status))
         first = []
         for words, bufs, out, status in runs:
             vqdev.run(words, bufs, out, status)
             first.append(out.download(np.uint32).copy())
-        say("gemv-direct repeats", 64)
-        for i in range(64):
-            words, bufs, out, status = runs[i % 2]
+        say("gemv-direct repeats", 96)
+        for i in range(96):
+            words, bufs, out, status = runs[i % 3]
             vqdev.run(words, bufs, out, status)
-            if i % 8 < 2:   # download now and then; the other calls queue back to back
-                assert np.array_equal(out.download(np.uint32), first[i % 2]), i
+            if i % 12 < 3:   # download now and then; the other calls queue back to back
+                assert np.array_equal(out.download(np.uint32), first[i % 3]), i
         for (words, bufs, out, status), ref in zip(runs, first):
             assert np.array_equal(out.download(np.uint32), ref)
             assert int(status.download(np.uint32)[0]) == 0
@@ -425,7 +454,7 @@ def test_gemv_pairs_saturated_windows_in_sequence(vqdev, sign):
 
 @pytest.mark.parametrize("m,k,group,flags", [(2, 20000, 8, 0), (8, 20000, 8, 0),
                                              (5, 12000, 16, 1), (6, 700, 32, 0)])
-def test_gemv_rows_split_slices(vqdev, m, k, group, flags):
+def test_gemv_rows_split_slices(vqdev, any_size, m, k, group, flags):
     """One product (no batch) over long k: k is split across blocks, and for
     g = 8, m = 8 the slices are also capped so one slice's A words fit the
     staging area; the split partials are summed by the finish kernel."""
@@ -433,7 +462,8 @@ def test_gemv_rows_split_slices(vqdev, m, k, group, flags):
     rng = np.random.default_rng(k + m)
     n = 512
     ops = _operands(rng, m, n, k, group, 1.0, 0.02)
-    assert vqdev.path_name((2, m, n, k, group, 16, flags, 0)) == "gemv-rows"
+    # the automatic choice is gemv-direct at these sizes; the test policy runs gemv-rows
+    assert vqdev.path_name((2, m, n, k, group, 16, flags, 0)) == small_auto_path(m, n, k)
     say("gemv-rows split", m, k, group, flags)
     out, status = _gpu(vqdev, ops, m, n, k, group, flags)
     assert status == 0
@@ -480,14 +510,14 @@ def test_gemv_rows_saturated_window(vqdev, sign):
     b_book = (np.arange(16 * group, dtype=np.float32).reshape(16, group) / 256.0).astype(np.float32)
     b_codes = o.pack_indices(np.full(k * n // group, 9, np.int64))
     one = (a_codes, a_book, b_codes, b_book)
-    count = 256
+    count = 64   # 128 row instances: too few for the row-pair kernel
     ops = tuple(np.tile(a.reshape(-1), count) for a in one)
-    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "gemv-rows"
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0), count=count) == "gemv-rows"
     say("gemv-rows saturated", sign)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
     ref = _ref64(one, m, n, k, group, 0)
-    for i in (0, 255):
+    for i in (0, count - 1):
         assert o.max_rel(out[i], ref) <= TOL
 
 
@@ -704,9 +734,10 @@ def _check_rows(out, ref, tol=TOL):
 def test_gemv_outlier_codebook_entry(vqdev, oracle, m, k, n, count):
     """One activation of 30 per row among N(0,1) ones: the fixed-point step
     follows the window's L1 norm, so the outlier costs no precision elsewhere.
-    m = 1, count = 1 takes gemv-direct by default and, under the test policy,
-    the pair bins with k split over blocks (finish kernel); 256 instances run
-    whole slices of one window per block, the config-3 path."""
+    One product takes gemv-direct by default and, under the test policy, the
+    fixed-point bins with k split over blocks (finish kernel); 256 instances
+    run whole slices of one window per block (m = 1, the config-3 path) or the
+    row instances (m > 1)."""
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(k + m + count)
     group = 16
@@ -714,16 +745,16 @@ def test_gemv_outlier_codebook_entry(vqdev, oracle, m, k, n, count):
     b_codes, b_book = image(rng, k * n, group, 0.02)
     one = (a_codes, a_book, b_codes, b_book)
     ops = tuple(np.tile(a.reshape(-1), count) for a in one)
-    if m == 1:
-        auto = m1_auto_path(n, k, count)
+    if m == 1 or count == 1:
+        auto = small_auto_path(m, n, k, count)
         assert vqdev.path_name((2, m, n, k, group, 16, 0, 0), count=count) == auto
-    else:   # one product's path (the batch of 256 takes the row instances)
-        auto = "gemv-rows"
-        assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == auto
+    else:   # the batch of 256 takes the row instances
+        auto = "gemv-row-pairs"
+        assert vqdev.path_name((2, m, n, k, group, 16, 0, 0), count=count) == auto
     say("gemv outlier entry", m, k, n, count, auto)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
     assert status == 0
-    if auto == "gemv-direct":   # the fixed-point pair bins too, under the test policy
+    if auto == "gemv-direct":   # the fixed-point bins too, under the test policy
         vqdev.device.set_policy(2)
         try:
             pairs, pairs_status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
@@ -745,7 +776,7 @@ def test_gemv_outlier_codebook_entry(vqdev, oracle, m, k, n, count):
 
 @pytest.mark.parametrize("m", [2, 5, 8])
 @pytest.mark.parametrize("count", [1, 256])
-def test_gemv_rows_each_row_its_own_scale(vqdev, oracle, m, count):
+def test_gemv_rows_each_row_its_own_scale(vqdev, oracle, any_size, m, count):
     """Rows of A 2^20 apart in magnitude in one launch (even rows ~1e-6,
     odd rows ~1 with an outlier of 30): every row, checked against its own
     largest output, keeps the 1e-5 bar; a shared scale would round the small
@@ -756,14 +787,17 @@ def test_gemv_rows_each_row_its_own_scale(vqdev, oracle, m, count):
     b_codes, b_book = image(rng, k * n, group, 0.02)
     one = (a_codes, a_book, b_codes, b_book)
     ops = tuple(np.tile(a.reshape(-1), count) for a in one)
-    say("gemv-rows own scale", m, count)
-    out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
-    assert status == 0
-    out = out.reshape(count, m, n)
     exact = _ref64(one, m, n, k, group, 0)
     assert np.abs(exact[0]).max() < 1e-3 < np.abs(exact[1]).max()
-    for i in sorted({0, count - 1}):
-        _check_rows(out[i], exact)
+    # the test policy (bins), then one product on the automatic gemv-direct
+    for policy in (2, 0) if count == 1 else (2,):
+        vqdev.device.set_policy(policy)
+        say("gemv-rows own scale", m, count, policy)
+        out, status = _gpu(vqdev, ops, m, n, k, group, 0, count=count)
+        assert status == 0
+        out = out.reshape(count, m, n)
+        for i in sorted({0, count - 1}):
+            _check_rows(out[i], exact)
 
 
 
@@ -774,7 +808,7 @@ ROW_PAIR_SHAPES = [
     (7, 2048, 512, 8, 40),       # 7 rows at g = 8 (cumulative bins, scalar output product)
     (8, 4096, 1024, 32, 40),     # g = 32, a 16-word tile: one-word loads, bins cleared
     (4, 1024, 8192, 16, 64),     # two windows per row: x restaged, FP32 window sums
-    (8, 65536, 512, 8, 1),       # one product whose rows alone fill the chip
+    (8, 65536, 576, 8, 1),       # one product whose rows alone fill the chip
 ]
 
 
@@ -809,13 +843,16 @@ def test_gemv_row_pairs_not_taken_where_rows_cannot_be_instances(vqdev):
     assert vqdev.path_name((2, 4, 4096, 520, 8, 16, 0, 0), count=64) == "gemv-rows"
     assert vqdev.path_name((2, 4, 4096, 512, 16, 16, 0, 0), count=63) == "gemv-rows"
     assert vqdev.path_name((2, 4, 4096, 512, 16, 16, 0, 0), count=64) == "gemv-row-pairs"
-    assert vqdev.path_name((2, 4, 4096, 512, 16, 16, 0, 0)) == "gemv-rows"
+    assert vqdev.path_name((2, 4, 8192, 4160, 16, 16, 0, 0)) == "gemv-rows"
+    # one small product: a single gemv-direct launch
+    assert vqdev.path_name((2, 4, 4096, 512, 16, 16, 0, 0)) == "gemv-direct"
 
 # ---- status word on the reordered paths ----------------------------------------
 # path, m, n, k, group, flags: shapes each path takes
 STATUS_PATHS = [("gemv-direct", 1, 512, 512, 16, 0), ("gemv-pairs", 1, 8192, 4160, 16, 0),
-                ("gemv-rows", 4, 512, 512, 16, 0),
-                ("gemv-rows", 7, 384, 1024, 8, 1), ("row-bins", 128, 512, 256, 16, 0),
+                ("gemv-direct", 4, 512, 512, 16, 0), ("gemv-direct", 7, 384, 1024, 8, 1),
+                ("gemv-rows", 4, 8192, 4160, 16, 0),
+                ("gemv-rows", 7, 8192, 4160, 8, 1), ("row-bins", 128, 512, 256, 16, 0),
                 ("gram-mfma", 64, 96, 1024, 16, 2)]
 
 

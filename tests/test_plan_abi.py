@@ -269,7 +269,9 @@ def _path(lib, entry, words):
     ((2, 1, 4096, 4096, 16, 16, 0, 0), "gemv-direct"),        # one weight of 2^24 values
     ((2, 1, 8192, 8192, 16, 16, 0, 0), "gemv-pairs"),         # past 2^25 values: pair bins
     ((2, 1, 4096, 4096, 16, 16, 1, 0), "gemv-direct"),        # m = 1: A's layout is moot
-    ((2, 8, 4096, 4096, 16, 16, 1, 0), "gemv-rows"),
+    ((2, 8, 4096, 4096, 16, 16, 1, 0), "gemv-direct"),        # up to 8 rows, A either way
+    ((2, 8, 8192, 8192, 16, 16, 1, 0), "gemv-rows"),
+    ((2, 9, 4096, 4096, 16, 16, 0, 0), "gemv-rows"),          # past 8 rows
     ((2, 32, 4096, 4096, 16, 16, 0, 0), "gemv-rows"),          # chunks of 8 rows
     ((2, 32, 512, 512, 16, 16, 0, 0), "general"),              # small weight: bit-exact kernel
     ((2, 2048, 14336, 4096, 32, 16, 0, 0), "row-bins"),
@@ -287,6 +289,7 @@ def test_kernel_path_choice(lib, words, path):
     ((2, 1, 4096, 4096, 16, 16, 0, 0), "gemv-direct"),
     ((2, 1, 8192, 8192, 16, 16, 0, 0), "gemv-pairs"),
     ((2, 19, 2048, 3072, 8, 16, 0, 0), "gemv-rows"),
+    ((2, 5, 2048, 3000, 8, 16, 1, 0), "gemv-direct"),         # ragged k, x stored k x m
     ((2, 128, 768, 512, 8, 16, 0, 0), "row-bins"),            # dense A: group 8 admitted
     ((2, 2048, 4096, 14336, 32, 16, 2, 0), "general"),         # no Gram path for dense A
     ((2, 9, 200, 64, 16, 16, 1, 0), "general")])

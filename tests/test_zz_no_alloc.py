@@ -53,7 +53,8 @@ def _call(vqdev, entry, words, arrays, out_bytes):
 PAIRS = [
     [(1, 8192, 8192, 16, 0, "gemv-pairs"), (1, 8192, 4160, 16, 0, "gemv-pairs")],
     [(1, 4096, 4096, 16, 0, "gemv-direct"), (1, 2048, 1024, 16, 0, "gemv-direct")],
-    [(8, 4096, 4096, 16, 0, "gemv-rows"), (3, 1024, 2048, 8, 0, "gemv-rows")],
+    [(8, 4096, 4096, 16, 0, "gemv-direct"), (3, 1024, 2048, 8, 1, "gemv-direct")],
+    [(8, 4096, 8320, 16, 0, "gemv-rows"), (3, 4096, 8320, 8, 0, "gemv-rows")],
     [(24, 2048, 8192, 16, 0, "gemv-rows"), (12, 1024, 4096, 16, 1, "gemv-rows")],
     [(256, 4096, 4096, 32, 0, "row-bins"), (64, 1024, 1024, 16, 0, "row-bins")],
 ]
