@@ -587,8 +587,7 @@ def main(argv=None) -> int:
         hstep = None
         if not args.no_extra:
             for m in (4, 8):
-                r = bench_gemv(device, dev, args.items, max(3, args.steps // 2), 1, m=m,
-                               single=False)
+                r = bench_gemv(device, dev, args.items, max(3, args.steps // 2), 1, m=m)
                 wide[m] = r
             c5 = bench_config5(device, dev, max(3, args.steps // 4), 1)
             hstep = bench_harness(device, dev)
@@ -648,7 +647,11 @@ def main(argv=None) -> int:
     for m, r in wide.items():
         extra[f"gemv_m{m}"] = {"workload": f"config 3 at M={m}, same cache-cold batch",
                                "gbs": tidy(r["gbs"]), "hbm_frac": tidy(r["gbs"] / HBM_PEAK_GBS),
-                               "path": r["path"], "max_rel_vs_oracle": tidy(r["max_rel"])}
+                               "path": r["path"], "max_rel_vs_oracle": tidy(r["max_rel"]),
+                               "single_matrix_us": tidy(r["single_ms"] * 1e3),
+                               "single_matrix_path": r["single_path"],
+                               "single_matrix_max_rel": tidy(r["single_err"]),
+                               "single_dense_x": tidy(r["dense"])}
     if c5:
         extra["config5"] = {"workload": "config 5: 8192x8192 row-normalised N(0,1) weight, "
                                         "group 8; N(0,1e-3) gradient",
