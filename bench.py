@@ -85,9 +85,10 @@ def timed(device, fn, steps, warmup):
     return ms / steps
 
 
-def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
+def bench_gemv(device, dev, items, steps, warmup, m=1, single=True, flags=0):
     """Config 3 at activation height m: one batched launch over `items`
-    relabelled 4096x4096 g16 weights, HIP-event timed on the library stream."""
+    relabelled 4096x4096 g16 weights, HIP-event timed on the library stream.
+    flags bit 0: the activations are stored 4096 x m (A transposed)."""
     from alelyon_compute_kit import vq
     from oracle.vq4_numpy import ShaderOracle, max_rel
     rng = np.random.default_rng(3)
@@ -95,7 +96,8 @@ def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
     w = (rng.standard_normal((4096, 4096)) * 0.02).astype(np.float32)
     w_img = dev.encode(w, vq.fit_codebook(w, group=16), group=16)
     x = rng.standard_normal((m, 4096)).astype(np.float32)
-    x_img = dev.encode(x, vq.fit_codebook(x, group=16), group=16)
+    xs = np.ascontiguousarray(x.T) if flags & 1 else x     # as A is stored
+    x_img = dev.encode(xs, vq.fit_codebook(xs, group=16), group=16)
     log(f"building {items} relabelled weights")
     codes, books = relabelled_items(w_img.codes, w_img.codebook, items, 4)
     xa = np.tile(x_img.codes, items)
@@ -106,7 +108,7 @@ def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
     out = device.buffer(items * m * 4096 * 4)
     status = device.buffer(4)
     status.upload(np.zeros(1, np.uint32))
-    words = (2, m, 4096, 4096, 16, 16, 0, 0)
+    words = (2, m, 4096, 4096, 16, 16, flags, 0)
     path = dev.path_name(words, count=items)
     single_ms = single_path = y_single = None
     dense = None
@@ -115,7 +117,7 @@ def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
             dev.run(words, bufs, out, status, count=items)
         log(f"timing {steps} launches of {items} items, m={m}, path {path}")
         ms = timed(device, launch, steps, warmup)
-        flags = int(status.download(np.uint32)[0])
+        status_word = int(status.download(np.uint32)[0])
         y = out.download(np.float32).reshape(items, m, 4096)
         if single:
             # single-matrix latency (resident, cache-warm): one ack_vq of item 0
@@ -128,23 +130,24 @@ def bench_gemv(device, dev, items, steps, warmup, m=1, single=True):
             single_path = dev.path_name(words)
             y_single = s_out.download(np.float32).reshape(m, 4096)
             # the dense-activation product on the same weight: x as float32
-            d_x = device.buffer(x.nbytes)
-            d_x.upload(x)
+            d_x = device.buffer(xs.nbytes)
+            d_x.upload(xs)
             dense_ms = timed(device, lambda: dev.run_dense(words, d_x, s_bufs[2], s_bufs[3],
                                                            s_out, status), 50, 5)
             dense = {"single_us": dense_ms * 1e3, "path": dev.dense_path_name(words),
                      "max_rel_vs_float64": None}
             y_dense = s_out.download(np.float32).reshape(m, 4096)
+            status_word |= int(status.download(np.uint32)[0])   # the single products' bits
             for b in s_bufs + [s_out, d_x]:
                 b.free()
     finally:
         for b in bufs + [out, status]:
             b.free()
-    if flags:
-        raise SystemExit(f"status word {flags} after the timed GEMV launches (m={m})")
+    if status_word:
+        raise SystemExit(f"status word {status_word} after the GEMV launches (m={m})")
     oracle = ShaderOracle()
     ref, _ = oracle.matmul(x_img.codes, x_img.codebook, w_img.codes, w_img.codebook,
-                           m, 4096, 4096, 16, 0)
+                           m, 4096, 4096, 16, flags)
     err = max(max_rel(y[0], ref), float(np.max(np.abs(y - y[0]))) / float(np.max(np.abs(ref))))
     if dense is not None:
         exact = x.astype(np.float64) @ w_img.decode().astype(np.float64)
@@ -188,7 +191,9 @@ def bench_sustained(device, dev, items, launches):
     return ms
 
 
-def bench_prefill(device, dev, steps, warmup):
+def bench_prefill(device, dev, steps, warmup, policy=0, dense=True):
+    """Config 4 forward and backward (and the dense-X forward), every output
+    checked against a float64 product. policy 1 forces the general kernel."""
     from alelyon_compute_kit import vq
     rng = np.random.default_rng(4)
     m, k, n = 2048, 4096, 14336
@@ -213,11 +218,13 @@ def bench_prefill(device, dev, steps, warmup):
         status.upload(np.zeros(1, np.uint32))
         words = (2, m, nn, kk, 32, 16, flags, 0)
         try:
-            log(f"timing {name}: {m}x{nn}x{kk}, path {dev.path_name(words)}")
+            device.set_policy(policy)
+            log(f"timing {name}: {m}x{nn}x{kk}, path {dev.path_name(words)}, policy {policy}")
             ms = timed(device, lambda: dev.run(words, bufs, out, status), steps, warmup)
             flags_out = int(status.download(np.uint32)[0])
             y = out.download(np.float32).reshape(m, nn)
         finally:
+            device.set_policy(0)
             for b in bufs + [out, status]:
                 b.free()
         if flags_out:
@@ -228,7 +235,7 @@ def bench_prefill(device, dev, steps, warmup):
                                                                          else wd.T))
         del wd
         flop = 2.0 * m * nn * kk
-        path = dev.path_name(words)
+        path = "general" if policy == 1 else dev.path_name(words)
         entry = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "path": path,
                  "max_rel": err, "max_row_rel": row_err}
         # what the kernel actually executes, against that work's own peak
@@ -246,6 +253,8 @@ def bench_prefill(device, dev, steps, warmup):
                                  "peak": FP16_MFMA_PEAK_TFLOPS,
                                  "frac": ops / (ms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS}
         results[name] = entry
+    if not dense:
+        return results
     # the forward product with X handed over dense (no activation encode)
     words = (2, m, n, k, 32, 16, 0, 0)
     bufs = [device.buffer(arr.nbytes) for arr in (x, w_img.codes, w_img.codebook)]
@@ -270,6 +279,26 @@ def bench_prefill(device, dev, steps, warmup):
     results["forward_dense_x"] = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "path": path,
                                   "max_rel": err, "max_row_rel": row_err}
     return results
+
+
+def other_paths(items, steps, warmup):
+    """The kernels no headline workload takes, on the headline shapes:
+    k_gemv_rows (config 3 batch at M = 4 and 8 with A stored 4096 x M, where
+    rows cannot run as pair-bin instances) and k_matmul_general (config 4
+    forward and backward under policy 1)."""
+    from alelyon_compute_kit import ack, vq
+    out = {}
+    with ack.Device() as device:
+        dev = vq.VQDevice(device)
+        for m in (4, 8):
+            r = bench_gemv(device, dev, items, steps, warmup, m=m, single=False, flags=1)
+            out[f"gemv_m{m}_a_transposed"] = {
+                "workload": f"config 3 at M={m}, A stored 4096 x {m}, same cache-cold batch",
+                "ms": r["ms"], "gbs": r["gbs"], "hbm_frac": r["gbs"] / HBM_PEAK_GBS,
+                "path": r["path"], "max_rel_vs_oracle": r["max_rel"]}
+        out["config4_general"] = bench_prefill(device, dev, max(2, steps // 4), 1, policy=1,
+                                               dense=False)
+    return out
 
 
 def _all_rows_error(y: np.ndarray, ref: np.ndarray):
@@ -559,6 +588,10 @@ def main(argv=None) -> int:
     parser.add_argument("--no-extra", action="store_true",
                         help="skip the secondary lines (config 3 at m=4/8, config 5)")
     parser.add_argument("--no-cpu", action="store_true")
+    parser.add_argument("--other-paths", action="store_true",
+                        help="only time the kernels the headline workloads do not take and exit: "
+                             "config 3 at M=4 and 8 with A stored 4096 x M (k_gemv_rows) and "
+                             "config 4 on the general kernel (the shader's order), one JSON line")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run the HBM calibration and exit: a 512 MiB device-to-"
                              "device copy (the reference for scaling FETCH_SIZE/WRITE_SIZE "
@@ -574,6 +607,9 @@ def main(argv=None) -> int:
         return 2
     if args.copy_calibration:
         print(json.dumps(hbm_calibration()))
+        return 0
+    if args.other_paths:
+        print(json.dumps(other_paths(args.items, args.steps, args.warmup)))
         return 0
     from alelyon_compute_kit import ack, vq
     with ack.Device() as device:
