@@ -35,7 +35,7 @@ HIP_FLAGS = [f"--offload-arch={ARCH}", "-x", "hip", "-fhip-fp32-correctly-rounde
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 HIP_SOURCES = ["vq4_codec.hip", "vq4_matmul.hip", "vq4_rowbins.hip", "vq4_gram.hip", "vq4_fit.hip",
-               "vq4_direct.hip", "hbm_probe.hip", "abi.cpp"]
+               "vq4_direct.hip", "vq4_onehot.hip", "hbm_probe.hip", "abi.cpp"]
 CXX_SOURCES = ["host_fit.cpp"]
 
 

@@ -38,6 +38,8 @@ enum class MatmulPath : int {
                      // a GemvPairs instance, the rows of one product on one XCD
   GemvDirect = 7,    // m <= 8, few weights (kDirectMaxWeights): decode and FMA per output,
                      // split k reduced by the last block of each tile, one launch
+  OneHotMfma = 8,    // m >= kOneHotMinRows, packed A along k, B along n: A's book rows x
+                     // one-hot of B's codes on fp16 MFMA, then the 16-term codebook product
 };
 
 const char* matmul_path_name(MatmulPath p);
@@ -64,6 +66,15 @@ size_t direct_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t group
                               uint32_t count);
 hipError_t launch_direct(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                          uint32_t group, uint32_t flags, bool dense, void* workspace);
+
+// onehot-mfma (vq4_onehot.hip): large packed products, A grouped along k and
+// B along n (g 16 or 32); below kOneHotMinRows rows of A the row bins serve.
+constexpr uint32_t kOneHotMinRows = 256;
+bool onehot_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                    uint32_t count);
+size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group);
+hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                         uint32_t group, void* workspace);
 
 bool rowbins_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
 bool rowbins_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);

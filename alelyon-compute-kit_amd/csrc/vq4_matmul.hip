@@ -1831,6 +1831,7 @@ const char* matmul_path_name(MatmulPath p) {
     case MatmulPath::GemvTable: return "gemv-table";
     case MatmulPath::GramMfma: return "gram-mfma";
     case MatmulPath::RowBins: return "row-bins";
+    case MatmulPath::OneHotMfma: return "onehot-mfma";
     case MatmulPath::GemvDirect: return "gemv-direct";
   }
   return "unknown";
@@ -1839,6 +1840,7 @@ const char* matmul_path_name(MatmulPath p) {
 MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                               uint32_t count, uint32_t policy) {
   if (policy == 1) return MatmulPath::General;
+  if (onehot_applies(m, n, k, group, flags, count)) return MatmulPath::OneHotMfma;
   if (count == 1 && rowbins_applies(m, n, k, group, flags)) return MatmulPath::RowBins;
   if (gram_applies(m, n, k, group, flags, policy == 2)) return MatmulPath::GramMfma;
   if (policy == 0 && direct_applies(m, n, k, group, flags, count)) return MatmulPath::GemvDirect;
@@ -1851,6 +1853,7 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
 size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                               uint32_t flags, uint32_t count) {
   if (p == MatmulPath::RowBins) return rowbins_workspace_bytes(n, k, group);
+  if (p == MatmulPath::OneHotMfma) return onehot_workspace_bytes(n, k, group);
   if (p == MatmulPath::GemvDirect) return direct_workspace_bytes(m, n, k, group, count);
   if (p != MatmulPath::GemvRows && p != MatmulPath::GemvPairs) return 0;
   uint32_t ks, splits;
@@ -1877,6 +1880,7 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
                          size_t workspace_bytes) {
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins(s, o, m, n, k, group, workspace);
+  if (path == MatmulPath::OneHotMfma) return launch_onehot(s, o, m, n, k, group, workspace);
   if (path == MatmulPath::GemvDirect)
     return launch_direct(s, o, m, n, k, group, flags, false, workspace);
   if (path == MatmulPath::GramMfma) return launch_gram(s, o, m, n, k, group);

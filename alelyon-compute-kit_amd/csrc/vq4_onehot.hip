@@ -1,0 +1,338 @@
+// Large packed products with B grouped along n, on gfx950 matrix cores:
+// "onehot-mfma".
+//
+// For C = A . B with B stored (k, n), its groups along n, and A row-major
+// with its groups along k (op 2, flags 0 of
+// src/alelyon_compute_kit/_kit/kernels/vq4.comp:165-176), output group j of
+// row r is
+//   y[r][G j + t] = sum_e S[r][(j, e)] C_B[e][t],
+//   S[r][(j, e)]  = sum_kk A[r][kk] [b(kk, j) = e],
+// so S = A . P with P[kk][(j, e)] the one-hot of B's code: a GEMM of inner
+// dimension k and 16 n / G columns. It runs on v_mfma_f32_32x32x16_bf16:
+//  - P is exact in bf16. Each lane builds its fragment (8 inner indices of one
+//    (j, e) column) from one word of B's "nibble columns" (the 8 codes of group
+//    j at 8 consecutive inner indices, written by a pre-pass) with a few
+//    integer operations.
+//  - A's values are rows of its book, so A's fragment (8 inner indices of one
+//    row, inside one group) is read from an LDS table of the book scaled by a
+//    power of two (largest magnitude below 2^15) and split into three bf16
+//    terms hi + mid + lo: 24 significant bits with FP32's exponent range, so
+//    every FP32 entry is carried exactly, however far below the largest (fp16
+//    terms would stop at fp16's subnormal floor). Each 16-step of k costs three
+//    MFMAs per 32 x 32 block and the accumulation is FP32.
+// Then the 16-term products with C_B run on the VALU from S staged in LDS.
+// Neither operand is decoded to memory.
+//
+// The sum order differs from the shader's sequential one; results agree to
+// FP32 rounding (FP32 sums of exact A values, then 16 FP32 multiply-adds).
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "kernels.hpp"
+
+namespace ackvq {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kOHThreads = 256;  // 4 waves, 2 x 2 over 256 rows x 128 S columns
+constexpr uint32_t kOHRows = 256;     // rows of A per block
+constexpr int kOHX = 4;               // 32-row blocks per wave
+constexpr int kOHTerms = 3;           // bf16 terms of each scaled A value
+
+__device__ __forceinline__ bool finite_f32(float x) { return fabsf(x) <= FLT_MAX; }
+
+// Nibbles of vectors v .. v+7 (vector v in bits 0..3). Both loads are
+// unconditional: the word index is clamped to the array (a clamped word only
+// supplies nibbles past the last vector, which the caller never uses).
+__device__ __forceinline__ uint32_t nibbles8(const uint32_t* codes, uint64_t v, uint64_t last) {
+  const uint64_t w = v >> 3;
+  const uint32_t lo = codes[w < last ? w : last];
+  const uint32_t hi = codes[w + 1 < last ? w + 1 : last];
+  return __builtin_amdgcn_alignbit(hi, lo, uint32_t(v & 7u) * 4u);
+}
+
+// One-hot fragment from a nibble-column word w (nibble i: B's code at inner
+// index kk0 + i): bf16 element i is 1.0 where nibble i equals the lane's code
+// c; ee = c * 0x11111111.
+__device__ __forceinline__ bf16x8 one_hot_column(uint32_t w, uint32_t ee) {
+  const uint32_t z = w ^ ee;  // nibble i is zero where it matches
+  uint32_t t = z | (z >> 1);
+  t |= t >> 2;                                          // bit 4i: nibble i nonzero
+  const uint32_t g = (t & 0x11111111u) ^ 0x11111111u;   // bit 4i: nibble i matches
+  const uint32_t fe = g & 0x01010101u, fo = (g >> 4) & 0x01010101u;
+  const uint32_t FE = (fe << 8) - fe, FO = (fo << 8) - fo;  // 0xFF bytes: even, odd nibbles
+  // dword d: element 0 from nibble 2d (byte d of FE in both of its bytes),
+  // element 1 from nibble 2d + 1 (of FO); bf16 1.0 is 0x3F80
+  u32x4 v;
+  v[0] = __builtin_amdgcn_perm(FO, FE, 0x04040000u) & 0x3F803F80u;
+  v[1] = __builtin_amdgcn_perm(FO, FE, 0x05050101u) & 0x3F803F80u;
+  v[2] = __builtin_amdgcn_perm(FO, FE, 0x06060202u) & 0x3F803F80u;
+  v[3] = __builtin_amdgcn_perm(FO, FE, 0x07070303u) & 0x3F803F80u;
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Nibble columns of B: nc[j * (k / 8) + kk8] holds the codes of group j at
+// inner indices 8 kk8 .. 8 kk8 + 7 (nibble i: index 8 kk8 + i). A block reads
+// 64 rows of 32 word columns (coalesced) into LDS and writes the 256 groups'
+// 8 words each. Requires k % 8 == 0.
+constexpr uint32_t kNCRows = 64, kNCCols = 32;
+__global__ __launch_bounds__(256) void k_nibble_columns(const uint32_t* __restrict__ codes,
+                                                        uint32_t* __restrict__ nc, uint32_t k,
+                                                        uint32_t rw) {
+  __shared__ uint32_t tile[kNCRows][kNCCols + 1];
+  const uint32_t q0 = blockIdx.x * kNCCols, k0 = blockIdx.y * kNCRows;
+  const uint32_t tid = threadIdx.x;
+  for (uint32_t i = tid; i < kNCRows * kNCCols; i += 256) {
+    const uint32_t r = i / kNCCols, c = i % kNCCols;
+    tile[r][c] = (k0 + r < k && q0 + c < rw) ? codes[uint64_t(k0 + r) * rw + q0 + c] : 0u;
+  }
+  __syncthreads();
+  const uint32_t c = tid / 8, p = tid % 8;  // word column q0 + c, nibble p: group 8 (q0 + c) + p
+  if (q0 + c >= rw) return;
+  const uint32_t k8 = k / 8;
+  uint32_t* dst = nc + uint64_t(8 * (q0 + c) + p) * k8 + k0 / 8;
+#pragma unroll
+  for (uint32_t r8 = 0; r8 < kNCRows / 8; ++r8) {
+    if (k0 / 8 + r8 >= k8) break;
+    uint32_t w = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i)
+      w |= __builtin_amdgcn_ubfe(tile[8 * r8 + i][c], 4 * p, 4) << (4 * i);
+    dst[r8] = w;
+  }
+}
+
+// grid: (n / (8 G) word columns of B, ceil(m / 256)). A block covers 256 rows
+// of A and the 8 groups of one word column of B (128 S columns); wave (wy, wx)
+// takes rows 128 wy .. +127 and groups 4 wx .. 4 wx + 3. Requires k % 16 == 0,
+// k % G == 0 and n % (8 G) == 0; one instance.
+template <int G>
+__global__ __launch_bounds__(kOHThreads, 2) void k_onehot_mfma(Operands o, uint32_t m, uint32_t n,
+                                                              uint32_t k,
+                                                              const uint32_t* __restrict__ nc) {
+  static_assert(G == 16 || G == 32, "a 16-step of k lies in one group of A");
+  // A's table: [term][8-entry chunk of the group][code][8]; code 16 is empty
+  // (rows past m). The 16 lanes of a read phase read one chunk, so distinct
+  // codes land in distinct banks.
+  __shared__ __align__(16) __bf16 tabA[kOHTerms][G / 8][17][8];
+  __shared__ __align__(16) float sS[4][64][64];  // one wave's S, 64 rows at a time
+  __shared__ float sbook[16 * G];
+  __shared__ float sred[4];
+  const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const uint32_t i32 = lane % 32, h = lane / 32;
+  const uint32_t wy = wave / 2, wx = wave % 2;
+  const uint32_t q = blockIdx.x;
+  const uint32_t row0 = blockIdx.y * kOHRows + 128 * wy;
+  const uint32_t J = k / G;
+  const uint64_t a_last = (uint64_t(m) * J + 7) / 8 - 1;
+  const uint32_t* a_codes = static_cast<const uint32_t*>(o.in[0]);
+  const float* a_book = static_cast<const float*>(o.in[1]);
+  const float* b_book = static_cast<const float*>(o.in[3]);
+  float* out = static_cast<float*>(o.out);
+  // Rows past m read the last row's codes and use the empty table entry.
+  uint64_t av[kOHX];
+  bool dead[kOHX];
+#pragma unroll
+  for (int x = 0; x < kOHX; ++x) {
+    const uint32_t r = row0 + 32 * x + i32;
+    av[x] = uint64_t(r < m ? r : m - 1) * J;
+    dead[x] = r >= m;
+  }
+  // The lane's S columns: code i32 % 16 of groups 8 q + 4 wx + 2 y + i32 / 16
+  // (y = 0, 1), and its nibble-column words (K entries 8 h .. 8 h + 7).
+  const uint32_t ee = (i32 % 16) * 0x11111111u;
+  const uint32_t k8 = k / 8;
+  const uint32_t* nc0 = nc + uint64_t(8 * q + 4 * wx + i32 / 16) * k8 + h;
+  const uint32_t* nc1 = nc0 + 2 * uint64_t(k8);
+
+  // ---- tables: B's book as is; A's scaled below 2^15 and split into three
+  // bf16 terms (each the bf16 rounding of what the previous ones leave; the
+  // differences are exact in FP32, and the last one holds the rest exactly)
+  bool bad = false;
+  float amax = 0.0f;
+  for (uint32_t i = tid; i < 16 * G; i += kOHThreads) {
+    const float a = a_book[i], b = b_book[i];
+    sbook[i] = b;
+    if (blockIdx.x == 0 && blockIdx.y == 0) bad |= !finite_f32(a) || !finite_f32(b);
+    amax = fmaxf(amax, finite_f32(a) ? fabsf(a) : 0.0f);
+  }
+  for (int off = 1; off < 64; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  if (lane == 0) sred[wave] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
+  int shift = 0;
+  if (amax > 0.0f) {
+    int ex;
+    frexpf(amax, &ex);  // amax < 2^ex
+    shift = 15 - ex;
+    shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
+  }
+  for (uint32_t i = tid; i < 17 * G; i += kOHThreads) {
+    const float scaled = i < 16 * G ? ldexpf(a_book[i], shift) : 0.0f;
+    const __bf16 hi = __bf16(scaled);
+    const float r1 = scaled - float(hi);
+    const __bf16 mid = __bf16(r1);
+    tabA[0][(i % G) / 8][i / G][i % 8] = hi;
+    tabA[1][(i % G) / 8][i / G][i % 8] = mid;
+    tabA[2][(i % G) / 8][i / G][i % 8] = __bf16(r1 - float(mid));
+  }
+  const float unscale = ldexpf(1.0f, -shift);
+  __syncthreads();
+
+  // ---- main loop: passes over 8 groups of A (8 G inner indices, G / 2 steps
+  // of 16), A's code words one pass ahead, B's words two steps ahead in a
+  // ring of four, and term t of the next step's A fragments read as soon as
+  // this step's term-t MFMAs are issued, into the same registers
+  f32x16 acc[kOHX][2];
+#pragma unroll
+  for (int x = 0; x < kOHX; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = (f32x16)0.0f;
+  constexpr uint32_t kSteps = G / 2;
+  constexpr uint32_t kChunk = 17 * 16;          // bytes of one chunk's table
+  constexpr uint32_t kTerm = (G / 8) * kChunk;  // bytes of one term's table
+  static_assert(kSteps % 4 == 0, "the B ring position repeats every pass");
+  const char* tab_lane = reinterpret_cast<const char*>(&tabA[0][0][0][0]) + h * kChunk;
+  uint32_t aw[kOHX], an[kOHX];
+#pragma unroll
+  for (int x = 0; x < kOHX; ++x) an[x] = nibbles8(a_codes, av[x], a_last);
+  uint32_t wb[4][2];
+  wb[0][0] = nc0[0];
+  wb[0][1] = nc1[0];
+  if (16 < k) {
+    wb[1][0] = nc0[2];
+    wb[1][1] = nc1[2];
+  }
+  // the table row of step s_ (both halves of the wave are in one group; the
+  // lane's chunk is c8 + h)
+  auto a_ptr = [&](const uint32_t (&wd)[kOHX], uint32_t s_, int x) __attribute__((always_inline)) {
+    const uint32_t g_in = (16 * s_) / G, c8 = (16 * s_ % G) / 8;
+    const uint32_t code = dead[x] ? 16u : __builtin_amdgcn_ubfe(wd[x], 4 * g_in, 4);
+    return tab_lane + c8 * kChunk + code * 16;
+  };
+  bf16x8 af[kOHX][kOHTerms];
+#pragma unroll
+  for (int x = 0; x < kOHX; ++x) {
+    const char* pa = a_ptr(an, 0, x);
+#pragma unroll
+    for (int t = 0; t < kOHTerms; ++t) af[x][t] = *reinterpret_cast<const bf16x8*>(pa + t * kTerm);
+  }
+  for (uint32_t p0 = 0; p0 < k; p0 += 8 * G) {
+#pragma unroll
+    for (int x = 0; x < kOHX; ++x) {
+      aw[x] = an[x];
+      if (p0 + 8 * G < k) an[x] = nibbles8(a_codes, av[x] + (p0 + 8 * G) / G, a_last);
+    }
+#pragma unroll
+    for (uint32_t s = 0; s < kSteps; ++s) {
+      const uint32_t kk0 = p0 + 16 * s;
+      if (kk0 >= k) break;
+      if (kk0 + 32 < k) {
+        wb[(s + 2) % 4][0] = nc0[(kk0 + 32) / 8];
+        wb[(s + 2) % 4][1] = nc1[(kk0 + 32) / 8];
+      }
+      const bool more = kk0 + 16 < k;
+      const char* pn[kOHX];
+#pragma unroll
+      for (int x = 0; x < kOHX; ++x) pn[x] = s + 1 < kSteps ? a_ptr(aw, s + 1, x) : a_ptr(an, 0, x);
+      bf16x8 bf[2];
+      bf[0] = one_hot_column(wb[s % 4][0], ee);
+      bf[1] = one_hot_column(wb[s % 4][1], ee);
+#pragma unroll
+      for (int t = 0; t < kOHTerms; ++t) {
+#pragma unroll
+        for (int x = 0; x < kOHX; ++x)
+#pragma unroll
+          for (int y = 0; y < 2; ++y)
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[x][t], bf[y], acc[x][y], 0, 0, 0);
+        if (more) {
+#pragma unroll
+          for (int x = 0; x < kOHX; ++x)
+            af[x][t] = *reinterpret_cast<const bf16x8*>(pn[x] + t * kTerm);
+        }
+      }
+    }
+  }
+
+  // ---- S to LDS, 64 rows at a time (lane: column i32, item t holds row
+  // (t % 4) + 4 h + 8 (t / 4) of its 32-row block), then
+  // y[r][G j + t] = sum_e S[r][(j, e)] C_B[e][t], e ascending; a lane's t is
+  // fixed (the row stride 64 is a multiple of G)
+  const uint32_t tc = lane % G;
+  float cb[16];
+#pragma unroll
+  for (int f = 0; f < 16; ++f) cb[f] = sbook[f * G + tc];
+#pragma unroll
+  for (int hv = 0; hv < 2; ++hv) {
+    if (hv) __syncthreads();  // the first half has been read
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+          sS[wave][32 * x + (t % 4) + 4 * h + 8 * (t / 4)][32 * y + i32] =
+              acc[2 * hv + x][y][t] * unscale;
+    __syncthreads();
+    for (uint32_t idx = lane; idx < 64 * 4 * G; idx += 64) {
+      const uint32_t row = idx / (4 * G), jl = (idx % (4 * G)) / G;
+      const uint32_t r = row0 + 64 * hv + row;
+      if (r >= m) break;
+      const float4* sp = reinterpret_cast<const float4*>(&sS[wave][row][16 * jl]);
+      const float4 s0 = sp[0], s1 = sp[1], s2 = sp[2], s3 = sp[3];
+      float y = 0.0f;
+      y = fmaf(s0.x, cb[0], y);
+      y = fmaf(s0.y, cb[1], y);
+      y = fmaf(s0.z, cb[2], y);
+      y = fmaf(s0.w, cb[3], y);
+      y = fmaf(s1.x, cb[4], y);
+      y = fmaf(s1.y, cb[5], y);
+      y = fmaf(s1.z, cb[6], y);
+      y = fmaf(s1.w, cb[7], y);
+      y = fmaf(s2.x, cb[8], y);
+      y = fmaf(s2.y, cb[9], y);
+      y = fmaf(s2.z, cb[10], y);
+      y = fmaf(s2.w, cb[11], y);
+      y = fmaf(s3.x, cb[12], y);
+      y = fmaf(s3.y, cb[13], y);
+      y = fmaf(s3.z, cb[14], y);
+      y = fmaf(s3.w, cb[15], y);
+      out[uint64_t(r) * n + (8 * q + 4 * wx + jl) * G + tc] = y;
+      bad |= !finite_f32(y);
+    }
+  }
+  if (__any(bad) && lane == 0) atomicOr(o.status, 1u);
+}
+
+}  // namespace
+
+bool onehot_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                    uint32_t count) {
+  return count == 1 && flags == 0 && (group == 16 || group == 32) && m >= kOneHotMinRows &&
+         n % (8 * group) == 0 && k % 16 == 0 && k % group == 0;
+}
+
+size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group) {
+  return size_t(n / group) * (k / 8) * 4;
+}
+
+hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                         uint32_t group, void* workspace) {
+  const uint32_t rw = n / (8 * group);
+  uint32_t* nc = static_cast<uint32_t*>(workspace);
+  dim3 ngrid((rw + kNCCols - 1) / kNCCols, (k + kNCRows - 1) / kNCRows);
+  k_nibble_columns<<<ngrid, 256, 0, s>>>(static_cast<const uint32_t*>(o.in[2]), nc, k, rw);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  dim3 grid(rw, (m + kOHRows - 1) / kOHRows);
+  if (group == 16) k_onehot_mfma<16><<<grid, kOHThreads, 0, s>>>(o, m, n, k, nc);
+  else k_onehot_mfma<32><<<grid, kOHThreads, 0, s>>>(o, m, n, k, nc);
+  return hipGetLastError();
+}
+
+}  // namespace ackvq

@@ -244,6 +244,14 @@ def bench_prefill(device, dev, steps, warmup, policy=0, dense=True):
             entry["executed"] = {"what": "FP32 VALU adds", "tops": ops / (ms * 1e-3) / 1e12,
                                  "peak": FP32_VALU_OPS_PEAK_T,
                                  "frac": ops / (ms * 1e-3) / 1e12 / FP32_VALU_OPS_PEAK_T}
+        elif path == "onehot-mfma":
+            # A's book rows (three fp16 terms) times the one-hot of B's codes:
+            # inner dimension kk, 16 nn / 32 S columns
+            ops = 2.0 * m * (16 * nn // 32) * kk * 3
+            entry["executed"] = {"what": "fp16 MFMA flops (3-term A operand, FP32-exact)",
+                                 "tflops": ops / (ms * 1e-3) / 1e12,
+                                 "peak": FP16_MFMA_PEAK_TFLOPS,
+                                 "frac": ops / (ms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS}
         elif path == "gram-mfma":
             # one-hot x Gram GEMM of inner dimension 16 k/g, each Gram entry as
             # three fp16 terms (hi + mid + lo: 33 significant bits)
@@ -679,7 +687,8 @@ def main(argv=None) -> int:
             # kernel is held to the roofline of the work it does execute
             # (*_executed), never to the FP32 matrix peak
             "note": "tflops = 2*M*N*K / time (algorithmic); roofline fractions are of "
-                    "executed work: FP32 VALU adds (row-bins), fp16 MFMA (gram-mfma)"}
+                    "executed work: fp16 MFMA (onehot-mfma, gram-mfma), FP32 VALU adds "
+                    "(row-bins)"}
     for m, r in wide.items():
         extra[f"gemv_m{m}"] = {"workload": f"config 3 at M={m}, same cache-cold batch",
                                "gbs": tidy(r["gbs"]), "hbm_frac": tidy(r["gbs"] / HBM_PEAK_GBS),

@@ -567,7 +567,7 @@ def test_transposed_products_agree_with_float64(vqdev):
 
 
 ROW_BINS_SHAPES = [(64, 256, 64, 16), (100, 512, 96, 32), (130, 2048, 256, 16),
-                   (256, 1024, 512, 32), (333, 768, 1024, 16)]
+                   (255, 1024, 512, 32), (200, 768, 1024, 16)]
 
 
 @pytest.mark.parametrize("m,n,k,group", ROW_BINS_SHAPES)
@@ -587,6 +587,56 @@ def test_row_bins_within_tolerance(vqdev, oracle, m, n, k, group):
     assert o.max_rel(out, _ref64(ops, m, n, k, group, 0)) <= TOL
 
 
+# (m, n, k, group): one 16-step of k, a last pass shorter than 8 groups of A
+# (k not a multiple of 8 g), rows past m in the last block, 1 and 8 word columns
+ONEHOT_SHAPES = [(256, 1024, 512, 32), (333, 768, 1024, 16), (256, 256, 16, 16),
+                 (300, 512, 1040, 16), (1000, 4096, 288, 32), (513, 2048, 4096, 32)]
+
+
+@pytest.mark.parametrize("m,n,k,group", ONEHOT_SHAPES)
+def test_onehot_mfma_within_tolerance(vqdev, oracle, m, n, k, group):
+    """m >= 256 rows of a packed A (groups along k) times B grouped along n:
+    A's book rows (three fp16 terms) times the one-hot of B's codes on fp16
+    MFMA, then the 16-term product with B's book. Within 1e-5 of the oracle
+    and of the float64 product, every row against its own largest output."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(m + n + k + group)
+    words = (2, m, n, k, group, 16, 0, 0)
+    assert vqdev.path_name(words) == "onehot-mfma"
+    say("onehot-mfma", m, n, k, group)
+    ops = _operands(rng, m, n, k, group, 1.0, 0.02)
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0)
+    assert status == 0
+    if m * n * k <= 1 << 28:
+        ref, _ = oracle.matmul(*ops, m, n, k, group, 0)
+        assert o.max_rel(out, ref) <= TOL
+    _check_rows(out, _ref64(ops, m, n, k, group, 0))
+
+
+def test_onehot_mfma_rows_of_very_different_magnitude(vqdev):
+    """A's book holds entries near 1 and near 2^-24: even rows use only the
+    small ones. The book is split after one power-of-two scale, and every
+    entry within 2^-40 of the largest keeps all its bits, so each row keeps
+    the 1e-5 bar against its own largest output."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(77)
+    m, n, k, group = 512, 1024, 1024, 32
+    a_book = rng.standard_normal((16, group)).astype(np.float32)
+    a_book[:8] *= np.float32(2.0 ** -24)
+    idx = rng.integers(8, 16, (m, k // group))
+    idx[0::2] = rng.integers(0, 8, (m // 2, k // group))
+    a_codes = o.pack_indices(idx.reshape(-1))
+    b_codes, b_book = image(rng, k * n, group, 0.02)
+    ops = (a_codes, a_book, b_codes, b_book)
+    assert vqdev.path_name((2, m, n, k, group, 16, 0, 0)) == "onehot-mfma"
+    say("onehot-mfma magnitudes")
+    out, status = _gpu(vqdev, ops, m, n, k, group, 0)
+    assert status == 0
+    exact = _ref64(ops, m, n, k, group, 0)
+    assert np.abs(exact[0]).max() < 1e-5 < np.abs(exact[1]).max()
+    _check_rows(out, exact)
+
+
 def test_config4_forward_against_float64(vqdev):
     """BASELINE config 4 forward at full size: X 2048x4096 . W 4096x14336 at
     group 32; every output against the float64 product of the decoded
@@ -598,7 +648,7 @@ def test_config4_forward_against_float64(vqdev):
     w_img = vqdev.encode(w, vq.fit_codebook(w, group=32), group=32)
     x = rng.standard_normal((2048, 4096)).astype(np.float32)
     x_img = vqdev.encode(x, vq.fit_codebook(x, group=32), group=32)
-    assert vqdev.path_name((2, 2048, 14336, 4096, 32, 16, 0, 0)) == "row-bins"
+    assert vqdev.path_name((2, 2048, 14336, 4096, 32, 16, 0, 0)) == "onehot-mfma"
     say("config4 forward")
     y = vqdev.matmul(x_img, w_img)
     ref = x_img.decode().astype(np.float64) @ w_img.decode().astype(np.float64)
@@ -853,6 +903,7 @@ STATUS_PATHS = [("gemv-direct", 1, 512, 512, 16, 0), ("gemv-pairs", 1, 8192, 416
                 ("gemv-direct", 4, 512, 512, 16, 0), ("gemv-direct", 7, 384, 1024, 8, 1),
                 ("gemv-rows", 4, 8192, 4160, 16, 0),
                 ("gemv-rows", 7, 8192, 4160, 8, 1), ("row-bins", 128, 512, 256, 16, 0),
+                ("onehot-mfma", 256, 512, 256, 16, 0), ("onehot-mfma", 300, 1024, 288, 32, 0),
                 ("gram-mfma", 64, 96, 1024, 16, 2)]
 
 

@@ -56,7 +56,8 @@ PAIRS = [
     [(8, 4096, 4096, 16, 0, "gemv-direct"), (3, 1024, 2048, 8, 1, "gemv-direct")],
     [(8, 4096, 8320, 16, 0, "gemv-rows"), (3, 4096, 8320, 8, 0, "gemv-rows")],
     [(24, 2048, 8192, 16, 0, "gemv-rows"), (12, 1024, 4096, 16, 1, "gemv-rows")],
-    [(256, 4096, 4096, 32, 0, "row-bins"), (64, 1024, 1024, 16, 0, "row-bins")],
+    [(128, 4096, 4096, 32, 0, "row-bins"), (64, 1024, 1024, 16, 0, "row-bins")],
+    [(512, 4096, 4096, 32, 0, "onehot-mfma"), (256, 1024, 1024, 16, 0, "onehot-mfma")],
 ]
 
 
