@@ -9,12 +9,12 @@
 //           = sum_j Gram[a(r,j)][b(c,j)],   Gram = C_A . C_B^T  (16 x 16).
 // That is a GEMM with inner dimension 16 * k / G:
 //   C = P . Q,  P[r][(j,e)] = [a(r,j) == e],  Q[(j,e)][c] = Gram[e][b(c,j)],
-// and it runs on v_mfma_f32_32x32x16_f16 with one 16-step of K per group j:
-// P is a one-hot row (exact in fp16), and Q is Gram scaled by a power of two
-// and split into three fp16 terms hi + mid + lo (33 significant bits: every
-// FP32 Gram entry within 2^-40 of the largest one is carried exactly, the
-// rest to 2^-40 of the largest), so each j costs three MFMAs per 32 x 32
-// output block and the accumulation is FP32. Neither operand is decoded:
+// and it runs on v_mfma_f32_32x32x16_bf16 with one 16-step of K per group j:
+// P is a one-hot row (exact in bf16), and Q is Gram scaled by a power of two
+// and split into three bf16 terms hi + mid + lo (24 significant bits with
+// FP32's exponent range: every FP32 Gram entry is carried exactly, however
+// far below the largest), so each j costs three MFMAs per 32 x 32 output
+// block and the accumulation is FP32. Neither operand is decoded:
 // P's fragments are read from a 768-byte LDS table of the one-hot rows
 // addressed by A's nibble, Q's from a 1.5 KiB LDS table addressed by B's.
 //
@@ -30,7 +30,7 @@
 namespace ackvq {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -57,18 +57,18 @@ __device__ __forceinline__ uint32_t nibbles8(const uint32_t* codes, uint64_t v, 
 
 // One-hot MFMA A operand: this lane holds K entries 8h .. 8h+7 of its row;
 // d = code - 8h selects the entry set to 1.0 (none when d is outside 0..7).
-__device__ __forceinline__ half8 one_hot(uint32_t d) {
-  const uint32_t one = (d & 1u) ? 0x3C000000u : 0x00003C00u;  // fp16 1.0 in the low or high half
+__device__ __forceinline__ bf16x8 one_hot(uint32_t d) {
+  const uint32_t one = (d & 1u) ? 0x3F800000u : 0x00003F80u;  // bf16 1.0 in the low or high half
   const uint32_t pair = d >> 1;
   u32x4 v;
   v.x = pair == 0 ? one : 0u;
   v.y = pair == 1 ? one : 0u;
   v.z = pair == 2 ? one : 0u;
   v.w = pair == 3 ? one : 0u;
-  return __builtin_bit_cast(half8, v);
+  return __builtin_bit_cast(bf16x8, v);
 }
 
-constexpr int kGramTerms = 3;  // fp16 terms of each scaled Gram entry
+constexpr int kGramTerms = 3;  // bf16 terms of each scaled Gram entry
 
 struct GramTile {
   f32x16 acc[2][2];
@@ -81,16 +81,16 @@ struct GramTile {
 __device__ __forceinline__ void gram_step(GramTile& t, uint32_t aw0, uint32_t aw1, uint32_t bw0,
                                           uint32_t bw1, uint32_t jj, uint32_t sel0, uint32_t sel1,
                                           const char* tab_lane, const char* lut) {
-  half8 af[2];
-  af[0] = *reinterpret_cast<const half8*>(lut + 16 * (__builtin_amdgcn_ubfe(aw0, 4 * jj, 4) | sel0));
-  af[1] = *reinterpret_cast<const half8*>(lut + 16 * (__builtin_amdgcn_ubfe(aw1, 4 * jj, 4) | sel1));
-  half8 bf[2][kGramTerms];
+  bf16x8 af[2];
+  af[0] = *reinterpret_cast<const bf16x8*>(lut + 16 * (__builtin_amdgcn_ubfe(aw0, 4 * jj, 4) | sel0));
+  af[1] = *reinterpret_cast<const bf16x8*>(lut + 16 * (__builtin_amdgcn_ubfe(aw1, 4 * jj, 4) | sel1));
+  bf16x8 bf[2][kGramTerms];
   const char* p0 = tab_lane + 16 * __builtin_amdgcn_ubfe(bw0, 4 * jj, 4);
   const char* p1 = tab_lane + 16 * __builtin_amdgcn_ubfe(bw1, 4 * jj, 4);
 #pragma unroll
   for (int s = 0; s < kGramTerms; ++s) {
-    bf[0][s] = *reinterpret_cast<const half8*>(p0 + 512 * s);
-    bf[1][s] = *reinterpret_cast<const half8*>(p1 + 512 * s);
+    bf[0][s] = *reinterpret_cast<const bf16x8*>(p0 + 512 * s);
+    bf[1][s] = *reinterpret_cast<const bf16x8*>(p1 + 512 * s);
   }
 #pragma unroll
   for (int s = 0; s < kGramTerms; ++s)
@@ -98,7 +98,7 @@ __device__ __forceinline__ void gram_step(GramTile& t, uint32_t aw0, uint32_t aw
     for (int x = 0; x < 2; ++x)
 #pragma unroll
       for (int y = 0; y < 2; ++y)
-        t.acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[x], bf[y][s], t.acc[x][y], 0, 0, 0);
+        t.acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[x], bf[y][s], t.acc[x][y], 0, 0, 0);
 }
 
 // grid: (ceil(n / 128), ceil(m / 128), instances). Requires k % G == 0.
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
   // entries of its half (h = A code / 8) for its column's B code, and for one
   // half the 16 B codes' 16-byte rows fill the 64 banks once, so the 16 lanes
   // of a pass (one h) never conflict (equal codes broadcast)
-  __shared__ __align__(16) _Float16 tab[kGramTerms][2][16][8];
+  __shared__ __align__(16) __bf16 tab[kGramTerms][2][16][8];
   __shared__ float sred[kGramThreads / 64];
   // one-hot A fragments: entry 16 h + code holds one_hot(code - 8 h), entries
   // 32..47 (dead rows) are empty
@@ -146,9 +146,9 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
     float* out = reinterpret_cast<float*>(static_cast<char*>(o.out) + o.stride[4] * item);
 
     // ---- Gram table: entry (e, f) per thread, in float64, then scaled so
-    // the largest magnitude is below 2^15 and split into fp16 hi + mid + lo
-    // (each term the fp16 rounding of what the previous ones leave; the
-    // differences are exact in FP32).
+    // the largest magnitude is below 2^15 and split into bf16 hi + mid + lo
+    // (each term the bf16 rounding of what the previous ones leave; the
+    // differences are exact in FP32, and the last term holds the rest exactly).
     __syncthreads();  // the previous instance's table is no longer read
     for (uint32_t i = tid; i < 16 * G; i += kGramThreads) {
       sa[i] = a_book[i];
@@ -178,12 +178,12 @@ __global__ __launch_bounds__(kGramThreads, 2) void k_gram_mfma(Operands o, uint3
       shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
     }
     const float scaled = ldexpf(gv, shift);
-    const _Float16 hi = _Float16(scaled);
+    const __bf16 hi = __bf16(scaled);
     const float r1 = scaled - float(hi);
-    const _Float16 mid = _Float16(r1);
+    const __bf16 mid = __bf16(r1);
     tab[0][e / 8][f][e % 8] = hi;
     tab[1][e / 8][f][e % 8] = mid;
-    tab[2][e / 8][f][e % 8] = _Float16(r1 - float(mid));
+    tab[2][e / 8][f][e % 8] = __bf16(r1 - float(mid));
     const float unscale = ldexpf(1.0f, -shift);
     __syncthreads();
 

@@ -47,7 +47,7 @@ for p in (str(ROOT / "alelyon-compute-kit_amd"), str(ROOT)):
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
-FP16_MFMA_PEAK_TFLOPS = 2500.0     # dense
+BF16_MFMA_PEAK_TFLOPS = 2500.0     # dense (bf16 and fp16 alike)
 # FP32 VALU: 256 CUs x 64 lanes x 2.4 GHz, one non-fused add or multiply per lane
 # and clock (157.3 TFLOP/s counts packed FMAs: 2 lanes x 2 flops)
 FP32_VALU_OPS_PEAK_T = 256 * 64 * 2.4e9 / 1e12
@@ -245,21 +245,21 @@ def bench_prefill(device, dev, steps, warmup, policy=0, dense=True):
                                  "peak": FP32_VALU_OPS_PEAK_T,
                                  "frac": ops / (ms * 1e-3) / 1e12 / FP32_VALU_OPS_PEAK_T}
         elif path == "onehot-mfma":
-            # A's book rows (three fp16 terms) times the one-hot of B's codes:
+            # A's book rows (three bf16 terms) times the one-hot of B's codes:
             # inner dimension kk, 16 nn / 32 S columns
             ops = 2.0 * m * (16 * nn // 32) * kk * 3
-            entry["executed"] = {"what": "fp16 MFMA flops (3-term A operand, FP32-exact)",
+            entry["executed"] = {"what": "bf16 MFMA flops (3-term A operand, FP32-exact)",
                                  "tflops": ops / (ms * 1e-3) / 1e12,
-                                 "peak": FP16_MFMA_PEAK_TFLOPS,
-                                 "frac": ops / (ms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS}
+                                 "peak": BF16_MFMA_PEAK_TFLOPS,
+                                 "frac": ops / (ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS}
         elif path == "gram-mfma":
             # one-hot x Gram GEMM of inner dimension 16 k/g, each Gram entry as
-            # three fp16 terms (hi + mid + lo: 33 significant bits)
+            # three bf16 terms (hi + mid + lo: every FP32 entry exactly)
             ops = 2.0 * m * nn * (3 * 16 * kk // 32)
-            entry["executed"] = {"what": "fp16 MFMA flops (3-term Gram operand, FP32-exact)",
+            entry["executed"] = {"what": "bf16 MFMA flops (3-term Gram operand, FP32-exact)",
                                  "tflops": ops / (ms * 1e-3) / 1e12,
-                                 "peak": FP16_MFMA_PEAK_TFLOPS,
-                                 "frac": ops / (ms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS}
+                                 "peak": BF16_MFMA_PEAK_TFLOPS,
+                                 "frac": ops / (ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS}
         results[name] = entry
     if not dense:
         return results
@@ -687,7 +687,7 @@ def main(argv=None) -> int:
             # kernel is held to the roofline of the work it does execute
             # (*_executed), never to the FP32 matrix peak
             "note": "tflops = 2*M*N*K / time (algorithmic); roofline fractions are of "
-                    "executed work: fp16 MFMA (onehot-mfma, gram-mfma), FP32 VALU adds "
+                    "executed work: bf16 MFMA (onehot-mfma, gram-mfma), FP32 VALU adds "
                     "(row-bins)"}
     for m, r in wide.items():
         extra[f"gemv_m{m}"] = {"workload": f"config 3 at M={m}, same cache-cold batch",

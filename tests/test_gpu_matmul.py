@@ -637,6 +637,31 @@ def test_onehot_mfma_rows_of_very_different_magnitude(vqdev):
     _check_rows(out, exact)
 
 
+def test_gram_mfma_rows_of_very_different_magnitude(vqdev):
+    """B stored (n, k), both grouped along k; A's book holds entries near 1
+    and near 2^-24 and even rows use only the small ones, so their Gram
+    entries sit 2^-24 below the largest. The Gram table's three bf16 terms
+    carry every entry exactly, so each row keeps the 1e-5 bar against its own
+    largest output."""
+    rng = np.random.default_rng(78)
+    m, n, k, group = 512, 384, 2048, 16
+    a_book = rng.standard_normal((16, group)).astype(np.float32)
+    a_book[:8] *= np.float32(2.0 ** -24)
+    from oracle import vq4_numpy as o
+    idx = rng.integers(8, 16, (m, k // group))
+    idx[0::2] = rng.integers(0, 8, (m // 2, k // group))
+    a_codes = o.pack_indices(idx.reshape(-1))
+    b_codes, b_book = image(rng, k * n, group, 0.02)
+    ops = (a_codes, a_book, b_codes, b_book)
+    assert vqdev.path_name((2, m, n, k, group, 16, 2, 0)) == "gram-mfma"
+    say("gram-mfma magnitudes")
+    out, status = _gpu(vqdev, ops, m, n, k, group, 2)
+    assert status == 0
+    exact = _ref64(ops, m, n, k, group, 2)
+    assert np.abs(exact[0]).max() < 1e-5 < np.abs(exact[1]).max()
+    _check_rows(out, exact)
+
+
 def test_config4_forward_against_float64(vqdev):
     """BASELINE config 4 forward at full size: X 2048x4096 . W 4096x14336 at
     group 32; every output against the float64 product of the decoded
