@@ -159,7 +159,8 @@ size_t round_up(size_t bytes) { return (bytes + 255) / 256 * 256; }
 
 // ---- the allocation-free entry's scratch ----------------------------------------
 // ack_vq_noalloc takes the workspace of the paths that need one (the GEMV's
-// split-k partials, row-bins' transposed code words) from this array instead
+// split-k partials, gemv-direct's slice partials, row-bins' transposed code
+// words, onehot-mfma's nibble columns) from this array instead
 // of allocating it. Every GPU the library runs on holds its own copy until
 // the process ends. In host code `scratch` names a host-side stand-in, never
 // a device address: the address is resolved per GPU with

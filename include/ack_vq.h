@@ -128,8 +128,9 @@ int32_t ack_vq_batch(const AckDevice* dev, const AckBuffer* b0, const AckBuffer*
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). Same arguments,
  * check order, codes and results as ack_vq; the workspace some product paths
- * need (split-k partials of the GEMV kernels, the transposed code words of
- * row-bins) comes from a fixed 8 MiB device array that each GPU holds until
+ * need (split-k partials of the GEMV kernels, gemv-direct's slice partials,
+ * the transposed code words of row-bins and the nibble columns of
+ * onehot-mfma) comes from a fixed 8 MiB device array that each GPU holds until
  * the process ends, in place of memory ack_vq would allocate. A plan needing
  * more than 8 MiB of it is refused with ACK_ERR_SIZE. Calls share their GPU's
  * array: calls on one device handle are ordered on its stream, but calls
