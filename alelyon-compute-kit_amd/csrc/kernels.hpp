@@ -39,14 +39,15 @@ enum class MatmulPath : int {
   GemvDirect = 7,    // m <= 8, few weights (kDirectMaxWeights): decode and FMA per output,
                      // split k reduced by the last block of each tile, one launch
   OneHotMfma = 8,    // m >= kOneHotMinRows, packed A along k, B along n: A's book rows x
-                     // one-hot of B's codes on fp16 MFMA, then the 16-term codebook product
+                     // one-hot of B's codes on bf16 MFMA, then the 16-term codebook product
 };
 
 const char* matmul_path_name(MatmulPath p);
 
 // Chooses the path for a product; `policy` 1 forces General, 2 takes a
 // factorised path wherever its shape applies, whatever the size (tests; it
-// never takes gemv-direct, which only the automatic choice does).
+// never takes gemv-direct or onehot-mfma, which only the automatic choice
+// does, so the bin kernels stay covered at the same shapes).
 MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                               uint32_t count, uint32_t policy);
 
@@ -67,9 +68,11 @@ size_t direct_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t group
 hipError_t launch_direct(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                          uint32_t group, uint32_t flags, bool dense, void* workspace);
 
-// onehot-mfma (vq4_onehot.hip): large packed products, A grouped along k and
-// B along n (g 16 or 32); below kOneHotMinRows rows of A the row bins serve.
-constexpr uint32_t kOneHotMinRows = 256;
+// onehot-mfma (vq4_onehot.hip): the automatic choice for packed products of
+// at least kOneHotMinRows rows, A grouped along k and B along n (g 16 or 32).
+// The test policy (2) takes the row bins there instead, which keep serving
+// dense activations.
+constexpr uint32_t kOneHotMinRows = 64;
 bool onehot_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                     uint32_t count);
 size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group);

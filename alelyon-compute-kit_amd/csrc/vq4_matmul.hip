@@ -1840,7 +1840,7 @@ const char* matmul_path_name(MatmulPath p) {
 MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                               uint32_t count, uint32_t policy) {
   if (policy == 1) return MatmulPath::General;
-  if (onehot_applies(m, n, k, group, flags, count)) return MatmulPath::OneHotMfma;
+  if (policy == 0 && onehot_applies(m, n, k, group, flags, count)) return MatmulPath::OneHotMfma;
   if (count == 1 && rowbins_applies(m, n, k, group, flags)) return MatmulPath::RowBins;
   if (gram_applies(m, n, k, group, flags, policy == 2)) return MatmulPath::GramMfma;
   if (policy == 0 && direct_applies(m, n, k, group, flags, count)) return MatmulPath::GemvDirect;

@@ -39,10 +39,12 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kOHThreads = 256;  // 4 waves, 2 x 2 over 256 rows x 128 S columns
-constexpr uint32_t kOHRows = 256;     // rows of A per block
-constexpr int kOHX = 4;               // 32-row blocks per wave
+constexpr uint32_t kOHThreads = 256;  // 4 waves, 2 x 2 over 64 X rows x 128 S columns
 constexpr int kOHTerms = 3;           // bf16 terms of each scaled A value
+// X = 4 (256 rows per block) reuses each one-hot fragment over 12 MFMAs; X = 1
+// (64 rows) gives four times the waves, for products whose 256-row grid would
+// leave most of the chip idle.
+constexpr uint32_t kOHBigGrid = 256;  // blocks of the X = 4 grid from which it is taken
 
 __device__ __forceinline__ bool finite_f32(float x) { return fabsf(x) <= FLT_MAX; }
 
@@ -107,27 +109,29 @@ __global__ __launch_bounds__(256) void k_nibble_columns(const uint32_t* __restri
   }
 }
 
-// grid: (n / (8 G) word columns of B, ceil(m / 256)). A block covers 256 rows
-// of A and the 8 groups of one word column of B (128 S columns); wave (wy, wx)
-// takes rows 128 wy .. +127 and groups 4 wx .. 4 wx + 3. Requires k % 16 == 0,
-// k % G == 0 and n % (8 G) == 0; one instance.
-template <int G>
-__global__ __launch_bounds__(kOHThreads, 2) void k_onehot_mfma(Operands o, uint32_t m, uint32_t n,
-                                                              uint32_t k,
-                                                              const uint32_t* __restrict__ nc) {
+// grid: (n / (8 G) word columns of B, ceil(m / (64 X))). A block covers 64 X
+// rows of A and the 8 groups of one word column of B (128 S columns); wave
+// (wy, wx) takes rows 32 X wy .. +32 X - 1 and groups 4 wx .. 4 wx + 3.
+// Requires k % 16 == 0, k % G == 0 and n % (8 G) == 0; one instance.
+template <int G, int X>
+__global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
+    Operands o, uint32_t m, uint32_t n, uint32_t k, const uint32_t* __restrict__ nc) {
   static_assert(G == 16 || G == 32, "a 16-step of k lies in one group of A");
+  static_assert(X == 1 || X == 2 || X == 4, "row blocks per wave");
+  constexpr int kOHX = X;
+  constexpr uint32_t kChunkRows = X < 2 ? 32 * X : 64;  // S rows staged per epilogue round
   // A's table: [term][8-entry chunk of the group][code][8]; code 16 is empty
   // (rows past m). The 16 lanes of a read phase read one chunk, so distinct
   // codes land in distinct banks.
   __shared__ __align__(16) __bf16 tabA[kOHTerms][G / 8][17][8];
-  __shared__ __align__(16) float sS[4][64][64];  // one wave's S, 64 rows at a time
+  __shared__ __align__(16) float sS[4][kChunkRows][64];  // one wave's S, a round at a time
   __shared__ float sbook[16 * G];
   __shared__ float sred[4];
   const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const uint32_t i32 = lane % 32, h = lane / 32;
   const uint32_t wy = wave / 2, wx = wave % 2;
   const uint32_t q = blockIdx.x;
-  const uint32_t row0 = blockIdx.y * kOHRows + 128 * wy;
+  const uint32_t row0 = blockIdx.y * (64 * X) + 32 * X * wy;
   const uint32_t J = k / G;
   const uint64_t a_last = (uint64_t(m) * J + 7) / 8 - 1;
   const uint32_t* a_codes = static_cast<const uint32_t*>(o.in[0]);
@@ -259,29 +263,30 @@ __global__ __launch_bounds__(kOHThreads, 2) void k_onehot_mfma(Operands o, uint3
     }
   }
 
-  // ---- S to LDS, 64 rows at a time (lane: column i32, item t holds row
-  // (t % 4) + 4 h + 8 (t / 4) of its 32-row block), then
+  // ---- S to LDS, kChunkRows rows at a time (lane: column i32, item t holds
+  // row (t % 4) + 4 h + 8 (t / 4) of its 32-row block), then
   // y[r][G j + t] = sum_e S[r][(j, e)] C_B[e][t], e ascending; a lane's t is
   // fixed (the row stride 64 is a multiple of G)
   const uint32_t tc = lane % G;
   float cb[16];
 #pragma unroll
   for (int f = 0; f < 16; ++f) cb[f] = sbook[f * G + tc];
+  constexpr int kTilesPerRound = kChunkRows / 32;
 #pragma unroll
-  for (int hv = 0; hv < 2; ++hv) {
-    if (hv) __syncthreads();  // the first half has been read
+  for (int hv = 0; hv < X / kTilesPerRound; ++hv) {
+    if (hv) __syncthreads();  // the previous round has been read
 #pragma unroll
-    for (int x = 0; x < 2; ++x)
+    for (int x = 0; x < kTilesPerRound; ++x)
 #pragma unroll
       for (int y = 0; y < 2; ++y)
 #pragma unroll
         for (int t = 0; t < 16; ++t)
           sS[wave][32 * x + (t % 4) + 4 * h + 8 * (t / 4)][32 * y + i32] =
-              acc[2 * hv + x][y][t] * unscale;
+              acc[kTilesPerRound * hv + x][y][t] * unscale;
     __syncthreads();
-    for (uint32_t idx = lane; idx < 64 * 4 * G; idx += 64) {
+    for (uint32_t idx = lane; idx < kChunkRows * 4 * G; idx += 64) {
       const uint32_t row = idx / (4 * G), jl = (idx % (4 * G)) / G;
-      const uint32_t r = row0 + 64 * hv + row;
+      const uint32_t r = row0 + kChunkRows * hv + row;
       if (r >= m) break;
       const float4* sp = reinterpret_cast<const float4*>(&sS[wave][row][16 * jl]);
       const float4 s0 = sp[0], s1 = sp[1], s2 = sp[2], s3 = sp[3];
@@ -321,6 +326,25 @@ size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group) {
   return size_t(n / group) * (k / 8) * 4;
 }
 
+namespace {
+
+template <int G, int X>
+void launch_onehot_x(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                     const uint32_t* nc) {
+  dim3 grid(n / (8 * G), (m + 64 * X - 1) / (64 * X));
+  k_onehot_mfma<G, X><<<grid, kOHThreads, 0, s>>>(o, m, n, k, nc);
+}
+
+template <int G>
+void launch_onehot_g(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                     const uint32_t* nc) {
+  const uint64_t big = uint64_t(n / (8 * G)) * ((m + 255) / 256);
+  if (big >= kOHBigGrid) launch_onehot_x<G, 4>(s, o, m, n, k, nc);
+  else launch_onehot_x<G, 1>(s, o, m, n, k, nc);
+}
+
+}  // namespace
+
 hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                          uint32_t group, void* workspace) {
   const uint32_t rw = n / (8 * group);
@@ -329,9 +353,8 @@ hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
   k_nibble_columns<<<ngrid, 256, 0, s>>>(static_cast<const uint32_t*>(o.in[2]), nc, k, rw);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  dim3 grid(rw, (m + kOHRows - 1) / kOHRows);
-  if (group == 16) k_onehot_mfma<16><<<grid, kOHThreads, 0, s>>>(o, m, n, k, nc);
-  else k_onehot_mfma<32><<<grid, kOHThreads, 0, s>>>(o, m, n, k, nc);
+  if (group == 16) launch_onehot_g<16>(s, o, m, n, k, nc);
+  else launch_onehot_g<32>(s, o, m, n, k, nc);
   return hipGetLastError();
 }
 

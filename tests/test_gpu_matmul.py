@@ -571,13 +571,14 @@ ROW_BINS_SHAPES = [(64, 256, 64, 16), (100, 512, 96, 32), (130, 2048, 256, 16),
 
 
 @pytest.mark.parametrize("m,n,k,group", ROW_BINS_SHAPES)
-def test_row_bins_within_tolerance(vqdev, oracle, m, n, k, group):
+def test_row_bins_within_tolerance(vqdev, oracle, any_size, m, n, k, group):
     """Large-m product with B's groups along n: wave-uniform codes, bins in
-    registers (rows past m in the last wave are masked)."""
+    registers (rows past m in the last wave are masked). The automatic choice
+    takes onehot-mfma for packed A; the test policy runs the row bins."""
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(m + n + k)
     words = (2, m, n, k, group, 16, 0, 0)
-    assert vqdev.path_name(words) == "row-bins"
+    assert vqdev.path_name(words) == "onehot-mfma"
     say("row-bins", m, n, k, group)
     ops = _operands(rng, m, n, k, group, 1.0, 0.02)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0)
@@ -588,14 +589,18 @@ def test_row_bins_within_tolerance(vqdev, oracle, m, n, k, group):
 
 
 # (m, n, k, group): one 16-step of k, a last pass shorter than 8 groups of A
-# (k not a multiple of 8 g), rows past m in the last block, 1 and 8 word columns
-ONEHOT_SHAPES = [(256, 1024, 512, 32), (333, 768, 1024, 16), (256, 256, 16, 16),
-                 (300, 512, 1040, 16), (1000, 4096, 288, 32), (513, 2048, 4096, 32)]
+# (k not a multiple of 8 g), rows past m in the last block, 1 and 8 word
+# columns; grids below 256 blocks of 256 rows run 64-row blocks, the last two
+# shapes the 256-row blocks
+ONEHOT_SHAPES = [(64, 256, 64, 16), (100, 512, 96, 32), (130, 2048, 256, 16),
+                 (256, 1024, 512, 32), (333, 768, 1024, 16), (256, 256, 16, 16),
+                 (300, 512, 1040, 16), (1000, 4096, 288, 32), (513, 2048, 4096, 32),
+                 (1000, 16384, 256, 32), (2100, 4096, 1040, 16)]
 
 
 @pytest.mark.parametrize("m,n,k,group", ONEHOT_SHAPES)
 def test_onehot_mfma_within_tolerance(vqdev, oracle, m, n, k, group):
-    """m >= 256 rows of a packed A (groups along k) times B grouped along n:
+    """m >= 64 rows of a packed A (groups along k) times B grouped along n:
     A's book rows (three fp16 terms) times the one-hot of B's codes on fp16
     MFMA, then the 16-term product with B's book. Within 1e-5 of the oracle
     and of the float64 product, every row against its own largest output."""
@@ -927,7 +932,7 @@ def test_gemv_row_pairs_not_taken_where_rows_cannot_be_instances(vqdev):
 STATUS_PATHS = [("gemv-direct", 1, 512, 512, 16, 0), ("gemv-pairs", 1, 8192, 4160, 16, 0),
                 ("gemv-direct", 4, 512, 512, 16, 0), ("gemv-direct", 7, 384, 1024, 8, 1),
                 ("gemv-rows", 4, 8192, 4160, 16, 0),
-                ("gemv-rows", 7, 8192, 4160, 8, 1), ("row-bins", 128, 512, 256, 16, 0),
+                ("gemv-rows", 7, 8192, 4160, 8, 1), ("onehot-mfma", 128, 512, 256, 16, 0),
                 ("onehot-mfma", 256, 512, 256, 16, 0), ("onehot-mfma", 300, 1024, 288, 32, 0),
                 ("gram-mfma", 64, 96, 1024, 16, 2)]
 

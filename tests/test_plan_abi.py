@@ -275,7 +275,8 @@ def _path(lib, entry, words):
     ((2, 32, 4096, 4096, 16, 16, 0, 0), "gemv-rows"),          # chunks of 8 rows
     ((2, 32, 512, 512, 16, 16, 0, 0), "general"),              # small weight: bit-exact kernel
     ((2, 2048, 14336, 4096, 32, 16, 0, 0), "onehot-mfma"),    # config 4 forward
-    ((2, 255, 14336, 4096, 32, 16, 0, 0), "row-bins"),         # below 256 rows of A
+    ((2, 64, 14336, 4096, 32, 16, 0, 0), "onehot-mfma"),
+    ((2, 63, 14336, 4096, 32, 16, 0, 0), "gemv-rows"),         # below 64 rows: chunks of 8
     ((2, 2048, 14336, 4096, 8, 16, 0, 0), "general"),          # g 8: neither
     ((2, 2048, 4096, 14336, 32, 16, 2, 0), "gram-mfma"),
     ((2, 4, 4096, 4096, 16, 16, 2, 0), "gram-mfma"),           # both grouped along k
