@@ -73,6 +73,7 @@ hipError_t launch_direct(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
 // The test policy (2) takes the row bins there instead, which keep serving
 // dense activations.
 constexpr uint32_t kOneHotMinRows = 64;
+constexpr uint32_t kOneHotMinRowsShortK = 16;  // from here when k <= 256 m and B >= 2^20 values
 bool onehot_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                     uint32_t count);
 size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group);

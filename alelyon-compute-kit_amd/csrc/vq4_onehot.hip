@@ -316,10 +316,19 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
 
 }  // namespace
 
+// From kOneHotMinRows rows of A always; from 16 rows when B holds at least
+// 2^20 values (smaller products keep the bit-exact general kernel) and k is at
+// most 256 m: a small grid walks all of k in each block, where the chunked
+// GEMV splits it (12 x 4096 x 14336 g16: 226 against 91 us; 32 x 4096 x 4096
+// g32: 76 against 179).
 bool onehot_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                     uint32_t count) {
-  return count == 1 && flags == 0 && (group == 16 || group == 32) && m >= kOneHotMinRows &&
-         n % (8 * group) == 0 && k % 16 == 0 && k % group == 0;
+  if (count != 1 || flags != 0 || (group != 16 && group != 32) || n % (8 * group) != 0 ||
+      k % 16 != 0 || k % group != 0)
+    return false;
+  if (m >= kOneHotMinRows) return true;
+  return m >= kOneHotMinRowsShortK && uint64_t(n) * k >= (uint64_t(1) << 20) &&
+         uint64_t(k) <= 256ull * m;
 }
 
 size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group) {

@@ -244,17 +244,26 @@ def test_gemv_direct_on_two_handles_of_one_gpu(vqdev):
                     b.free()
 
 
+def _chunk_auto_path(m, n, k, group, flags):
+    """The automatic choice for 9 <= m < 64 over at least 2^20 weights: the
+    one-hot MFMA path from 16 rows of a row-major A at g 16/32 when k <= 256 m,
+    else the chunked row-pair GEMV."""
+    if flags == 0 and group in (16, 32) and m >= 16 and k <= 256 * m:
+        return "onehot-mfma"
+    return "gemv-rows"
+
+
 @pytest.mark.parametrize("m,flags", [(9, 0), (16, 0), (17, 1), (32, 0), (40, 1), (63, 0)])
-def test_gemv_rows_in_chunks_of_eight(vqdev, oracle, m, flags):
-    """9 <= m < 64 with a weight of at least 2^20 values runs the row-pair
-    kernel over consecutive chunks of 8 rows of A (the last one shorter), each
-    written at its own output rows; A transposed interleaves every row along
-    k. Smaller weights keep the general kernel."""
+def test_gemv_rows_in_chunks_of_eight(vqdev, oracle, any_size, m, flags):
+    """9 <= m < 64 with a weight of at least 2^20 values runs, under the test
+    policy, the row-pair kernel over consecutive chunks of 8 rows of A (the
+    last one shorter), each written at its own output rows; A transposed
+    interleaves every row along k. Smaller weights keep the general kernel."""
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(60 + m)
     for k, n, group in ((1024, 1024, 16), (2048, 512, 8), (512, 2048, 32)):
         words = (2, m, n, k, group, 16, flags, 0)
-        assert vqdev.path_name(words) == "gemv-rows"
+        assert vqdev.path_name(words) == _chunk_auto_path(m, n, k, group, flags)
         say("gemv-rows chunks", m, k, n, group, flags)
         ops = _operands(rng, m, n, k, group, 1.0, 0.02)
         out, status = _gpu(vqdev, ops, m, n, k, group, flags)
@@ -592,7 +601,8 @@ def test_row_bins_within_tolerance(vqdev, oracle, any_size, m, n, k, group):
 # (k not a multiple of 8 g), rows past m in the last block, 1 and 8 word
 # columns; grids below 256 blocks of 256 rows run 64-row blocks, the last two
 # shapes the 256-row blocks
-ONEHOT_SHAPES = [(64, 256, 64, 16), (100, 512, 96, 32), (130, 2048, 256, 16),
+ONEHOT_SHAPES = [(16, 1024, 1024, 16), (40, 2048, 512, 32), (63, 4096, 4096, 16),
+                 (64, 256, 64, 16), (100, 512, 96, 32), (130, 2048, 256, 16),
                  (256, 1024, 512, 32), (333, 768, 1024, 16), (256, 256, 16, 16),
                  (300, 512, 1040, 16), (1000, 4096, 288, 32), (513, 2048, 4096, 32),
                  (1000, 16384, 256, 32), (2100, 4096, 1040, 16)]
@@ -600,7 +610,8 @@ ONEHOT_SHAPES = [(64, 256, 64, 16), (100, 512, 96, 32), (130, 2048, 256, 16),
 
 @pytest.mark.parametrize("m,n,k,group", ONEHOT_SHAPES)
 def test_onehot_mfma_within_tolerance(vqdev, oracle, m, n, k, group):
-    """m >= 64 rows of a packed A (groups along k) times B grouped along n:
+    """m >= 64 rows of a packed A (or 16 with B of 2^20 values and k <= 256 m;
+    groups along k) times B grouped along n:
     A's book rows (three fp16 terms) times the one-hot of B's codes on fp16
     MFMA, then the 16-term product with B's book. Within 1e-5 of the oracle
     and of the float64 product, every row against its own largest output."""

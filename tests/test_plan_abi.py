@@ -272,11 +272,12 @@ def _path(lib, entry, words):
     ((2, 8, 4096, 4096, 16, 16, 1, 0), "gemv-direct"),        # up to 8 rows, A either way
     ((2, 8, 8192, 8192, 16, 16, 1, 0), "gemv-rows"),
     ((2, 9, 4096, 4096, 16, 16, 0, 0), "gemv-rows"),          # past 8 rows
-    ((2, 32, 4096, 4096, 16, 16, 0, 0), "gemv-rows"),          # chunks of 8 rows
+    ((2, 32, 4096, 4096, 16, 16, 0, 0), "onehot-mfma"),        # 16 rows on, k <= 256 m
+    ((2, 32, 4096, 16384, 16, 16, 0, 0), "gemv-rows"),         # longer k: chunks of 8 rows
     ((2, 32, 512, 512, 16, 16, 0, 0), "general"),              # small weight: bit-exact kernel
     ((2, 2048, 14336, 4096, 32, 16, 0, 0), "onehot-mfma"),    # config 4 forward
     ((2, 64, 14336, 4096, 32, 16, 0, 0), "onehot-mfma"),
-    ((2, 63, 14336, 4096, 32, 16, 0, 0), "gemv-rows"),         # below 64 rows: chunks of 8
+    ((2, 12, 14336, 4096, 32, 16, 0, 0), "gemv-rows"),         # below 16 rows: chunks of 8
     ((2, 2048, 14336, 4096, 8, 16, 0, 0), "general"),          # g 8: neither
     ((2, 2048, 4096, 14336, 32, 16, 2, 0), "gram-mfma"),
     ((2, 4, 4096, 4096, 16, 16, 2, 0), "gram-mfma"),           # both grouped along k
