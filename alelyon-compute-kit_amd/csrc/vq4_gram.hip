@@ -12,8 +12,9 @@
 // and it runs on v_mfma_f32_32x32x16_bf16 with one 16-step of K per group j:
 // P is a one-hot row (exact in bf16), and Q is Gram scaled by a power of two
 // and split into three bf16 terms hi + mid + lo (24 significant bits with
-// FP32's exponent range: every FP32 Gram entry is carried exactly, however
-// far below the largest), so each j costs three MFMAs per 32 x 32 output
+// FP32's exponent range: every FP32 Gram entry down to 2^-125 of the largest
+// is carried exactly, the last term staying a normal bf16), so each j costs
+// three MFMAs per 32 x 32 output
 // block and the accumulation is FP32. Neither operand is decoded:
 // P's fragments are read from a 768-byte LDS table of the one-hot rows
 // addressed by A's nibble, Q's from a 1.5 KiB LDS table addressed by B's.
