@@ -12,7 +12,7 @@
 // and it runs on v_mfma_f32_32x32x16_bf16 with one 16-step of K per group j:
 // P is a one-hot row (exact in bf16), and Q is Gram scaled by a power of two
 // and split into three bf16 terms hi + mid + lo (24 significant bits with
-// FP32's exponent range: every FP32 Gram entry down to 2^-125 of the largest
+// FP32's exponent range: every FP32 Gram entry down to 2^-118 of the largest
 // is carried exactly, the last term staying a normal bf16), so each j costs
 // three MFMAs per 32 x 32 output
 // block and the accumulation is FP32. Neither operand is decoded:

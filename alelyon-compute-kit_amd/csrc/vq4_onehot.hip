@@ -17,7 +17,7 @@
 //    row, inside one group) is read from an LDS table of the book scaled by a
 //    power of two (largest magnitude below 2^15) and split into three bf16
 //    terms hi + mid + lo: 24 significant bits with FP32's exponent range, so
-//    every FP32 entry down to 2^-125 of the largest is carried exactly (the
+//    every FP32 entry down to 2^-118 of the largest is carried exactly (the
 //    last term stays a normal bf16; fp16 terms would stop at fp16's subnormal
 //    floor, 2^-39 of the largest). Each 16-step of k costs three
 //    MFMAs per 32 x 32 block and the accumulation is FP32.
