@@ -74,11 +74,14 @@ hipError_t launch_direct(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
 // dense activations.
 constexpr uint32_t kOneHotMinRows = 64;
 constexpr uint32_t kOneHotMinRowsShortK = 16;  // from here when k <= 256 m and B >= 2^20 values
+constexpr uint32_t kOneHotMinRowsDense = 32;   // the same for dense activations
 bool onehot_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                     uint32_t count);
+bool onehot_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                          uint32_t count);
 size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group);
 hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
-                         uint32_t group, void* workspace);
+                         uint32_t group, bool dense, void* workspace);
 
 bool rowbins_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
 bool rowbins_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);

@@ -1880,7 +1880,7 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
                          size_t workspace_bytes) {
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins(s, o, m, n, k, group, workspace);
-  if (path == MatmulPath::OneHotMfma) return launch_onehot(s, o, m, n, k, group, workspace);
+  if (path == MatmulPath::OneHotMfma) return launch_onehot(s, o, m, n, k, group, false, workspace);
   if (path == MatmulPath::GemvDirect)
     return launch_direct(s, o, m, n, k, group, flags, false, workspace);
   if (path == MatmulPath::GramMfma) return launch_gram(s, o, m, n, k, group);
@@ -1898,6 +1898,8 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
 MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                              uint32_t count, uint32_t policy) {
   if (policy == 1) return MatmulPath::General;
+  if (policy == 0 && onehot_applies_dense(m, n, k, group, flags, count))
+    return MatmulPath::OneHotMfma;
   if (count == 1 && rowbins_applies_dense(m, n, k, group, flags)) return MatmulPath::RowBins;
   if (policy == 0 && direct_applies(m, n, k, group, flags, count)) return MatmulPath::GemvDirect;
   if (row_pairs_apply(m, n, k, group, flags, count, true)) return MatmulPath::GemvRowPairs;
@@ -1918,6 +1920,7 @@ hipError_t launch_matmul_dense(hipStream_t s, const Operands& o, uint32_t m, uin
                                void* workspace, size_t workspace_bytes) {
   (void)workspace_bytes;
   if (path == MatmulPath::RowBins) return launch_rowbins_dense(s, o, m, n, k, group, workspace);
+  if (path == MatmulPath::OneHotMfma) return launch_onehot(s, o, m, n, k, group, true, workspace);
   if (path == MatmulPath::GemvDirect)
     return launch_direct(s, o, m, n, k, group, flags, true, workspace);
   if (path == MatmulPath::GemvPairs || path == MatmulPath::GemvRows ||

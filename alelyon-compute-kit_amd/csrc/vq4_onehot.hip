@@ -79,6 +79,25 @@ __device__ __forceinline__ bf16x8 one_hot_column(uint32_t w, uint32_t ee) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// Dense activations: 8 FP32 values split into three bf16 terms hi + mid + lo
+// (each the bf16 rounding of what the previous ones leave; the differences are
+// exact in FP32 and the last term holds the rest exactly for values of at
+// least 2^-103, so no scale is needed).
+__device__ __forceinline__ void split_bf16x3(const float4 a, const float4 b, bool zero,
+                                             bf16x8 (&d)[3]) {
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float x = zero ? 0.0f : v[i];
+    const __bf16 hi = __bf16(x);
+    const float r1 = x - float(hi);
+    const __bf16 mid = __bf16(r1);
+    d[0][i] = hi;
+    d[1][i] = mid;
+    d[2][i] = __bf16(r1 - float(mid));
+  }
+}
+
 // Nibble columns of B: nc[j * (k / 8) + kk8] holds the codes of group j at
 // inner indices 8 kk8 .. 8 kk8 + 7 (nibble i: index 8 kk8 + i). A block reads
 // 64 rows of 32 word columns (coalesced) into LDS and writes the 256 groups'
@@ -113,8 +132,10 @@ __global__ __launch_bounds__(256) void k_nibble_columns(const uint32_t* __restri
 // grid: (n / (8 G) word columns of B, ceil(m / (64 X))). A block covers 64 X
 // rows of A and the 8 groups of one word column of B (128 S columns); wave
 // (wy, wx) takes rows 32 X wy .. +32 X - 1 and groups 4 wx .. 4 wx + 3.
-// Requires k % 16 == 0, k % G == 0 and n % (8 G) == 0; one instance.
-template <int G, int X>
+// Requires k % 16 == 0, k % G == 0 (packed A) and n % (8 G) == 0; one
+// instance. AD: A is dense FP32 in in[0], split into three bf16 terms as it is
+// read (a nonfinite x reaches every output of its row, which sets status bit 1).
+template <int G, int X, bool AD>
 __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
     Operands o, uint32_t m, uint32_t n, uint32_t k, const uint32_t* __restrict__ nc) {
   static_assert(G == 16 || G == 32, "a 16-step of k lies in one group of A");
@@ -136,6 +157,7 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
   const uint32_t J = k / G;
   const uint64_t a_last = (uint64_t(m) * J + 7) / 8 - 1;
   const uint32_t* a_codes = static_cast<const uint32_t*>(o.in[0]);
+  const float* xa = static_cast<const float*>(o.in[0]);
   const float* a_book = static_cast<const float*>(o.in[1]);
   const float* b_book = static_cast<const float*>(o.in[3]);
   float* out = static_cast<float*>(o.out);
@@ -161,7 +183,7 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
   bool bad = false;
   float amax = 0.0f;
   for (uint32_t i = tid; i < 16 * G; i += kOHThreads) {
-    const float a = a_book[i], b = b_book[i];
+    const float a = AD ? 0.0f : a_book[i], b = b_book[i];
     sbook[i] = b;
     if (blockIdx.x == 0 && blockIdx.y == 0) bad |= !finite_f32(a) || !finite_f32(b);
     amax = fmaxf(amax, finite_f32(a) ? fabsf(a) : 0.0f);
@@ -177,7 +199,7 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
     shift = 15 - ex;
     shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
   }
-  for (uint32_t i = tid; i < 17 * G; i += kOHThreads) {
+  for (uint32_t i = tid; i < (AD ? 0u : 17u * G); i += kOHThreads) {
     const float scaled = i < 16 * G ? ldexpf(a_book[i], shift) : 0.0f;
     const __bf16 hi = __bf16(scaled);
     const float r1 = scaled - float(hi);
@@ -186,7 +208,7 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
     tabA[1][(i % G) / 8][i / G][i % 8] = mid;
     tabA[2][(i % G) / 8][i / G][i % 8] = __bf16(r1 - float(mid));
   }
-  const float unscale = ldexpf(1.0f, -shift);
+  const float unscale = AD ? 1.0f : ldexpf(1.0f, -shift);
   __syncthreads();
 
   // ---- main loop: passes over 8 groups of A (8 G inner indices, G / 2 steps
@@ -205,7 +227,7 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
   const char* tab_lane = reinterpret_cast<const char*>(&tabA[0][0][0][0]) + h * kChunk;
   uint32_t aw[kOHX], an[kOHX];
 #pragma unroll
-  for (int x = 0; x < kOHX; ++x) an[x] = nibbles8(a_codes, av[x], a_last);
+  for (int x = 0; x < kOHX; ++x) an[x] = AD ? 0u : nibbles8(a_codes, av[x], a_last);
   uint32_t wb[4][2];
   wb[0][0] = nc0[0];
   wb[0][1] = nc1[0];
@@ -221,17 +243,29 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
     return tab_lane + c8 * kChunk + code * 16;
   };
   bf16x8 af[kOHX][kOHTerms];
+  // AD: the lane's 8 values of each row, one step ahead (rows past m read the
+  // last row and are zeroed by the split)
+  const float* xr[kOHX];
+  float4 xn[kOHX][2];
 #pragma unroll
   for (int x = 0; x < kOHX; ++x) {
-    const char* pa = a_ptr(an, 0, x);
+    if (AD) {
+      const uint32_t r = row0 + 32 * x + i32;
+      xr[x] = xa + uint64_t(r < m ? r : m - 1) * k + 8 * h;
+      xn[x][0] = *reinterpret_cast<const float4*>(xr[x]);
+      xn[x][1] = *reinterpret_cast<const float4*>(xr[x] + 4);
+    } else {
+      const char* pa = a_ptr(an, 0, x);
 #pragma unroll
-    for (int t = 0; t < kOHTerms; ++t) af[x][t] = *reinterpret_cast<const bf16x8*>(pa + t * kTerm);
+      for (int t = 0; t < kOHTerms; ++t)
+        af[x][t] = *reinterpret_cast<const bf16x8*>(pa + t * kTerm);
+    }
   }
   for (uint32_t p0 = 0; p0 < k; p0 += 8 * G) {
 #pragma unroll
     for (int x = 0; x < kOHX; ++x) {
       aw[x] = an[x];
-      if (p0 + 8 * G < k) an[x] = nibbles8(a_codes, av[x] + (p0 + 8 * G) / G, a_last);
+      if (!AD && p0 + 8 * G < k) an[x] = nibbles8(a_codes, av[x] + (p0 + 8 * G) / G, a_last);
     }
 #pragma unroll
     for (uint32_t s = 0; s < kSteps; ++s) {
@@ -244,7 +278,17 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
       const bool more = kk0 + 16 < k;
       const char* pn[kOHX];
 #pragma unroll
-      for (int x = 0; x < kOHX; ++x) pn[x] = s + 1 < kSteps ? a_ptr(aw, s + 1, x) : a_ptr(an, 0, x);
+      for (int x = 0; x < kOHX; ++x) {
+        if (AD) {
+          split_bf16x3(xn[x][0], xn[x][1], dead[x], af[x]);
+          if (more) {
+            xn[x][0] = *reinterpret_cast<const float4*>(xr[x] + kk0 + 16);
+            xn[x][1] = *reinterpret_cast<const float4*>(xr[x] + kk0 + 20);
+          }
+        } else {
+          pn[x] = s + 1 < kSteps ? a_ptr(aw, s + 1, x) : a_ptr(an, 0, x);
+        }
+      }
       bf16x8 bf[2];
       bf[0] = one_hot_column(wb[s % 4][0], ee);
       bf[1] = one_hot_column(wb[s % 4][1], ee);
@@ -255,7 +299,7 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
 #pragma unroll
           for (int y = 0; y < 2; ++y)
             acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[x][t], bf[y], acc[x][y], 0, 0, 0);
-        if (more) {
+        if (!AD && more) {
 #pragma unroll
           for (int x = 0; x < kOHX; ++x)
             af[x][t] = *reinterpret_cast<const bf16x8*>(pn[x] + t * kTerm);
@@ -338,33 +382,51 @@ size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group) {
 
 namespace {
 
-template <int G, int X>
+template <int G, int X, bool AD>
 void launch_onehot_x(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                      const uint32_t* nc) {
   dim3 grid(n / (8 * G), (m + 64 * X - 1) / (64 * X));
-  k_onehot_mfma<G, X><<<grid, kOHThreads, 0, s>>>(o, m, n, k, nc);
+  k_onehot_mfma<G, X, AD><<<grid, kOHThreads, 0, s>>>(o, m, n, k, nc);
+}
+
+uint64_t big_grid(uint32_t m, uint32_t n, uint32_t group) {
+  return uint64_t(n / (8 * group)) * ((m + 255) / 256);
 }
 
 template <int G>
 void launch_onehot_g(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
-                     const uint32_t* nc) {
-  const uint64_t big = uint64_t(n / (8 * G)) * ((m + 255) / 256);
-  if (big >= kOHBigGrid) launch_onehot_x<G, 4>(s, o, m, n, k, nc);
-  else launch_onehot_x<G, 1>(s, o, m, n, k, nc);
+                     bool dense, const uint32_t* nc) {
+  if (dense) launch_onehot_x<G, 1, true>(s, o, m, n, k, nc);  // small grids only
+  else if (big_grid(m, n, G) >= kOHBigGrid) launch_onehot_x<G, 4, false>(s, o, m, n, k, nc);
+  else launch_onehot_x<G, 1, false>(s, o, m, n, k, nc);
 }
 
 }  // namespace
 
+// Dense activations: the small grids only (64-row blocks), where splitting x
+// into three bf16 terms as it is read costs less than the row bins' passes
+// (128 x 4096 x 4096 g32: 113 against 248 us); below 64 rows from 32 rows
+// with the packed rule's k bound (16 rows: 97 against 85 on the chunked GEMV).
+bool onehot_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
+                          uint32_t count) {
+  if (count != 1 || flags != 0 || (group != 16 && group != 32) || n % (8 * group) != 0 ||
+      k % 16 != 0 || big_grid(m, n, group) >= kOHBigGrid)
+    return false;
+  if (m >= kOneHotMinRows) return true;
+  return m >= kOneHotMinRowsDense && uint64_t(n) * k >= (uint64_t(1) << 20) &&
+         uint64_t(k) <= 256ull * m;
+}
+
 hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
-                         uint32_t group, void* workspace) {
+                         uint32_t group, bool dense, void* workspace) {
   const uint32_t rw = n / (8 * group);
   uint32_t* nc = static_cast<uint32_t*>(workspace);
   dim3 ngrid((rw + kNCCols - 1) / kNCCols, (k + kNCRows - 1) / kNCRows);
   k_nibble_columns<<<ngrid, 256, 0, s>>>(static_cast<const uint32_t*>(o.in[2]), nc, k, rw);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (group == 16) launch_onehot_g<16>(s, o, m, n, k, nc);
-  else launch_onehot_g<32>(s, o, m, n, k, nc);
+  if (group == 16) launch_onehot_g<16>(s, o, m, n, k, dense, nc);
+  else launch_onehot_g<32>(s, o, m, n, k, dense, nc);
   return hipGetLastError();
 }
 

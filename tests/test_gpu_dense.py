@@ -27,7 +27,7 @@ def _check(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol=1e-5, binned
     from alelyon_compute_kit import vq
     m, n, k, flags = vq.VQDevice.dense_geometry(x, w, transpose_a, transpose_b)
     if path == "small":
-        path = small_auto_path(m, n, k)
+        path = _dense_onehot(m, n, k, w.group, flags) or small_auto_path(m, n, k)
     if path == "gemv-direct":
         vqdev.device.set_policy(2)
         try:
@@ -40,6 +40,19 @@ def _check(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol=1e-5, binned
     assert vqdev.dense_path_name(words) == path
     say("dense matmul", path, m, n, k, w.group, flags)
     return _check_run(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol)
+
+
+def _dense_onehot(m, n, k, group, flags):
+    """"onehot-mfma" where the automatic dense choice takes it: 64-row blocks
+    (grids of fewer than 256 blocks of 256 rows), from 64 rows, or from 32
+    with B of at least 2^20 values and k <= 256 m; None otherwise."""
+    if flags != 0 or group not in (16, 32) or n % (8 * group) or k % 16:
+        return None
+    if (n // (8 * group)) * ((m + 255) // 256) >= 256:
+        return None
+    if m >= 64 or (m >= 32 and n * k >= 1 << 20 and k <= 256 * m):
+        return "onehot-mfma"
+    return None
 
 
 def _check_run(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol):
@@ -147,11 +160,72 @@ def test_dense_gemv_tiny_activations(vqdev, oracle, m):
 
 @pytest.mark.parametrize("group", [8, 16, 32])
 def test_dense_row_bins(vqdev, oracle, group):
+    """Dense rows on the row bins: group 8 by default; groups 16 and 32 take
+    onehot-mfma by default and the row bins under the test policy."""
     rng = np.random.default_rng(group + 1)
     m, k, n = 128, 512, 8 * group * 6
     w = _weight(rng, (k, n), group)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    _check(vqdev, oracle, x, w, False, False, "row-bins")
+    if group == 8:
+        _check(vqdev, oracle, x, w, False, False, "row-bins")
+        return
+    _check(vqdev, oracle, x, w, False, False, "onehot-mfma")
+    vqdev.device.set_policy(2)
+    try:
+        say("dense matmul", "row-bins (test policy)", m, n, k, group)
+        _check_run(vqdev, oracle, x, w, False, False, "row-bins", 1e-5)
+    finally:
+        vqdev.device.set_policy(0)
+
+
+# (m, k, n, group): from 32 rows (k <= 256 m), rows past m in the 64-row block,
+# k not a multiple of 8 g, one and several word columns
+DENSE_ONEHOT_SHAPES = [(32, 1024, 1024, 16), (40, 512, 2048, 32), (64, 64, 256, 16),
+                       (130, 256, 2048, 16), (200, 4096, 4096, 32), (255, 1040, 768, 16)]
+
+
+@pytest.mark.parametrize("m,k,n,group", DENSE_ONEHOT_SHAPES)
+def test_dense_onehot_mfma(vqdev, oracle, m, k, n, group):
+    """Dense activations on the one-hot MFMA path (64-row blocks): x split
+    into three bf16 terms as it is read; every row within 1e-5 of the float64
+    product against its own largest output."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(m + k + n + group)
+    w = _weight(rng, (k, n), group)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[1] *= 1e-6                               # rows of very different magnitude
+    if m > 3:
+        x[3] *= 1e20
+    y = _check(vqdev, oracle, x, w, False, False, "onehot-mfma")
+    _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
+
+
+def test_dense_onehot_mfma_nonfinite_activation(vqdev):
+    """A NaN or Inf activation reaches every output of its row: status bit 1."""
+    from alelyon_compute_kit import vq
+    rng = np.random.default_rng(5)
+    m, k, n, group = 64, 512, 1024, 16
+    w = _weight(rng, (k, n), group)
+    for bad in (np.nan, np.inf):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        x[7, 100] = bad
+        words = (2, m, n, k, group, 16, 0, 0)
+        assert vqdev.dense_path_name(words) == "onehot-mfma"
+        device = vqdev.device
+        bufs = [device.buffer(a.nbytes) for a in (x, w.codes, w.codebook)]
+        out, status = device.buffer(4 * m * n), device.buffer(4)
+        try:
+            for b_, a in zip(bufs, (x, w.codes, w.codebook)):
+                b_.upload(a)
+            status.upload(np.zeros(1, np.uint32))
+            say("dense onehot nonfinite", bad)
+            vqdev.run_dense(words, *bufs, out, status)
+            assert int(status.download(np.uint32)[0]) == 1
+            y = out.download(np.float32).reshape(m, n)
+            assert not np.isfinite(y[7]).any() and np.isfinite(np.delete(y, 7, 0)).all()
+        finally:
+            for b_ in bufs + [out, status]:
+                b_.free()
 
 
 @pytest.mark.parametrize("m,n,k,ta,tb", [(3, 40, 100, False, True), (20, 64, 48, True, True),
