@@ -319,6 +319,48 @@ def _all_rows_error(y: np.ndarray, ref: np.ndarray):
     return whole, float(per_row.max())
 
 
+def bench_chunk(device, dev, steps, warmup, m=128):
+    """A smaller prefill chunk: X m x 4096 . W 4096 x 4096 g32, packed and dense
+    X (the one-hot path's 64-row blocks), every output against float64."""
+    from alelyon_compute_kit import vq
+    rng = np.random.default_rng(6)
+    k = n = 4096
+    w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+    w_img = dev.encode(w, vq.fit_codebook(w, group=32), group=32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x_img = dev.encode(x, vq.fit_codebook(x, group=32), group=32)
+    words = (2, m, n, k, 32, 16, 0, 0)
+    wd = w_img.decode().astype(np.float64)
+    res = {"workload": f"X {m}x{k} . W {k}x{n} g32, one product"}
+    for name, arrays, dense in (("packed", (x_img.codes, x_img.codebook, w_img.codes,
+                                            w_img.codebook), False),
+                                ("dense_x", (x, w_img.codes, w_img.codebook), True)):
+        bufs = [device.buffer(a.nbytes) for a in arrays]
+        for b_, a in zip(bufs, arrays):
+            b_.upload(a)
+        out, status = device.buffer(m * n * 4), device.buffer(4)
+        status.upload(np.zeros(1, np.uint32))
+        try:
+            if dense:
+                fn, path = (lambda: dev.run_dense(words, *bufs, out, status)), dev.dense_path_name(words)
+            else:
+                fn, path = (lambda: dev.run(words, bufs, out, status)), dev.path_name(words)
+            log(f"timing the {m}-row chunk ({name}), path {path}")
+            ms = timed(device, fn, steps, warmup)
+            flags_out = int(status.download(np.uint32)[0])
+            y = out.download(np.float32).reshape(m, n)
+        finally:
+            for b_ in bufs + [out, status]:
+                b_.free()
+        if flags_out:
+            raise SystemExit(f"status word {flags_out} after the {m}-row chunk ({name})")
+        a64 = x.astype(np.float64) if dense else x_img.decode().astype(np.float64)
+        err, row_err = _all_rows_error(y, a64 @ wd)
+        res[name] = {"us": ms * 1e3, "path": path, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
+                     "max_rel": err, "max_row_rel": row_err}
+    return res
+
+
 def bench_config5(device, dev, steps, warmup):
     """Config 5: 8192x8192 row-normalised N(0,1) weight at group 8 -- GPU
     encode and decode throughput, op-3 AdamW, and the fused VQAdamW step
@@ -626,6 +668,7 @@ def main(argv=None) -> int:
         gemv = bench_gemv(device, dev, args.items, args.steps, args.warmup)
         prefill = None if args.no_prefill else bench_prefill(device, dev, max(3, args.steps // 4),
                                                               1)
+        chunk = None if args.no_prefill else bench_chunk(device, dev, max(5, args.steps), 2)
         wide = {}
         c5 = None
         hstep = None
@@ -677,6 +720,8 @@ def main(argv=None) -> int:
         extra["gemv_dense_x"] = {"workload": "config 3 weight, one 1x4096 float32 activation "
                                              "row handed over dense (ack_vq_matmul_dense)",
                                  **tidy(gemv["dense"])}
+    if chunk:
+        extra["prefill_chunk"] = tidy(chunk)
     if prefill:
         extra["prefill"] = {
             "workload": "config 4: X 2048x4096 . W 4096x14336 g32 (forward), dY 2048x14336 . W^T "
