@@ -181,7 +181,8 @@ def test_dense_row_bins(vqdev, oracle, group):
 # (m, k, n, group): from 32 rows (k <= 256 m), rows past m in the 64-row block,
 # k not a multiple of 8 g, one and several word columns
 DENSE_ONEHOT_SHAPES = [(32, 1024, 1024, 16), (40, 512, 2048, 32), (64, 64, 256, 16),
-                       (130, 256, 2048, 16), (200, 4096, 4096, 32), (255, 1040, 768, 16)]
+                       (130, 256, 2048, 16), (200, 4096, 4096, 32), (255, 1040, 768, 16),
+                       (96, 1040, 1024, 32)]     # k not a multiple of g (dense rows need not be)
 
 
 @pytest.mark.parametrize("m,k,n,group", DENSE_ONEHOT_SHAPES)
