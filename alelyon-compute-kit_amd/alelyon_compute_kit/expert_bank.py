@@ -47,7 +47,7 @@ MAX_OPTIMIZER_STEP = 1 << 53
 PUBLISH_ATTEMPTS = 50
 PUBLISH_PAUSE_S = 0.02
 
-_POINTER_FILE = re.compile(r"expert-(\d+)-(\d+)\.json")
+_POINTER_FILE = re.compile(r"expert-([0-9]+)-([0-9]+)\.json")
 _HEX64 = re.compile(r"[0-9a-f]{64}")
 _HEX32 = re.compile(r"[0-9a-f]{32}")
 _POINTER_KEYS = frozenset(("schema", "config_sha256", "layer", "expert", "generation",

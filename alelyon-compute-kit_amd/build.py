@@ -34,9 +34,13 @@ HIP_FLAGS = [f"--offload-arch={ARCH}", "-x", "hip", "-fhip-fp32-correctly-rounde
              "-fno-gpu-flush-denormals-to-zero",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
-HIP_SOURCES = ["vq4_codec.hip", "vq4_matmul.hip", "vq4_rowbins.hip", "vq4_gram.hip", "vq4_fit.hip",
-               "vq4_direct.hip", "vq4_onehot.hip", "hbm_probe.hip", "abi.cpp"]
+HIP_SOURCES = ["vq4_codec.hip", "vq4_matmul.hip", "vq4_gram.hip", "vq4_fit.hip",
+               "vq4_direct.hip", "vq4_onehot.hip", "abi.cpp"]
 CXX_SOURCES = ["host_fit.cpp"]
+# The benchmark's HBM read probe: a library of its own, never linked into
+# libackvq.so (bench.py --copy-calibration loads it).
+PROBE_SOURCE = "hbm_probe.hip"
+PROBE_LIBRARY = LIBDIR / "libackprobe.so"
 
 
 def _run(cmd: list[str]) -> None:
@@ -49,7 +53,7 @@ def _run(cmd: list[str]) -> None:
 def _compile(source: str) -> Path:
     obj = BUILD / (Path(source).stem + ".o")
     src = CSRC / source
-    if source in HIP_SOURCES:
+    if source in HIP_SOURCES or source == PROBE_SOURCE:
         cmd = [HIPCC, *HIP_FLAGS, *COMMON, "-c", str(src), "-o", str(obj)]
     else:
         cmd = ["g++", *COMMON, "-c", str(src), "-o", str(obj)]
@@ -62,11 +66,13 @@ def build(jobs: int = 4) -> Path:
     BUILD.mkdir(exist_ok=True)
     LIBDIR.mkdir(exist_ok=True)
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
-        objects = list(pool.map(_compile, HIP_SOURCES + CXX_SOURCES))
-    tmp = LIBRARY.with_name(LIBRARY.name + ".tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-          *map(str, objects)])
-    os.replace(tmp, LIBRARY)
+        objects = list(pool.map(_compile, HIP_SOURCES + CXX_SOURCES + [PROBE_SOURCE]))
+    probe = objects.pop()
+    for lib, objs in ((LIBRARY, objects), (PROBE_LIBRARY, [probe])):
+        tmp = lib.with_name(lib.name + ".tmp")
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+              *map(str, objs)])
+        os.replace(tmp, lib)
     return LIBRARY
 
 

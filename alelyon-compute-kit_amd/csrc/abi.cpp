@@ -603,22 +603,6 @@ int32_t ack_stream_timer(const AckDevice* handle, uint32_t phase, float* ms_out)
   return ACK_OK;
 }
 
-int32_t ack_hbm_read_probe(const AckDevice* handle, const AckBuffer* buffer) {
-  std::shared_ptr<Device> dev;
-  std::unique_lock<std::mutex> lock;
-  if (int32_t rc = enter(handle, &dev, &lock)) return rc;
-  BufferRec* buf = nullptr;
-  if (int32_t rc = lookup_buffer(*dev, buffer, &buf)) return rc;
-  if (buf->bytes < 16 || buf->bytes >= (uint64_t(1) << 31)) {
-    set_error("ack_hbm_read_probe: the buffer must hold 16 bytes to 2 GiB");
-    return ACK_ERR_SIZE;
-  }
-  hipError_t e = ackvq::launch_read_probe(dev->stream, buf->ptr, buf->bytes,
-                                          static_cast<uint32_t*>(buf->ptr));
-  if (e != hipSuccess) return hip_failure(*dev, "read probe launch refused", e, false);
-  return ACK_OK;
-}
-
 int32_t ack_vq_set_policy(const AckDevice* handle, uint32_t policy) {
   if (policy > 2) {
     set_error("ack_vq_set_policy: policy must be 0 (automatic), 1 (general) or 2 (any size)");

@@ -32,7 +32,8 @@ enum class MatmulPath : int {
   GemvRows = 1,   // 2 <= m <= 8, B groups along n: nibble bins, two rows per 64-bit atomic
   GemvTable = 2,  // B groups along k (B stored (n,k)): dot-product table, small m
   GramMfma = 3,   // both operands grouped along k: one-hot x Gram table on fp16 MFMA
-  RowBins = 4,    // large m, B groups along n: wave-uniform codes, bins in VGPRs
+  // 4 is retired: row bins, an FP32 add per (row, nibble) through VGPR index
+  // mode, served dense activations of large m before onehot-mfma took them
   GemvPairs = 5,  // m = 1, B groups along n: one atomic per byte into 256-way pair bins
   GemvRowPairs = 6,  // 2 <= m <= 8 (row-major A, batches that fill the chip): each row of A
                      // a GemvPairs instance, the rows of one product on one XCD
@@ -46,8 +47,9 @@ const char* matmul_path_name(MatmulPath p);
 
 // Chooses the path for a product; `policy` 1 forces General, 2 takes a
 // factorised path wherever its shape applies, whatever the size (tests; it
-// never takes gemv-direct or onehot-mfma, which only the automatic choice
-// does, so the bin kernels stay covered at the same shapes).
+// never takes gemv-direct, and onehot-mfma only from kOneHotMinRows rows,
+// where no bin kernel applies, so the bin kernels stay covered at the same
+// shapes).
 MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                               uint32_t count, uint32_t policy);
 
@@ -68,10 +70,9 @@ size_t direct_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t group
 hipError_t launch_direct(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                          uint32_t group, uint32_t flags, bool dense, void* workspace);
 
-// onehot-mfma (vq4_onehot.hip): the automatic choice for packed products of
-// at least kOneHotMinRows rows, A grouped along k and B along n (g 16 or 32).
-// The test policy (2) takes the row bins there instead, which keep serving
-// dense activations.
+// onehot-mfma (vq4_onehot.hip): the automatic choice for products of at least
+// kOneHotMinRows rows with B grouped along n: packed A grouped along k (g 16
+// or 32), or dense activations (any group).
 constexpr uint32_t kOneHotMinRows = 64;
 constexpr uint32_t kOneHotMinRowsShortK = 16;  // from here when k <= 256 m and B >= 2^20 values
 constexpr uint32_t kOneHotMinRowsDense = 32;   // the same for dense activations
@@ -83,23 +84,12 @@ size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group);
 hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                          uint32_t group, bool dense, void* workspace);
 
-bool rowbins_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
-bool rowbins_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags);
-size_t rowbins_workspace_bytes(uint32_t n, uint32_t k, uint32_t group);
-hipError_t launch_rowbins(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
-                          uint32_t group, void* workspace);
-hipError_t launch_rowbins_dense(hipStream_t s, const Operands& o, uint32_t m, uint32_t n,
-                                uint32_t k, uint32_t group, void* workspace);
-
 // Bytes of device workspace a path needs (split-k partials, counters).
 size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                               uint32_t flags, uint32_t count);
 
 hipError_t launch_encode(hipStream_t s, const Operands& o, uint32_t m, uint32_t group);
 
-// One streaming read of `bytes` (< 2^31) at `data` with the GEMV's loads,
-// nothing written (benchmarks' HBM read ceiling; hbm_probe.hip).
-hipError_t launch_read_probe(hipStream_t s, const void* data, uint64_t bytes, uint32_t* sink);
 hipError_t launch_decode(hipStream_t s, const Operands& o, uint32_t m, uint32_t group);
 hipError_t launch_adamw(hipStream_t s, const Operands& o, uint32_t m, uint32_t group);
 hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
@@ -107,8 +97,9 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
                          size_t workspace_bytes);
 
 // The dense-activation product: op 2's geometry and flags with A a dense FP32
-// array in in[0] (in[1] unused). Paths: row-bins (m >= 64), the GEMV paths
-// (m <= 8; each window's fixed-point scale comes from x itself), else General.
+// array in in[0] (in[1] unused). Paths: onehot-mfma (m >= 32 on large B, every
+// m >= 64), the GEMV paths (m <= 8; each window's fixed-point scale comes from
+// x itself), else General.
 MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                              uint32_t count, uint32_t policy);
 size_t dense_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,

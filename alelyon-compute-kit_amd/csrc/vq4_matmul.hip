@@ -187,7 +187,10 @@ bool row_pairs_apply(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_
 
 // A window's fixed-point scale: x -> rint(x 2^shift), from the window's L1.
 __device__ __forceinline__ int window_shift(float l1) {
-  if (!(l1 > 0.0f && l1 <= FLT_MAX)) return 0;  // zero, NaN or Inf (status bit 1 covers the last two)
+  // zero, NaN or Inf: callers raise status bit 1 for the last two (a NaN or
+  // Inf value, or finite values whose L1 overflows FP32, which no int32
+  // scale can hold), so whatever the bins then hold is never trusted
+  if (!(l1 > 0.0f && l1 <= FLT_MAX)) return 0;
   float t = l1 * (1.0f + 0x1p-8f);
   t = t <= FLT_MAX ? t : FLT_MAX;
   int ex;
@@ -655,6 +658,8 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
 #pragma unroll
     for (int w = 0; w < kPairWaves; ++w) l1 += wl1[w];
     shift = window_shift(l1);
+    // finite values whose L1 overflows FP32: no scale holds the window
+    if (!(l1 <= FLT_MAX) && tid == 0) atomicOr(o.status, 1u);
   };
   auto read_x = [&](uint32_t b, float (&xs)[RX]) __attribute__((always_inline)) {
     asm volatile("" : "+s"(b));
@@ -707,7 +712,9 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       const float r = __shfl(part, int(code * (G / 4)));
       if (lane * 8 + c < groups) l1 += r;
     }
-    return __builtin_amdgcn_readfirstlane(window_shift(wave_sum_rows(l1)));
+    l1 = wave_sum_rows(l1);
+    if (!(l1 <= FLT_MAX) && tid == 0) atomicOr(o.status, 1u);  // book rows whose L1 overflows
+    return __builtin_amdgcn_readfirstlane(window_shift(l1));
   };
   static_assert(!PK || G == 8 || G == 16, "book row norms over 2 or 4 lanes");
   // CUM at G = 16 with one k slice: y^T = C_B^T . S^T on v_mfma_f32_16x16x4f32,
@@ -1456,6 +1463,7 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
 #pragma unroll
       for (int w = 0; w < kRowThreads / 64; ++w) l1 += wl1[w * 8 + t];
       wsh[t] = window_shift(l1);
+      if (!(l1 <= FLT_MAX)) atomicOr(o.status, 1u);  // finite x whose L1 overflows FP32
     }
     __syncthreads();
   };
@@ -1830,7 +1838,6 @@ const char* matmul_path_name(MatmulPath p) {
     case MatmulPath::GemvRowPairs: return "gemv-row-pairs";
     case MatmulPath::GemvTable: return "gemv-table";
     case MatmulPath::GramMfma: return "gram-mfma";
-    case MatmulPath::RowBins: return "row-bins";
     case MatmulPath::OneHotMfma: return "onehot-mfma";
     case MatmulPath::GemvDirect: return "gemv-direct";
   }
@@ -1840,8 +1847,8 @@ const char* matmul_path_name(MatmulPath p) {
 MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                               uint32_t count, uint32_t policy) {
   if (policy == 1) return MatmulPath::General;
-  if (policy == 0 && onehot_applies(m, n, k, group, flags, count)) return MatmulPath::OneHotMfma;
-  if (count == 1 && rowbins_applies(m, n, k, group, flags)) return MatmulPath::RowBins;
+  if ((policy == 0 || m >= kOneHotMinRows) && onehot_applies(m, n, k, group, flags, count))
+    return MatmulPath::OneHotMfma;
   if (gram_applies(m, n, k, group, flags, policy == 2)) return MatmulPath::GramMfma;
   if (policy == 0 && direct_applies(m, n, k, group, flags, count)) return MatmulPath::GemvDirect;
   if (row_pairs_apply(m, n, k, group, flags, count, false)) return MatmulPath::GemvRowPairs;
@@ -1852,7 +1859,6 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
 
 size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                               uint32_t flags, uint32_t count) {
-  if (p == MatmulPath::RowBins) return rowbins_workspace_bytes(n, k, group);
   if (p == MatmulPath::OneHotMfma) return onehot_workspace_bytes(n, k, group);
   if (p == MatmulPath::GemvDirect) return direct_workspace_bytes(m, n, k, group, count);
   if (p != MatmulPath::GemvRows && p != MatmulPath::GemvPairs) return 0;
@@ -1879,7 +1885,6 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
                          uint32_t group, uint32_t flags, MatmulPath path, void* workspace,
                          size_t workspace_bytes) {
   (void)workspace_bytes;
-  if (path == MatmulPath::RowBins) return launch_rowbins(s, o, m, n, k, group, workspace);
   if (path == MatmulPath::OneHotMfma) return launch_onehot(s, o, m, n, k, group, false, workspace);
   if (path == MatmulPath::GemvDirect)
     return launch_direct(s, o, m, n, k, group, flags, false, workspace);
@@ -1898,9 +1903,8 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
 MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                              uint32_t count, uint32_t policy) {
   if (policy == 1) return MatmulPath::General;
-  if (policy == 0 && onehot_applies_dense(m, n, k, group, flags, count))
+  if ((policy == 0 || m >= kOneHotMinRows) && onehot_applies_dense(m, n, k, group, flags, count))
     return MatmulPath::OneHotMfma;
-  if (count == 1 && rowbins_applies_dense(m, n, k, group, flags)) return MatmulPath::RowBins;
   if (policy == 0 && direct_applies(m, n, k, group, flags, count)) return MatmulPath::GemvDirect;
   if (row_pairs_apply(m, n, k, group, flags, count, true)) return MatmulPath::GemvRowPairs;
   if (rows_apply(m, n, k, group, flags))
@@ -1919,7 +1923,6 @@ hipError_t launch_matmul_dense(hipStream_t s, const Operands& o, uint32_t m, uin
                                uint32_t k, uint32_t group, uint32_t flags, MatmulPath path,
                                void* workspace, size_t workspace_bytes) {
   (void)workspace_bytes;
-  if (path == MatmulPath::RowBins) return launch_rowbins_dense(s, o, m, n, k, group, workspace);
   if (path == MatmulPath::OneHotMfma) return launch_onehot(s, o, m, n, k, group, true, workspace);
   if (path == MatmulPath::GemvDirect)
     return launch_direct(s, o, m, n, k, group, flags, true, workspace);

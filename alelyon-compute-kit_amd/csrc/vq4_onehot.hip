@@ -82,14 +82,21 @@ __device__ __forceinline__ bf16x8 one_hot_column(uint32_t w, uint32_t ee) {
 // Dense activations: 8 FP32 values split into three bf16 terms hi + mid + lo
 // (each the bf16 rounding of what the previous ones leave; the differences are
 // exact in FP32 and the last term holds the rest exactly for values of at
-// least 2^-103, so no scale is needed).
+// least 2^-103, so no scale is needed). hi is the rounding of x clamped to the
+// largest bf16 (0x1.fep127): a finite x past it would otherwise round hi up to
+// infinity; its rest, below 2^121, still splits exactly into mid and lo. A NaN
+// or infinite x leaves a NaN or infinite rest, which reaches the output and
+// raises status bit 1. The main loop adds lo, then mid, then hi, so a partial
+// sum of one value's terms never passes the value itself (hi + mid alone can:
+// FLT_MAX splits into the largest bf16 + 2^120 - 2^104, and hi + mid is 2^128).
+constexpr float kBf16Max = 0x1.fep127f;
 __device__ __forceinline__ void split_bf16x3(const float4 a, const float4 b, bool zero,
                                              bf16x8 (&d)[3]) {
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float x = zero ? 0.0f : v[i];
-    const __bf16 hi = __bf16(x);
+    const __bf16 hi = __bf16(fminf(fmaxf(x, -kBf16Max), kBf16Max));
     const float r1 = x - float(hi);
     const __bf16 mid = __bf16(r1);
     d[0][i] = hi;
@@ -136,9 +143,9 @@ __global__ __launch_bounds__(256) void k_nibble_columns(const uint32_t* __restri
 // instance. AD: A is dense FP32 in in[0], split into three bf16 terms as it is
 // read (a nonfinite x reaches every output of its row, which sets status bit 1).
 template <int G, int X, bool AD>
-__global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
+__global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
     Operands o, uint32_t m, uint32_t n, uint32_t k, const uint32_t* __restrict__ nc) {
-  static_assert(G == 16 || G == 32, "a 16-step of k lies in one group of A");
+  static_assert(G == 16 || G == 32 || (AD && G == 8), "a 16-step of k lies in one group of A");
   static_assert(X == 1 || X == 2 || X == 4, "row blocks per wave");
   constexpr int kOHX = X;
   constexpr uint32_t kChunkRows = X < 2 ? 32 * X : 64;  // S rows staged per epilogue round
@@ -208,7 +215,6 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
     tabA[1][(i % G) / 8][i / G][i % 8] = mid;
     tabA[2][(i % G) / 8][i / G][i % 8] = __bf16(r1 - float(mid));
   }
-  const float unscale = AD ? 1.0f : ldexpf(1.0f, -shift);
   __syncthreads();
 
   // ---- main loop: passes over 8 groups of A (8 G inner indices, G / 2 steps
@@ -292,8 +298,9 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
       bf16x8 bf[2];
       bf[0] = one_hot_column(wb[s % 4][0], ee);
       bf[1] = one_hot_column(wb[s % 4][1], ee);
+      // terms smallest first: lo, mid, hi
 #pragma unroll
-      for (int t = 0; t < kOHTerms; ++t) {
+      for (int t = kOHTerms - 1; t >= 0; --t) {
 #pragma unroll
         for (int x = 0; x < kOHX; ++x)
 #pragma unroll
@@ -311,7 +318,10 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
   // ---- S to LDS, kChunkRows rows at a time (lane: column i32, item t holds
   // row (t % 4) + 4 h + 8 (t / 4) of its 32-row block), then
   // y[r][G j + t] = sum_e S[r][(j, e)] C_B[e][t], e ascending; a lane's t is
-  // fixed (the row stride 64 is a multiple of G)
+  // fixed (the row stride 64 is a multiple of G). S stays scaled by 2^shift
+  // through the product and y is unscaled last (one ldexp, exact unless y is
+  // subnormal), so A values near FLT_MAX / k cannot overflow a bucket sum
+  // whose products with C_B are finite.
   const uint32_t tc = lane % G;
   float cb[16];
 #pragma unroll
@@ -327,7 +337,7 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
 #pragma unroll
         for (int t = 0; t < 16; ++t)
           sS[wave][32 * x + (t % 4) + 4 * h + 8 * (t / 4)][32 * y + i32] =
-              acc[kTilesPerRound * hv + x][y][t] * unscale;
+              acc[kTilesPerRound * hv + x][y][t];
     __syncthreads();
     for (uint32_t idx = lane; idx < kChunkRows * 4 * G; idx += 64) {
       const uint32_t row = idx / (4 * G), jl = (idx % (4 * G)) / G;
@@ -352,6 +362,7 @@ __global__ __launch_bounds__(kOHThreads, X == 4 ? 2 : 4) void k_onehot_mfma(
       y = fmaf(s3.y, cb[13], y);
       y = fmaf(s3.z, cb[14], y);
       y = fmaf(s3.w, cb[15], y);
+      if (!AD) y = ldexpf(y, -shift);
       out[uint64_t(r) * n + (8 * q + 4 * wx + jl) * G + tc] = y;
       bad |= !finite_f32(y);
     }
@@ -393,25 +404,46 @@ uint64_t big_grid(uint32_t m, uint32_t n, uint32_t group) {
   return uint64_t(n / (8 * group)) * ((m + 255) / 256);
 }
 
+// The dense grid's row blocks: 128 rows (X = 2: each one-hot fragment feeds
+// two row blocks, and each split of x into bf16 terms feeds the wave's two
+// column blocks) once that grid holds kOHBigGrid blocks; 64 rows (X = 1, four
+// blocks per CU) below.
+uint64_t dense_grid_x2(uint32_t m, uint32_t n, uint32_t group) {
+  return uint64_t(n / (8 * group)) * ((m + 127) / 128);
+}
+
 template <int G>
 void launch_onehot_g(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                      bool dense, const uint32_t* nc) {
-  if (dense) launch_onehot_x<G, 1, true>(s, o, m, n, k, nc);  // small grids only
-  else if (big_grid(m, n, G) >= kOHBigGrid) launch_onehot_x<G, 4, false>(s, o, m, n, k, nc);
-  else launch_onehot_x<G, 1, false>(s, o, m, n, k, nc);
+  if (dense) {
+    if (dense_grid_x2(m, n, G) >= kOHBigGrid) launch_onehot_x<G, 2, true>(s, o, m, n, k, nc);
+    else launch_onehot_x<G, 1, true>(s, o, m, n, k, nc);
+  } else if (big_grid(m, n, G) >= kOHBigGrid) {
+    launch_onehot_x<G, 4, false>(s, o, m, n, k, nc);
+  } else {
+    launch_onehot_x<G, 1, false>(s, o, m, n, k, nc);
+  }
+}
+
+// Group 8 is admitted for dense activations only (packed A's 16-steps of k
+// would straddle its groups).
+template <>
+void launch_onehot_g<8>(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                        bool dense, const uint32_t* nc) {
+  (void)dense;
+  if (dense_grid_x2(m, n, 8) >= kOHBigGrid) launch_onehot_x<8, 2, true>(s, o, m, n, k, nc);
+  else launch_onehot_x<8, 1, true>(s, o, m, n, k, nc);
 }
 
 }  // namespace
 
-// Dense activations: the small grids only (64-row blocks), where splitting x
-// into three bf16 terms as it is read costs less than the row bins' passes
-// (128 x 4096 x 4096 g32: 113 against 248 us); below 64 rows from 32 rows
-// with the packed rule's k bound (16 rows: 97 against 85 on the chunked GEMV).
+// Dense activations (no A groups to straddle, so group 8 as well): from 64
+// rows, and from 32 rows with the packed rule's k bound (16 rows: 97 against
+// 85 us on the chunked GEMV). x is split into three bf16 terms as it is read,
+// VALU work that the packed path's table reads do not have.
 bool onehot_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                           uint32_t count) {
-  if (count != 1 || flags != 0 || (group != 16 && group != 32) || n % (8 * group) != 0 ||
-      k % 16 != 0 || big_grid(m, n, group) >= kOHBigGrid)
-    return false;
+  if (count != 1 || flags != 0 || n % (8 * group) != 0 || k % 16 != 0) return false;
   if (m >= kOneHotMinRows) return true;
   return m >= kOneHotMinRowsDense && uint64_t(n) * k >= (uint64_t(1) << 20) &&
          uint64_t(k) <= 256ull * m;
@@ -425,7 +457,8 @@ hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
   k_nibble_columns<<<ngrid, 256, 0, s>>>(static_cast<const uint32_t*>(o.in[2]), nc, k, rw);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (group == 16) launch_onehot_g<16>(s, o, m, n, k, dense, nc);
+  if (group == 8) launch_onehot_g<8>(s, o, m, n, k, dense, nc);
+  else if (group == 16) launch_onehot_g<16>(s, o, m, n, k, dense, nc);
   else launch_onehot_g<32>(s, o, m, n, k, dense, nc);
   return hipGetLastError();
 }

@@ -48,9 +48,6 @@ for p in (str(ROOT / "alelyon-compute-kit_amd"), str(ROOT)):
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0     # dense (bf16 and fp16 alike)
-# FP32 VALU: 256 CUs x 64 lanes x 2.4 GHz, one non-fused add or multiply per lane
-# and clock (157.3 TFLOP/s counts packed FMAs: 2 lanes x 2 flops)
-FP32_VALU_OPS_PEAK_T = 256 * 64 * 2.4e9 / 1e12
 W_BYTES = 524288 + 1024           # packed codes + codebook of one 4096x4096 g16 weight
 SUSTAINED_LAUNCHES = 80              # back-to-back launches for the sustained (power-limited) rate
 
@@ -239,27 +236,9 @@ def bench_prefill(device, dev, steps, warmup, policy=0, dense=True):
         entry = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "path": path,
                  "max_rel": err, "max_row_rel": row_err}
         # what the kernel actually executes, against that work's own peak
-        if path == "row-bins":      # one FP32 add per (row of A, nibble of B)
-            ops = float(m) * kk * (nn // 32)
-            entry["executed"] = {"what": "FP32 VALU adds", "tops": ops / (ms * 1e-3) / 1e12,
-                                 "peak": FP32_VALU_OPS_PEAK_T,
-                                 "frac": ops / (ms * 1e-3) / 1e12 / FP32_VALU_OPS_PEAK_T}
-        elif path == "onehot-mfma":
-            # A's book rows (three bf16 terms) times the one-hot of B's codes:
-            # inner dimension kk, 16 nn / 32 S columns
-            ops = 2.0 * m * (16 * nn // 32) * kk * 3
-            entry["executed"] = {"what": "bf16 MFMA flops (3-term A operand, FP32-exact)",
-                                 "tflops": ops / (ms * 1e-3) / 1e12,
-                                 "peak": BF16_MFMA_PEAK_TFLOPS,
-                                 "frac": ops / (ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS}
-        elif path == "gram-mfma":
-            # one-hot x Gram GEMM of inner dimension 16 k/g, each Gram entry as
-            # three bf16 terms (hi + mid + lo: every FP32 entry exactly)
-            ops = 2.0 * m * nn * (3 * 16 * kk // 32)
-            entry["executed"] = {"what": "bf16 MFMA flops (3-term Gram operand, FP32-exact)",
-                                 "tflops": ops / (ms * 1e-3) / 1e12,
-                                 "peak": BF16_MFMA_PEAK_TFLOPS,
-                                 "frac": ops / (ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS}
+        executed = _executed(path, m, nn, kk, ms)
+        if executed:
+            entry["executed"] = executed
         results[name] = entry
     if not dense:
         return results
@@ -286,7 +265,31 @@ def bench_prefill(device, dev, steps, warmup, policy=0, dense=True):
     flop = 2.0 * m * n * k
     results["forward_dense_x"] = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "path": path,
                                   "max_rel": err, "max_row_rel": row_err}
+    executed = _executed(path, m, n, k, ms)
+    if executed:
+        results["forward_dense_x"]["executed"] = executed
     return results
+
+
+def _executed(path, m, nn, kk, ms):
+    """The work a factorised config-4 kernel executes, against that work's own
+    peak (the codebook factorisation executes far fewer operations than the
+    algorithmic 2 M N K), or None for the general kernel."""
+    if path == "onehot-mfma":
+        # A's values (book rows, or dense x) as three bf16 terms times the
+        # one-hot of B's codes: inner dimension kk, 16 nn / 32 S columns
+        ops = 2.0 * m * (16 * nn // 32) * kk * 3
+        what = "bf16 MFMA flops (3-term A operand, FP32-exact)"
+    elif path == "gram-mfma":
+        # one-hot x Gram GEMM of inner dimension 16 k/g, each Gram entry as
+        # three bf16 terms (hi + mid + lo: every FP32 entry exactly)
+        ops = 2.0 * m * nn * (3 * 16 * kk // 32)
+        what = "bf16 MFMA flops (3-term Gram operand, FP32-exact)"
+    else:
+        return None
+    tflops = ops / (ms * 1e-3) / 1e12
+    return {"what": what, "tflops": tflops, "peak": BF16_MFMA_PEAK_TFLOPS,
+            "frac": tflops / BF16_MFMA_PEAK_TFLOPS}
 
 
 def other_paths(items, steps, warmup):
@@ -392,12 +395,14 @@ def bench_config5(device, dev, steps, warmup):
                          "path": dev.path_name(enc)}
         valu = load_counter("encode_config5_counters.json", "valu_lane_ops_per_launch")
         if valu:
-            # lane operations the screened argmin executed per launch (PMC
-            # SQ_INSTS_VALU x 64 lanes, profiles/), over this run's kernel time
+            # lane operations the screened argmin executes per launch (PMC
+            # SQ_INSTS_VALU x 64 lanes, recorded under profiles/). A counter
+            # from one run over another run's time is no roofline, so only
+            # the count is reported here; its fraction of the VALU rate is
+            # the profile's, from that profile's own kernel time.
             out["encode"]["valu_executed"] = {
-                "what": "VALU lane operations (SQ_INSTS_VALU x 64)",
-                "tops": valu / (ms * 1e-3) / 1e12, "peak": FP32_VALU_OPS_PEAK_T,
-                "frac": valu / (ms * 1e-3) / 1e12 / FP32_VALU_OPS_PEAK_T}
+                "what": "VALU lane operations per launch (SQ_INSTS_VALU x 64)",
+                "lane_ops": valu, "source": "profiles/encode_config5_counters.json"}
         dec = (1, m, 1, 1, g, 16, 0, 0)
         ms = timed(device, lambda: dev.run(dec, [codes, bk], dense, status), steps, warmup)
         moved = 4.0 * m + 4.0 * words
@@ -575,10 +580,12 @@ def cpu_baseline(x_img, w_img, budget_s=10.0):
 def hbm_calibration() -> dict:
     """What plain memory kernels reach on this GPU: a 512 MiB copy (three
     launches; the byte count the traffic counters are scaled by) and the
-    library's read probe streaming 1.5 GiB with the GEMV's code loads (the
-    read ceiling the GEMV is held to), median of ten event-timed launches."""
+    read probe (libackprobe.so, built beside the library) streaming 1.5 GiB
+    with the GEMV's code loads (the read ceiling the GEMV is held to), median
+    of ten event-timed launches after two."""
+    import ctypes
+
     import torch
-    from alelyon_compute_kit import ack
     src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -592,20 +599,19 @@ def hbm_calibration() -> dict:
     copy_ms = start.elapsed_time(stop)
     del src, dst
     read_bytes = 3 << 29
-    with ack.Device() as device:
-        buf = device.buffer(read_bytes)
-        try:
-            buf.upload(np.ones(read_bytes // 4, np.uint32))
-            times = []
-            for i in range(12):
-                device.timer_start()
-                device.call("ack_hbm_read_probe", buf.handle, context="read probe")
-                ms = device.timer_stop()
-                if i >= 2:
-                    times.append(ms)
-        finally:
-            buf.free()
-    read_ms = float(np.median(times))
+    probe = ctypes.CDLL(str(ROOT / "alelyon-compute-kit_amd" / "alelyon_compute_kit" / "_lib"
+                            / "libackprobe.so"))
+    probe.ack_probe_read_ms.argtypes = (ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32,
+                                        ctypes.POINTER(ctypes.c_float))
+    probe.ack_probe_read_ms.restype = ctypes.c_int32
+    buf = torch.ones(read_bytes // 4, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    times = (ctypes.c_float * 12)()
+    rc = probe.ack_probe_read_ms(ctypes.c_void_p(buf.data_ptr()), read_bytes, 12, times)
+    del buf
+    if rc != 0:
+        raise SystemExit(f"read probe failed: {rc}")
+    read_ms = float(np.median(list(times)[2:]))
     return {"copy_bytes": 512 << 20, "launches": 3,
             "copy_gbs": round(2 * (512 << 20) / (copy_ms * 1e-3) / 1e9, 1),
             "read_bytes": read_bytes, "read_ms": round(read_ms, 4),
@@ -732,8 +738,7 @@ def main(argv=None) -> int:
             # kernel is held to the roofline of the work it does execute
             # (*_executed), never to the FP32 matrix peak
             "note": "tflops = 2*M*N*K / time (algorithmic); roofline fractions are of "
-                    "executed work: bf16 MFMA (onehot-mfma, gram-mfma), FP32 VALU adds "
-                    "(row-bins)"}
+                    "executed work: bf16 MFMA (onehot-mfma, gram-mfma)"}
     for m, r in wide.items():
         extra[f"gemv_m{m}"] = {"workload": f"config 3 at M={m}, same cache-cold batch",
                                "gbs": tidy(r["gbs"]), "hbm_frac": tidy(r["gbs"] / HBM_PEAK_GBS),

@@ -212,13 +212,6 @@ int32_t ack_buffer_copy(const AckDevice* dev, const AckBuffer* dst, uint64_t dst
 /* Wait for every operation enqueued on the device. */
 int32_t ack_sync(const AckDevice* dev);
 
-/* Enqueue one streaming read of the whole buffer (16 bytes to 2 GiB) with
- * the loads and per-block contiguous streams the GEMV kernels read their
- * codes with (one block per compute unit), writing nothing. No
- * counterpart in the reference: for benchmarks, which time it with
- * ack_stream_timer to state the HBM read rate the GEMV is measured against. */
-int32_t ack_hbm_read_probe(const AckDevice* dev, const AckBuffer* buffer);
-
 /* Name of the kernel path ack_vq would take for `plan` on this library
  * (for tests that must know a fast path ran). */
 int32_t ack_vq_path_name(const uint8_t* plan, size_t plan_len, char* out, size_t len);

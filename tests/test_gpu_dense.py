@@ -1,7 +1,7 @@
 """The dense-activation product (ack_vq_matmul_dense): op 2's plan with the
 activations handed over as dense float32 instead of a vq4 image. The General
 path must equal the oracle's op-2 loop with A read from x bit for bit; the
-factorised paths (m = 1, 2..8, >= 64) must agree with the float64 product
+factorised paths (m = 1, 2..8, >= 32) must agree with the float64 product
 within 1e-5 max-rel and with the oracle within FP32 rounding."""
 from __future__ import annotations
 
@@ -43,16 +43,19 @@ def _check(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol=1e-5, binned
 
 
 def _dense_onehot(m, n, k, group, flags):
-    """"onehot-mfma" where the automatic dense choice takes it: 64-row blocks
-    (grids of fewer than 256 blocks of 256 rows), from 64 rows, or from 32
-    with B of at least 2^20 values and k <= 256 m; None otherwise."""
-    if flags != 0 or group not in (16, 32) or n % (8 * group) or k % 16:
-        return None
-    if (n // (8 * group)) * ((m + 255) // 256) >= 256:
+    """"onehot-mfma" where the automatic dense choice takes it: from 64 rows,
+    or from 32 with B of at least 2^20 values and k <= 256 m; None otherwise."""
+    if flags != 0 or n % (8 * group) or k % 16:
         return None
     if m >= 64 or (m >= 32 and n * k >= 1 << 20 and k <= 256 * m):
         return "onehot-mfma"
     return None
+
+
+def _dense_x2(m, n, group):
+    """Whether the dense one-hot product runs 128-row blocks (X = 2): its grid
+    of 128-row blocks has at least 256 blocks."""
+    return (n // (8 * group)) * ((m + 127) // 128) >= 256
 
 
 def _check_run(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol):
@@ -159,21 +162,126 @@ def test_dense_gemv_tiny_activations(vqdev, oracle, m):
 
 
 @pytest.mark.parametrize("group", [8, 16, 32])
-def test_dense_row_bins(vqdev, oracle, group):
-    """Dense rows on the row bins: group 8 by default; groups 16 and 32 take
-    onehot-mfma by default and the row bins under the test policy."""
+def test_dense_large_m_every_group(vqdev, oracle, group):
+    """Dense rows of m >= 64 take onehot-mfma in every group, group 8 included
+    (dense A has no groups to straddle), by default and under the test policy
+    (no bin kernel serves m >= 64)."""
     rng = np.random.default_rng(group + 1)
     m, k, n = 128, 512, 8 * group * 6
     w = _weight(rng, (k, n), group)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    if group == 8:
-        _check(vqdev, oracle, x, w, False, False, "row-bins")
-        return
     _check(vqdev, oracle, x, w, False, False, "onehot-mfma")
     vqdev.device.set_policy(2)
     try:
-        say("dense matmul", "row-bins (test policy)", m, n, k, group)
-        _check_run(vqdev, oracle, x, w, False, False, "row-bins", 1e-5)
+        say("dense matmul", "onehot-mfma (test policy)", m, n, k, group)
+        _check_run(vqdev, oracle, x, w, False, False, "onehot-mfma", 1e-5)
+    finally:
+        vqdev.device.set_policy(0)
+
+
+# (m, k, n, group): grids of at least 256 blocks of 128 rows (X = 2): ragged
+# last row block, group 8, k not a multiple of g
+DENSE_X2_SHAPES = [(512, 1024, 4096, 8), (257, 512, 16384, 16), (300, 528, 24576, 32),
+                   (384, 1040, 12288, 16)]
+
+
+@pytest.mark.parametrize("m,k,n,group", DENSE_X2_SHAPES)
+def test_dense_onehot_mfma_128_row_blocks(vqdev, oracle, m, k, n, group):
+    """Dense activations on large grids: 128-row blocks, each one-hot fragment
+    feeding two row blocks; every row within 1e-5 of the float64 product
+    against its own largest output, rows of very different magnitude."""
+    assert _dense_x2(m, n, group)
+    rng = np.random.default_rng(m + k + n + group)
+    w = _weight(rng, (k, n), group)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[1] *= 1e-6
+    x[130] *= 1e20
+    x[m - 1] *= 1e-30
+    y = _check(vqdev, oracle, x, w, False, False, "onehot-mfma")
+    _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
+
+
+def _run_status(vqdev, x, w, words):
+    """One dense product through the resident entry: (output, status word)."""
+    m, n = words[1], words[2]
+    device = vqdev.device
+    bufs = [device.buffer(a.nbytes) for a in (x, w.codes, w.codebook)]
+    out, status = device.buffer(4 * m * n), device.buffer(4)
+    try:
+        for b_, a in zip(bufs, (x, w.codes, w.codebook)):
+            b_.upload(a)
+        status.upload(np.zeros(1, np.uint32))
+        vqdev.run_dense(words, *bufs, out, status)
+        return out.download(np.float32).reshape(m, n), int(status.download(np.uint32)[0])
+    finally:
+        for b_ in bufs + [out, status]:
+            b_.free()
+
+
+def _small_book(w, group, top=2.0 ** -10):
+    """w's image with its book scaled so that every |C_B| <= top."""
+    from alelyon_compute_kit import vq
+    book = (w.codebook / np.abs(w.codebook).max() * top).astype(np.float32)
+    return vq.VQArray(w.shape, group, w.codes, book)
+
+
+def test_dense_onehot_mfma_activations_near_float_max(vqdev, oracle):
+    """Single activations between the largest bf16 (0x1.fep127) and just
+    below FLT_MAX: the bf16 split's first term stops at the largest bf16
+    instead of rounding to infinity, and the terms are accumulated smallest
+    first, so where every code bucket's sum of x stays clear of FLT_MAX the
+    output is finite, no status bit is raised and every row is within 1e-5 of
+    the float64 product. (A bucket sum within about an ulp of FLT_MAX can
+    overflow: the bf16 MFMA aligns its small addends to the largest by
+    truncation, so -FLT_MAX plus negative neighbours reaches -2^128. That
+    case raises status bit 1.)"""
+    rng = np.random.default_rng(77)
+    for m, k, n, group in ((64, 256, 1024, 16), (256, 512, 16384, 8)):
+        w = _small_book(_weight(rng, (k, n), group, scale=1.0), group)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        x[0, 5] = np.float32(3.4e38)                          # past the largest bf16
+        x[2, 9] = np.float32(3.402e38)                        # 2^-12 below FLT_MAX
+        x[2, 100] = np.float32(-3.39e38)
+        x[5, 17] = -np.float32(3.402e38)
+        exact = x.astype(np.float64) @ w.decode().astype(np.float64)
+        assert np.isfinite(exact).all()
+        y = _check(vqdev, oracle, x, w, False, False, "onehot-mfma")
+        assert np.isfinite(y).all()
+        _rows_within(y, exact)
+
+
+def test_dense_bucket_sums_past_float_max_raise_status(vqdev):
+    """The factorised products sum x per code bucket before applying C_B.
+    Where those sums overflow FP32 (a row of activations all near FLT_MAX)
+    the result cannot be formed in FP32 even though the shader's running sum
+    of x b stays finite: status bit 1 refuses the output, never a silent
+    wrong value. onehot-mfma (the bucket sum overflows) and, under the test
+    policy, the fixed-point GEMV (the window's L1 overflows, so no int32
+    scale exists); gemv-direct (the automatic m = 1 choice) multiplies
+    first, like the shader, and returns the finite product."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(78)
+    m, k, n, group = 64, 256, 1024, 16
+    w = _small_book(_weight(rng, (k, n), group, scale=1.0), group)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[0] = np.float32(3.4e38) * np.sign(x[0])
+    words = (2, m, n, k, group, 16, 0, 0)
+    assert vqdev.dense_path_name(words) == "onehot-mfma"
+    say("dense onehot bucket overflow")
+    _, status = _run_status(vqdev, x, w, words)
+    assert status & 1
+    x1 = np.ascontiguousarray(x[:1])
+    words1 = (2, 1, n, k, group, 16, 0, 0)
+    assert vqdev.dense_path_name(words1) == "gemv-direct"
+    say("dense gemv-direct near FLT_MAX")
+    y, status = _run_status(vqdev, x1, w, words1)
+    exact = x1.astype(np.float64) @ w.decode().astype(np.float64)
+    assert status == 0 and o.max_rel(y, exact) <= 1e-5
+    vqdev.device.set_policy(2)
+    try:
+        say("dense gemv-pairs (test policy) L1 overflow")
+        _, status = _run_status(vqdev, x1, w, words1)
+        assert status & 1
     finally:
         vqdev.device.set_policy(0)
 
@@ -187,7 +295,8 @@ DENSE_ONEHOT_SHAPES = [(32, 1024, 1024, 16), (40, 512, 2048, 32), (64, 64, 256, 
 
 @pytest.mark.parametrize("m,k,n,group", DENSE_ONEHOT_SHAPES)
 def test_dense_onehot_mfma(vqdev, oracle, m, k, n, group):
-    """Dense activations on the one-hot MFMA path (64-row blocks): x split
+    """Dense activations on the one-hot MFMA path (64-row blocks on these
+    grids): x split
     into three bf16 terms as it is read; every row within 1e-5 of the float64
     product against its own largest output."""
     from oracle import vq4_numpy as o

@@ -575,20 +575,20 @@ def test_transposed_products_agree_with_float64(vqdev):
         assert o.max_rel(out, _ref64(ops, m, n, k, group, flags)) <= TOL
 
 
-ROW_BINS_SHAPES = [(64, 256, 64, 16), (100, 512, 96, 32), (130, 2048, 256, 16),
-                   (255, 1024, 512, 32), (200, 768, 1024, 16)]
+LARGE_M_SHAPES = [(64, 256, 64, 16), (100, 512, 96, 32), (130, 2048, 256, 16),
+                  (255, 1024, 512, 32), (200, 768, 1024, 16)]
 
 
-@pytest.mark.parametrize("m,n,k,group", ROW_BINS_SHAPES)
-def test_row_bins_within_tolerance(vqdev, oracle, any_size, m, n, k, group):
-    """Large-m product with B's groups along n: wave-uniform codes, bins in
-    registers (rows past m in the last wave are masked). The automatic choice
-    takes onehot-mfma for packed A; the test policy runs the row bins."""
+@pytest.mark.parametrize("m,n,k,group", LARGE_M_SHAPES)
+def test_large_m_under_the_test_policy(vqdev, oracle, any_size, m, n, k, group):
+    """Large-m products with B's groups along n take onehot-mfma by default
+    and under the test policy alike (no bin kernel serves m >= 64); rows past
+    m in the last block are masked."""
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(m + n + k)
     words = (2, m, n, k, group, 16, 0, 0)
     assert vqdev.path_name(words) == "onehot-mfma"
-    say("row-bins", m, n, k, group)
+    say("onehot-mfma (test policy)", m, n, k, group)
     ops = _operands(rng, m, n, k, group, 1.0, 0.02)
     out, status = _gpu(vqdev, ops, m, n, k, group, 0)
     assert status == 0
@@ -612,9 +612,11 @@ ONEHOT_SHAPES = [(16, 1024, 1024, 16), (40, 2048, 512, 32), (63, 4096, 4096, 16)
 def test_onehot_mfma_within_tolerance(vqdev, oracle, m, n, k, group):
     """m >= 64 rows of a packed A (or 16 with B of 2^20 values and k <= 256 m;
     groups along k) times B grouped along n:
-    A's book rows (three fp16 terms) times the one-hot of B's codes on fp16
-    MFMA, then the 16-term product with B's book. Within 1e-5 of the oracle
-    and of the float64 product, every row against its own largest output."""
+    A's book rows (scaled by a power of two and split into three bf16 terms,
+    exact for every entry down to 2^-118 of the largest) times the one-hot of
+    B's codes on bf16 MFMA, then the 16-term product with B's book. Within
+    1e-5 of the oracle and of the float64 product, every row against its own
+    largest output."""
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(m + n + k + group)
     words = (2, m, n, k, group, 16, 0, 0)

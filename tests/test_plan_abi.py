@@ -294,7 +294,8 @@ def test_kernel_path_choice(lib, words, path):
     ((2, 1, 8192, 8192, 16, 16, 0, 0), "gemv-pairs"),
     ((2, 19, 2048, 3072, 8, 16, 0, 0), "gemv-rows"),
     ((2, 5, 2048, 3000, 8, 16, 1, 0), "gemv-direct"),         # ragged k, x stored k x m
-    ((2, 128, 768, 512, 8, 16, 0, 0), "row-bins"),            # dense A: group 8 admitted
+    ((2, 128, 768, 512, 8, 16, 0, 0), "onehot-mfma"),         # dense A: group 8 admitted
+    ((2, 2048, 14336, 4096, 32, 16, 0, 0), "onehot-mfma"),     # config 4 forward, dense X
     ((2, 2048, 4096, 14336, 32, 16, 2, 0), "general"),         # no Gram path for dense A
     ((2, 9, 200, 64, 16, 16, 1, 0), "general")])
 def test_dense_product_path_choice(lib, words, path):

@@ -75,26 +75,6 @@ def test_noalloc_equals_ack_vq_on_consecutive_calls(vqdev, pair):
         np.testing.assert_array_equal(got, want)
 
 
-def test_noalloc_row_bins_under_the_test_policy(vqdev):
-    """Packed large-m products take onehot-mfma by default; under the test
-    policy they run the row bins, whose transposed code words also come from
-    the scratch: equal to ack_vq bit for bit on two calls in a row."""
-    rng = np.random.default_rng(11)
-    vqdev.device.set_policy(2)
-    try:
-        for m, n, k, group in ((128, 4096, 4096, 32), (64, 1024, 1024, 16)):
-            words = (2, m, n, k, group, 16, 0, 0)
-            ops = _operands(rng, m, n, k, group, 0)
-            say("noalloc row-bins", m, n, k, group)
-            rc, got, status = _call(vqdev, "ack_vq_noalloc", words, ops, 4 * m * n)
-            assert rc == 0 and status == 0
-            rc, want, ref_status = _call(vqdev, "ack_vq", words, ops, 4 * m * n)
-            assert rc == 0 and ref_status == 0
-            np.testing.assert_array_equal(got, want)
-    finally:
-        vqdev.device.set_policy(0)
-
-
 def test_noalloc_other_ops_and_status(vqdev, oracle):
     """Ops without a workspace run unchanged; status bits still come back."""
     rng = np.random.default_rng(7)
