@@ -1913,9 +1913,10 @@ MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group,
 }
 
 // The factorised paths' split-k partials (the GEMV kernels take each window's
-// scale from x themselves, so the dense product needs nothing more).
+// scale from x themselves) and onehot-mfma's nibble columns and bf16 planes.
 size_t dense_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                              uint32_t flags, uint32_t count) {
+  if (p == MatmulPath::OneHotMfma) return onehot_dense_workspace_bytes(m, n, k, group);
   return matmul_workspace_bytes(p, m, n, k, group, flags, count);
 }
 

@@ -68,7 +68,12 @@ __device__ __forceinline__ bf16x8 one_hot_column(uint32_t w, uint32_t ee) {
   t |= t >> 2;                                          // bit 4i: nibble i nonzero
   const uint32_t g = (t & 0x11111111u) ^ 0x11111111u;   // bit 4i: nibble i matches
   const uint32_t fe = g & 0x01010101u, fo = (g >> 4) & 0x01010101u;
-  const uint32_t FE = (fe << 8) - fe, FO = (fo << 8) - fo;  // 0xFF bytes: even, odd nibbles
+  // 0xFF bytes where fe, fo hold a 1 (even, odd nibbles). The shifted copies
+  // are opaque so that the compiler keeps a shift and a subtract (full rate)
+  // instead of folding them into v_mul_lo_u32 (quarter rate).
+  uint32_t fe8 = fe << 8, fo8 = fo << 8;
+  asm("" : "+v"(fe8), "+v"(fo8));
+  const uint32_t FE = fe8 - fe, FO = fo8 - fo;
   // dword d: element 0 from nibble 2d (byte d of FE in both of its bytes),
   // element 1 from nibble 2d + 1 (of FO); bf16 1.0 is 0x3F80
   u32x4 v;
@@ -237,10 +242,8 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
   uint32_t wb[4][2];
   wb[0][0] = nc0[0];
   wb[0][1] = nc1[0];
-  if (16 < k) {
-    wb[1][0] = nc0[2];
-    wb[1][1] = nc1[2];
-  }
+  wb[1][0] = nc0[16 < k ? 2 : 0];
+  wb[1][1] = nc1[16 < k ? 2 : 0];
   // the table row of step s_ (both halves of the wave are in one group; the
   // lane's chunk is c8 + h)
   auto a_ptr = [&](const uint32_t (&wd)[kOHX], uint32_t s_, int x) __attribute__((always_inline)) {
@@ -267,34 +270,40 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
         af[x][t] = *reinterpret_cast<const bf16x8*>(pa + t * kTerm);
     }
   }
-  for (uint32_t p0 = 0; p0 < k; p0 += 8 * G) {
+  // Every load of a step is issued unconditionally (indices past the last
+  // step are clamped to it, and the A table and nibbles8 stay in bounds), and
+  // only the ragged last pass can leave the unrolled loop early: a load behind
+  // a branch leaves the compiler unable to count the loads in flight, and it
+  // then waits for all of them, the ones just issued for later steps included.
+  const uint32_t klast = k - 16;  // the last step's first inner index
+  auto pass = [&](uint32_t p0, bool ragged) __attribute__((always_inline)) {
 #pragma unroll
     for (int x = 0; x < kOHX; ++x) {
       aw[x] = an[x];
-      if (!AD && p0 + 8 * G < k) an[x] = nibbles8(a_codes, av[x] + (p0 + 8 * G) / G, a_last);
+      if (!AD) an[x] = nibbles8(a_codes, av[x] + (p0 + 8 * G) / G, a_last);
     }
 #pragma unroll
     for (uint32_t s = 0; s < kSteps; ++s) {
       const uint32_t kk0 = p0 + 16 * s;
-      if (kk0 >= k) break;
-      if (kk0 + 32 < k) {
-        wb[(s + 2) % 4][0] = nc0[(kk0 + 32) / 8];
-        wb[(s + 2) % 4][1] = nc1[(kk0 + 32) / 8];
-      }
-      const bool more = kk0 + 16 < k;
+      if (ragged && kk0 >= k) break;
+      const uint32_t kb = kk0 + 32 < klast ? kk0 + 32 : klast;
+      wb[(s + 2) % 4][0] = nc0[kb / 8];
+      wb[(s + 2) % 4][1] = nc1[kb / 8];
+      const uint32_t kn = kk0 + 16 < klast ? kk0 + 16 : klast;
       const char* pn[kOHX];
 #pragma unroll
       for (int x = 0; x < kOHX; ++x) {
         if (AD) {
           split_bf16x3(xn[x][0], xn[x][1], dead[x], af[x]);
-          if (more) {
-            xn[x][0] = *reinterpret_cast<const float4*>(xr[x] + kk0 + 16);
-            xn[x][1] = *reinterpret_cast<const float4*>(xr[x] + kk0 + 20);
-          }
+          xn[x][0] = *reinterpret_cast<const float4*>(xr[x] + kn);
+          xn[x][1] = *reinterpret_cast<const float4*>(xr[x] + kn + 4);
         } else {
           pn[x] = s + 1 < kSteps ? a_ptr(aw, s + 1, x) : a_ptr(an, 0, x);
         }
       }
+      // the loads for later steps go out before this step's work (left to
+      // itself the scheduler sinks them next to their use and waits on them)
+      __builtin_amdgcn_sched_barrier(0);
       bf16x8 bf[2];
       bf[0] = one_hot_column(wb[s % 4][0], ee);
       bf[1] = one_hot_column(wb[s % 4][1], ee);
@@ -306,14 +315,18 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
 #pragma unroll
           for (int y = 0; y < 2; ++y)
             acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[x][t], bf[y], acc[x][y], 0, 0, 0);
-        if (!AD && more) {
+        if (!AD) {
 #pragma unroll
           for (int x = 0; x < kOHX; ++x)
             af[x][t] = *reinterpret_cast<const bf16x8*>(pn[x] + t * kTerm);
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-  }
+  };
+  const uint32_t whole = k / (8 * G) * (8 * G);  // inner indices of whole passes
+  for (uint32_t p0 = 0; p0 < whole; p0 += 8 * G) pass(p0, false);
+  if (whole < k) pass(whole, true);
 
   // ---- S to LDS, kChunkRows rows at a time (lane: column i32, item t holds
   // row (t % 4) + 4 h + 8 (t / 4) of its 32-row block), then
@@ -370,6 +383,219 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
   if (__any(bad) && lane == 0) atomicOr(o.status, 1u);
 }
 
+// ---- dense activations on large grids: bf16 planes -------------------------
+// Splitting x as it is read repeats the split for every column block that
+// reads the same rows (56 of them at config 4), and that VALU work outweighs
+// the MFMAs. So a pre-pass splits every value once into three bf16 planes
+// (t = hi, mid, lo; rows m .. mp - 1 zero), stored in the MFMA's fragment
+// order: for 32-row block rb and 16-step s of k, one 1 KiB chunk per term in
+// which lane l = (r % 32) + 32 h holds the 8 values of row 32 rb + (r % 32)
+// at inner indices 16 s + 8 h .. + 7. A wave's fragment is then one
+// contiguous 1 KiB read (row-major planes would touch 32 cache lines for 32
+// bytes each, four times the bytes through L2).
+__device__ __forceinline__ uint64_t plane_chunk(uint32_t rb, uint32_t s, uint32_t steps) {
+  return (uint64_t(rb) * steps + s) * 512;  // in bf16 elements: 64 lanes x 8
+}
+
+// One thread per destination lane: chunk i (of mp / 32 * steps) and lane l.
+__global__ __launch_bounds__(256) void k_split_planes(const float* __restrict__ x,
+                                                      __bf16* __restrict__ planes, uint32_t m,
+                                                      uint32_t mp, uint32_t k) {
+  const uint32_t steps = k / 16;
+  const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= uint64_t(mp) * steps * 2) return;  // (mp / 32) * steps chunks of 64 lanes
+  const uint32_t lane = uint32_t(i % 64);
+  const uint64_t chunk = i / 64;
+  const uint32_t rb = uint32_t(chunk / steps), s = uint32_t(chunk % steps);
+  const uint32_t r = 32 * rb + lane % 32, kk = 16 * s + 8 * (lane / 32);
+  float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
+  if (r < m) {
+    const float4* p = reinterpret_cast<const float4*>(x + uint64_t(r) * k + kk);
+    a = p[0];
+    b = p[1];
+  }
+  bf16x8 d[3];
+  split_bf16x3(a, b, false, d);
+  const uint64_t plane = uint64_t(mp) * k, at = plane_chunk(rb, s, steps) + 8 * lane;
+#pragma unroll
+  for (int t = 0; t < kOHTerms; ++t) *reinterpret_cast<bf16x8*>(planes + t * plane + at) = d[t];
+}
+
+// grid: (n / (8 G) word columns of B, mp / (128 X)). The block's 4 waves
+// stack along rows: wave w takes rows 32 X w .. 32 X w + 32 X - 1 of the
+// block's 128 X and all 8 groups of word column q (128 S columns, four 32 x 32
+// blocks y), so each A fragment read from the planes feeds four MFMAs per
+// term and each one-hot fragment X. A fragments are read one step ahead, B's
+// nibble-column words two steps ahead in a ring of four. The epilogue is that
+// of k_onehot_mfma: S through LDS, 32 rows at a time, then the 16-term
+// products with C_B (no scale: the planes hold x itself).
+// Requires k % 16 == 0, n % (8 G) == 0, mp a multiple of 128 X; one instance.
+constexpr uint32_t kPlaneSRow = 132;  // sS row stride in floats: the two row halves of
+                                      // an accumulator write land 16 banks apart
+template <int G, int X>
+__global__ __launch_bounds__(kOHThreads, 2) void k_onehot_planes(
+    Operands o, uint32_t m, uint32_t n, uint32_t k, uint32_t mp, const uint32_t* __restrict__ nc,
+    const __bf16* __restrict__ planes) {
+  static_assert(G == 8 || G == 16 || G == 32, "groups of B");
+  static_assert(X == 1 || X == 2, "row blocks per wave");
+  __shared__ __align__(16) float sS[4][32][kPlaneSRow];
+  __shared__ float sbook[16 * G];
+  const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const uint32_t i32 = lane % 32, h = lane / 32;
+  const uint32_t q = blockIdx.x;
+  const uint32_t row0 = blockIdx.y * (128 * X) + 32 * X * wave;
+  const float* b_book = static_cast<const float*>(o.in[3]);
+  float* out = static_cast<float*>(o.out);
+  bool bad = false;
+  for (uint32_t i = tid; i < 16 * G; i += kOHThreads) {
+    const float b = b_book[i];
+    sbook[i] = b;
+    if (blockIdx.x == 0 && blockIdx.y == 0) bad |= !finite_f32(b);
+  }
+  // the lane's S columns: code i32 % 16 of groups 8 q + 2 y + i32 / 16
+  const uint32_t ee = (i32 % 16) * 0x11111111u;
+  const uint32_t k8 = k / 8;
+  const uint32_t* ncl = nc + uint64_t(8 * q + i32 / 16) * k8 + h;  // group of y: + 2 y k8
+  // the lane's 16 bytes of each fragment chunk; block x: + x steps chunks,
+  // step s: + s chunks, term t: + t planes
+  const uint64_t plane = uint64_t(mp) * k;
+  const uint32_t steps = k / 16;
+  const __bf16* pa = planes + plane_chunk(row0 / 32, 0, steps) + 8 * lane;
+  const uint64_t xstride = plane_chunk(1, 0, steps);
+
+  f32x16 acc[X][4];
+#pragma unroll
+  for (int x = 0; x < X; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y) acc[x][y] = (f32x16)0.0f;
+  // Loads as in k_onehot_mfma: unconditional (indices clamped to the last
+  // step), and only the last 0-3 steps, past the whole groups of four, are
+  // taken outside the unrolled loop. B's nibble-column words are read three
+  // steps ahead (a ring of four), A's fragments one step ahead, and the
+  // one-hot fragments of the next step are built between this step's MFMAs,
+  // so their VALU work runs while the matrix core is busy.
+  const uint32_t klast = k - 16;
+  uint32_t wb[4][4];
+  bf16x8 fa[2][X][kOHTerms];
+  bf16x8 bf[2][4];
+#pragma unroll
+  for (int y = 0; y < 4; ++y) {
+#pragma unroll
+    for (uint32_t s = 0; s < 3; ++s) wb[s][y] = ncl[2 * y * k8 + (16 * s < k ? 2 * s : 0)];
+    bf[0][y] = one_hot_column(wb[0][y], ee);
+  }
+#pragma unroll
+  for (int x = 0; x < X; ++x)
+#pragma unroll
+    for (int t = 0; t < kOHTerms; ++t)
+      fa[0][x][t] = *reinterpret_cast<const bf16x8*>(pa + t * plane + x * xstride);
+  auto step = [&](uint32_t kk0, uint32_t s) __attribute__((always_inline)) {
+    const uint32_t kb = kk0 + 48 < klast ? kk0 + 48 : klast;
+#pragma unroll
+    for (int y = 0; y < 4; ++y) wb[(s + 3) % 4][y] = ncl[2 * y * k8 + kb / 8];
+    const uint32_t kn = kk0 + 16 < klast ? kk0 + 16 : klast;
+#pragma unroll
+    for (int x = 0; x < X; ++x)
+#pragma unroll
+      for (int t = 0; t < kOHTerms; ++t)
+        fa[(s + 1) % 2][x][t] = *reinterpret_cast<const bf16x8*>(
+            pa + t * plane + x * xstride + plane_chunk(0, kn / 16, steps));
+    // keep the loads for later steps ahead of this step's work: left to
+    // itself the scheduler sinks them next to their use and waits on them
+    __builtin_amdgcn_sched_barrier(0);
+    // terms smallest first: lo, mid, hi
+#pragma unroll
+    for (int t = kOHTerms - 1; t >= 0; --t)
+#pragma unroll
+      for (int x = 0; x < X; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y)
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s % 2][x][t], bf[s % 2][y],
+                                                              acc[x][y], 0, 0, 0);
+#pragma unroll
+    for (int y = 0; y < 4; ++y) bf[(s + 1) % 2][y] = one_hot_column(wb[(s + 1) % 4][y], ee);
+    // interleave: one MFMA, then up to four VALU instructions
+#pragma unroll
+    for (int i = 0; i < kOHTerms * X * 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  const uint32_t four = steps / 4 * 4;
+  for (uint32_t k0 = 0; k0 < 16 * four; k0 += 64) {
+#pragma unroll
+    for (uint32_t s = 0; s < 4; ++s) step(k0 + 16 * s, s);
+  }
+#pragma unroll
+  for (uint32_t s = 0; s < 3; ++s)
+    if (four + s < steps) step(16 * (four + s), s);
+
+  // ---- S to LDS one 32-row block at a time (item t of acc[x][y] is row
+  // (t % 4) + 4 h + 8 (t / 4), column 32 y + i32), then
+  // y[r][G j + t] = sum_e S[r][(j, e)] C_B[e][t], e ascending; a lane's t is
+  // fixed (64 is a multiple of G)
+  __syncthreads();  // sbook
+  const uint32_t tc = lane % G;
+  float cb[16];
+#pragma unroll
+  for (int f = 0; f < 16; ++f) cb[f] = sbook[f * G + tc];
+#pragma unroll
+  for (int x = 0; x < X; ++x) {
+    if (x) __syncthreads();  // the previous block's S has been read
+#pragma unroll
+    for (int y = 0; y < 4; ++y)
+#pragma unroll
+      for (int t = 0; t < 16; ++t)
+        sS[wave][(t % 4) + 4 * h + 8 * (t / 4)][32 * y + i32] = acc[x][y][t];
+    __syncthreads();
+    for (uint32_t idx = lane; idx < 32 * 8 * G; idx += 64) {
+      const uint32_t row = idx / (8 * G), j = (idx / G) % 8;
+      const uint32_t r = row0 + 32 * x + row;
+      if (r >= m) break;
+      const float4* sp = reinterpret_cast<const float4*>(&sS[wave][row][16 * j]);
+      const float4 s0 = sp[0], s1 = sp[1], s2 = sp[2], s3 = sp[3];
+      float yv = 0.0f;
+      yv = fmaf(s0.x, cb[0], yv);
+      yv = fmaf(s0.y, cb[1], yv);
+      yv = fmaf(s0.z, cb[2], yv);
+      yv = fmaf(s0.w, cb[3], yv);
+      yv = fmaf(s1.x, cb[4], yv);
+      yv = fmaf(s1.y, cb[5], yv);
+      yv = fmaf(s1.z, cb[6], yv);
+      yv = fmaf(s1.w, cb[7], yv);
+      yv = fmaf(s2.x, cb[8], yv);
+      yv = fmaf(s2.y, cb[9], yv);
+      yv = fmaf(s2.z, cb[10], yv);
+      yv = fmaf(s2.w, cb[11], yv);
+      yv = fmaf(s3.x, cb[12], yv);
+      yv = fmaf(s3.y, cb[13], yv);
+      yv = fmaf(s3.z, cb[14], yv);
+      yv = fmaf(s3.w, cb[15], yv);
+      out[uint64_t(r) * n + (8 * q + j) * G + tc] = yv;
+      bad |= !finite_f32(yv);
+    }
+  }
+  if (__any(bad) && lane == 0) atomicOr(o.status, 1u);
+}
+
+// Dense activations take the bf16 planes (k_onehot_planes) once the grid of
+// 128 X-row blocks has kOHBigGrid blocks: X = 2 (256 rows) where that grid is
+// large enough, else X = 1 (128 rows); smaller grids split x as they read it
+// (k_onehot_mfma with 64-row blocks), where the pre-pass would not pay.
+uint32_t dense_planes_x(uint32_t m, uint32_t n, uint32_t group) {
+  const uint64_t cols = n / (8 * group);
+  if (cols * ((m + 255) / 256) >= kOHBigGrid) return 2;
+  if (cols * ((m + 127) / 128) >= kOHBigGrid) return 1;
+  return 0;
+}
+
+uint32_t planes_rows(uint32_t m, uint32_t px) { return (m + 128 * px - 1) / (128 * px) * (128 * px); }
+
+size_t nc_bytes(uint32_t n, uint32_t k, uint32_t group) {
+  return (size_t(n / group) * (k / 8) * 4 + 255) / 256 * 256;
+}
+
 }  // namespace
 
 // From kOneHotMinRows rows of A always; from 16 rows when B holds at least
@@ -391,6 +617,12 @@ size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group) {
   return size_t(n / group) * (k / 8) * 4;
 }
 
+size_t onehot_dense_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t group) {
+  const uint32_t px = dense_planes_x(m, n, group);
+  if (px == 0) return onehot_workspace_bytes(n, k, group);
+  return nc_bytes(n, k, group) + size_t(kOHTerms) * planes_rows(m, px) * k * sizeof(__bf16);
+}
+
 namespace {
 
 template <int G, int X, bool AD>
@@ -404,19 +636,23 @@ uint64_t big_grid(uint32_t m, uint32_t n, uint32_t group) {
   return uint64_t(n / (8 * group)) * ((m + 255) / 256);
 }
 
-// The dense grid's row blocks: 128 rows (X = 2: each one-hot fragment feeds
-// two row blocks, and each split of x into bf16 terms feeds the wave's two
-// column blocks) once that grid holds kOHBigGrid blocks; 64 rows (X = 1, four
-// blocks per CU) below.
-uint64_t dense_grid_x2(uint32_t m, uint32_t n, uint32_t group) {
-  return uint64_t(n / (8 * group)) * ((m + 127) / 128);
+template <int G>
+void launch_planes(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
+                   uint32_t px, const uint32_t* nc, __bf16* planes) {
+  const uint32_t mp = planes_rows(m, px);
+  const uint64_t lanes = uint64_t(mp) * (k / 16) * 2;  // 64 lanes per (32 rows, 16-step)
+  k_split_planes<<<dim3(uint32_t((lanes + 255) / 256)), 256, 0, s>>>(
+      static_cast<const float*>(o.in[0]), planes, m, mp, k);
+  dim3 grid(n / (8 * G), mp / (128 * px));
+  if (px == 2) k_onehot_planes<G, 2><<<grid, kOHThreads, 0, s>>>(o, m, n, k, mp, nc, planes);
+  else k_onehot_planes<G, 1><<<grid, kOHThreads, 0, s>>>(o, m, n, k, mp, nc, planes);
 }
 
 template <int G>
 void launch_onehot_g(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
-                     bool dense, const uint32_t* nc) {
+                     bool dense, const uint32_t* nc, __bf16* planes) {
   if (dense) {
-    if (dense_grid_x2(m, n, G) >= kOHBigGrid) launch_onehot_x<G, 2, true>(s, o, m, n, k, nc);
+    if (const uint32_t px = dense_planes_x(m, n, G)) launch_planes<G>(s, o, m, n, k, px, nc, planes);
     else launch_onehot_x<G, 1, true>(s, o, m, n, k, nc);
   } else if (big_grid(m, n, G) >= kOHBigGrid) {
     launch_onehot_x<G, 4, false>(s, o, m, n, k, nc);
@@ -429,9 +665,9 @@ void launch_onehot_g(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, u
 // would straddle its groups).
 template <>
 void launch_onehot_g<8>(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
-                        bool dense, const uint32_t* nc) {
+                        bool dense, const uint32_t* nc, __bf16* planes) {
   (void)dense;
-  if (dense_grid_x2(m, n, 8) >= kOHBigGrid) launch_onehot_x<8, 2, true>(s, o, m, n, k, nc);
+  if (const uint32_t px = dense_planes_x(m, n, 8)) launch_planes<8>(s, o, m, n, k, px, nc, planes);
   else launch_onehot_x<8, 1, true>(s, o, m, n, k, nc);
 }
 
@@ -457,9 +693,10 @@ hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
   k_nibble_columns<<<ngrid, 256, 0, s>>>(static_cast<const uint32_t*>(o.in[2]), nc, k, rw);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (group == 8) launch_onehot_g<8>(s, o, m, n, k, dense, nc);
-  else if (group == 16) launch_onehot_g<16>(s, o, m, n, k, dense, nc);
-  else launch_onehot_g<32>(s, o, m, n, k, dense, nc);
+  __bf16* planes = reinterpret_cast<__bf16*>(static_cast<char*>(workspace) + nc_bytes(n, k, group));
+  if (group == 8) launch_onehot_g<8>(s, o, m, n, k, dense, nc, planes);
+  else if (group == 16) launch_onehot_g<16>(s, o, m, n, k, dense, nc, planes);
+  else launch_onehot_g<32>(s, o, m, n, k, dense, nc, planes);
   return hipGetLastError();
 }
 
