@@ -74,6 +74,54 @@ _TRANSFER_TYPES = frozenset([("b", 1)] + [(k, s) for k in "iu" for s in (1, 2, 4
 
 _P, _U32, _U64, _I32, _SZ = (ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32,
                              ctypes.c_size_t)
+
+
+class AckAbiInfo(ctypes.Structure):
+    """What ``ack_abi_info`` fills in: the layout of the reference's struct
+    (src/alelyon_compute_kit/_kit/src/ffi.rs:1005-1060). This library holds
+    the vq4/v1 entries only: its operator bits, operator schemas and
+    capabilities are 0, which the reference defines as absent."""
+
+    _fields_ = [("size", ctypes.c_uint32), ("version", ctypes.c_uint32),
+                ("operators", ctypes.c_uint64), ("shaders", ctypes.c_uint64),
+                ("build", ctypes.c_uint64)] + [
+        (name, ctypes.c_uint32) for name in (
+            "op_schema_matmul_bf16", "op_schema_cast", "capability_streams", "capability_rng",
+            "capability_optimizer", "capability_serialization", "op_schema_matmul_f32",
+            "op_schema_pointwise", "op_schema_reduce", "op_schema_rowwise", "op_schema_loss",
+            "op_schema_embedding", "op_schema_matmul_f16", "op_schema_index",
+            "op_schema_convert", "op_schema_intwise")]
+
+
+class AckDeviceInfo(ctypes.Structure):
+    """What ``ack_device_info`` fills in for an open device: the layout of the
+    reference's struct (ffi.rs:1212-1250), its values from the HIP runtime."""
+
+    _fields_ = [(name, ctypes.c_uint32) for name in (
+        "size", "version", "api_version", "driver_version_raw", "driver_id", "vendor_id",
+        "device_id", "device_type")] + [
+        ("device_uuid", ctypes.c_uint8 * 16), ("driver_uuid", ctypes.c_uint8 * 16),
+        ("features", ctypes.c_uint64), ("subgroup_size", ctypes.c_uint32),
+        ("timestamp_valid_bits", ctypes.c_uint32), ("timestamp_period_ns", ctypes.c_float),
+        ("max_push_constant_bytes", ctypes.c_uint32), ("device_local_bytes", ctypes.c_uint64),
+        ("max_storage_buffer_bytes", ctypes.c_uint64),
+        ("max_workgroup_invocations", ctypes.c_uint32),
+        ("max_workgroup_count", ctypes.c_uint32 * 3), ("max_workgroup_size", ctypes.c_uint32 * 3)] + [
+        (name, ctypes.c_uint32) for name in (
+            "matmul_tile", "matmul_k_multiple", "matmul_layouts", "matmul_operand_dtype",
+            "matmul_result_dtype", "cast_modes", "reserved")] + [
+        ("identity", ctypes.c_uint64), ("device_name", ctypes.c_char * 256),
+        ("driver_name", ctypes.c_char * 64), ("driver_info", ctypes.c_char * 128)]
+
+
+# the reference's feature bits (ffi.rs:983-1000) and dtype codes (:1002-1003)
+ACK_FEATURE_BITS = {
+    "cooperative_matrix": 1, "bf16_type": 2, "bf16_dot_product": 4,
+    "bf16_cooperative_matrix": 8, "subgroup_size_control": 16,
+    "coopmat_bf16_16x16x16_subgroup": 32, "shader_int16": 64, "shader_float16": 128,
+    "coopmat_f16_16x16x16_subgroup": 256,
+}
+ACK_DTYPE_NAMES = {1: "bf16", 2: "f32"}
 # name: (argument types, result type), as include/ack_vq.h declares them
 _ENTRY_POINTS = {
     "ack_vq_schema": ((), _U32),
@@ -102,6 +150,8 @@ _ENTRY_POINTS = {
     "ack_vq_fit_codebook": ((_P,) * 5 + (_U64, _U32, _U32, _U32), _I32),
     "ack_vq_matmul_dense": ((_P,) * 7 + (_SZ,), _I32),
     "ack_vq_adamw_step": ((_P,) * 9 + (_SZ, _U32, _U32), _I32),
+    "ack_abi_info": ((ctypes.POINTER(AckAbiInfo), _SZ), _I32),
+    "ack_device_info": ((_P, ctypes.POINTER(AckDeviceInfo), _SZ), _I32),
 }
 
 
@@ -268,12 +318,18 @@ class Device:
         self.close()
 
     # -- stream control and diagnostics ----------------------------------------
-    def capability_record(self) -> dict:
-        """What this device and library declare, JSON-serialisable."""
+    def info(self) -> AckDeviceInfo:
+        """``ack_device_info`` of this device."""
+        out = AckDeviceInfo()
         with self.lock:
-            self.handle
-            return {"device": self.name, "library": str(self.lib.path),
-                    "vq_schema": int(self.lib.cdll.ack_vq_schema())}
+            self.lib.check(self.lib.cdll.ack_device_info(self.handle, ctypes.byref(out),
+                                                         ctypes.sizeof(out)), "device info")
+        return out
+
+    def capability_record(self) -> dict:
+        """The record of what this run ran on, in the reference's shape
+        (``capability_record(abi_info(), self.info())``)."""
+        return capability_record(abi_info(self.lib), self.info())
 
     def synchronize(self) -> None:
         self.call("ack_sync", context="sync")
@@ -353,3 +409,92 @@ class Buffer:
         handle, self._handle = self._handle, None
         self._finalizer.detach()
         self._device._release(handle)
+
+
+def abi_info(lib: Library | None = None) -> AckAbiInfo:
+    """``ack_abi_info`` of the loaded library."""
+    lib = lib or library()
+    out = AckAbiInfo()
+    lib.check(lib.cdll.ack_abi_info(ctypes.byref(out), ctypes.sizeof(out)), "abi info")
+    return out
+
+
+def _api_version_string(packed: int) -> str:
+    return f"{(packed >> 22) & 0x7F}.{(packed >> 12) & 0x3FF}.{packed & 0xFFF}"
+
+
+def capability_record(abi: AckAbiInfo, info: AckDeviceInfo) -> dict:
+    """A JSON-serialisable record of what a run ran on, with the keys of the
+    reference's record (src/alelyon_compute_kit/_kit/python/ack.py:527-596)
+    plus ``abi.vq_schema`` (the vq4 schema this library serves). Every value
+    is declared by this library and the HIP runtime; the operator families the
+    reference lists are absent here (0)."""
+    lib = library()
+    return {
+        "schema": 1,
+        "abi": {
+            "version": abi.version,
+            "operators": abi.operators,
+            "vq_schema": int(lib.cdll.ack_vq_schema()),
+            "op_schema_matmul_bf16": abi.op_schema_matmul_bf16,
+            "op_schema_cast": abi.op_schema_cast,
+            "op_schema_matmul_f32": abi.op_schema_matmul_f32,
+            "op_schema_matmul_f16": abi.op_schema_matmul_f16,
+            "op_schema_index": abi.op_schema_index,
+            "op_schema_convert": abi.op_schema_convert,
+            "op_schema_intwise": abi.op_schema_intwise,
+            "op_schema_pointwise": abi.op_schema_pointwise,
+            "reserved_op_schemas": {
+                "reduce": abi.op_schema_reduce,
+                "rowwise": abi.op_schema_rowwise,
+                "loss": abi.op_schema_loss,
+                "embedding": abi.op_schema_embedding,
+            },
+            "shaders": f"{abi.shaders:016x}",
+            "build": f"{abi.build:016x}",
+            "capabilities": {
+                "streams": abi.capability_streams,
+                "rng": abi.capability_rng,
+                "optimizer": abi.capability_optimizer,
+                "serialization": abi.capability_serialization,
+            },
+        },
+        "device": {
+            "name": info.device_name.decode("utf-8", errors="replace"),
+            "vendor_id": info.vendor_id,
+            "device_id": info.device_id,
+            "device_type": info.device_type,
+            "device_uuid": bytes(info.device_uuid).hex(),
+            "driver_uuid": bytes(info.driver_uuid).hex(),
+            "driver_id": info.driver_id,
+            "driver_version_raw": info.driver_version_raw,
+            "driver_name": info.driver_name.decode("utf-8", errors="replace"),
+            "driver_info": info.driver_info.decode("utf-8", errors="replace"),
+            "api_version": _api_version_string(info.api_version),
+            "features": sorted(name for name, bit in ACK_FEATURE_BITS.items()
+                               if info.features & bit),
+            "subgroup_size": info.subgroup_size,
+            "timestamp_valid_bits": info.timestamp_valid_bits,
+            "timestamp_period_ns": info.timestamp_period_ns,
+            "device_local_bytes": info.device_local_bytes,
+            "limits": {
+                "max_storage_buffer_bytes": info.max_storage_buffer_bytes,
+                "max_push_constant_bytes": info.max_push_constant_bytes,
+                "max_workgroup_invocations": info.max_workgroup_invocations,
+                "max_workgroup_count": list(info.max_workgroup_count),
+                "max_workgroup_size": list(info.max_workgroup_size),
+            },
+            "matmul": {
+                "tile": info.matmul_tile,
+                "k_multiple": info.matmul_k_multiple,
+                "layouts": [n for i, n in enumerate(("NN", "NT", "TN", "TT"))
+                            if info.matmul_layouts & (1 << i)],
+                "operand_dtype": ACK_DTYPE_NAMES.get(info.matmul_operand_dtype,
+                                                     info.matmul_operand_dtype),
+                "result_dtype": ACK_DTYPE_NAMES.get(info.matmul_result_dtype,
+                                                    info.matmul_result_dtype),
+            },
+            "cast_modes": info.cast_modes,
+            "identity": f"{info.identity:016x}",
+        },
+    }

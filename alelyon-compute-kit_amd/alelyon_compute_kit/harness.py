@@ -529,13 +529,16 @@ def main(argv=None) -> int:
     parser.add_argument("--lr", type=float, default=1e-3)
     parser.add_argument("--max-grad-norm", type=float, default=1.0)
     parser.add_argument("--device", action="store_true", help="explicitly open the GPU")
+    parser.add_argument("--resident", action="store_true",
+                        help="keep the expert's optimizer state on the GPU between steps "
+                             "(the same commits as without it)")
     parser.add_argument("--force", action="store_true")
     args = parser.parse_args(argv)
     if not args.device:
         parser.error("--device is required; execution is never implicit")
     inputs = _read_matrix(args.input, "input")
     where = {"layer": args.layer, "expert": args.expert}
-    with ExpertHarness.open(args.bank) as runner:
+    with ExpertHarness.open(args.bank, resident=args.resident) as runner:
         report = {"device": runner._device.capability_record(), "model_quality_validated": False}
         if args.target is not None:
             targets = _read_matrix(args.target, "target")

@@ -50,11 +50,22 @@ def _run(cmd: list[str]) -> None:
         raise SystemExit(f"build failed: {' '.join(cmd)}")
 
 
+def shaders_id() -> int:
+    """FNV-1a over the kernel sources (HIP files and headers, in name order):
+    the `shaders` identity ack_abi_info reports for this build."""
+    h = 0xCBF29CE484222325
+    for path in sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.hpp")), key=lambda p: p.name):
+        for b in path.read_bytes():
+            h = ((h ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
 def _compile(source: str) -> Path:
     obj = BUILD / (Path(source).stem + ".o")
     src = CSRC / source
     if source in HIP_SOURCES or source == PROBE_SOURCE:
-        cmd = [HIPCC, *HIP_FLAGS, *COMMON, "-c", str(src), "-o", str(obj)]
+        defines = [f"-DACK_SHADERS_ID=0x{shaders_id():016x}ull"] if source == "abi.cpp" else []
+        cmd = [HIPCC, *HIP_FLAGS, *COMMON, *defines, "-c", str(src), "-o", str(obj)]
     else:
         cmd = ["g++", *COMMON, "-c", str(src), "-o", str(obj)]
     _run(cmd)

@@ -15,6 +15,7 @@
 
 #include <atomic>
 #include <cstdarg>
+#include <cstddef>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -159,8 +160,8 @@ size_t round_up(size_t bytes) { return (bytes + 255) / 256 * 256; }
 
 // ---- the allocation-free entry's scratch ----------------------------------------
 // ack_vq_noalloc takes the workspace of the paths that need one (the GEMV's
-// split-k partials, gemv-direct's slice partials, row-bins' transposed code
-// words, onehot-mfma's nibble columns) from this array instead
+// split-k partials, gemv-direct's slice partials, onehot-mfma's nibble
+// columns) from this array instead
 // of allocating it. Every GPU the library runs on holds its own copy until
 // the process ends. In host code `scratch` names a host-side stand-in, never
 // a device address: the address is resolved per GPU with
@@ -172,6 +173,18 @@ constexpr int kMaxGpus = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxGpus] = {};
 bool g_scratch_done[kMaxGpus] = {};
+
+// The scratch of a GPU belongs to one device handle at a time: the handle
+// whose ack_vq_noalloc launch used it last, with an event recorded on that
+// handle's stream after the launch. Calls on one handle are ordered by its
+// stream; another handle's call is refused while the event is pending, so
+// two handles never have work on one GPU's scratch at the same time. Claim,
+// launch and record happen under g_scratch_mu.
+struct ScratchOwner {
+  uint64_t device = 0;      // id of the owning handle, 0 before the first use
+  hipEvent_t done = nullptr;  // recorded after the owner's last launch
+};
+ScratchOwner g_scratch_owner[kMaxGpus];
 
 // This GPU's `scratch`, resolved once per GPU with that GPU current (the
 // caller has selected it). Null when resolution failed.
@@ -285,6 +298,34 @@ int32_t run_vq(const AckDevice* handle, const AckBuffer* const slots[6], const u
         }
         work = dev->scratch;
         work_bytes = kScratchBytes;
+        if (ws > 0) {  // the path writes the scratch: claim it, launch, mark the launch's end
+          std::lock_guard<std::mutex> own_lock(g_scratch_mu);
+          ScratchOwner& own = g_scratch_owner[dev->hip_device];
+          if (own.device != 0 && own.device != dev->id && own.done != nullptr) {
+            const hipError_t q = hipEventQuery(own.done);
+            (void)hipGetLastError();  // a pending query must not read as a launch failure
+            if (q == hipErrorNotReady) {
+              set_error("vq noalloc: this GPU's scratch is in use by device handle " +
+                        std::to_string(own.device) +
+                        " (its enqueued ack_vq_noalloc work has not finished); synchronize "
+                        "that handle first, or use ack_vq");
+              return ACK_ERR_DEVICE;
+            }
+          }
+          if (own.done == nullptr) {
+            he = hipEventCreateWithFlags(&own.done, hipEventDisableTiming);
+            if (he != hipSuccess) {
+              own.done = nullptr;
+              return hip_failure(*dev, "vq noalloc: scratch event", he, false);
+            }
+          }
+          he = ackvq::launch_matmul(dev->stream, o, m, n, k, g, plan.flags(), path, work,
+                                    work_bytes);
+          if (he == hipSuccess) he = hipEventRecord(own.done, dev->stream);
+          if (he != hipSuccess) return hip_failure(*dev, "vq: kernel launch refused", he, false);
+          own.device = dev->id;
+          return ACK_OK;
+        }
       } else {
         if (int32_t rc = ensure_workspace(*dev, ws)) return rc;
         work = dev->workspace;
@@ -452,6 +493,105 @@ int32_t ack_device_name(const AckDevice* handle, char* out, size_t len) {
   const size_t n = dev->name.size() < len - 1 ? dev->name.size() : len - 1;
   std::memcpy(out, dev->name.data(), n);
   out[n] = '\0';
+  return ACK_OK;
+}
+
+// FNV-1a over a byte stream (the reference's identity hash, ffi.rs:1419).
+static uint64_t fnv1a(uint64_t h, const void* data, size_t len) {
+  const unsigned char* p = static_cast<const unsigned char*>(data);
+  for (size_t i = 0; i < len; ++i) {
+    h ^= p[i];
+    h *= 0x00000100000001b3ull;
+  }
+  return h;
+}
+constexpr uint64_t kFnvBasis = 0xcbf29ce484222325ull;
+// The kernel sources' hash, from the build (build.py); 0 in a build without it.
+#ifndef ACK_SHADERS_ID
+#define ACK_SHADERS_ID 0ull
+#endif
+static_assert(sizeof(AckAbiInfo) == 96, "the layout of ffi.rs AckAbiInfo");
+static_assert(sizeof(AckDeviceInfo) == 616 && offsetof(AckDeviceInfo, identity) == 160,
+              "the layout of ffi.rs AckDeviceInfo");
+constexpr uint32_t kAbiLayoutVersion = 14;  // the AckAbiInfo layout's ABI version
+constexpr uint32_t kDeviceInfoVersion = 1;
+
+int32_t ack_abi_info(AckAbiInfo* out, size_t size) {
+  if (out == nullptr) return ACK_ERR_NULL;
+  if (size < sizeof(AckAbiInfo)) {
+    set_error("AckAbiInfo of " + std::to_string(size) + " bytes is smaller than this library's " +
+              std::to_string(sizeof(AckAbiInfo)));
+    return ACK_ERR_ABI;
+  }
+  AckAbiInfo info;
+  std::memset(&info, 0, sizeof info);  // no operator family, schema or capability: 0 (absent)
+  info.size = sizeof(AckAbiInfo);
+  info.version = kAbiLayoutVersion;
+  info.shaders = ACK_SHADERS_ID;
+  const char kName[] = "libackvq vq4/v1 gfx950";
+  const uint64_t shaders = info.shaders;
+  info.build = fnv1a(fnv1a(kFnvBasis, kName, sizeof kName - 1), &shaders, sizeof shaders);
+  std::memcpy(out, &info, sizeof info);
+  return ACK_OK;
+}
+
+int32_t ack_device_info(const AckDevice* handle, AckDeviceInfo* out, size_t size) {
+  if (out == nullptr) return ACK_ERR_NULL;
+  if (size < sizeof(AckDeviceInfo)) {
+    set_error("AckDeviceInfo of " + std::to_string(size) + " bytes is smaller than this library's " +
+              std::to_string(sizeof(AckDeviceInfo)));
+    return ACK_ERR_ABI;
+  }
+  std::shared_ptr<Device> dev;
+  std::unique_lock<std::mutex> lock;
+  if (int32_t rc = enter(handle, &dev, &lock, false)) return rc;
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, dev->hip_device);
+  int chip = 0, wall_khz = 0, runtime = 0, driver = 0;
+  hipUUID uuid;
+  std::memset(&uuid, 0, sizeof uuid);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&chip, hipDeviceAttributePciChipId, dev->hip_device);
+  if (e == hipSuccess)
+    e = hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, dev->hip_device);
+  if (e == hipSuccess) e = hipRuntimeGetVersion(&runtime);
+  if (e == hipSuccess) e = hipDriverGetVersion(&driver);
+  if (e == hipSuccess) e = hipDeviceGetUuid(&uuid, dev->hip_device);
+  if (e != hipSuccess) return hip_failure(*dev, "device info", e, false);
+  AckDeviceInfo info;
+  std::memset(&info, 0, sizeof info);
+  info.size = sizeof(AckDeviceInfo);
+  info.version = kDeviceInfoVersion;
+  // HIP's version number is major * 10^7 + minor * 10^5 + patch
+  const uint32_t major = uint32_t(runtime / 10000000), minor = uint32_t(runtime / 100000 % 100),
+                 patch = uint32_t(runtime % 100000);
+  info.api_version = (major << 22) | ((minor & 0x3FFu) << 12) | (patch & 0xFFFu);
+  info.driver_version_raw = uint32_t(driver);
+  info.vendor_id = 0x1002;  // AMD
+  info.device_id = uint32_t(chip);
+  info.device_type = 2;  // discrete GPU
+  std::memcpy(info.device_uuid, uuid.bytes, 16);
+  // cooperative matrix (1), bf16 type (2), bf16 dot product (4), bf16 matrix
+  // (8), bf16 16x16x16 (32), int16 (64), fp16 (128), fp16 16x16x16 (256)
+  info.features = 1u | 2u | 4u | 8u | 32u | 64u | 128u | 256u;
+  info.subgroup_size = uint32_t(prop.warpSize);
+  info.timestamp_valid_bits = 64;
+  info.timestamp_period_ns = wall_khz > 0 ? float(1e6 / wall_khz) : 0.0f;
+  info.max_push_constant_bytes = 4096;  // kernel argument space
+  info.device_local_bytes = uint64_t(prop.totalGlobalMem);
+  info.max_storage_buffer_bytes = uint64_t(prop.totalGlobalMem);
+  info.max_workgroup_invocations = uint32_t(prop.maxThreadsPerBlock);
+  for (int i = 0; i < 3; ++i) {
+    info.max_workgroup_count[i] = uint32_t(prop.maxGridSize[i]);
+    info.max_workgroup_size[i] = uint32_t(prop.maxThreadsDim[i]);
+  }
+  const uint64_t shaders = ACK_SHADERS_ID;
+  info.identity = fnv1a(fnv1a(kFnvBasis, reinterpret_cast<const char*>(&info) + 8, 152), &shaders,
+                        sizeof shaders);
+  std::snprintf(info.device_name, sizeof info.device_name, "%s", dev->name.c_str());
+  std::snprintf(info.driver_name, sizeof info.driver_name, "HIP (ROCm)");
+  std::snprintf(info.driver_info, sizeof info.driver_info, "HIP runtime %d, driver %d, %s", runtime,
+                driver, prop.gcnArchName);
+  std::memcpy(out, &info, sizeof info);
   return ACK_OK;
 }
 

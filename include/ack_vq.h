@@ -83,6 +83,91 @@ int32_t ack_device_name(const AckDevice* dev, char* out, size_t len);
 /* Replaces ack_last_error (ffi.rs:3325-3339): this thread's last message. */
 int32_t ack_last_error(char* out, size_t len);
 
+/* The library's ABI description, the layout of ffi.rs:1005-1060 (96 bytes).
+ * This library implements the vq4/v1 entries only, so `operators`, every
+ * op_schema_* and every capability_* read 0 (absent, as the reference
+ * defines 0); `version` is the layout's ABI version (14); `shaders` is a
+ * hash of the kernel sources this library was built from and `build` the
+ * FNV-1a of the library name and that hash. */
+typedef struct AckAbiInfo {
+  uint32_t size;
+  uint32_t version;
+  uint64_t operators;
+  uint64_t shaders;
+  uint64_t build;
+  uint32_t op_schema_matmul_bf16;
+  uint32_t op_schema_cast;
+  uint32_t capability_streams;
+  uint32_t capability_rng;
+  uint32_t capability_optimizer;
+  uint32_t capability_serialization;
+  uint32_t op_schema_matmul_f32;
+  uint32_t op_schema_pointwise;
+  uint32_t op_schema_reduce;
+  uint32_t op_schema_rowwise;
+  uint32_t op_schema_loss;
+  uint32_t op_schema_embedding;
+  uint32_t op_schema_matmul_f16;
+  uint32_t op_schema_index;
+  uint32_t op_schema_convert;
+  uint32_t op_schema_intwise;
+} AckAbiInfo;
+
+/* Replaces ack_abi_info (ffi.rs:1981-2027): ACK_ERR_NULL for a null `out`,
+ * ACK_ERR_ABI when `size` is smaller than this library's struct. */
+int32_t ack_abi_info(AckAbiInfo* out, size_t size);
+
+/* An open device's identity and limits, the layout of ffi.rs:1212-1250
+ * (616 bytes), filled from the HIP runtime: vendor and PCI product ids, the
+ * device UUID (the driver UUID has no HIP counterpart and reads zero), HIP
+ * runtime and driver versions (api_version packed major << 22 | minor << 12
+ * | patch as the reference packs Vulkan's), device type 2 (discrete GPU),
+ * feature bits for what the hardware has (matrix cores with bf16 and fp16
+ * 16x16x16 shapes, bf16 and 16-bit types, bf16 dot products; no subgroup
+ * size control: waves are 64 wide), wave size, the 64-bit wall clock,
+ * global memory, launch limits. The matmul and cast fields describe the
+ * reference's bf16 matmul and cast families, which this library does not
+ * implement: they read 0. `identity` is FNV-1a over bytes 8 to 160 and then
+ * the library's `shaders` hash, as the reference defines it. */
+typedef struct AckDeviceInfo {
+  uint32_t size;
+  uint32_t version;
+  uint32_t api_version;
+  uint32_t driver_version_raw;
+  uint32_t driver_id;
+  uint32_t vendor_id;
+  uint32_t device_id;
+  uint32_t device_type;
+  uint8_t device_uuid[16];
+  uint8_t driver_uuid[16];
+  uint64_t features;
+  uint32_t subgroup_size;
+  uint32_t timestamp_valid_bits;
+  float timestamp_period_ns;
+  uint32_t max_push_constant_bytes;
+  uint64_t device_local_bytes;
+  uint64_t max_storage_buffer_bytes;
+  uint32_t max_workgroup_invocations;
+  uint32_t max_workgroup_count[3];
+  uint32_t max_workgroup_size[3];
+  uint32_t matmul_tile;
+  uint32_t matmul_k_multiple;
+  uint32_t matmul_layouts;
+  uint32_t matmul_operand_dtype;
+  uint32_t matmul_result_dtype;
+  uint32_t cast_modes;
+  uint32_t reserved;
+  uint64_t identity;
+  char device_name[256];
+  char driver_name[64];
+  char driver_info[128];
+} AckDeviceInfo;
+
+/* Replaces ack_device_info (ffi.rs:2410-2530): ACK_ERR_NULL for a null
+ * `out`, ACK_ERR_ABI when `size` is smaller than this library's struct, then
+ * the device lookup codes of ack_device_name. */
+int32_t ack_device_info(const AckDevice* dev, AckDeviceInfo* out, size_t size);
+
 /* Replaces ack_buffer_alloc (ffi.rs:3345-3375): device memory of `bytes`
  * (> 0); null with ack_last_error set on failure. */
 AckBuffer* ack_buffer_alloc(const AckDevice* dev, uint64_t bytes);
@@ -128,13 +213,15 @@ int32_t ack_vq_batch(const AckDevice* dev, const AckBuffer* b0, const AckBuffer*
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). Same arguments,
  * check order, codes and results as ack_vq; the workspace some product paths
- * need (split-k partials of the GEMV kernels, gemv-direct's slice partials,
- * the transposed code words of row-bins and the nibble columns of
- * onehot-mfma) comes from a fixed 8 MiB device array that each GPU holds until
- * the process ends, in place of memory ack_vq would allocate. A plan needing
- * more than 8 MiB of it is refused with ACK_ERR_SIZE. Calls share their GPU's
- * array: calls on one device handle are ordered on its stream, but calls
- * that overlap on one GPU through different device handles race on it. */
+ * need (split-k partials of the GEMV kernels, gemv-direct's slice partials
+ * and the nibble columns of onehot-mfma) comes from a fixed 8 MiB device
+ * array that each GPU holds until the process ends, in place of memory ack_vq
+ * would allocate. A plan needing more than 8 MiB of it is refused with
+ * ACK_ERR_SIZE. The array belongs to one device handle at a time: calls on
+ * one handle are ordered on its stream, and a call through another handle
+ * of the same GPU is refused with ACK_ERR_DEVICE (the message names the
+ * scratch) while the previous owner's enqueued noalloc work has not
+ * finished; after ack_sync on that handle it proceeds. */
 int32_t ack_vq_noalloc(const AckDevice* dev, const AckBuffer* b0, const AckBuffer* b1,
                        const AckBuffer* b2, const AckBuffer* b3, const AckBuffer* out,
                        const AckBuffer* status, const uint8_t* plan, size_t plan_len);

@@ -528,3 +528,27 @@ def test_cli_forward_and_train_on_the_gpu(tmp_path, capsys):
     report = json.loads(capsys.readouterr().out.strip().splitlines()[-1])
     assert report["mode"] == "train" and [s["optimizer_step"] for s in report["steps"]] == [1, 2]
     assert bank.read_expert_state(0, 0).revision == 3
+    assert report["device"]["abi"]["vq_schema"] == 1
+
+
+@pytest.mark.gpu
+def test_cli_resident_commits_the_same_bytes(tmp_path, capsys):
+    """--resident on the command line keeps the optimizer state on the GPU
+    and commits the images the default run commits, byte for byte."""
+    from gpu_util import say
+    x, t = tmp_path / "x.npy", tmp_path / "t.npy"
+    rng = np.random.default_rng(4)
+    np.save(x, rng.standard_normal((2, 4)).astype(np.float32))
+    np.save(t, rng.standard_normal((2, 3)).astype(np.float32))
+    images = []
+    for flag in ([], ["--resident"]):
+        bank = _small_bank(tmp_path, "resident" if flag else "default")
+        say("cli train", *flag)
+        assert harness.main(["--device", "--bank", str(bank.root), "--input", str(x),
+                             "--target", str(t), "--steps", "2", "--output",
+                             str(tmp_path / "y.npy"), "--force", *flag]) == 0
+        capsys.readouterr()
+        state = bank.read_expert_state(0, 0)
+        assert state.revision == 3
+        images.append([img.to_bytes() for img in state.tensors])
+    assert images[0] == images[1]

@@ -257,6 +257,43 @@ def test_library_exports_every_declared_symbol(lib):
         assert hasattr(lib.cdll, name), f"libackvq.so does not export {name}"
 
 
+# ---- ack_abi_info / ack_device_info (ffi.rs:1005-1060, :1212-1250) -----------
+def test_info_struct_layouts_are_the_references():
+    """The C structs' layouts as ffi.rs declares them: AckAbiInfo 96 bytes,
+    AckDeviceInfo 616 with `identity` at byte 160 (the end of the hashed
+    numeric fields, 8..160)."""
+    from alelyon_compute_kit import ack
+    assert ctypes.sizeof(ack.AckAbiInfo) == 96
+    assert ctypes.sizeof(ack.AckDeviceInfo) == 616
+    assert ack.AckDeviceInfo.identity.offset == 160
+    assert ack.AckDeviceInfo.device_name.offset == 168
+
+
+def test_abi_info_reports_no_operator_family(lib):
+    """This library serves vq4/v1 only: every operator bit, operator schema
+    and capability reads 0 (absent); the layout's ABI version is 14; the
+    shader and build identities are set. A null or short struct is refused
+    as the reference refuses it."""
+    from alelyon_compute_kit import ack
+    info = ack.abi_info(lib)
+    assert (info.size, info.version, info.operators) == (96, 14, 0)
+    assert info.shaders != 0 and info.build != 0
+    assert all(getattr(info, name) == 0 for name, _ in ack.AckAbiInfo._fields_[5:])
+    assert lib.cdll.ack_abi_info(None, 96) == ACK_ERR_NULL
+    small = ack.AckAbiInfo()
+    assert lib.cdll.ack_abi_info(ctypes.byref(small), 95) == ack.ACK_ERR_ABI
+    assert "smaller than this library's 96" in lib.last_error()
+
+
+def test_device_info_refuses_before_any_device_lookup(lib):
+    from alelyon_compute_kit import ack
+    out = ack.AckDeviceInfo()
+    assert lib.cdll.ack_device_info(FORGED, None, 616) == ACK_ERR_NULL
+    assert lib.cdll.ack_device_info(FORGED, ctypes.byref(out), 615) == ack.ACK_ERR_ABI
+    assert lib.cdll.ack_device_info(None, ctypes.byref(out), 616) == ACK_ERR_NULL
+    assert lib.cdll.ack_device_info(FORGED, ctypes.byref(out), 616) == ACK_ERR_CLOSED
+
+
 # ---- this library's extensions ------------------------------------------------
 def _path(lib, entry, words):
     out = ctypes.create_string_buffer(32)

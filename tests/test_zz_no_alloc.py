@@ -75,6 +75,70 @@ def test_noalloc_equals_ack_vq_on_consecutive_calls(vqdev, pair):
         np.testing.assert_array_equal(got, want)
 
 
+def test_noalloc_scratch_belongs_to_one_handle_at_a_time(vqdev):
+    """Two device handles on one GPU share its scratch. A handle's noalloc
+    calls follow each other on its stream; a second handle's call while the
+    first handle's noalloc work may still be running is refused with
+    ACK_ERR_DEVICE naming the scratch (or, if that work has already finished,
+    accepted), and once the first handle is synchronized the second handle's
+    call runs: every accepted result equals ack_vq's bit for bit."""
+    from alelyon_compute_kit import ack
+    rng = np.random.default_rng(12)
+    m, n, k, group = 512, 4096, 4096, 32
+    words = (2, m, n, k, group, 16, 0, 0)
+    assert vqdev.path_name(words) == "onehot-mfma"
+    ops = _operands(rng, m, n, k, group)
+    plan = np.asarray(words, dtype="<u4").tobytes()
+    say("noalloc reference", m, n, k, group)
+    rc, want, status = _call(vqdev, "ack_vq", words, ops, 4 * m * n)
+    assert rc == 0 and status == 0
+    first = vqdev.device
+    with ack.Device() as second:
+        held = {}
+        try:
+            for name, dev in (("first", first), ("second", second)):
+                bufs = [dev.buffer(a.nbytes) for a in ops]
+                for b, a in zip(bufs, ops):
+                    b.upload(a)
+                out, st = dev.buffer(4 * m * n), dev.buffer(4)
+                st.upload(np.zeros(1, np.uint32))
+                held[name] = (dev, bufs, out, st)
+
+            def launch(name):
+                dev, bufs, out, st = held[name]
+                with dev.lock:
+                    return dev.lib.cdll.ack_vq_noalloc(dev.handle, *(b.handle for b in bufs),
+                                                       out.handle, st.handle, plan, len(plan))
+
+            def result(name):
+                dev, _, out, st = held[name]
+                return out.download(np.uint32), int(st.download(np.uint32)[0])
+
+            say("noalloc: second handle twice, then the first handle at once")
+            assert launch("second") == 0
+            assert launch("second") == 0                  # one handle: ordered on its stream
+            rc = launch("first")
+            if rc != 0:
+                assert rc == ack.ACK_ERR_DEVICE
+                assert "scratch" in first.lib.last_error()
+            got, st = result("second")                   # synchronizes the second handle
+            assert st == 0
+            np.testing.assert_array_equal(got, want)
+            if rc == 0:                                   # accepted: the earlier work had ended
+                got, st = result("first")
+                assert st == 0
+                np.testing.assert_array_equal(got, want)
+            say("noalloc: the first handle after the second synchronized")
+            assert launch("first") == 0
+            got, st = result("first")
+            assert st == 0
+            np.testing.assert_array_equal(got, want)
+        finally:
+            for dev, bufs, out, st in held.values():
+                for b in bufs + [out, st]:
+                    b.free()
+
+
 def test_noalloc_other_ops_and_status(vqdev, oracle):
     """Ops without a workspace run unchanged; status bits still come back."""
     rng = np.random.default_rng(7)
