@@ -151,14 +151,16 @@ __global__ __launch_bounds__(kGThreads) void k_matmul_general(Operands o, uint32
 // Rows of k are binned in windows; at a window's end its bins are flushed into
 // FP32 registers, scaled back by 2^-s.
 //
-// The scale of a window comes from L1 = sum |x| over its rows (per row of A):
-// a bin holds the sum over a subset of those rows, so every bin, and every
-// sum of bins taken later, is at most 2^s L1 + rows/2 in magnitude. Choosing
-// 2^s L1 (1 + 2^-8) < 2^31 keeps all of them inside int32 whatever the codes
-// (the margin covers the FP32 rounding of the L1 sum itself, ~20 ulps), and
-// makes the rounding step 2^-s at most 2^-30 (1 + 2^-8) L1. So each x is
-// rounded by at most 2^-31 (1 + 2^-8) L1 absolutely: an outlier raises L1 by
-// its own magnitude only, not the step of every other value to its scale.
+// The scale of a window comes from its positive and negative masses (per row
+// of A), P = sum of its x > 0 and N = sum of |x| over its x < 0: a bin holds
+// the sum over a subset of those rows, so every bin, and every sum of bins
+// taken later, lies in [-(2^s N + rows/2), 2^s P + rows/2]. With M = max(P, N),
+// choosing 2^s M (1 + 2^-8) < 2^31 keeps all of them inside int32 whatever the
+// codes (the margin covers the FP32 rounding of the two sums, ~20 ulps, and
+// the half-units), and makes the rounding step 2^-s at most 2^-30 (1 + 2^-8) M.
+// So each x is rounded by at most 2^-31 (1 + 2^-8) M absolutely: an outlier
+// raises M by its own magnitude only, and for activations of either sign M is
+// about half the L1 norm P + N, one bit finer than a scale from L1.
 constexpr int kTileWords = 32;
 constexpr int kTileGroups = kTileWords * 8;
 constexpr uint32_t kGemvMaxM = 8;    // rows of A one GEMV launch bins
@@ -624,7 +626,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   // and each wave's share of their L1 norm in wl1. The caller's barrier
   // publishes both; take_scale() then sets the window's scale.
   auto stage_x = [&](uint32_t xb0) __attribute__((always_inline)) {
-    float l1 = 0.0f;
+    float lp = 0.0f, ln = 0.0f;  // the window's positive and negative masses
     bool bad = false;
     for (uint32_t r4 = opaque(tid) * 4; r4 < kPairXRows; r4 += 4 * kPairThreads) {
       const uint32_t row = xb0 + r4;
@@ -643,20 +645,33 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
         if (row + 2 >= kend) f.z = 0.0f;
         if (row + 3 >= kend) f.w = 0.0f;
       }
-      l1 += fabsf(f.x);
-      l1 += fabsf(f.y);
-      l1 += fabsf(f.z);
-      l1 += fabsf(f.w);
+      lp += fmaxf(f.x, 0.0f);
+      ln += fmaxf(-f.x, 0.0f);
+      lp += fmaxf(f.y, 0.0f);
+      ln += fmaxf(-f.y, 0.0f);
+      lp += fmaxf(f.z, 0.0f);
+      ln += fmaxf(-f.z, 0.0f);
+      lp += fmaxf(f.w, 0.0f);
+      ln += fmaxf(-f.w, 0.0f);
       *reinterpret_cast<float4*>(sx + r4) = f;
     }
-    l1 = wave_sum(l1);
-    if (lane == 0) wl1[wave] = l1;
+    lp = wave_sum(lp);
+    ln = wave_sum(ln);
+    if (lane == 0) {
+      wl1[wave] = lp;
+      wl1[kPairWaves + wave] = ln;
+    }
     if (AD && tile == 0 && __any(bad) && lane == 0) atomicOr(o.status, 1u);
   };
   auto take_scale = [&]() __attribute__((always_inline)) {
-    float l1 = 0.0f;
+    float lp = 0.0f, ln = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kPairWaves; ++w) l1 += wl1[w];
+    for (int w = 0; w < kPairWaves; ++w) {
+      lp += wl1[w];
+      ln += wl1[kPairWaves + w];
+    }
+    // NaN when either mass is NaN or infinite (status bit 1 follows)
+    const float l1 = fmaxf(lp, ln) + (lp - lp) + (ln - ln);
     shift = window_shift(l1);
     // finite values whose L1 overflows FP32: no scale holds the window
     if (!(l1 <= FLT_MAX) && tid == 0) atomicOr(o.status, 1u);
@@ -698,21 +713,33 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   // norms (entry e = its G / 4 lanes' sums) meet the slice's codes (lane l:
   // word l); every lane of every wave forms the same sums in the same order.
   auto pk_shift = [&](const PairAhead& h) __attribute__((always_inline)) {
-    float part = fabsf(h.a4.x);
-    part += fabsf(h.a4.y);
-    part += fabsf(h.a4.z);
-    part += fabsf(h.a4.w);
-    part += dpp_f32<kDppXor1>(part);  // entry e's G / 4 lanes (aligned, 2 or 4)
-    if (G / 4 == 4) part += dpp_f32<kDppXor2>(part);
+    // entry e's positive and negative masses over its G / 4 lanes (aligned, 2 or 4)
+    float pp = fmaxf(h.a4.x, 0.0f), pn = fmaxf(-h.a4.x, 0.0f);
+    pp += fmaxf(h.a4.y, 0.0f);
+    pn += fmaxf(-h.a4.y, 0.0f);
+    pp += fmaxf(h.a4.z, 0.0f);
+    pn += fmaxf(-h.a4.z, 0.0f);
+    pp += fmaxf(h.a4.w, 0.0f);
+    pn += fmaxf(-h.a4.w, 0.0f);
+    pp += dpp_f32<kDppXor1>(pp);
+    pn += dpp_f32<kDppXor1>(pn);
+    if (G / 4 == 4) {
+      pp += dpp_f32<kDppXor2>(pp);
+      pn += dpp_f32<kDppXor2>(pn);
+    }
     const uint32_t groups = (kend - k0 + G - 1) / G;
-    float l1 = 0.0f;
+    float lp = 0.0f, ln = 0.0f;
 #pragma unroll
     for (uint32_t c = 0; c < 8; ++c) {
       const uint32_t code = (h.w0 >> (4 * c)) & 15u;
-      const float r = __shfl(part, int(code * (G / 4)));
-      if (lane * 8 + c < groups) l1 += r;
+      const float rp = __shfl(pp, int(code * (G / 4)));
+      const float rn = __shfl(pn, int(code * (G / 4)));
+      if (lane * 8 + c < groups) {
+        lp += rp;
+        ln += rn;
+      }
     }
-    l1 = wave_sum_rows(l1);
+    const float l1 = fmaxf(wave_sum_rows(lp), wave_sum_rows(ln));
     if (!(l1 <= FLT_MAX) && tid == 0) atomicOr(o.status, 1u);  // book rows whose L1 overflows
     return __builtin_amdgcn_readfirstlane(window_shift(l1));
   };
@@ -1263,8 +1290,9 @@ struct RowLds {
   static constexpr uint32_t af = xs + xr * MP * 8;
   static constexpr uint32_t bb = af + 16 * G * 4;
   static constexpr uint32_t aw = bb + 16 * G * 4;
-  static constexpr uint32_t wl1 = aw + kRowAWords * 4;       // [wave][row] L1 partials
-  static constexpr uint32_t wsh = wl1 + (kRowThreads / 64) * 8 * 4;  // [row] window shifts
+  // [sign][wave][row] positive and negative mass partials
+  static constexpr uint32_t wl1 = aw + kRowAWords * 4;
+  static constexpr uint32_t wsh = wl1 + 2 * (kRowThreads / 64) * 8 * 4;  // [row] window shifts
   static constexpr uint32_t total = wsh + 8 * 4;
 };
 
@@ -1439,7 +1467,7 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
     bool bad = false;
 #pragma unroll 1
     for (uint32_t r = 0; r < 2 * MP; ++r) {
-      float l1 = 0.0f;
+      float lp = 0.0f, ln = 0.0f;  // the row's positive and negative masses
       if (r < m) {
         float v[kPerWin];
 #pragma unroll
@@ -1450,18 +1478,28 @@ __global__ __launch_bounds__(kRowThreads, 2) void k_gemv_rows(Operands o, uint32
 #pragma unroll
         for (int j = 0; j < kPerWin; ++j) {
           bad |= !finite_f32(v[j]);
-          l1 += fabsf(v[j]);
+          lp += fmaxf(v[j], 0.0f);
+          ln += fmaxf(-v[j], 0.0f);
         }
       }
-      l1 = wave_sum(l1);
-      if (lane == 0) wl1[wave * 8 + r] = l1;
+      lp = wave_sum(lp);
+      ln = wave_sum(ln);
+      if (lane == 0) {
+        wl1[wave * 8 + r] = lp;
+        wl1[(kRowThreads / 64 + wave) * 8 + r] = ln;
+      }
     }
     if (AD && tile == 0 && __any(bad) && lane == 0) atomicOr(o.status, 1u);
     __syncthreads();
     if (t < 2 * MP) {
-      float l1 = 0.0f;
+      float lp = 0.0f, ln = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kRowThreads / 64; ++w) l1 += wl1[w * 8 + t];
+      for (int w = 0; w < kRowThreads / 64; ++w) {
+        lp += wl1[w * 8 + t];
+        ln += wl1[(kRowThreads / 64 + w) * 8 + t];
+      }
+      // NaN when either mass is NaN or infinite (status bit 1 follows)
+      const float l1 = fmaxf(lp, ln) + (lp - lp) + (ln - ln);
       wsh[t] = window_shift(l1);
       if (!(l1 <= FLT_MAX)) atomicOr(o.status, 1u);  // finite x whose L1 overflows FP32
     }
