@@ -161,12 +161,12 @@ size_t round_up(size_t bytes) { return (bytes + 255) / 256 * 256; }
 // ---- the allocation-free entry's scratch ----------------------------------------
 // ack_vq_noalloc takes the workspace of the paths that need one (the GEMV's
 // split-k partials, gemv-direct's slice partials, onehot-mfma's nibble
-// columns) from this array instead
+// columns and split-k partials) from this array instead
 // of allocating it. Every GPU the library runs on holds its own copy until
 // the process ends. In host code `scratch` names a host-side stand-in, never
 // a device address: the address is resolved per GPU with
 // hipGetSymbolAddress (scratch_address) and only that pointer is passed on.
-constexpr size_t kScratchBytes = size_t(8) << 20;
+constexpr size_t kScratchBytes = size_t(16) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxGpus = 64;

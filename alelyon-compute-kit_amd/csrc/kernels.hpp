@@ -80,7 +80,7 @@ bool onehot_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t
                     uint32_t count);
 bool onehot_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                           uint32_t count);
-size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group);
+size_t onehot_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t group);
 // dense activations: the nibble columns and, on large grids, x's bf16 planes
 size_t onehot_dense_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t group);
 hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,

@@ -1897,7 +1897,7 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
 
 size_t matmul_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
                               uint32_t flags, uint32_t count) {
-  if (p == MatmulPath::OneHotMfma) return onehot_workspace_bytes(n, k, group);
+  if (p == MatmulPath::OneHotMfma) return onehot_workspace_bytes(m, n, k, group);
   if (p == MatmulPath::GemvDirect) return direct_workspace_bytes(m, n, k, group, count);
   if (p != MatmulPath::GemvRows && p != MatmulPath::GemvPairs) return 0;
   uint32_t ks, splits;

@@ -49,6 +49,16 @@ constexpr uint32_t kOHBigGrid = 256;  // blocks of the X = 4 grid from which it 
 
 __device__ __forceinline__ bool finite_f32(float x) { return fabsf(x) <= FLT_MAX; }
 
+// The power of two that brings A's book below 2^15 (amax its largest finite
+// magnitude): 15 - e for amax in [2^(e-1), 2^e), 0 for an all-zero book.
+__device__ __forceinline__ int book_shift(float amax) {
+  if (!(amax > 0.0f)) return 0;
+  int ex;
+  frexpf(amax, &ex);
+  const int shift = 15 - ex;
+  return shift < -126 ? -126 : (shift > 126 ? 126 : shift);
+}
+
 // Nibbles of vectors v .. v+7 (vector v in bits 0..3). Both loads are
 // unconditional: the word index is clamped to the array (a clamped word only
 // supplies nibbles past the last vector, which the caller never uses).
@@ -147,9 +157,15 @@ __global__ __launch_bounds__(256) void k_nibble_columns(const uint32_t* __restri
 // Requires k % 16 == 0, k % G == 0 (packed A) and n % (8 G) == 0; one
 // instance. AD: A is dense FP32 in in[0], split into three bf16 terms as it is
 // read (a nonfinite x reaches every output of its row, which sets status bit 1).
+// Split k (small grids): block z covers inner indices [z kpart, (z + 1) kpart)
+// (kpart a multiple of 8 G) and writes its S, still scaled by 2^shift, to
+// partial[z][r][16 j + e] instead of finishing the product; k_onehot_finish
+// adds the splits in order and applies C_B. partial is null when k is not
+// split (gridDim.z 1, kpart k).
 template <int G, int X, bool AD>
 __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
-    Operands o, uint32_t m, uint32_t n, uint32_t k, const uint32_t* __restrict__ nc) {
+    Operands o, uint32_t m, uint32_t n, uint32_t k, const uint32_t* __restrict__ nc,
+    uint32_t kpart, float* __restrict__ partial) {
   static_assert(G == 16 || G == 32 || (AD && G == 8), "a 16-step of k lies in one group of A");
   static_assert(X == 1 || X == 2 || X == 4, "row blocks per wave");
   constexpr int kOHX = X;
@@ -188,6 +204,9 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
   const uint32_t k8 = k / 8;
   const uint32_t* nc0 = nc + uint64_t(8 * q + 4 * wx + i32 / 16) * k8 + h;
   const uint32_t* nc1 = nc0 + 2 * uint64_t(k8);
+  // this block's inner indices [kb, ke)
+  const uint32_t kb = blockIdx.z * kpart;
+  const uint32_t ke = (kb + kpart) < k ? (kb + kpart) : k;
 
   // ---- tables: B's book as is; A's scaled below 2^15 and split into three
   // bf16 terms (each the bf16 rounding of what the previous ones leave; the
@@ -204,13 +223,7 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
   if (lane == 0) sred[wave] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
-  int shift = 0;
-  if (amax > 0.0f) {
-    int ex;
-    frexpf(amax, &ex);  // amax < 2^ex
-    shift = 15 - ex;
-    shift = shift < -126 ? -126 : (shift > 126 ? 126 : shift);
-  }
+  const int shift = book_shift(amax);
   for (uint32_t i = tid; i < (AD ? 0u : 17u * G); i += kOHThreads) {
     const float scaled = i < 16 * G ? ldexpf(a_book[i], shift) : 0.0f;
     const __bf16 hi = __bf16(scaled);
@@ -238,12 +251,12 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
   const char* tab_lane = reinterpret_cast<const char*>(&tabA[0][0][0][0]) + h * kChunk;
   uint32_t aw[kOHX], an[kOHX];
 #pragma unroll
-  for (int x = 0; x < kOHX; ++x) an[x] = AD ? 0u : nibbles8(a_codes, av[x], a_last);
+  for (int x = 0; x < kOHX; ++x) an[x] = AD ? 0u : nibbles8(a_codes, av[x] + kb / G, a_last);
   uint32_t wb[4][2];
-  wb[0][0] = nc0[0];
-  wb[0][1] = nc1[0];
-  wb[1][0] = nc0[16 < k ? 2 : 0];
-  wb[1][1] = nc1[16 < k ? 2 : 0];
+  wb[0][0] = nc0[kb / 8];
+  wb[0][1] = nc1[kb / 8];
+  wb[1][0] = nc0[(kb + 16 < ke ? kb + 16 : kb) / 8];
+  wb[1][1] = nc1[(kb + 16 < ke ? kb + 16 : kb) / 8];
   // the table row of step s_ (both halves of the wave are in one group; the
   // lane's chunk is c8 + h)
   auto a_ptr = [&](const uint32_t (&wd)[kOHX], uint32_t s_, int x) __attribute__((always_inline)) {
@@ -261,8 +274,8 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
     if (AD) {
       const uint32_t r = row0 + 32 * x + i32;
       xr[x] = xa + uint64_t(r < m ? r : m - 1) * k + 8 * h;
-      xn[x][0] = *reinterpret_cast<const float4*>(xr[x]);
-      xn[x][1] = *reinterpret_cast<const float4*>(xr[x] + 4);
+      xn[x][0] = *reinterpret_cast<const float4*>(xr[x] + kb);
+      xn[x][1] = *reinterpret_cast<const float4*>(xr[x] + kb + 4);
     } else {
       const char* pa = a_ptr(an, 0, x);
 #pragma unroll
@@ -275,7 +288,7 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
   // only the ragged last pass can leave the unrolled loop early: a load behind
   // a branch leaves the compiler unable to count the loads in flight, and it
   // then waits for all of them, the ones just issued for later steps included.
-  const uint32_t klast = k - 16;  // the last step's first inner index
+  const uint32_t klast = ke - 16;  // the last step's first inner index
   auto pass = [&](uint32_t p0, bool ragged) __attribute__((always_inline)) {
 #pragma unroll
     for (int x = 0; x < kOHX; ++x) {
@@ -285,10 +298,10 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
 #pragma unroll
     for (uint32_t s = 0; s < kSteps; ++s) {
       const uint32_t kk0 = p0 + 16 * s;
-      if (ragged && kk0 >= k) break;
-      const uint32_t kb = kk0 + 32 < klast ? kk0 + 32 : klast;
-      wb[(s + 2) % 4][0] = nc0[kb / 8];
-      wb[(s + 2) % 4][1] = nc1[kb / 8];
+      if (ragged && kk0 >= ke) break;
+      const uint32_t kw = kk0 + 32 < klast ? kk0 + 32 : klast;
+      wb[(s + 2) % 4][0] = nc0[kw / 8];
+      wb[(s + 2) % 4][1] = nc1[kw / 8];
       const uint32_t kn = kk0 + 16 < klast ? kk0 + 16 : klast;
       const char* pn[kOHX];
 #pragma unroll
@@ -324,9 +337,26 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  const uint32_t whole = k / (8 * G) * (8 * G);  // inner indices of whole passes
-  for (uint32_t p0 = 0; p0 < whole; p0 += 8 * G) pass(p0, false);
-  if (whole < k) pass(whole, true);
+  const uint32_t whole = kb + (ke - kb) / (8 * G) * (8 * G);  // end of the whole passes
+  for (uint32_t p0 = kb; p0 < whole; p0 += 8 * G) pass(p0, false);
+  if (whole < ke) pass(whole, true);
+
+  if (partial != nullptr) {  // this split's S, scaled, for k_onehot_finish
+    const uint32_t cols = 16 * (n / G);
+    float* pz = partial + uint64_t(blockIdx.z) * m * cols + 16 * (8 * q + 4 * wx) + i32;
+#pragma unroll
+    for (int x = 0; x < kOHX; ++x)
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const uint32_t r = row0 + 32 * x + (t % 4) + 4 * h + 8 * (t / 4);
+        if (r < m) {
+          pz[uint64_t(r) * cols] = acc[x][0][t];
+          pz[uint64_t(r) * cols + 32] = acc[x][1][t];
+        }
+      }
+    if (__any(bad) && lane == 0) atomicOr(o.status, 1u);
+    return;
+  }
 
   // ---- S to LDS, kChunkRows rows at a time (lane: column i32, item t holds
   // row (t % 4) + 4 h + 8 (t / 4) of its 32-row block), then
@@ -381,6 +411,55 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
     }
   }
   if (__any(bad) && lane == 0) atomicOr(o.status, 1u);
+}
+
+// Split k, second half: S[r][(j, e)] = the splits' partial sums added in split
+// order, then k_onehot_mfma's epilogue, y[r][G j + t] = sum_e S[r][(j, e)]
+// C_B[e][t] (e ascending), unscaled by 2^-shift for packed A. grid:
+// (ceil(n / 256), m), one thread per output.
+template <int G, bool AD>
+__global__ __launch_bounds__(256) void k_onehot_finish(Operands o, uint32_t m, uint32_t n,
+                                                       uint32_t splits,
+                                                       const float* __restrict__ partial) {
+  __shared__ float sred[4];
+  const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  int shift = 0;
+  if (!AD) {
+    const float* a_book = static_cast<const float*>(o.in[1]);
+    float amax = 0.0f;
+    for (uint32_t i = tid; i < 16 * G; i += 256) {
+      const float a = a_book[i];
+      amax = fmaxf(amax, finite_f32(a) ? fabsf(a) : 0.0f);
+    }
+    for (int off = 1; off < 64; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if (lane == 0) sred[wave] = amax;
+    __syncthreads();
+    shift = book_shift(fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3])));
+  }
+  const uint32_t col = blockIdx.x * 256 + tid, r = blockIdx.y;
+  if (col >= n) return;
+  const uint32_t j = col / G, tc = col % G, cols = 16 * (n / G);
+  const float* b_book = static_cast<const float*>(o.in[3]);
+  float sv[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) sv[e] = 0.0f;
+  for (uint32_t z = 0; z < splits; ++z) {
+    const float4* p = reinterpret_cast<const float4*>(partial + (uint64_t(z) * m + r) * cols + 16 * j);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const float4 v = p[f];
+      sv[4 * f] += v.x;
+      sv[4 * f + 1] += v.y;
+      sv[4 * f + 2] += v.z;
+      sv[4 * f + 3] += v.w;
+    }
+  }
+  float y = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) y = fmaf(sv[e], b_book[e * G + tc], y);
+  if (!AD) y = ldexpf(y, -shift);
+  static_cast<float*>(o.out)[uint64_t(r) * n + col] = y;
+  if (__any(!finite_f32(y)) && lane == 0) atomicOr(o.status, 1u);
 }
 
 // ---- dense activations on large grids: bf16 planes -------------------------
@@ -596,6 +675,36 @@ size_t nc_bytes(uint32_t n, uint32_t k, uint32_t group) {
   return (size_t(n / group) * (k / 8) * 4 + 255) / 256 * 256;
 }
 
+uint64_t big_grid(uint32_t m, uint32_t n, uint32_t group) {
+  return uint64_t(n / (8 * group)) * ((m + 255) / 256);
+}
+
+// Split k for the 64-row grid (packed A below kOHBigGrid blocks of 256 rows,
+// dense A below the planes' grid): with fewer than kOHSplitBlocks blocks the
+// chip idles while each block walks all of k, so k is cut into `count` parts
+// of `kpart` inner indices (whole passes of 8 G, at least two each) run as
+// blocks z of a 3D grid, their partial S in the workspace (at most
+// kOHPartialMax bytes) and k_onehot_finish adding them.
+constexpr uint32_t kOHSplitBlocks = 256;
+constexpr size_t kOHPartialMax = size_t(8) << 20;
+
+struct Split {
+  uint32_t count, kpart;
+};
+
+Split onehot_split(uint32_t m, uint32_t n, uint32_t k, uint32_t group, bool dense) {
+  const bool x1 = dense ? dense_planes_x(m, n, group) == 0 : big_grid(m, n, group) < kOHBigGrid;
+  const uint64_t blocks = uint64_t(n / (8 * group)) * ((m + 63) / 64);
+  const uint32_t pass = 8 * group, passes = (k + pass - 1) / pass;
+  const size_t per_split = size_t(m) * (16 * (n / group)) * sizeof(float);
+  uint64_t want = (kOHSplitBlocks + blocks - 1) / blocks;
+  if (want > passes / 2) want = passes / 2;
+  if (want > kOHPartialMax / per_split) want = kOHPartialMax / per_split;
+  if (!x1 || want < 2) return {1, k};
+  const uint32_t per = (passes + uint32_t(want) - 1) / uint32_t(want);  // passes per split
+  return {(passes + per - 1) / per, per * pass};
+}
+
 }  // namespace
 
 // From kOneHotMinRows rows of A always; from 16 rows when B holds at least
@@ -613,27 +722,34 @@ bool onehot_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t
          uint64_t(k) <= 256ull * m;
 }
 
-size_t onehot_workspace_bytes(uint32_t n, uint32_t k, uint32_t group) {
-  return size_t(n / group) * (k / 8) * 4;
+// Workspace: B's nibble columns, then the planes (dense A on a large grid) or
+// the split partial sums.
+size_t onehot_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t group) {
+  const Split sp = onehot_split(m, n, k, group, false);
+  if (sp.count == 1) return size_t(n / group) * (k / 8) * 4;
+  return nc_bytes(n, k, group) + size_t(sp.count) * m * (16 * (n / group)) * sizeof(float);
 }
 
 size_t onehot_dense_workspace_bytes(uint32_t m, uint32_t n, uint32_t k, uint32_t group) {
   const uint32_t px = dense_planes_x(m, n, group);
-  if (px == 0) return onehot_workspace_bytes(n, k, group);
-  return nc_bytes(n, k, group) + size_t(kOHTerms) * planes_rows(m, px) * k * sizeof(__bf16);
+  if (px != 0)
+    return nc_bytes(n, k, group) + size_t(kOHTerms) * planes_rows(m, px) * k * sizeof(__bf16);
+  const Split sp = onehot_split(m, n, k, group, true);
+  if (sp.count == 1) return size_t(n / group) * (k / 8) * 4;
+  return nc_bytes(n, k, group) + size_t(sp.count) * m * (16 * (n / group)) * sizeof(float);
 }
 
 namespace {
 
 template <int G, int X, bool AD>
 void launch_onehot_x(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
-                     const uint32_t* nc) {
-  dim3 grid(n / (8 * G), (m + 64 * X - 1) / (64 * X));
-  k_onehot_mfma<G, X, AD><<<grid, kOHThreads, 0, s>>>(o, m, n, k, nc);
-}
-
-uint64_t big_grid(uint32_t m, uint32_t n, uint32_t group) {
-  return uint64_t(n / (8 * group)) * ((m + 255) / 256);
+                     const uint32_t* nc, float* partial) {
+  const Split sp = X == 1 ? onehot_split(m, n, k, G, AD) : Split{1, k};
+  dim3 grid(n / (8 * G), (m + 64 * X - 1) / (64 * X), sp.count);
+  k_onehot_mfma<G, X, AD><<<grid, kOHThreads, 0, s>>>(o, m, n, k, nc, sp.kpart,
+                                                      sp.count > 1 ? partial : nullptr);
+  if (sp.count > 1)
+    k_onehot_finish<G, AD><<<dim3((n + 255) / 256, m), 256, 0, s>>>(o, m, n, sp.count, partial);
 }
 
 template <int G>
@@ -650,14 +766,16 @@ void launch_planes(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uin
 
 template <int G>
 void launch_onehot_g(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
-                     bool dense, const uint32_t* nc, __bf16* planes) {
+                     bool dense, const uint32_t* nc, void* rest) {
+  float* partial = static_cast<float*>(rest);
   if (dense) {
-    if (const uint32_t px = dense_planes_x(m, n, G)) launch_planes<G>(s, o, m, n, k, px, nc, planes);
-    else launch_onehot_x<G, 1, true>(s, o, m, n, k, nc);
+    if (const uint32_t px = dense_planes_x(m, n, G))
+      launch_planes<G>(s, o, m, n, k, px, nc, static_cast<__bf16*>(rest));
+    else launch_onehot_x<G, 1, true>(s, o, m, n, k, nc, partial);
   } else if (big_grid(m, n, G) >= kOHBigGrid) {
-    launch_onehot_x<G, 4, false>(s, o, m, n, k, nc);
+    launch_onehot_x<G, 4, false>(s, o, m, n, k, nc, nullptr);
   } else {
-    launch_onehot_x<G, 1, false>(s, o, m, n, k, nc);
+    launch_onehot_x<G, 1, false>(s, o, m, n, k, nc, partial);
   }
 }
 
@@ -665,10 +783,11 @@ void launch_onehot_g(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, u
 // would straddle its groups).
 template <>
 void launch_onehot_g<8>(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
-                        bool dense, const uint32_t* nc, __bf16* planes) {
+                        bool dense, const uint32_t* nc, void* rest) {
   (void)dense;
-  if (const uint32_t px = dense_planes_x(m, n, 8)) launch_planes<8>(s, o, m, n, k, px, nc, planes);
-  else launch_onehot_x<8, 1, true>(s, o, m, n, k, nc);
+  if (const uint32_t px = dense_planes_x(m, n, 8))
+    launch_planes<8>(s, o, m, n, k, px, nc, static_cast<__bf16*>(rest));
+  else launch_onehot_x<8, 1, true>(s, o, m, n, k, nc, static_cast<float*>(rest));
 }
 
 }  // namespace
@@ -693,10 +812,10 @@ hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
   k_nibble_columns<<<ngrid, 256, 0, s>>>(static_cast<const uint32_t*>(o.in[2]), nc, k, rw);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  __bf16* planes = reinterpret_cast<__bf16*>(static_cast<char*>(workspace) + nc_bytes(n, k, group));
-  if (group == 8) launch_onehot_g<8>(s, o, m, n, k, dense, nc, planes);
-  else if (group == 16) launch_onehot_g<16>(s, o, m, n, k, dense, nc, planes);
-  else launch_onehot_g<32>(s, o, m, n, k, dense, nc, planes);
+  void* rest = static_cast<char*>(workspace) + nc_bytes(n, k, group);  // planes or partial sums
+  if (group == 8) launch_onehot_g<8>(s, o, m, n, k, dense, nc, rest);
+  else if (group == 16) launch_onehot_g<16>(s, o, m, n, k, dense, nc, rest);
+  else launch_onehot_g<32>(s, o, m, n, k, dense, nc, rest);
   return hipGetLastError();
 }
 

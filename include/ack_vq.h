@@ -214,10 +214,10 @@ int32_t ack_vq_batch(const AckDevice* dev, const AckBuffer* b0, const AckBuffer*
  * tight serving loops, harnesses that forbid hipMalloc). Same arguments,
  * check order, codes and results as ack_vq; the workspace some product paths
  * need (split-k partials of the GEMV kernels, gemv-direct's slice partials
- * and the nibble columns of onehot-mfma) comes from a fixed 8 MiB device
- * array that each GPU holds until the process ends, in place of memory ack_vq
- * would allocate. A plan needing more than 8 MiB of it is refused with
- * ACK_ERR_SIZE. The array belongs to one device handle at a time: calls on
+ * and the nibble columns and split-k partials of onehot-mfma) comes from a
+ * fixed 16 MiB device array that each GPU holds until the process ends, in
+ * place of memory ack_vq would allocate. A plan needing more than 16 MiB of
+ * it is refused with ACK_ERR_SIZE. The array belongs to one device handle at a time: calls on
  * one handle are ordered on its stream, and a call through another handle
  * of the same GPU is refused with ACK_ERR_DEVICE (the message names the
  * scratch) while the previous owner's enqueued noalloc work has not

@@ -287,9 +287,13 @@ def test_dense_bucket_sums_past_float_max_raise_status(vqdev):
 
 
 # (m, k, n, group): from 32 rows (k <= 256 m), rows past m in the 64-row block,
-# k not a multiple of 8 g, one and several word columns
+# k not a multiple of 8 g, one and several word columns; k split over blocks
+# on these small grids (4 ways at 32 x 1024 x 1024 and 200 x 4096 x 4096, 8 at
+# the 128-row chunk, 2 at 96 x 1040 x 1024 with a 16-step in the last part,
+# 11 at 48 x 4112 x 2048)
 DENSE_ONEHOT_SHAPES = [(32, 1024, 1024, 16), (40, 512, 2048, 32), (64, 64, 256, 16),
                        (130, 256, 2048, 16), (200, 4096, 4096, 32), (255, 1040, 768, 16),
+                       (128, 4096, 4096, 32), (48, 4112, 2048, 16),
                        (96, 1040, 1024, 32)]     # k not a multiple of g (dense rows need not be)
 
 

@@ -600,11 +600,15 @@ def test_large_m_under_the_test_policy(vqdev, oracle, any_size, m, n, k, group):
 # (m, n, k, group): one 16-step of k, a last pass shorter than 8 groups of A
 # (k not a multiple of 8 g), rows past m in the last block, 1 and 8 word
 # columns; grids below 256 blocks of 256 rows run 64-row blocks, the last two
-# shapes the 256-row blocks
+# shapes the 256-row blocks. 64-row grids of fewer than 256 blocks split k
+# (4 ways at 16 x 1024 x 1024, 8 at 63 x 4096 x 4096 and at the 128-row
+# chunk, 3 at 513 x 2048 x 4096; 48 x 2048 x 4112 into 11 parts of 3 passes,
+# the last one 2 passes and a 16-step)
 ONEHOT_SHAPES = [(16, 1024, 1024, 16), (40, 2048, 512, 32), (63, 4096, 4096, 16),
                  (64, 256, 64, 16), (100, 512, 96, 32), (130, 2048, 256, 16),
                  (256, 1024, 512, 32), (333, 768, 1024, 16), (256, 256, 16, 16),
                  (300, 512, 1040, 16), (1000, 4096, 288, 32), (513, 2048, 4096, 32),
+                 (48, 2048, 4112, 16), (128, 4096, 4096, 32),
                  (1000, 16384, 256, 32), (2100, 4096, 1040, 16)]
 
 

@@ -57,6 +57,7 @@ PAIRS = [
     [(8, 4096, 8320, 16, 0, "gemv-rows"), (3, 4096, 8320, 8, 0, "gemv-rows")],
     [(24, 2048, 8192, 16, 0, "gemv-rows"), (12, 1024, 4096, 16, 1, "gemv-rows")],
     [(512, 4096, 4096, 32, 0, "onehot-mfma"), (64, 1024, 1024, 16, 0, "onehot-mfma")],
+    [(2048, 8192, 512, 16, 0, "onehot-mfma"), (128, 4096, 4096, 32, 0, "onehot-mfma")],
 ]
 
 
