@@ -218,6 +218,12 @@ __device__ __forceinline__ int32_t quantize(float x, int shift) {
   return int32_t(fminf(fmaxf(v, -kQuantMax), kQuantMax));
 }
 
+// four values quantised, as int32 bit patterns in float lanes
+__device__ __forceinline__ float4 quantize4(float4 a, int shift) {
+  return make_float4(__int_as_float(quantize(a.x, shift)), __int_as_float(quantize(a.y, shift)),
+                     __int_as_float(quantize(a.z, shift)), __int_as_float(quantize(a.w, shift)));
+}
+
 // Sum over the 64 lanes of a wave by xor butterfly: every lane ends with the
 // same value (each step adds the same two operands on both sides).
 __device__ __forceinline__ float wave_sum(float v) {
@@ -329,10 +335,13 @@ __global__ __launch_bounds__(256) void k_gemv_finish(Operands o, uint32_t n, uin
 //   S[2p+1][e] = sum over lo of P[p][16 e + lo]   (high nibble = group 8q+2p+1)
 //
 // Bin of byte value v at byte position p of word column q (32-word tile):
-//   dword (p >> 1) * 16384 + v * 64 + (p & 1) * 32 + q
-// so the 32 lanes of a half-wave (one word column each) hit 32 distinct banks,
+//   dword (p >> 1) * 16384 + v * 64 + (p & 1) * 32 + (q ^ p)
 // and the byte address is a single v_perm of the code word with a per-lane
-// constant: byte 0 = 4q (+128 for odd p), byte 1 = v, byte 2 = the region.
+// constant (byte 0 = 4 (q ^ p), +128 for odd p; byte 2 = the region p >> 1)
+// that takes the code byte as byte 1. A half-wave hits 32 distinct banks: one
+// row of 32 word columns at one byte position, or (16-byte loads) 8 word
+// columns of 4 rows whose lanes take the 4 byte positions at each step, the
+// column swizzle q ^ p keeping them apart.
 //
 // Pipeline: each lane owns R rows of its word column per batch; D register
 // buffers form a ring (the loop is unrolled by D, so no in-flight register is
@@ -391,15 +400,22 @@ struct PairLds {
   static constexpr bool cum = G <= 16;  // room for the cumulative partials
   static constexpr uint32_t xs = kPairBins * 4;
   static constexpr uint32_t af = xs + (cum ? kCumWords : kPairXRows) * 4;
-  static constexpr uint32_t bb = af + 16 * G * 4;
+  static constexpr uint32_t bb = af + 17 * G * 4;  // PK: a 17th (zero) row of A's table
   static constexpr uint32_t aw = bb + 2 * 16 * G * 4;
   static constexpr uint32_t wl1 = aw + kPairMaxAWords * 4;
   static constexpr uint32_t total = wl1 + 16 * 4;
 };
 
 __device__ __forceinline__ uint32_t pair_dword(uint32_t v, uint32_t p, uint32_t q) {
-  return (p >> 1) * 16384 + v * 64 + (p & 1) * 32 + q;
+  return (p >> 1) * 16384 + v * 64 + (p & 1) * 32 + (q ^ p);
 }
+
+// v_perm constant and selector that turn byte p of a code word into the byte
+// address of its bin in word column q (pair_dword times 4)
+__device__ __forceinline__ uint32_t pair_const(uint32_t p, uint32_t q) {
+  return (4 * (q ^ p) + 128 * (p & 1)) | ((p >> 1) << 16);
+}
+__device__ __forceinline__ uint32_t pair_sel(uint32_t p) { return 0x0c020400u + (p << 8); }
 
 // Finalise partials pl/ph: [half][p][e][q ^ (2 (e & 3) + 8 p)]. The writes
 // (lanes = word columns q) and the product's reads (a wave's 16 groups x 4
@@ -484,7 +500,7 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   // PK: one A word per lane covers a window (kPairWindow rows), one float4 per
   // lane covers the A book, and the A book's second copy fits the words' area
   static_assert(!PK || (kPairWindow / (8 * G) <= 64 && 16 * G <= 4 * 64 &&
-                        16 * G <= kPairMaxAWords), "PK registers and LDS");
+                        17 * G <= kPairMaxAWords), "PK registers and LDS");
   extern __shared__ int32_t smem[];
   char* lds = reinterpret_cast<char*>(smem);
   int32_t* bins = smem;
@@ -517,19 +533,18 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   // bins no output reads
   const uint32_t col = X4 ? tile * kTileWords + 4 * chunk
                           : ((tile * kTileWords + q < rw) ? tile * kTileWords + q : rw - 1);
-  // byte 0: 4 x word column (+128 for odd byte positions), byte 2: region 1
-  uint32_t lcs[X4 ? 4 : 1];
-  if (X4) {
+  // bin address constants (pair_const): X4, step s of word t bins byte
+  // (s + slot) % 4 of word column 4 chunk + t, so the four row slots of a
+  // half-wave take the four byte positions; otherwise step p bins byte p of
+  // column q
+  uint32_t bc[X4 ? 4 : 1][4], bsel[4];
 #pragma unroll
-    for (uint32_t t = 0; t < 4; ++t) {
-      const uint32_t qt = 4 * chunk + ((t + slot) & 3u);
-      lcs[t] = (qt * 4) | ((qt * 4 + 128) << 8) | (1u << 16);
-    }
-  } else {
-    lcs[0] = (q * 4) | ((q * 4 + 128) << 8) | (1u << 16);
+  for (uint32_t st = 0; st < 4; ++st) {
+    const uint32_t ps = X4 ? (st + slot) & 3u : st;
+    bsel[st] = pair_sel(ps);
+#pragma unroll
+    for (uint32_t t = 0; t < (X4 ? 4u : 1u); ++t) bc[t][st] = pair_const(ps, X4 ? 4 * chunk + t : q);
   }
-  const bool rot1 = (slot & 1u) != 0, rot2 = (slot & 2u) != 0;
-  constexpr uint32_t kSel[4] = {0x0c0c0400u, 0x0c0c0501u, 0x0c020600u, 0x0c020701u};
   const uint32_t a_w0 = k0 / G / 8;
   const uint32_t a_words = (kend - 1) / G / 8 - a_w0 + 1;
 
@@ -678,27 +693,33 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
   };
   auto read_x = [&](uint32_t b, float (&xs)[RX]) __attribute__((always_inline)) {
     asm volatile("" : "+s"(b));
-    if (k0 + b * BR >= kend) {  // a padding batch: nothing staged for it
+    // a padding batch: nothing staged for it (PK reads the table's zero row,
+    // so that no branch separates the read from its use)
+    if (!PK && k0 + b * BR >= kend) {
 #pragma unroll
       for (uint32_t u = 0; u < RX; ++u) xs[u] = 0.0f;
       return;
     }
     if (PK) {
       // the wave's 2 R rows of the batch (slice rows b BR + 2 R wave ..) lie in
-      // word (b BR + 2 R wave) / (8 G) of the slice, held by that lane
+      // word (b BR + 2 R wave) / (8 G) of the slice, held by that lane; the
+      // table holds x quantised (int32 bits), rows past the slice read row 16
+      // (zeros: the slice length is a multiple of 4). Nothing uses the read
+      // until the next batch, after this batch's atomics: a use right after
+      // it would wait for the wave's previous atomics, which LDS completes
+      // first.
       const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
       const uint32_t word =
           uint32_t(__builtin_amdgcn_readlane(int(wreg), int((b * BR + 2 * R * wv) / (8 * G))));
-      const uint32_t len = kend - k0;
 #pragma unroll
       for (uint32_t c4 = 0; c4 < RX / 4; ++c4) {
         const uint32_t row = b * BR + lane_row + 4 * c4;  // of the slice
-        const uint32_t code = (word >> (((row / G) % 8u) * 4u)) & 15u;
+        const uint32_t code = row < kend - k0 ? (word >> (((row / G) % 8u) * 4u)) & 15u : 16u;
         const float4 v = *reinterpret_cast<const float4*>(af_cur + code * G + row % G);
-        xs[4 * c4] = row < len ? v.x : 0.0f;  // rows past the slice bin nothing
-        xs[4 * c4 + 1] = row + 1 < len ? v.y : 0.0f;
-        xs[4 * c4 + 2] = row + 2 < len ? v.z : 0.0f;
-        xs[4 * c4 + 3] = row + 3 < len ? v.w : 0.0f;
+        xs[4 * c4] = v.x;
+        xs[4 * c4 + 1] = v.y;
+        xs[4 * c4 + 2] = v.z;
+        xs[4 * c4 + 3] = v.w;
       }
       return;
     }
@@ -884,29 +905,28 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
     const bool restage = !SW && k0 + done < kend && k0 + done - xbase >= kPairXRows;
     const bool wend = SW ? last : (done % kPairWindow == 0 || last);
     if (!restage && !last) read_x(b + 1, xn);
-    if (b < nb) {  // padding batches (past the slice) bin nothing
+    // the lane's row u of batch b as binned: PK reads it quantised (rows past
+    // the slice read the table's zero row), else x is quantised here
+    auto x_q = [&](uint32_t u) __attribute__((always_inline)) {
+      return PK ? __float_as_int(xs[u]) : quantize(xs[u], shift);
+    };
+    if (PK || b < nb) {  // padding batches (past the slice) bin nothing (PK: zeros)
       if (X4) {
 #pragma unroll
         for (uint32_t u = 0; u < RX; ++u) {
-          // word t of the rotated row is word (t + slot) % 4 of the chunk
-          const uint32_t a0 = rot1 ? w[4 * u + 1] : w[4 * u];
-          const uint32_t a1 = rot1 ? w[4 * u + 2] : w[4 * u + 1];
-          const uint32_t a2 = rot1 ? w[4 * u + 3] : w[4 * u + 2];
-          const uint32_t a3 = rot1 ? w[4 * u] : w[4 * u + 3];
-          const uint32_t r[4] = {rot2 ? a2 : a0, rot2 ? a3 : a1, rot2 ? a0 : a2, rot2 ? a1 : a3};
-          const int32_t xv = quantize(xs[u], shift);
+          const int32_t xv = x_q(u);
 #pragma unroll
           for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int p = 0; p < 4; ++p) lds_add(__builtin_amdgcn_perm(r[t], lcs[t], kSel[p]), xv);
+            for (int st = 0; st < 4; ++st)
+              lds_add(__builtin_amdgcn_perm(w[4 * u + t], bc[t][st], bsel[st]), xv);
         }
       } else {
 #pragma unroll
         for (uint32_t u = 0; u < R; ++u) {
-          const uint32_t ww = w[u];
-          const int32_t xv = quantize(xs[u], shift);
+          const int32_t xv = x_q(u);
 #pragma unroll
-          for (int p = 0; p < 4; ++p) lds_add(__builtin_amdgcn_perm(ww, lcs[0], kSel[p]), xv);
+          for (int st = 0; st < 4; ++st) lds_add(__builtin_amdgcn_perm(w[u], bc[0][st], bsel[st]), xv);
         }
       }
     }
@@ -956,8 +976,17 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
 #pragma unroll
   for (uint32_t i = 0; i < kPairBins / (4 * kPairThreads); ++i)
     bins4[tid + i * kPairThreads] = make_int4(0, 0, 0, 0);
-  if (PK) {  // the first instance's A book; instances alternate copies from here
-    if (4 * tid < 16 * G) *reinterpret_cast<float4*>(af + 4 * tid) = cur.a4;
+  // PK: A's book quantised with an instance's scale is that instance's table
+  // of x; the tables alternate between two copies by instance, and the next
+  // instance's is written one instance ahead, with its scale (nshift)
+  int nshift = 0;
+  if (PK) {
+    if (tid < G) {  // row 16, which rows past the slice read: zeros, never rewritten
+      af[16 * G + tid] = 0.0f;
+      afx[16 * G + tid] = 0.0f;
+    }
+    nshift = pk_shift(cur);
+    if (4 * tid < 16 * G) *reinterpret_cast<float4*>(af + 4 * tid) = quantize4(cur.a4, nshift);
     __syncthreads();
   }
   for (; item < ninst; item += zn) {
@@ -977,7 +1006,10 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       // instance's) by the previous instance's loop; every wave has passed
       // the previous instance's flush barrier, which follows both.
       if (st < 16 * G) bb[st] = cur.b;
-      if (4 * st < 16 * G) *reinterpret_cast<float4*>((par ? af : afx) + 4 * st) = nxt.a4;
+      shift = nshift;
+      nshift = pk_shift(nxt);
+      if (4 * st < 16 * G)
+        *reinterpret_cast<float4*>((par ? af : afx) + 4 * st) = quantize4(nxt.a4, nshift);
       if (tile == 0 && split == 0) {  // nonfinite book values, from the set-up registers
         const bool bad = (4 * st < 16 * G && (!finite_f32(cur.a4.x) || !finite_f32(cur.a4.y) ||
                                               !finite_f32(cur.a4.z) || !finite_f32(cur.a4.w))) ||
@@ -986,7 +1018,6 @@ __global__ __launch_bounds__(kPairThreads, 2) void k_gemv_pairs(Operands o, uint
       }
       af_cur = par ? afx : af;
       wreg = cur.w0;
-      shift = pk_shift(cur);
       read_x(0, xa);
     } else {
       if (st < 16 * G) {
@@ -1749,7 +1780,9 @@ hipError_t launch_pairs(hipStream_t s, const Operands& o, uint32_t n, uint32_t k
   uint32_t zc = per_z >= 256 ? 1u : 256u / per_z;
   zc = zc < ninst ? zc : ninst;
   const size_t shmem = pairs_shmem(G);
-  const bool one_window = ks <= kPairWindow;
+  // one window; packed A also needs a slice length that is a multiple of 4
+  // (x is read from the quantised book four rows at a time)
+  const bool one_window = ks <= kPairWindow && (AD || k % 4 == 0);
   // 16-byte loads need rows of whole tiles (then every chunk is 16-byte aligned)
   const bool x4 = (n / (8 * G)) % kTileWords == 0;
   const void* fn = one_window
