@@ -199,11 +199,14 @@ __global__ __launch_bounds__(1024) void k_gemv_direct(Operands o, uint32_t m, ui
   const uint32_t slot = item * tiles + tile;
   float* part = partial + uint64_t(slot) * splits * M * kDirectCols;
   // Publish the partials, then count the arrival; the last block of the tile
-  // adds the partials in slice order. The partials are device-coherent atomic
-  // stores and loads (they bypass the per-XCD L2s), and every store has
-  // completed (vmcnt 0) before the block's arrival is counted, so the last
-  // block reads them all without a device-wide fence (which writes back and
-  // invalidates the whole L2: measured at 30 us on this kernel).
+  // adds the partials in slice order. The partials are agent-scope atomic
+  // stores and loads (device-coherent: they bypass the per-XCD L2s). The
+  // block's barrier orders its threads' stores before thread 0's arrival, a
+  // release at agent scope; the last block's thread 0 then takes an
+  // agent-scope acquire fence, and its barrier orders the block's loads after
+  // it: every block's partials happen before the last block reads them. Only
+  // the last block of a tile pays the acquire (an L2 invalidation); a full
+  // device fence in every block measured 30 us on this kernel.
   // thread (quarter q, column) publishes rows q, q + 4, ...: the quarters in order
   for (uint32_t r = quarter; r < uint32_t(M); r += kDirectQuarters) {
     float mine = s_red[r * kDirectCols + cl];
@@ -212,11 +215,13 @@ __global__ __launch_bounds__(1024) void k_gemv_direct(Operands o, uint32_t m, ui
     __hip_atomic_store(&part[(split * M + r) * kDirectCols + cl], mine, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   }
-  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (tid == 0)
-    s_last = __hip_atomic_fetch_add(&o.arrivals[slot], 1u, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT) == splits - 1 ? 1u : 0u;
+  if (tid == 0) {
+    const bool last = __hip_atomic_fetch_add(&o.arrivals[slot], 1u, __ATOMIC_RELEASE,
+                                             __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    s_last = last ? 1u : 0u;
+  }
   __syncthreads();
   if (s_last == 0) return;
   // thread (quarter q, column) sums rows q, q + 4, ... over the slices, in
