@@ -137,6 +137,8 @@ _ENTRY_POINTS = {
     "ack_upload": ((_P, _P, _P, _SZ), _I32),
     "ack_download": ((_P, _P, _P, _SZ), _I32),
     "ack_buffer_copy": ((_P, _P, _U64, _P, _U64, _U64), _I32),
+    "ack_vq_sum_squares": ((_P, _P, _U64, _P), _I32),
+    "ack_vq_scale": ((_P, _P, _U64, ctypes.c_float), _I32),
     "ack_sync": ((_P,), _I32),
     "ack_stream_timer": ((_P, _U32, ctypes.POINTER(ctypes.c_float)), _I32),
     "ack_vq_plan_query": ((_P, _SZ, _U32, _P, _P, _P), _I32),

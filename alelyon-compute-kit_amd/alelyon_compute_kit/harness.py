@@ -117,6 +117,7 @@ class _DeviceState:
         first = images[0]
         self.words = first.layout["code_bytes"] // 4
         self.book = vq.ENTRIES * first.group
+        self.pool: dict[str, ack.Buffer] = {}  # a step's buffers, kept for the next step
         with ExitStack() as undo:
             self.codes4 = device.buffer(16 * self.words)
             undo.callback(self.codes4.free)
@@ -137,9 +138,24 @@ class _DeviceState:
     def holds(self, images) -> bool:
         return len(images) >= 3 and all(a == b for a, b in zip(self.images, images[:3]))
 
+    def scratch(self, device: ack.Device):
+        """A buffer source for one step that reuses this state's buffers from
+        step to step: slot ``key`` keeps its buffer while its size stays."""
+        def get(nbytes: int, key: str) -> ack.Buffer:
+            buf = self.pool.get(key)
+            if buf is None or buf.nbytes != nbytes:
+                if buf is not None:
+                    buf.free()
+                    del self.pool[key]
+                buf = self.pool[key] = device.buffer(nbytes)
+            return buf
+        return get
+
     def free(self) -> None:
         self.codes4.free()
         self.books4.free()
+        while self.pool:
+            self.pool.popitem()[1].free()
 
 
 class ExpertHarness:
@@ -340,21 +356,24 @@ class ExpertHarness:
             held.load(state.tensors)
         return held
 
-    def _device_image(self, values: np.ndarray, group: int, scratch, status, resident=None):
+    def _device_image(self, shape, group: int, scratch, status, name: str, values=None,
+                      resident=None):
         """``encode_activations`` on the device: the codebook fitted and the
-        values encoded there, left in device buffers. ``resident``, a buffer
-        already holding ``values`` as float32, saves the upload."""
-        flat = values.reshape(-1)
-        if resident is not None and flat.size >= group:
-            source, count = resident, flat.size
-        else:
-            sample = np.ascontiguousarray(_calibration_sample(flat, group), dtype=np.float32)
-            source, count = scratch(sample.nbytes), sample.size
+        values encoded there, left in device buffers. The values come from the
+        host array ``values`` or, when ``resident`` (a buffer holding them as
+        float32) is given and holds at least one vector, from the device."""
+        count = int(np.prod(shape))
+        if resident is not None and count >= group:
+            source, fitted = resident, count
+        else:  # the values, zero-padded to one vector for the fit if fewer
+            sample = np.ascontiguousarray(_calibration_sample(values.reshape(-1), group),
+                                          dtype=np.float32)
+            source, fitted = scratch(sample.nbytes, name + ".values"), sample.size
             source.upload(sample)
-        book = scratch(4 * vq.ENTRIES * group)
-        self.backend.fit_resident(source, count, book, status, group=group)
-        codes = scratch(vq.storage_layout(values.shape, group)["code_bytes"])
-        self.backend.run((0, flat.size, 1, 1, group, vq.ENTRIES, 0, 0), [source, book], codes,
+        book = scratch(4 * vq.ENTRIES * group, name + ".book")
+        self.backend.fit_resident(source, fitted, book, status, group=group)
+        codes = scratch(vq.storage_layout(shape, group)["code_bytes"], name + ".codes")
+        self.backend.run((0, count, 1, 1, group, vq.ENTRIES, 0, 0), [source, book], codes,
                          status)
         return codes, book
 
@@ -367,7 +386,7 @@ class ExpertHarness:
     def _scratch_space(self, stack: ExitStack):
         device = self.backend.device
 
-        def scratch(nbytes: int) -> ack.Buffer:
+        def scratch(nbytes: int, key: str = "") -> ack.Buffer:
             buf = device.buffer(nbytes)
             stack.callback(buf.free)
             return buf
@@ -379,7 +398,7 @@ class ExpertHarness:
             scratch = self._scratch_space(stack)
             status = scratch(4)
             status.upload(np.zeros(1, np.uint32))
-            xc, xb = self._device_image(x, group, scratch, status)
+            xc, xb = self._device_image(x.shape, group, scratch, status, "x", values=x)
             y = scratch(4 * m * n)
             self.backend.run((2, m, n, k, group, vq.ENTRIES, 0, 0),
                              [xc, xb, held.codes4, held.books4], y, status)
@@ -401,59 +420,71 @@ class ExpertHarness:
     def _device_step(self, held: _DeviceState, state, x, target, hyper,
                      max_grad_norm) -> _StepResult:
         """``_step`` on resident state: the same arithmetic in the same order,
-        with fits and encodes on the device and the float64 reductions on the
-        host."""
+        with fits and encodes on the device, the loss on the host and the
+        gradient's norm from the device's float64 sum of squares whenever that
+        certifies the clip numpy's norm would give (else the gradient comes to
+        the host for numpy's norm). The step's buffers persist in ``held``."""
         weight = state.tensors[0]
         (m, k), n, group = x.shape, weight.shape[1], weight.group
         run = self.backend.run
-        with ExitStack() as stack:
-            scratch = self._scratch_space(stack)
-            status = scratch(4)
-            status.upload(np.zeros(1, np.uint32))
-            xc, xb = self._device_image(x, group, scratch, status)
-            tc, tb = self._device_image(target, group, scratch, status)
-            prediction, decoded = scratch(4 * m * n), scratch(4 * m * n)
-            run((2, m, n, k, group, vq.ENTRIES, 0, 0), [xc, xb, held.codes4, held.books4],
-                prediction, status)
-            run((1, m * n, 1, 1, group, vq.ENTRIES, 0, 0), [tc, tb], decoded, status)
-            self._settled(status)
-            residual = prediction.download(np.float32).reshape(m, n) - \
-                decoded.download(np.float32).reshape(m, n)
-            loss = _mse(residual)
-            residual *= np.float32(2.0 / residual.size)
-            rc, rb = self._device_image(residual, group, scratch, status)
-            dense = scratch(4 * k * n)
-            run((2, k, n, m, group, vq.ENTRIES, 1, 0), [xc, xb, rc, rb], dense, status)
-            self._settled(status)
+        scratch = held.scratch(self.backend.device)
+        status = scratch(4, "status")
+        status.upload(np.zeros(1, np.uint32))
+        xc, xb = self._device_image(x.shape, group, scratch, status, "x", values=x)
+        tc, tb = self._device_image(target.shape, group, scratch, status, "t", values=target)
+        prediction, decoded = scratch(4 * m * n, "prediction"), scratch(4 * m * n, "decoded")
+        run((2, m, n, k, group, vq.ENTRIES, 0, 0), [xc, xb, held.codes4, held.books4],
+            prediction, status)
+        run((1, m * n, 1, 1, group, vq.ENTRIES, 0, 0), [tc, tb], decoded, status)
+        self._settled(status)
+        residual = prediction.download(np.float32).reshape(m, n) - \
+            decoded.download(np.float32).reshape(m, n)
+        loss = _mse(residual)
+        residual *= np.float32(2.0 / residual.size)
+        rc, rb = self._device_image(residual.shape, group, scratch, status, "r", values=residual)
+        dense = scratch(4 * k * n, "gradient")
+        run((2, k, n, m, group, vq.ENTRIES, 1, 0), [xc, xb, rc, rb], dense, status)
+        total = scratch(8, "sum_squares")
+        self.backend.sum_squares_resident(dense, k * n, total)
+        self._settled(status)
+        clip = _certified_clip(float(total.download(np.float64)[0]), k * n, max_grad_norm)
+        if clip is None or k * n < group:
+            # numpy's norm could round the scale (or the verdict) differently
             gradient = dense.download(np.float32).reshape(k, n)
             norm, scale = _clip_factor(gradient, max_grad_norm)
             gradient *= np.float32(scale)
             # unclipped, the device copy already holds the gradient to encode
-            gc, gb = self._device_image(gradient, group, scratch, status,
+            gc, gb = self._device_image((k, n), group, scratch, status, "g", values=gradient,
                                         resident=dense if scale == 1.0 else None)
-            held.codes4.copy_from(gc, 4 * held.words, offset=12 * held.words)
-            held.books4.copy_from(gb, 4 * held.book, offset=12 * held.book)
-            try:
-                block = vq.adamw_coefficients(hyper["lr"], hyper["beta1"], hyper["beta2"],
-                                              hyper["eps"], hyper["weight_decay"],
-                                              state.optimizer_step + 1)
-            except ValueError as exc:
-                raise HarnessError(f"expert optimizer refused the update: {exc}") from exc
-            coefficients = scratch(block.nbytes)
-            coefficients.upload(block)
-            new_codes, new_books = scratch(12 * held.words), scratch(12 * held.book)
-            changed = scratch(4)
-            self.backend.adamw_step_resident(held.codes4, held.books4, coefficients, new_codes,
-                                             new_books, changed, status,
-                                             count=weight.layout["elements"], group=group)
-            self._settled(status)
-            codes = new_codes.download(np.uint32).reshape(3, held.words)
-            books = new_books.download(np.float32).reshape(3, vq.ENTRIES, group)
-            images = tuple(vq.VQArray(weight.shape, group, c, b) for c, b in zip(codes, books))
-            held.codes4.copy_from(new_codes, 12 * held.words)
-            held.books4.copy_from(new_books, 12 * held.book)
-            held.images = images
-        layouts = tuple(vq.storage_layout(a.shape, group) for a in (x, target, gradient))
+        else:
+            norm, scale = clip
+            if scale != 1.0:
+                self.backend.scale_resident(dense, k * n, np.float32(scale))
+            gc, gb = self._device_image((k, n), group, scratch, status, "g", resident=dense)
+        held.codes4.copy_from(gc, 4 * held.words, offset=12 * held.words)
+        held.books4.copy_from(gb, 4 * held.book, offset=12 * held.book)
+        try:
+            block = vq.adamw_coefficients(hyper["lr"], hyper["beta1"], hyper["beta2"],
+                                          hyper["eps"], hyper["weight_decay"],
+                                          state.optimizer_step + 1)
+        except ValueError as exc:
+            raise HarnessError(f"expert optimizer refused the update: {exc}") from exc
+        coefficients = scratch(block.nbytes, "coefficients")
+        coefficients.upload(block)
+        new_codes = scratch(12 * held.words, "new_codes")
+        new_books = scratch(12 * held.book, "new_books")
+        changed = scratch(4, "changed")
+        self.backend.adamw_step_resident(held.codes4, held.books4, coefficients, new_codes,
+                                         new_books, changed, status,
+                                         count=weight.layout["elements"], group=group)
+        self._settled(status)
+        codes = new_codes.download(np.uint32).reshape(3, held.words)
+        books = new_books.download(np.float32).reshape(3, vq.ENTRIES, group)
+        images = tuple(vq.VQArray(weight.shape, group, c, b) for c, b in zip(codes, books))
+        held.codes4.copy_from(new_codes, 12 * held.words)
+        held.books4.copy_from(new_books, 12 * held.book)
+        held.images = images
+        layouts = tuple(vq.storage_layout(shape, group) for shape in (x.shape, target.shape, (k, n)))
         return _StepResult(loss, norm, scale, images, layouts)
 
 
@@ -462,6 +493,28 @@ def _mse(residual: np.ndarray) -> float:
     if not math.isfinite(loss):
         raise HarnessError("expert loss is nonfinite")
     return loss
+
+
+def _certified_clip(total: float, count: int, max_grad_norm: float):
+    """(norm, scale) from a float64 sum of squares of ``count`` float32 values
+    taken within (count / 65536 + 15)·2^-53 of the exact sum (the device's),
+    when numpy's ``np.linalg.norm`` of the same values (a float64 dot product,
+    within (count − 1)·2^-53 in any order) would lead to the same float32
+    scale and the same clip verdict; None when it might not. The norm reported
+    is this sum's; numpy's own differs from it in the last bits, as it does
+    between BLAS builds and thread counts."""
+    if not math.isfinite(total):
+        raise HarnessError("expert gradient norm is nonfinite")
+    slack = (count + count / 65536 + 64) * 2.0 ** -53 * 1.01
+
+    def scale_of(sum_of_squares: float) -> float:
+        return min(1.0, max_grad_norm / (math.sqrt(sum_of_squares) + 1e-6))
+
+    # the scale falls as the sum rises: the two ends bracket numpy's
+    high, low = scale_of(total * (1 - slack)), scale_of(total * (1 + slack))
+    if np.float32(high) != np.float32(low) or (high < 1.0) != (low < 1.0):
+        return None
+    return math.sqrt(total), scale_of(total)
 
 
 def _clip_factor(gradient: np.ndarray, max_grad_norm: float) -> tuple[float, float]:

@@ -422,6 +422,21 @@ class VQDevice:
                          None if init is None else init.handle, book.handle, status.handle,
                          elements, group, iterations, sample_vectors, context="fit_codebook")
 
+    def sum_squares_resident(self, values: ack.Buffer, count: int, out: ack.Buffer) -> None:
+        """Enqueue the float64 sum of squares of ``count`` float32 values of a
+        device buffer into the first 8 bytes of ``out``: a fixed order, within
+        (count / 65536 + 15)·2^-53 of the exact sum, relatively."""
+        count = _bounded_int(count, "count", 0, 2 ** 62)
+        self.device.call("ack_vq_sum_squares", values.handle, count, out.handle,
+                         context="sum_squares")
+
+    def scale_resident(self, values: ack.Buffer, count: int, factor) -> None:
+        """Enqueue ``values[i] *= float32(factor)`` for ``count`` float32 values
+        of a device buffer, in place (numpy's float32 multiply, bit for bit)."""
+        count = _bounded_int(count, "count", 0, 2 ** 62)
+        self.device.call("ack_vq_scale", values.handle, count, float(np.float32(factor)),
+                         context="scale")
+
     def adamw_step_resident(self, codes: ack.Buffer, books: ack.Buffer, coefficients: ack.Buffer,
                             out_codes: ack.Buffer, out_books: ack.Buffer, changed: ack.Buffer,
                             status: ack.Buffer, *, count: int, group: int,

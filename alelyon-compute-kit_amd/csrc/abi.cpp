@@ -714,6 +714,44 @@ int32_t ack_buffer_copy(const AckDevice* handle, const AckBuffer* dst, uint64_t 
   return ACK_OK;
 }
 
+int32_t ack_vq_sum_squares(const AckDevice* handle, const AckBuffer* x, uint64_t count,
+                           const AckBuffer* out) {
+  std::shared_ptr<Device> dev;
+  std::unique_lock<std::mutex> lock;
+  if (int32_t rc = enter(handle, &dev, &lock)) return rc;
+  BufferRec* xb = nullptr;
+  BufferRec* ob = nullptr;
+  if (int32_t rc = lookup_buffer(*dev, x, &xb)) return rc;
+  if (int32_t rc = lookup_buffer(*dev, out, &ob)) return rc;
+  if (count > xb->bytes / sizeof(float) || ob->bytes < sizeof(double)) {
+    set_error("sum of squares: " + std::to_string(count) + " values or the 8-byte result "
+              "do not fit their buffers");
+    return ACK_ERR_SIZE;
+  }
+  if (int32_t rc = ensure_workspace(*dev, 256 * sizeof(double))) return rc;
+  hipError_t e = ackvq::launch_sum_squares(dev->stream, static_cast<const float*>(xb->ptr), count,
+                                           static_cast<double*>(dev->workspace),
+                                           static_cast<double*>(ob->ptr));
+  if (e != hipSuccess) return hip_failure(*dev, "sum of squares", e, true);
+  return ACK_OK;
+}
+
+int32_t ack_vq_scale(const AckDevice* handle, const AckBuffer* x, uint64_t count, float factor) {
+  std::shared_ptr<Device> dev;
+  std::unique_lock<std::mutex> lock;
+  if (int32_t rc = enter(handle, &dev, &lock)) return rc;
+  BufferRec* xb = nullptr;
+  if (int32_t rc = lookup_buffer(*dev, x, &xb)) return rc;
+  if (count > xb->bytes / sizeof(float)) {
+    set_error("scale: " + std::to_string(count) + " values do not fit the buffer");
+    return ACK_ERR_SIZE;
+  }
+  if (count == 0) return ACK_OK;
+  hipError_t e = ackvq::launch_scale(dev->stream, static_cast<float*>(xb->ptr), count, factor);
+  if (e != hipSuccess) return hip_failure(*dev, "scale", e, true);
+  return ACK_OK;
+}
+
 int32_t ack_sync(const AckDevice* handle) {
   std::shared_ptr<Device> dev;
   std::unique_lock<std::mutex> lock;

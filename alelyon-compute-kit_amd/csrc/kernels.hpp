@@ -55,6 +55,12 @@ MatmulPath choose_matmul_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group
 
 bool gram_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                   bool any_size);
+// Float64 sum of squares of count float32 values: 256 block partials into
+// `partial`, then their ordered total into *out.
+hipError_t launch_sum_squares(hipStream_t s, const float* x, uint64_t count, double* partial,
+                              double* out);
+// x[i] *= f in FP32, in place.
+hipError_t launch_scale(hipStream_t s, float* x, uint64_t count, float f);
 hipError_t launch_gram(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t group);
 

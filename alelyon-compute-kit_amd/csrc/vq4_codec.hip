@@ -708,6 +708,68 @@ hipError_t launch_adamw_keep(hipStream_t s, const AdamwInputs& in, const FitArgs
   return hipGetLastError();
 }
 
+// ---- sum of squares in float64 (the harness's gradient norm) -------------------
+// Each square of an FP32 value is exact in float64. Thread t of the grid sums
+// the squares of values t, t + T, t + 2T, ... (T = kSumBlocks x kThreads) in
+// order, a wave sums its 64 lanes by a fixed butterfly, the block its waves in
+// order; k_sumsq_final adds the block sums in block order. The order is fixed,
+// so the result is deterministic, and every path from a square to the total
+// has at most count / T + 15 additions: its error is within
+// (count / T + 15) u64 of the sum.
+constexpr uint32_t kSumBlocks = 256;
+
+__global__ __launch_bounds__(kThreads) void k_sumsq_partial(const float* __restrict__ x,
+                                                            uint64_t count,
+                                                            double* __restrict__ partial) {
+  __shared__ double wsum[kThreads / 64];
+  const uint64_t stride = uint64_t(kSumBlocks) * kThreads;
+  double acc = 0.0;
+  for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < count; i += stride) {
+    const double v = double(x[i]);
+    acc += v * v;
+  }
+  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+  if (threadIdx.x % 64 == 0) wsum[threadIdx.x / 64] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double b = wsum[0];
+    for (uint32_t w = 1; w < kThreads / 64; ++w) b += wsum[w];
+    partial[blockIdx.x] = b;
+  }
+}
+
+__global__ __launch_bounds__(64) void k_sumsq_final(const double* __restrict__ partial,
+                                                    double* __restrict__ out) {
+  if (threadIdx.x == 0) {
+    double t = partial[0];
+    for (uint32_t b = 1; b < kSumBlocks; ++b) t += partial[b];
+    *out = t;
+  }
+}
+
+// x[i] = x[i] * f, one rounded FP32 multiply per value (the harness's clip).
+__global__ __launch_bounds__(kThreads) void k_scale_f32(float* __restrict__ x, uint64_t count,
+                                                        float f) {
+  const uint64_t stride = uint64_t(gridDim.x) * kThreads;
+  for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < count; i += stride)
+    x[i] = x[i] * f;
+}
+
+hipError_t launch_scale(hipStream_t s, float* x, uint64_t count, float f) {
+  const uint64_t want = (count + kThreads - 1) / kThreads;
+  k_scale_f32<<<dim3(uint32_t(want < 4096 ? (want ? want : 1) : 4096)), kThreads, 0, s>>>(x, count, f);
+  return hipGetLastError();
+}
+
+hipError_t launch_sum_squares(hipStream_t s, const float* x, uint64_t count, double* partial,
+                              double* out) {
+  k_sumsq_partial<<<kSumBlocks, kThreads, 0, s>>>(x, count, partial);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  k_sumsq_final<<<1, 64, 0, s>>>(partial, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_adamw_encode(hipStream_t s, const AdamwInputs& in, const float* books3,
                                uint32_t* out_codes, uint32_t* changed, uint32_t* status) {
   const uint32_t vectors = in.m / in.group + (in.m % in.group != 0);

@@ -296,6 +296,25 @@ int32_t ack_stream_timer(const AckDevice* dev, uint32_t phase, float* ms_out);
 int32_t ack_buffer_copy(const AckDevice* dev, const AckBuffer* dst, uint64_t dst_offset,
                         const AckBuffer* src, uint64_t src_offset, uint64_t bytes);
 
+/* Sum of squares of `count` float32 values at the start of buffer `x`, in
+ * float64, written to the first 8 bytes of `out` (enqueued like ack_vq). No
+ * counterpart in the reference, whose harness takes the gradient's norm on the
+ * host (src/alelyon_compute_kit/harness.py:196): for the resident harness,
+ * which keeps the gradient on the device. Each square is exact in float64 and
+ * the sum is taken in a fixed order, within (count / 65536 + 15) ulp-units
+ * (2^-53) of the exact sum, relatively. ACK_ERR_SIZE when `count` values or 8
+ * bytes do not fit the buffers. */
+int32_t ack_vq_sum_squares(const AckDevice* dev, const AckBuffer* x, uint64_t count,
+                           const AckBuffer* out);
+
+/* x[i] = x[i] * factor for the first `count` float32 values of `x`, one
+ * rounded FP32 multiply each, in place (enqueued like ack_vq). No counterpart
+ * in the reference, whose harness scales the clipped gradient on the host
+ * (src/alelyon_compute_kit/harness.py:200): for the resident harness. The
+ * results equal numpy's float32 multiply bit for bit. ACK_ERR_SIZE when
+ * `count` values do not fit the buffer. */
+int32_t ack_vq_scale(const AckDevice* dev, const AckBuffer* x, uint64_t count, float factor);
+
 /* Wait for every operation enqueued on the device. */
 int32_t ack_sync(const AckDevice* dev);
 

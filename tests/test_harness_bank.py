@@ -360,14 +360,22 @@ def test_config2_chain_and_clipped_step_match_the_oracle(vqdev):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape,group,batch", [((128, 128), 16, 32), ((512, 384), 8, 64),
-                                               ((96, 256), 32, 3)])
-def test_resident_harness_commits_the_default_images(tmp_path, vqdev, shape, group, batch):
+@pytest.mark.parametrize("shape,group,batch,certified", [((128, 128), 16, 32, True),
+                                                         ((512, 384), 8, 64, True),
+                                                         ((96, 256), 32, 3, True),
+                                                         ((128, 128), 16, 32, False)])
+def test_resident_harness_commits_the_default_images(tmp_path, vqdev, monkeypatch, shape, group,
+                                                      batch, certified):
     """The resident harness (optimizer state kept on the device, codebooks
-    fitted there) commits byte-identical generations to the default GPU
-    harness over three steps, the middle one clipped; a write by another
-    harness in between is picked up."""
+    fitted there, the clip from the device's sum of squares) commits
+    byte-identical generations to the default GPU harness over three steps,
+    the middle one clipped; a write by another harness in between is picked
+    up. certified False: every clip falls back to numpy's norm of the
+    downloaded gradient, the path taken when the device sum cannot certify
+    numpy's float32 scale."""
     from gpu_util import say
+    if not certified:
+        monkeypatch.setattr(harness, "_certified_clip", lambda *args: None)
     a_bank, b_bank = _twin_banks(tmp_path, (shape,) * 3, group, 11, True)
     rng = np.random.default_rng(shape[0] + batch)
     x = rng.standard_normal((batch, shape[0])).astype(np.float32)
@@ -381,6 +389,11 @@ def test_resident_harness_commits_the_default_images(tmp_path, vqdev, shape, gro
             b = plain.train_step(x, t, lr=1e-3, beta1=0.9, beta2=0.999, max_grad_norm=norm)
             da, db = a.to_dict(), b.to_dict()
             da.pop("elapsed_seconds"), db.pop("elapsed_seconds")
+            # the resident norm is the device's float64 sum of squares, within
+            # the certified slack of numpy's dot product
+            na, nb = da.pop("gradient_norm_before_clip"), db.pop("gradient_norm_before_clip")
+            count = shape[0] * shape[1]
+            assert abs(na - nb) <= nb * (count + 64) * 2.0 ** -53
             assert da == db
             for ta, tb in zip(a_bank.read_expert(0, 0), b_bank.read_expert(0, 0)):
                 assert ta.to_bytes() == tb.to_bytes()
@@ -396,6 +409,66 @@ def test_resident_harness_commits_the_default_images(tmp_path, vqdev, shape, gro
             assert ta.to_bytes() == tb.to_bytes()
     finally:
         res.close()
+
+
+def test_certified_clip_brackets_numpys_norm():
+    """The device's float64 sum of squares certifies numpy's clip only when
+    every sum within the slack gives the same float32 scale and verdict; the
+    certified scale then equals numpy's, and the norm agrees within it."""
+    import math
+    rng = np.random.default_rng(0)
+    certified = 0
+    for trial in range(300):
+        g = (rng.standard_normal(1000) * 10.0 ** rng.uniform(-4, 1)).astype(np.float32)
+        exact = math.fsum(np.square(g.astype(np.float64)))  # exact squares, exactly rounded sum
+        clip = harness._certified_clip(exact, g.size, 1.0)
+        norm, scale = harness._clip_factor(g, 1.0)
+        if clip is None:
+            continue
+        certified += 1
+        assert np.float32(clip[1]) == np.float32(scale) and (clip[1] < 1.0) == (scale < 1.0)
+        assert abs(clip[0] - norm) <= norm * 1024 * 2.0 ** -53
+    assert certified >= 290
+    # a scale half a float32 ulp from a rounding boundary, and a norm at the
+    # clip's threshold, are not certified
+    f = np.float32(0.3)
+    mid = float(f) + float(np.spacing(f)) / 2
+    assert harness._certified_clip((1.0 / mid - 1e-6) ** 2, 10 ** 6, 1.0) is None
+    assert harness._certified_clip((1.0 - 1e-6) ** 2, 10 ** 6, 1.0) is None
+    assert harness._certified_clip(4.0, 10 ** 6, 1.0)[1] == 1.0 / (2.0 + 1e-6)
+    with pytest.raises(harness.HarnessError, match="nonfinite"):
+        harness._certified_clip(float("inf"), 10, 1.0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("count", [1, 7, 4096, 1_000_003, 4_194_304])
+def test_device_sum_of_squares_and_scale(vqdev, count):
+    """ack_vq_sum_squares within its stated bound of the exactly rounded sum
+    of the (exact) float64 squares; ack_vq_scale equal to numpy's float32
+    multiply bit for bit; a nonfinite value makes the sum nonfinite."""
+    import math
+    from gpu_util import say
+    rng = np.random.default_rng(count)
+    x = (rng.standard_normal(count) * 3).astype(np.float32)
+    device = vqdev.device
+    buf, out = device.buffer(x.nbytes), device.buffer(8)
+    try:
+        say("sum of squares", count)
+        buf.upload(x)
+        vqdev.sum_squares_resident(buf, count, out)
+        got = float(out.download(np.float64)[0])
+        exact = math.fsum(np.square(x.astype(np.float64)))
+        assert abs(got - exact) <= exact * (count / 65536 + 15) * 2.0 ** -53
+        vqdev.scale_resident(buf, count, 0.7)
+        y = buf.download(np.float32)
+        np.testing.assert_array_equal(y.view(np.uint32), (x * np.float32(0.7)).view(np.uint32))
+        x[count // 2] = np.inf
+        buf.upload(x)
+        vqdev.sum_squares_resident(buf, count, out)
+        assert not math.isfinite(float(out.download(np.float64)[0]))
+    finally:
+        buf.free()
+        out.free()
 
 
 def test_resident_harness_needs_a_device_backend(tmp_path):
