@@ -712,7 +712,8 @@ GRAM_SHAPES = [(1, 256, 256, 16), (37, 53, 96, 8), (64, 96, 128, 32), (130, 200,
 @pytest.mark.parametrize("m,n,k,group", GRAM_SHAPES)
 def test_gram_mfma_within_tolerance(vqdev, oracle, any_size, m, n, k, group):
     """B stored (n, k) with both operands grouped along k: one-hot A times the
-    codebooks' Gram table on fp16 MFMA (hi + mid + lo split). Products below
+    codebooks' Gram table on bf16 MFMA (three bf16 terms hi + mid + lo, every
+    entry down to 2^-118 of the largest exact). Products below
     2^22 multiply-adds take the general kernel by default; the test policy
     sends them through the Gram kernel."""
     from oracle import vq4_numpy as o
