@@ -416,12 +416,17 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
 // Split k, second half: S[r][(j, e)] = the splits' partial sums added in split
 // order, then k_onehot_mfma's epilogue, y[r][G j + t] = sum_e S[r][(j, e)]
 // C_B[e][t] (e ascending), unscaled by 2^-shift for packed A. grid:
-// (ceil(n / 256), m), one thread per output.
+// (ceil(n / 256), m): block (x, r) finishes columns 256 x .. 256 x + 255 of row
+// r. Its threads first sum the block's 16 (256 / G) S entries over the splits
+// (each entry read once, coalesced, the loads of four splits issued before
+// their adds), then one thread per output takes its group's 16 from LDS.
 template <int G, bool AD>
 __global__ __launch_bounds__(256) void k_onehot_finish(Operands o, uint32_t m, uint32_t n,
                                                        uint32_t splits,
                                                        const float* __restrict__ partial) {
+  constexpr uint32_t kS = 16 * 256 / G;  // S entries of the block's 256 columns
   __shared__ float sred[4];
+  __shared__ float sS[kS];
   const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   int shift = 0;
   if (!AD) {
@@ -436,27 +441,34 @@ __global__ __launch_bounds__(256) void k_onehot_finish(Operands o, uint32_t m, u
     __syncthreads();
     shift = book_shift(fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3])));
   }
-  const uint32_t col = blockIdx.x * 256 + tid, r = blockIdx.y;
-  if (col >= n) return;
-  const uint32_t j = col / G, tc = col % G, cols = 16 * (n / G);
-  const float* b_book = static_cast<const float*>(o.in[3]);
-  float sv[16];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) sv[e] = 0.0f;
-  for (uint32_t z = 0; z < splits; ++z) {
-    const float4* p = reinterpret_cast<const float4*>(partial + (uint64_t(z) * m + r) * cols + 16 * j);
-#pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      const float4 v = p[f];
-      sv[4 * f] += v.x;
-      sv[4 * f + 1] += v.y;
-      sv[4 * f + 2] += v.z;
-      sv[4 * f + 3] += v.w;
+  const uint32_t r = blockIdx.y, c0 = blockIdx.x * 256;
+  const uint32_t cols = 16 * (n / G);                 // S entries per row
+  const uint32_t s0 = 16 * (c0 / G);                  // the block's first S entry
+  const uint64_t zstride = uint64_t(m) * cols;
+  for (uint32_t i = tid; i < kS; i += 256) {
+    if (s0 + i >= cols) break;
+    const float* p = partial + uint64_t(r) * cols + s0 + i;
+    float sum = 0.0f;
+    uint32_t z = 0;
+    for (; z + 4 <= splits; z += 4) {
+      const float a0 = p[z * zstride], a1 = p[(z + 1) * zstride];
+      const float a2 = p[(z + 2) * zstride], a3 = p[(z + 3) * zstride];
+      sum += a0;
+      sum += a1;
+      sum += a2;
+      sum += a3;
     }
+    for (; z < splits; ++z) sum += p[z * zstride];
+    sS[i] = sum;
   }
+  __syncthreads();
+  const uint32_t col = c0 + tid;
+  if (col >= n) return;
+  const uint32_t jl = tid / G, tc = col % G;
+  const float* b_book = static_cast<const float*>(o.in[3]);
   float y = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 16; ++e) y = fmaf(sv[e], b_book[e * G + tc], y);
+  for (int e = 0; e < 16; ++e) y = fmaf(sS[16 * jl + e], b_book[e * G + tc], y);
   if (!AD) y = ldexpf(y, -shift);
   static_cast<float*>(o.out)[uint64_t(r) * n + col] = y;
   if (__any(!finite_f32(y)) && lane == 0) atomicOr(o.status, 1u);
