@@ -162,26 +162,34 @@ __global__ __launch_bounds__(256) void k_nibble_columns(const uint32_t* __restri
 // partial[z][r][16 j + e] instead of finishing the product; k_onehot_finish
 // adds the splits in order and applies C_B. partial is null when k is not
 // split (gridDim.z 1, kpart k).
+// S rows a wave stages per epilogue round: one or two 32-row blocks
+template <int X>
+constexpr uint32_t oh_chunk_rows() { return X % 2 ? 32 : 64; }
+
+// A's table: [term][8-entry chunk of the group][code][8]; code 16 is empty
+// (rows past m). The 16 lanes of a read phase read one chunk, so distinct
+// codes land in distinct banks.
+template <int G>
+using OHTable = __bf16[kOHTerms][G / 8][17][8];
+
+// One block of k_onehot_mfma: word column q, rows rowb .. rowb + 64 X - 1,
+// split part z. The LDS areas come from the kernel: sS holds at least
+// 4 oh_chunk_rows<X>() x 64 floats (one wave's S, a round at a time).
 template <int G, int X, bool AD>
-__global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
-    Operands o, uint32_t m, uint32_t n, uint32_t k, const uint32_t* __restrict__ nc,
-    uint32_t kpart, float* __restrict__ partial) {
+__device__ __forceinline__ void onehot_block(const Operands& o, uint32_t m, uint32_t n,
+                                             uint32_t k, const uint32_t* __restrict__ nc,
+                                             uint32_t kpart, float* __restrict__ partial,
+                                             uint32_t q, uint32_t rowb, uint32_t z,
+                                             bool check_books, OHTable<G>& tabA, float* sS,
+                                             float* sbook, float* sred) {
   static_assert(G == 16 || G == 32 || (AD && G == 8), "a 16-step of k lies in one group of A");
-  static_assert(X == 1 || X == 2 || X == 4, "row blocks per wave");
+  static_assert(X >= 1 && X <= 4, "row blocks per wave");
   constexpr int kOHX = X;
-  constexpr uint32_t kChunkRows = X < 2 ? 32 * X : 64;  // S rows staged per epilogue round
-  // A's table: [term][8-entry chunk of the group][code][8]; code 16 is empty
-  // (rows past m). The 16 lanes of a read phase read one chunk, so distinct
-  // codes land in distinct banks.
-  __shared__ __align__(16) __bf16 tabA[kOHTerms][G / 8][17][8];
-  __shared__ __align__(16) float sS[4][kChunkRows][64];  // one wave's S, a round at a time
-  __shared__ float sbook[16 * G];
-  __shared__ float sred[4];
+  constexpr uint32_t kChunkRows = oh_chunk_rows<X>();
   const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const uint32_t i32 = lane % 32, h = lane / 32;
   const uint32_t wy = wave / 2, wx = wave % 2;
-  const uint32_t q = blockIdx.x;
-  const uint32_t row0 = blockIdx.y * (64 * X) + 32 * X * wy;
+  const uint32_t row0 = rowb + 32 * X * wy;
   const uint32_t J = k / G;
   const uint64_t a_last = (uint64_t(m) * J + 7) / 8 - 1;
   const uint32_t* a_codes = static_cast<const uint32_t*>(o.in[0]);
@@ -205,7 +213,7 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
   const uint32_t* nc0 = nc + uint64_t(8 * q + 4 * wx + i32 / 16) * k8 + h;
   const uint32_t* nc1 = nc0 + 2 * uint64_t(k8);
   // this block's inner indices [kb, ke)
-  const uint32_t kb = blockIdx.z * kpart;
+  const uint32_t kb = z * kpart;
   const uint32_t ke = (kb + kpart) < k ? (kb + kpart) : k;
 
   // ---- tables: B's book as is; A's scaled below 2^15 and split into three
@@ -216,7 +224,7 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
   for (uint32_t i = tid; i < 16 * G; i += kOHThreads) {
     const float a = AD ? 0.0f : a_book[i], b = b_book[i];
     sbook[i] = b;
-    if (blockIdx.x == 0 && blockIdx.y == 0) bad |= !finite_f32(a) || !finite_f32(b);
+    if (check_books) bad |= !finite_f32(a) || !finite_f32(b);
     amax = fmaxf(amax, finite_f32(a) ? fabsf(a) : 0.0f);
   }
   for (int off = 1; off < 64; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
@@ -343,7 +351,7 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
 
   if (partial != nullptr) {  // this split's S, scaled, for k_onehot_finish
     const uint32_t cols = 16 * (n / G);
-    float* pz = partial + uint64_t(blockIdx.z) * m * cols + 16 * (8 * q + 4 * wx) + i32;
+    float* pz = partial + uint64_t(z) * m * cols + 16 * (8 * q + 4 * wx) + i32;
 #pragma unroll
     for (int x = 0; x < kOHX; ++x)
 #pragma unroll
@@ -379,14 +387,14 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
       for (int y = 0; y < 2; ++y)
 #pragma unroll
         for (int t = 0; t < 16; ++t)
-          sS[wave][32 * x + (t % 4) + 4 * h + 8 * (t / 4)][32 * y + i32] =
+          sS[(wave * kChunkRows + 32 * x + (t % 4) + 4 * h + 8 * (t / 4)) * 64 + 32 * y + i32] =
               acc[kTilesPerRound * hv + x][y][t];
     __syncthreads();
     for (uint32_t idx = lane; idx < kChunkRows * 4 * G; idx += 64) {
       const uint32_t row = idx / (4 * G), jl = (idx % (4 * G)) / G;
       const uint32_t r = row0 + kChunkRows * hv + row;
       if (r >= m) break;
-      const float4* sp = reinterpret_cast<const float4*>(&sS[wave][row][16 * jl]);
+      const float4* sp = reinterpret_cast<const float4*>(&sS[(wave * kChunkRows + row) * 64 + 16 * jl]);
       const float4 s0 = sp[0], s1 = sp[1], s2 = sp[2], s3 = sp[3];
       float y = 0.0f;
       y = fmaf(s0.x, cb[0], y);
@@ -411,6 +419,57 @@ __global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
     }
   }
   if (__any(bad) && lane == 0) atomicOr(o.status, 1u);
+}
+
+// grid: (n / (8 G), ceil(m / (64 X)), split parts)
+template <int G, int X, bool AD>
+__global__ __launch_bounds__(kOHThreads, X == 1 ? 4 : 2) void k_onehot_mfma(
+    Operands o, uint32_t m, uint32_t n, uint32_t k, const uint32_t* __restrict__ nc,
+    uint32_t kpart, float* __restrict__ partial) {
+  __shared__ __align__(16) OHTable<G> tabA;
+  __shared__ __align__(16) float sS[4 * oh_chunk_rows<X>() * 64];
+  __shared__ float sbook[16 * G];
+  __shared__ float sred[4];
+  onehot_block<G, X, AD>(o, m, n, k, nc, kpart, partial, blockIdx.x, blockIdx.y * (64 * X),
+                         blockIdx.z, blockIdx.x == 0 && blockIdx.y == 0, tabA, sS, sbook, sred);
+}
+
+// Packed A on a grid with fewer 256-row blocks than the chip holds (two per
+// compute unit, kOHSlots), where whole 256-row blocks would leave slots idle
+// for the whole product (config 4: 448 blocks for 512 slots): the rows of
+// each word column are cut into 256-row (X = 4) and 192-row (X = 3) blocks, as
+// many of each as half the slots, so that each compute unit can hold one of
+// each and every unit does the same work. Columns 0 .. c1 - 1 hold a1 blocks
+// of 256 rows then b1 of 192; columns c1 .. hold a2 and b2. Blocks
+// 0 .. n4 - 1 are the 256-row ones, column-major; the rest the 192-row ones.
+struct OHMixed {
+  uint32_t c1, a1, b1, a2, b2;
+};
+
+template <int G>
+__global__ __launch_bounds__(kOHThreads, 2) void k_onehot_mixed(Operands o, uint32_t m, uint32_t n,
+                                                                uint32_t k,
+                                                                const uint32_t* __restrict__ nc,
+                                                                OHMixed mx) {
+  __shared__ __align__(16) OHTable<G> tabA;
+  __shared__ __align__(16) float sS[4 * 64 * 64];
+  __shared__ float sbook[16 * G];
+  __shared__ float sred[4];
+  const uint32_t b = blockIdx.x, n4 = mx.c1 * mx.a1 + (n / (8 * G) - mx.c1) * mx.a2;
+  if (b < n4) {
+    const uint32_t first = mx.c1 * mx.a1;
+    const uint32_t q = b < first ? b / mx.a1 : mx.c1 + (b - first) / mx.a2;
+    const uint32_t slot = b < first ? b % mx.a1 : (b - first) % mx.a2;
+    onehot_block<G, 4, false>(o, m, n, k, nc, k, nullptr, q, 256 * slot, 0, b == 0, tabA, sS,
+                              sbook, sred);
+  } else {
+    const uint32_t j = b - n4, first = mx.c1 * mx.b1;
+    const uint32_t q = j < first ? j / mx.b1 : mx.c1 + (j - first) / mx.b2;
+    const uint32_t slot = j < first ? j % mx.b1 : (j - first) % mx.b2;
+    const uint32_t above = 256 * (j < first ? mx.a1 : mx.a2);  // the column's 256-row blocks
+    onehot_block<G, 3, false>(o, m, n, k, nc, k, nullptr, q, above + 192 * slot, 0, false, tabA,
+                              sS, sbook, sred);
+  }
 }
 
 // Split k, second half: S[r][(j, e)] = the splits' partial sums added in split
@@ -717,6 +776,35 @@ Split onehot_split(uint32_t m, uint32_t n, uint32_t k, uint32_t group, bool dens
   return {(passes + per - 1) / per, per * pass};
 }
 
+// The mixed 256/192-row tiling of k_onehot_mixed: per word column, a 256-row
+// and b 192-row blocks with 4 a + 3 b = m / 64, two column classes, and
+// kOHSlots / 2 blocks of each size in all. False when the grid has no tail or
+// no such split exists (m not a multiple of 64, or no two classes fit).
+constexpr uint32_t kOHSlots = 512;  // blocks the chip holds at once: two per compute unit
+
+bool onehot_mixed_plan(uint32_t m, uint32_t n, uint32_t group, OHMixed* out) {
+  const uint32_t cols = n / (8 * group);
+  const uint64_t tiles = big_grid(m, n, group);
+  if (group == 8 || tiles < kOHBigGrid || tiles >= kOHSlots || m % 64 != 0) return false;
+  const uint32_t half = kOHSlots / 2, u = m / 64;
+  for (uint32_t a1 = 0; 4 * a1 <= u; ++a1) {
+    if ((u - 4 * a1) % 3 != 0) continue;
+    const uint32_t b1 = (u - 4 * a1) / 3;
+    for (uint32_t a2 = 0; 4 * a2 <= u; ++a2) {
+      if ((u - 4 * a2) % 3 != 0) continue;
+      const uint32_t b2 = (u - 4 * a2) / 3;
+      for (uint32_t c1 = 0; c1 <= cols; ++c1) {
+        const uint32_t c2 = cols - c1;
+        if (c1 * a1 + c2 * a2 == half && c1 * b1 + c2 * b2 == half) {
+          *out = OHMixed{c1, a1, b1, a2, b2};
+          return true;
+        }
+      }
+    }
+  }
+  return false;
+}
+
 }  // namespace
 
 // From kOneHotMinRows rows of A always; from 16 rows when B holds at least
@@ -785,7 +873,10 @@ void launch_onehot_g(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, u
       launch_planes<G>(s, o, m, n, k, px, nc, static_cast<__bf16*>(rest));
     else launch_onehot_x<G, 1, true>(s, o, m, n, k, nc, partial);
   } else if (big_grid(m, n, G) >= kOHBigGrid) {
-    launch_onehot_x<G, 4, false>(s, o, m, n, k, nc, nullptr);
+    OHMixed mx;
+    if (onehot_mixed_plan(m, n, G, &mx))
+      k_onehot_mixed<G><<<dim3(kOHSlots), kOHThreads, 0, s>>>(o, m, n, k, nc, mx);
+    else launch_onehot_x<G, 4, false>(s, o, m, n, k, nc, nullptr);
   } else {
     launch_onehot_x<G, 1, false>(s, o, m, n, k, nc, partial);
   }

@@ -603,13 +603,16 @@ def test_large_m_under_the_test_policy(vqdev, oracle, any_size, m, n, k, group):
 # shapes the 256-row blocks. 64-row grids of fewer than 256 blocks split k
 # (4 ways at 16 x 1024 x 1024, 8 at 63 x 4096 x 4096 and at the 128-row
 # chunk, 3 at 513 x 2048 x 4096; 48 x 2048 x 4112 into 11 parts of 3 passes,
-# the last one 2 passes and a 16-step)
+# the last one 2 passes and a 16-step). The last two shapes have fewer 256-row
+# blocks than the chip's 512 slots and take the mixed 256/192-row tiling: one
+# column class (4 + 4 blocks per column) and two (5 + 4 and 2 + 8, as config 4)
 ONEHOT_SHAPES = [(16, 1024, 1024, 16), (40, 2048, 512, 32), (63, 4096, 4096, 16),
                  (64, 256, 64, 16), (100, 512, 96, 32), (130, 2048, 256, 16),
                  (256, 1024, 512, 32), (333, 768, 1024, 16), (256, 256, 16, 16),
                  (300, 512, 1040, 16), (1000, 4096, 288, 32), (513, 2048, 4096, 32),
                  (48, 2048, 4112, 16), (128, 4096, 4096, 32),
-                 (1000, 16384, 256, 32), (2100, 4096, 1040, 16)]
+                 (1000, 16384, 256, 32), (2100, 4096, 1040, 16),
+                 (1792, 8192, 256, 16), (2048, 7168, 512, 16)]
 
 
 @pytest.mark.parametrize("m,n,k,group", ONEHOT_SHAPES)
