@@ -80,8 +80,8 @@ hipError_t launch_direct(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
 // kOneHotMinRows rows with B grouped along n: packed A grouped along k (g 16
 // or 32), or dense activations (any group).
 constexpr uint32_t kOneHotMinRows = 64;
-constexpr uint32_t kOneHotMinRowsShortK = 16;  // from here when k <= 256 m and B >= 2^20 values
-constexpr uint32_t kOneHotMinRowsDense = 32;   // the same for dense activations
+constexpr uint32_t kOneHotMinRowsSmall = 8;   // from here when B holds >= 2^20 values
+constexpr uint32_t kOneHotMinRowsDense = 9;   // the same for dense activations
 bool onehot_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                     uint32_t count);
 bool onehot_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,

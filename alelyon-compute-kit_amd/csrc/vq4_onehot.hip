@@ -807,19 +807,21 @@ bool onehot_mixed_plan(uint32_t m, uint32_t n, uint32_t group, OHMixed* out) {
 
 }  // namespace
 
-// From kOneHotMinRows rows of A always; from 16 rows when B holds at least
-// 2^20 values (smaller products keep the bit-exact general kernel) and k is at
-// most 256 m: a small grid walks all of k in each block, where the chunked
-// GEMV splits it (12 x 4096 x 14336 g16: 226 against 91 us; 32 x 4096 x 4096
-// g32: 76 against 179).
+// From kOneHotMinRows rows of A always; from 8 rows when B holds at least
+// 2^20 values (smaller products keep the bit-exact general kernel or the
+// GEMVs). Small grids split k, so the path's time hardly grows with m below 64
+// rows, where the GEMVs' grows with every row (one product, µs, one-hot against
+// the automatic choice before): 8 x 4096 x 14336 g16 36 against 58 (gemv-rows),
+// 8 x 4096^2 g16 17.5 against 21.4 (gemv-direct), 9 x 4096^2 g16 18 against 62,
+// 48 x 4096 x 14336 g16 40 against 346; at 4 rows the GEMVs still win 2 of 4
+// shapes.
 bool onehot_applies(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                     uint32_t count) {
   if (count != 1 || flags != 0 || (group != 16 && group != 32) || n % (8 * group) != 0 ||
       k % 16 != 0 || k % group != 0)
     return false;
   if (m >= kOneHotMinRows) return true;
-  return m >= kOneHotMinRowsShortK && uint64_t(n) * k >= (uint64_t(1) << 20) &&
-         uint64_t(k) <= 256ull * m;
+  return m >= kOneHotMinRowsSmall && uint64_t(n) * k >= (uint64_t(1) << 20);
 }
 
 // Workspace: B's nibble columns, then the planes (dense A on a large grid) or
@@ -896,15 +898,16 @@ void launch_onehot_g<8>(hipStream_t s, const Operands& o, uint32_t m, uint32_t n
 }  // namespace
 
 // Dense activations (no A groups to straddle, so group 8 as well): from 64
-// rows, and from 32 rows with the packed rule's k bound (16 rows: 97 against
-// 85 us on the chunked GEMV). x is split into three bf16 terms as it is read,
-// VALU work that the packed path's table reads do not have.
+// rows, and from 9 with B of at least 2^20 values. x is split into three bf16
+// terms as it is read, VALU work that the packed path's table reads do not
+// have, so at 8 rows the GEMVs still win some shapes (µs, gemv-rows against
+// one-hot): 8 x 8192^2 g16 47.7 against 55.8, 8 x 4096 x 14336 g16 55.0
+// against 49.9.
 bool onehot_applies_dense(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                           uint32_t count) {
   if (count != 1 || flags != 0 || n % (8 * group) != 0 || k % 16 != 0) return false;
   if (m >= kOneHotMinRows) return true;
-  return m >= kOneHotMinRowsDense && uint64_t(n) * k >= (uint64_t(1) << 20) &&
-         uint64_t(k) <= 256ull * m;
+  return m >= kOneHotMinRowsDense && uint64_t(n) * k >= (uint64_t(1) << 20);
 }
 
 hipError_t launch_onehot(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uint32_t k,

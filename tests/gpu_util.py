@@ -61,10 +61,24 @@ def image(rng, m, group, scale=1.0):
 DIRECT_MAX_WEIGHTS = 1 << 25
 
 
-def small_auto_path(m, n, k, count=1):
-    """gemv-direct where it applies, else gemv-pairs (m = 1) or gemv-rows; a
-    batch filling the chip with row instances is gemv-row-pairs, which this
-    helper does not model (callers pass count 1 there)."""
+def onehot_auto(m, n, k, group, flags=0, count=1, dense=False):
+    """Whether the automatic choice is onehot-mfma: one product with B grouped
+    along n (flags 0), from 64 rows, or from 8 (packed A at g 16 / 32) or 9
+    (dense A) rows with B of at least 2^20 values."""
+    if count != 1 or flags != 0 or n % (8 * group) or k % 16:
+        return False
+    if not dense and (group not in (16, 32) or k % group):
+        return False
+    return m >= 64 or (m >= (9 if dense else 8) and n * k >= 1 << 20)
+
+
+def small_auto_path(m, n, k, count=1, group=None, flags=0):
+    """onehot-mfma where it applies (when `group` is given), else gemv-direct
+    where it applies, else gemv-pairs (m = 1) or gemv-rows; a batch filling
+    the chip with row instances is gemv-row-pairs, which this helper does not
+    model (callers pass count 1 there)."""
+    if group is not None and onehot_auto(m, n, k, group, flags, count):
+        return "onehot-mfma"
     if m <= 8 and n * k * count <= DIRECT_MAX_WEIGHTS:
         return "gemv-direct"
     return "gemv-pairs" if m == 1 else "gemv-rows"

@@ -8,7 +8,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from gpu_util import binned_path, say, small_auto_path
+from gpu_util import binned_path, onehot_auto, say, small_auto_path
 
 pytestmark = pytest.mark.gpu
 
@@ -44,12 +44,8 @@ def _check(vqdev, oracle, x, w, transpose_a, transpose_b, path, tol=1e-5, binned
 
 def _dense_onehot(m, n, k, group, flags):
     """"onehot-mfma" where the automatic dense choice takes it: from 64 rows,
-    or from 32 with B of at least 2^20 values and k <= 256 m; None otherwise."""
-    if flags != 0 or n % (8 * group) or k % 16:
-        return None
-    if m >= 64 or (m >= 32 and n * k >= 1 << 20 and k <= 256 * m):
-        return "onehot-mfma"
-    return None
+    or from 9 with B of at least 2^20 values; None otherwise."""
+    return "onehot-mfma" if onehot_auto(m, n, k, group, flags, dense=True) else None
 
 
 def _dense_x2(m, n, group):

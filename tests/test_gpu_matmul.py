@@ -12,7 +12,8 @@ import itertools
 import numpy as np
 import pytest
 
-from gpu_util import binned_path, image, m1_auto_path, run_plan, say, small_auto_path
+from gpu_util import (binned_path, image, m1_auto_path, onehot_auto, run_plan, say,
+                      small_auto_path)
 
 pytestmark = pytest.mark.gpu
 
@@ -95,7 +96,7 @@ def test_gemv_within_tolerance(vqdev, oracle, m):
     rng = np.random.default_rng(50 + m)
     for (k, n, group), policy in itertools.product(GEMV_SHAPES, (0, 2)):
         words = (2, m, n, k, group, 16, 0, 0)
-        auto = small_auto_path(m, n, k)
+        auto = small_auto_path(m, n, k, group=group)
         assert vqdev.path_name(words) == auto
         say("gemv", m, k, n, group, auto if policy == 0 else binned_path(m))
         ops = _operands(rng, m, n, k, group, 1.0, 0.02)
@@ -144,7 +145,7 @@ def test_gemv_direct(vqdev, oracle, n, k, group, count):
 DIRECT_ROW_SHAPES = [(2, 4096, 4096, 16, 0, 1), (3, 1024, 1000, 8, 1, 1),
                      (4, 2048, 2048, 32, 0, 2), (5, 640, 1000, 16, 1, 3),
                      (6, 256, 63, 8, 0, 4), (7, 4096, 1024, 16, 1, 1),
-                     (8, 4096, 4096, 16, 0, 1), (8, 2048, 2048, 8, 1, 2), (8, 64, 4, 8, 0, 1)]
+                     (8, 4096, 4096, 8, 0, 1), (8, 2048, 2048, 8, 1, 2), (8, 64, 4, 8, 0, 1)]
 
 
 @pytest.mark.parametrize("m,n,k,group,flags,count", DIRECT_ROW_SHAPES)
@@ -246,11 +247,9 @@ def test_gemv_direct_on_two_handles_of_one_gpu(vqdev):
 
 def _chunk_auto_path(m, n, k, group, flags):
     """The automatic choice for 9 <= m < 64 over at least 2^20 weights: the
-    one-hot MFMA path from 16 rows of a row-major A at g 16/32 when k <= 256 m,
-    else the chunked row-pair GEMV."""
-    if flags == 0 and group in (16, 32) and m >= 16 and k <= 256 * m:
-        return "onehot-mfma"
-    return "gemv-rows"
+    one-hot MFMA path for a row-major A at g 16/32, else the chunked row-pair
+    GEMV."""
+    return "onehot-mfma" if onehot_auto(m, n, k, group, flags) else "gemv-rows"
 
 
 @pytest.mark.parametrize("m,flags", [(9, 0), (16, 0), (17, 1), (32, 0), (40, 1), (63, 0)])
@@ -472,7 +471,9 @@ def test_gemv_rows_split_slices(vqdev, any_size, m, k, group, flags):
     n = 512
     ops = _operands(rng, m, n, k, group, 1.0, 0.02)
     # the automatic choice is gemv-direct at these sizes; the test policy runs gemv-rows
-    assert vqdev.path_name((2, m, n, k, group, 16, flags, 0)) == small_auto_path(m, n, k)
+    assert vqdev.path_name((2, m, n, k, group, 16, flags, 0)) == small_auto_path(m, n, k,
+                                                                                 group=group,
+                                                                                 flags=flags)
     say("gemv-rows split", m, k, group, flags)
     out, status = _gpu(vqdev, ops, m, n, k, group, flags)
     assert status == 0
@@ -847,7 +848,7 @@ def test_gemv_outlier_codebook_entry(vqdev, oracle, m, k, n, count):
     one = (a_codes, a_book, b_codes, b_book)
     ops = tuple(np.tile(a.reshape(-1), count) for a in one)
     if m == 1 or count == 1:
-        auto = small_auto_path(m, n, k, count)
+        auto = small_auto_path(m, n, k, count, group=group)
         assert vqdev.path_name((2, m, n, k, group, 16, 0, 0), count=count) == auto
     else:   # the batch of 256 takes the row instances
         auto = "gemv-row-pairs"

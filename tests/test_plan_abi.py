@@ -308,13 +308,17 @@ def _path(lib, entry, words):
     ((2, 1, 4096, 4096, 16, 16, 1, 0), "gemv-direct"),        # m = 1: A's layout is moot
     ((2, 8, 4096, 4096, 16, 16, 1, 0), "gemv-direct"),        # up to 8 rows, A either way
     ((2, 8, 8192, 8192, 16, 16, 1, 0), "gemv-rows"),
-    ((2, 9, 4096, 4096, 16, 16, 0, 0), "gemv-rows"),          # past 8 rows
-    ((2, 32, 4096, 4096, 16, 16, 0, 0), "onehot-mfma"),        # 16 rows on, k <= 256 m
-    ((2, 32, 4096, 16384, 16, 16, 0, 0), "gemv-rows"),         # longer k: chunks of 8 rows
+    ((2, 9, 4096, 4096, 16, 16, 0, 0), "onehot-mfma"),        # past 8 rows
+    ((2, 8, 4096, 4096, 16, 16, 0, 0), "onehot-mfma"),        # 8 rows, B of 2^24 values
+    ((2, 4, 4096, 4096, 16, 16, 0, 0), "gemv-direct"),        # below 8 rows
+    ((2, 32, 4096, 4096, 16, 16, 0, 0), "onehot-mfma"),
+    ((2, 32, 4096, 16384, 16, 16, 0, 0), "onehot-mfma"),       # long k: split over blocks
+    ((2, 32, 4096, 16384, 8, 16, 0, 0), "gemv-rows"),          # packed g 8: chunks of 8 rows
     ((2, 32, 512, 512, 16, 16, 0, 0), "general"),              # small weight: bit-exact kernel
     ((2, 2048, 14336, 4096, 32, 16, 0, 0), "onehot-mfma"),    # config 4 forward
     ((2, 64, 14336, 4096, 32, 16, 0, 0), "onehot-mfma"),
-    ((2, 12, 14336, 4096, 32, 16, 0, 0), "gemv-rows"),         # below 16 rows: chunks of 8
+    ((2, 12, 14336, 4096, 32, 16, 0, 0), "onehot-mfma"),
+    ((2, 12, 14336, 4096, 32, 16, 1, 0), "gemv-rows"),         # A transposed: chunks of 8
     ((2, 2048, 14336, 4096, 8, 16, 0, 0), "general"),          # g 8: neither
     ((2, 2048, 4096, 14336, 32, 16, 2, 0), "gram-mfma"),
     ((2, 4, 4096, 4096, 16, 16, 2, 0), "gram-mfma"),           # both grouped along k
@@ -329,7 +333,9 @@ def test_kernel_path_choice(lib, words, path):
 @pytest.mark.parametrize("words,path", [
     ((2, 1, 4096, 4096, 16, 16, 0, 0), "gemv-direct"),
     ((2, 1, 8192, 8192, 16, 16, 0, 0), "gemv-pairs"),
-    ((2, 19, 2048, 3072, 8, 16, 0, 0), "gemv-rows"),
+    ((2, 19, 2048, 3072, 8, 16, 0, 0), "onehot-mfma"),        # dense A from 9 rows
+    ((2, 8, 2048, 3072, 8, 16, 0, 0), "gemv-direct"),
+    ((2, 19, 2048, 3072, 8, 16, 1, 0), "gemv-rows"),
     ((2, 5, 2048, 3000, 8, 16, 1, 0), "gemv-direct"),         # ragged k, x stored k x m
     ((2, 128, 768, 512, 8, 16, 0, 0), "onehot-mfma"),         # dense A: group 8 admitted
     ((2, 2048, 14336, 4096, 32, 16, 0, 0), "onehot-mfma"),     # config 4 forward, dense X

@@ -53,9 +53,10 @@ def _call(vqdev, entry, words, arrays, out_bytes):
 PAIRS = [
     [(1, 8192, 8192, 16, 0, "gemv-pairs"), (1, 8192, 4160, 16, 0, "gemv-pairs")],
     [(1, 4096, 4096, 16, 0, "gemv-direct"), (1, 2048, 1024, 16, 0, "gemv-direct")],
-    [(8, 4096, 4096, 16, 0, "gemv-direct"), (3, 1024, 2048, 8, 1, "gemv-direct")],
-    [(8, 4096, 8320, 16, 0, "gemv-rows"), (3, 4096, 8320, 8, 0, "gemv-rows")],
-    [(24, 2048, 8192, 16, 0, "gemv-rows"), (12, 1024, 4096, 16, 1, "gemv-rows")],
+    [(8, 4096, 4096, 8, 0, "gemv-direct"), (3, 1024, 2048, 8, 1, "gemv-direct")],
+    [(8, 4096, 8320, 16, 1, "gemv-rows"), (3, 4096, 8320, 8, 0, "gemv-rows")],
+    [(24, 2048, 8192, 8, 0, "gemv-rows"), (12, 1024, 4096, 16, 1, "gemv-rows")],
+    [(16, 4096, 14336, 16, 0, "onehot-mfma"), (8, 4096, 4096, 32, 0, "onehot-mfma")],
     [(512, 4096, 4096, 32, 0, "onehot-mfma"), (64, 1024, 1024, 16, 0, "onehot-mfma")],
     [(2048, 8192, 512, 16, 0, "onehot-mfma"), (128, 4096, 4096, 32, 0, "onehot-mfma")],
 ]
@@ -159,16 +160,16 @@ def test_noalloc_other_ops_and_status(vqdev, oracle):
 
 
 def test_noalloc_refuses_a_workspace_past_the_scratch(vqdev):
-    """8 activation rows over a 16384 x 16384 weight at group 16, one
-    product: k splits 64 ways over 4 column tiles, 32 MiB of split-k
+    """8 activation rows stored k x m over a 16384 x 16384 weight at group
+    16, one product: k splits 64 ways over 4 column tiles, 32 MiB of split-k
     partials. Refused with ACK_ERR_SIZE and a message naming the scratch;
     ack_vq would allocate them."""
     from alelyon_compute_kit import ack
     m, n, k, group = 8, 16384, 16384, 16
-    words = (2, m, n, k, group, 16, 0, 0)
+    words = (2, m, n, k, group, 16, 1, 0)
     assert vqdev.path_name(words) == "gemv-rows"
     rng = np.random.default_rng(8)
-    ops = _operands(rng, m, n, k, group)
+    ops = _operands(rng, m, n, k, group, 1)
     say("noalloc refusal")
     rc, _, _ = _call(vqdev, "ack_vq_noalloc", words, ops, 4 * m * n)
     assert rc == ack.ACK_ERR_SIZE
