@@ -122,9 +122,11 @@ __device__ __forceinline__ void split_bf16x3(const float4 a, const float4 b, boo
 
 // Nibble columns of B: nc[j * (k / 8) + kk8] holds the codes of group j at
 // inner indices 8 kk8 .. 8 kk8 + 7 (nibble i: index 8 kk8 + i). A block reads
-// 64 rows of 32 word columns (coalesced) into LDS and writes the 256 groups'
-// 8 words each. Requires k % 8 == 0.
-constexpr uint32_t kNCRows = 64, kNCCols = 32;
+// 16 rows of 32 word columns (coalesced) into LDS and writes the 256 groups'
+// 2 words each: small tiles, so that even a 4096-row weight spreads over 256
+// blocks (with 64-row tiles the pre-pass took 4.8 of a 128-row chunk's
+// 19.1 us; 16-row tiles: 18.3 us). Requires k % 8 == 0.
+constexpr uint32_t kNCRows = 16, kNCCols = 32;
 __global__ __launch_bounds__(256) void k_nibble_columns(const uint32_t* __restrict__ codes,
                                                         uint32_t* __restrict__ nc, uint32_t k,
                                                         uint32_t rw) {
