@@ -13,7 +13,7 @@ separators, no NaN), the pointer's fields and counters, the commit order --
 is the reference's (src/alelyon_compute_kit/_kit/python/expert_bank.py:29-355),
 so banks written here and there are interchangeable; so are the refusal
 texts. ``initialize_expert``'s seeded payloads follow expert_bank.py:357-390
-and define BASELINE config 2's inputs.
+and define benchmark config 2's inputs.
 
 One trusted writer, concurrent readers. Hashes detect changed bytes; they
 authenticate nothing.

@@ -1,9 +1,9 @@
 """Benchmark of the vq4 packed matmul on one MI355X.
 
-Metric (BASELINE.json): packed-weight GB/s (and % of HBM peak) at M=1, and
+Metric: packed-weight GB/s (and % of HBM peak) at M=1, and
 TFLOP/s at M=2048.
 
-Headline line (`value`): BASELINE config 3, the decode-shaped GEMV -- a
+Headline line (`value`): benchmark config 3, the decode-shaped GEMV -- a
 4096x4096 weight ~N(0, 0.02^2) at group 16 times one activation row
 ~N(0,1), both vq4-encoded -- measured cache-cold: one step is one batched
 launch (ack_vq_batch) over R distinct packed weights whose total exceeds
@@ -15,11 +15,11 @@ each (codes permuted, book rows permuted back): every item decodes to the
 same matrix, so all R outputs must agree, while no two items share bytes.
 
 Secondary lines (`extra`):
-* `prefill`: BASELINE config 4, X 2048x4096 times W 4096x14336 at group 32 and
+* `prefill`: benchmark config 4, X 2048x4096 times W 4096x14336 at group 32 and
   dY 2048x14336 times W^T: algorithmic TFLOP/s = 2*M*N*K / time, plus each
   kernel's executed-work rate against its own peak;
 * `gemv_m4`, `gemv_m8`: config 3 at M = 4 and 8, the same cache-cold batch;
-* `config5`: BASELINE config 5, an 8192x8192 row-normalised weight at group 8:
+* `config5`: benchmark config 5, an 8192x8192 row-normalised weight at group 8:
   GPU encode (read GB/s and FP32 VALU fraction), decode, op-3 AdamW, and one
   fused VQAdamW step end to end.
 

@@ -124,7 +124,7 @@ def fit_cases() -> dict:
 
 
 def config1() -> dict:
-    """256x256 N(0,1) seed 0, group 16, fit -> encode; x
+    """benchmark config 1: 256x256 N(0,1) seed 0, group 16, fit -> encode; x
     1x256 N(0,1) seed 1 fitted and encoded."""
     w = np.random.default_rng(0).standard_normal((256, 256)).astype(np.float32)
     book = ref_vq.fit_codebook(w, group=16)

@@ -28,7 +28,7 @@ def test_benchmark_image_sizes():
 
 
 def test_config1_image_is_byte_identical_to_the_reference():
-    """BASELINE config 1 through this package's CPU encode and fit gives the
+    """benchmark config 1 through this package's CPU encode and fit gives the
     reference's exact 3,128-byte image (recorded from the reference)."""
     from alelyon_compute_kit import vq
     g = golden("config1.npz")

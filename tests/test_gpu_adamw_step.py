@@ -121,7 +121,7 @@ def _oracle_encode_threads(oracle, x, book, group, parts=16):
 
 
 def test_config5_at_full_size(vqdev, oracle):
-    """W 8192 x 8192, rows ~ N(0,1) then L2-normalised,
+    """benchmark config 5: W 8192 x 8192, rows ~ N(0,1) then L2-normalised,
     group 8, book = fit_codebook(W). The GPU encode picks the oracle's code
     for every one of the 8,388,608 vectors, decode is the exact gather, and
     one fused VQAdamW step with an N(0, 1e-3) gradient equals the unfused

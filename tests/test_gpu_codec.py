@@ -138,7 +138,7 @@ def test_encode_status_bits(vqdev, oracle):
 
 
 def test_encode_through_vqdevice_matches_cpu_image(vqdev):
-    """the GPU encode of the fitted 256x256 weight gives
+    """benchmark config 1: the GPU encode of the fitted 256x256 weight gives
     the reference's 3,128-byte image."""
     from alelyon_compute_kit import vq
     from conftest import golden

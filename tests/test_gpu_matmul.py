@@ -532,7 +532,7 @@ def test_gemv_rows_saturated_window(vqdev, sign):
 
 
 def test_config1_matmul(vqdev, oracle):
-    """x (1x256) times W (256x256), group 16, both images
+    """benchmark config 1: x (1x256) times W (256x256), group 16, both images
     recorded from the reference."""
     from alelyon_compute_kit import vq
     from conftest import golden
@@ -549,7 +549,7 @@ def test_config1_matmul(vqdev, oracle):
 
 @pytest.mark.parametrize("m", [1, 4, 8])
 def test_config3_decode_shaped_gemv(vqdev, m):
-    """BASELINE config 3 at full size: W 4096x4096 ~N(0, 0.02^2) fitted at
+    """benchmark config 3 at full size: W 4096x4096 ~N(0, 0.02^2) fitted at
     group 16, X m x 4096 ~N(0,1) fitted and encoded; forward only."""
     from alelyon_compute_kit import vq
     from oracle import vq4_numpy as o
@@ -689,7 +689,7 @@ def test_gram_mfma_rows_of_very_different_magnitude(vqdev):
 
 
 def test_config4_forward_against_float64(vqdev):
-    """BASELINE config 4 forward at full size: X 2048x4096 . W 4096x14336 at
+    """benchmark config 4 forward at full size: X 2048x4096 . W 4096x14336 at
     group 32; every output against the float64 product of the decoded
     operands, over the whole matrix and row by row."""
     from alelyon_compute_kit import vq
@@ -757,7 +757,7 @@ def test_gram_mfma_status_on_overflow(vqdev, oracle, any_size):
 
 
 def test_config4_backward_against_float64(vqdev):
-    """BASELINE config 4 backward at full size: dY 2048x14336 ~ N(0, 1e-2) .
+    """benchmark config 4 backward at full size: dY 2048x14336 ~ N(0, 1e-2) .
     W^T with W 4096x14336 stored (n, k) at group 32; every output against the
     float64 product of the decoded operands, over the whole matrix and row by
     row."""

@@ -4,7 +4,7 @@ CPU tests pin the bank's format against the reference's seeded payloads
 (tests/golden/expert_payloads.npz, written from the reference's own
 ExpertBank.initialize_expert), its commit counters and refusals, and the
 harness flow with a host backend. GPU tests run the harness step and the
-BASELINE config-2 flow on the MI355X and require every committed image to be
+benchmark config-2 flow on the MI355X and require every committed image to be
 byte-identical to the same flow computed by the CPU oracle.
 """
 from __future__ import annotations
@@ -322,7 +322,7 @@ def test_harness_step_on_the_gpu_commits_the_oracle_images(tmp_path, vqdev):
 
 @pytest.mark.gpu
 def test_config2_chain_and_clipped_step_match_the_oracle(vqdev):
-    """three 128 x 128 matrices from initialize_expert(0, 0,
+    """benchmark config 2: three 128 x 128 matrices from initialize_expert(0, 0,
     seed=7) at group 16; x 32 x 128 ~ N(0,1) fitted and encoded and pushed
     through the three packed products in sequence (each output re-fitted and
     re-encoded); then one VQAdamW step (lr 1e-3, betas (0.9, 0.999)) per matrix
