@@ -290,13 +290,15 @@ def test_dense_bucket_sums_past_float_max_raise_status(vqdev):
 DENSE_ONEHOT_SHAPES = [(32, 1024, 1024, 16), (40, 512, 2048, 32), (64, 64, 256, 16),
                        (130, 256, 2048, 16), (200, 4096, 4096, 32), (255, 1040, 768, 16),
                        (128, 4096, 4096, 32), (48, 4112, 2048, 16),
-                       (96, 1040, 1024, 32)]     # k not a multiple of g (dense rows need not be)
+                       (96, 1040, 1024, 32),     # k not a multiple of g (dense rows need not be)
+                       (9, 1024, 1024, 16), (20, 4096, 4096, 8), (31, 14336, 4096, 32)]
 
 
 @pytest.mark.parametrize("m,k,n,group", DENSE_ONEHOT_SHAPES)
 def test_dense_onehot_mfma(vqdev, oracle, m, k, n, group):
     """Dense activations on the one-hot MFMA path (64-row blocks on these
-    grids): x split
+    grids, k split over blocks where they are few; from 9 rows with B of at
+    least 2^20 values): x split
     into three bf16 terms as it is read; every row within 1e-5 of the float64
     product against its own largest output."""
     from oracle import vq4_numpy as o

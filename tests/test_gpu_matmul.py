@@ -613,12 +613,13 @@ ONEHOT_SHAPES = [(16, 1024, 1024, 16), (40, 2048, 512, 32), (63, 4096, 4096, 16)
                  (300, 512, 1040, 16), (1000, 4096, 288, 32), (513, 2048, 4096, 32),
                  (48, 2048, 4112, 16), (128, 4096, 4096, 32),
                  (1000, 16384, 256, 32), (2100, 4096, 1040, 16),
-                 (1792, 8192, 256, 16), (2048, 7168, 512, 16)]
+                 (1792, 8192, 256, 16), (2048, 7168, 512, 16),
+                 (8, 4096, 4096, 16), (9, 1024, 1024, 16), (12, 4096, 14336, 32)]
 
 
 @pytest.mark.parametrize("m,n,k,group", ONEHOT_SHAPES)
 def test_onehot_mfma_within_tolerance(vqdev, oracle, m, n, k, group):
-    """m >= 64 rows of a packed A (or 16 with B of 2^20 values and k <= 256 m;
+    """m >= 64 rows of a packed A (or from 8 with B of at least 2^20 values;
     groups along k) times B grouped along n:
     A's book rows (scaled by a power of two and split into three bf16 terms,
     exact for every entry down to 2^-118 of the largest) times the one-hot of
