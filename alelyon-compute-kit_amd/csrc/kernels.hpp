@@ -105,9 +105,10 @@ hipError_t launch_matmul(hipStream_t s, const Operands& o, uint32_t m, uint32_t 
                          size_t workspace_bytes);
 
 // The dense-activation product: op 2's geometry and flags with A a dense FP32
-// array in in[0] (in[1] unused). Paths: onehot-mfma (m >= 32 on large B, every
-// m >= 64), the GEMV paths (m <= 8; each window's fixed-point scale comes from
-// x itself), else General.
+// array in in[0] (in[1] unused). Paths: onehot-mfma (m >= 9 with B of at least
+// 2^20 values, every m >= 64), the GEMV paths (m <= 8, and up to 64 rows in
+// chunks of 8 where the one-hot path does not apply, such as A stored k x m;
+// each window's fixed-point scale comes from x itself), else General.
 MatmulPath choose_dense_path(uint32_t m, uint32_t n, uint32_t k, uint32_t group, uint32_t flags,
                              uint32_t count, uint32_t policy);
 size_t dense_workspace_bytes(MatmulPath p, uint32_t m, uint32_t n, uint32_t k, uint32_t group,
