@@ -20,7 +20,10 @@ float64 product of the decoded operands:
   product), M and L1 over the whole row (a window's are smaller);
 * gemv-direct (FP32 multiply-adds in another order) is held to the bound of
   any FP32 summation order, gamma_K sum_k |x_k w_kt| -- the class of the
-  shader's own rounding error.
+  shader's own rounding error;
+* onehot-mfma (from 8 packed or 9 dense rows over large weights) adds each
+  activation as three exact bf16 terms in FP32 and then applies the book:
+  gamma_(3K + 17) (1 + 2^-7) sum_k |x_k w_kt|.
 
 The shader's own error (the oracle) is reported beside them: on these inputs
 the fixed-point paths' errors stay within a few times the shader's, and the
@@ -204,3 +207,67 @@ def test_gemv_row_pairs_under_cancellation(vqdev, oracle, k, eps):
             _report("gemv-row-pairs", out[0], y64, ref, bound)
         else:
             assert np.all(np.abs(out[i] - y64) <= bound), f"instance {i}"
+
+
+def _onehot_bound(x64, w64, k):
+    """The one-hot MFMA path's bound: each activation enters as three exact
+    bf16 terms (3 k FP32 additions of terms that sum to at most |x| (1 + 2^-7)),
+    then the 16-term product with the book: gamma_(3k + 17) sum_k |x_k w_kt|."""
+    n_ops = 3 * k + 17
+    return n_ops * U / (1 - n_ops * U) * (1 + 2.0 ** -7) * (np.abs(x64) @ np.abs(w64))
+
+
+@pytest.mark.parametrize("k,eps", CASES)
+def test_onehot_mfma_dense_under_cancellation(vqdev, oracle, k, eps):
+    """Sixteen dense activation rows on the one-hot MFMA path (k split over
+    blocks at this size), the pairs x, -x(1 + eps) of the GEMV cases: every
+    output within the bound of its FP32 sums."""
+    rng = np.random.default_rng(13 * k + int(1 / eps))
+    m, n, group = 16, 2048, 16
+    codes, book = _weight(rng, k, n, group, 1)
+    w64 = _decode(codes, book, k, n, group)
+    x = _dense_pairs(rng, m, k, eps)
+    x[1] *= 1e-3
+    x64 = x.astype(np.float64)
+    ref, st = oracle.matmul_dense(x, codes, book, m, n, k, group, 0)
+    assert st == 0
+    words = (2, m, n, k, group, 16, 0, 0)
+    assert vqdev.dense_path_name(words) == "onehot-mfma"
+    say("cancellation onehot-mfma dense", k, eps)
+    y = _run_dense(vqdev, words, x, codes, book)
+    _report("onehot-mfma dense", y, x64 @ w64, ref, _onehot_bound(x64, w64, k))
+
+
+@pytest.mark.parametrize("k,eps", CASES)
+def test_onehot_mfma_packed_under_cancellation(vqdev, oracle, k, eps):
+    """Twelve rows of packed activations on the one-hot MFMA path: the A
+    book holds pairs v, -v(1 + eps), groups 2i and 2i + 1 of a row take a
+    pair, and B's rows of group 2i + 1 copy those of group 2i."""
+    from gpu_util import run_plan
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(17 * k + int(1 / eps))
+    m, n, group = 12, 2048, 16
+    codes, book = _weight(rng, k, n, group, group)
+    w64 = _decode(codes, book, k, n, group)
+    v = rng.standard_normal((8, group))
+    a_book = np.empty((16, group), np.float32)
+    a_book[0::2] = v
+    a_book[1::2] = -v * (1 + eps)
+    groups = m * k // group
+    pick = rng.integers(0, 8, groups // 2)
+    idx = np.empty(groups, np.uint32)
+    idx[0::2] = 2 * pick
+    idx[1::2] = 2 * pick + 1
+    a_codes = np.zeros(groups // 8, np.uint32)
+    for lane in range(8):
+        a_codes |= idx[lane::8] << np.uint32(4 * lane)
+    x64 = o.decode(a_codes, a_book, m * k, group).reshape(m, k).astype(np.float64)
+    plan = (2, m, n, k, group, 16, 0, 0)
+    assert vqdev.path_name(plan) == "onehot-mfma"
+    say("cancellation onehot-mfma packed", k, eps)
+    out, status = run_plan(vqdev, plan, (a_codes, a_book.reshape(-1), codes, book.reshape(-1)),
+                           4 * m * n, np.float32)
+    assert status == 0
+    ref, st = oracle.matmul(a_codes, a_book, codes, book, m, n, k, group, 0)
+    assert st == 0
+    _report("onehot-mfma packed", out.reshape(m, n), x64 @ w64, ref, _onehot_bound(x64, w64, k))
