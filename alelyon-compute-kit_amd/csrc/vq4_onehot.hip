@@ -42,6 +42,11 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kOHThreads = 256;  // 4 waves, 2 x 2 over 64 X rows x 128 S columns
 constexpr int kOHTerms = 3;           // bf16 terms of each scaled A value
+// VALU operations the scheduler places after each MFMA of a step: with the
+// next step's one-hot builds interleaved so, config 4's forward measured
+// ~300 against ~310 us and an 8 x 4096 x 14336 g16 product 35.4 against
+// 39.6 us (3, 4, 6 and 8 within noise of 5)
+constexpr int kOHPipeValu = 5;
 // X = 4 (256 rows per block) reuses each one-hot fragment over 12 MFMAs; X = 1
 // (64 rows) gives four times the waves, for products whose 256-row grid would
 // leave most of the chip idle.
@@ -246,9 +251,10 @@ __device__ __forceinline__ void onehot_block(const Operands& o, uint32_t m, uint
   __syncthreads();
 
   // ---- main loop: passes over 8 groups of A (8 G inner indices, G / 2 steps
-  // of 16), A's code words one pass ahead, B's words two steps ahead in a
-  // ring of four, and term t of the next step's A fragments read as soon as
-  // this step's term-t MFMAs are issued, into the same registers
+  // of 16), A's code words one pass ahead, B's words three steps ahead in a
+  // ring of four, the next step's one-hot fragments built between this step's
+  // MFMAs, and term t of the next step's A fragments read as soon as this
+  // step's term-t MFMAs are issued, into the same registers
   f32x16 acc[kOHX][2];
 #pragma unroll
   for (int x = 0; x < kOHX; ++x)
@@ -267,6 +273,13 @@ __device__ __forceinline__ void onehot_block(const Operands& o, uint32_t m, uint
   wb[0][1] = nc1[kb / 8];
   wb[1][0] = nc0[(kb + 16 < ke ? kb + 16 : kb) / 8];
   wb[1][1] = nc1[(kb + 16 < ke ? kb + 16 : kb) / 8];
+  wb[2][0] = nc0[(kb + 32 < ke ? kb + 32 : kb) / 8];
+  wb[2][1] = nc1[(kb + 32 < ke ? kb + 32 : kb) / 8];
+  // one-hot fragments of the current step; the next step's are built between
+  // this step's MFMAs
+  bf16x8 bfc[2];
+  bfc[0] = one_hot_column(wb[0][0], ee);
+  bfc[1] = one_hot_column(wb[0][1], ee);
   // the table row of step s_ (both halves of the wave are in one group; the
   // lane's chunk is c8 + h)
   auto a_ptr = [&](const uint32_t (&wd)[kOHX], uint32_t s_, int x) __attribute__((always_inline)) {
@@ -309,9 +322,9 @@ __device__ __forceinline__ void onehot_block(const Operands& o, uint32_t m, uint
     for (uint32_t s = 0; s < kSteps; ++s) {
       const uint32_t kk0 = p0 + 16 * s;
       if (ragged && kk0 >= ke) break;
-      const uint32_t kw = kk0 + 32 < klast ? kk0 + 32 : klast;
-      wb[(s + 2) % 4][0] = nc0[kw / 8];
-      wb[(s + 2) % 4][1] = nc1[kw / 8];
+      const uint32_t kw = kk0 + 48 < klast ? kk0 + 48 : klast;
+      wb[(s + 3) % 4][0] = nc0[kw / 8];
+      wb[(s + 3) % 4][1] = nc1[kw / 8];
       const uint32_t kn = kk0 + 16 < klast ? kk0 + 16 : klast;
       const char* pn[kOHX];
 #pragma unroll
@@ -327,9 +340,9 @@ __device__ __forceinline__ void onehot_block(const Operands& o, uint32_t m, uint
       // the loads for later steps go out before this step's work (left to
       // itself the scheduler sinks them next to their use and waits on them)
       __builtin_amdgcn_sched_barrier(0);
-      bf16x8 bf[2];
-      bf[0] = one_hot_column(wb[s % 4][0], ee);
-      bf[1] = one_hot_column(wb[s % 4][1], ee);
+      bf16x8 bfn[2];
+      bfn[0] = one_hot_column(wb[(s + 1) % 4][0], ee);
+      bfn[1] = one_hot_column(wb[(s + 1) % 4][1], ee);
       // terms smallest first: lo, mid, hi
 #pragma unroll
       for (int t = kOHTerms - 1; t >= 0; --t) {
@@ -337,14 +350,28 @@ __device__ __forceinline__ void onehot_block(const Operands& o, uint32_t m, uint
         for (int x = 0; x < kOHX; ++x)
 #pragma unroll
           for (int y = 0; y < 2; ++y)
-            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[x][t], bf[y], acc[x][y], 0, 0, 0);
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[x][t], bfc[y], acc[x][y], 0, 0, 0);
         if (!AD) {
 #pragma unroll
           for (int x = 0; x < kOHX; ++x)
             af[x][t] = *reinterpret_cast<const bf16x8*>(pn[x] + t * kTerm);
         }
       }
+      // each MFMA followed by up to kOHPipeValu VALU operations (the next
+      // step's one-hot builds, addresses), each term's table reads after its
+      // MFMAs: the matrix pipe stays fed by this wave alone
+#pragma unroll
+      for (int t = 0; t < kOHTerms; ++t) {
+#pragma unroll
+        for (int i = 0; i < 2 * kOHX; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, kOHPipeValu, 0);
+        }
+        if (!AD) __builtin_amdgcn_sched_group_barrier(0x100, kOHX, 0);
+      }
       __builtin_amdgcn_sched_barrier(0);
+      bfc[0] = bfn[0];
+      bfc[1] = bfn[1];
     }
   };
   const uint32_t whole = kb + (ke - kb) / (8 * G) * (8 * G);  // end of the whole passes
