@@ -333,8 +333,9 @@ int32_t ack_vq_batch_path_name(const uint8_t* plan, size_t plan_len, uint32_t co
  * for every matmul (a second implementation to cross-check fast paths),
  * 2 = a factorised path wherever its shape applies, below the size at which
  * the automatic choice would keep the general kernel (tests of small shapes);
- * it never takes gemv-direct or onehot-mfma, so the bin kernels those replace
- * in the automatic choice are exercised at the same shapes. */
+ * it never takes gemv-direct, and onehot-mfma only from 64 rows (where no bin
+ * kernel applies), so the bin kernels those replace in the automatic choice
+ * are exercised at the same shapes. */
 int32_t ack_vq_set_policy(const AckDevice* dev, uint32_t policy);
 
 /* CPU reference encode (vq.py:154-179): nearest entry by float64 squared
