@@ -123,3 +123,39 @@ def test_random_shape_within_tolerance(vqdev, case):
         scale = np.abs(ref).max(axis=1, keepdims=True)
         err = np.abs(out[i] - ref) / np.maximum(scale, np.finfo(np.float64).tiny)
         assert err.max() <= TOL, f"instance {i} on {path}: row-relative error {err.max():.3g}"
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_random_shape_dense_activations(vqdev, case):
+    """The same shapes (one instance) with dense FP32 activations
+    (ack_vq_matmul_dense: onehot-mfma, its bf16 planes, gemv-direct,
+    gemv-pairs, gemv-rows, gram is not offered, general), rows of very
+    different magnitude: every row within 1e-5 of the float64 product."""
+    m, n, k, group, flags, _ = CASES[case]
+    rng = np.random.default_rng(11 * case + 5)
+    b_codes, b_book = image(rng, k * n, group, 0.02)
+    x = rng.standard_normal((k, m) if flags & 1 else (m, k)).astype(np.float32)
+    if m > 2:
+        x.reshape(-1)[::7] *= np.float32(1e3)
+    words = (2, m, n, k, group, 16, flags, 0)
+    path = vqdev.dense_path_name(words)
+    say("random shape dense", case, m, n, k, group, flags, path)
+    device = vqdev.device
+    bufs = [device.buffer(a.nbytes) for a in (x, b_codes, b_book)]
+    out, status = device.buffer(4 * m * n), device.buffer(4)
+    try:
+        for b_, a in zip(bufs, (x, b_codes, b_book)):
+            b_.upload(a)
+        status.upload(np.zeros(1, np.uint32))
+        vqdev.run_dense(words, *bufs, out, status)
+        assert int(status.download(np.uint32)[0]) == 0
+        y = out.download(np.float32).reshape(m, n)
+    finally:
+        for b_ in bufs + [out, status]:
+            b_.free()
+    a = x.astype(np.float64)
+    b = _decoded(b_codes, b_book, k * n, (n, k) if flags & 2 else (k, n), group)
+    ref = (a.T if flags & 1 else a) @ (b.T if flags & 2 else b)
+    scale = np.abs(ref).max(axis=1, keepdims=True)
+    err = np.abs(y - ref) / np.maximum(scale, np.finfo(np.float64).tiny)
+    assert err.max() <= TOL, f"{path}: row-relative error {err.max():.3g}"
