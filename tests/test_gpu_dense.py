@@ -49,8 +49,8 @@ def _dense_onehot(m, n, k, group, flags):
 
 
 def _dense_x2(m, n, group):
-    """Whether the dense one-hot product runs 128-row blocks (X = 2): its grid
-    of 128-row blocks has at least 256 blocks."""
+    """Whether the dense one-hot product takes x's bf16 planes: its grid of
+    128-row blocks has at least 256 blocks."""
     return (n // (8 * group)) * ((m + 127) // 128) >= 256
 
 
@@ -175,17 +175,19 @@ def test_dense_large_m_every_group(vqdev, oracle, group):
         vqdev.device.set_policy(0)
 
 
-# (m, k, n, group): grids of at least 256 blocks of 128 rows (X = 2): ragged
-# last row block, group 8, k not a multiple of g
+# (m, k, n, group): grids of at least 256 blocks of 128 rows (x's bf16 planes,
+# 128-row blocks, or 256-row blocks where their grid is as large: 257 rows):
+# ragged last row block, group 8, k not a multiple of g
 DENSE_X2_SHAPES = [(512, 1024, 4096, 8), (257, 512, 16384, 16), (300, 528, 24576, 32),
                    (384, 1040, 12288, 16)]
 
 
 @pytest.mark.parametrize("m,k,n,group", DENSE_X2_SHAPES)
 def test_dense_onehot_mfma_128_row_blocks(vqdev, oracle, m, k, n, group):
-    """Dense activations on large grids: 128-row blocks, each one-hot fragment
-    feeding two row blocks; every row within 1e-5 of the float64 product
-    against its own largest output, rows of very different magnitude."""
+    """Dense activations on large grids: x split once into bf16 planes, read
+    by 128-row blocks (each one-hot fragment feeding the 32-row blocks of a
+    wave); every row within 1e-5 of the float64 product against its own
+    largest output, rows of very different magnitude."""
     assert _dense_x2(m, n, group)
     rng = np.random.default_rng(m + k + n + group)
     w = _weight(rng, (k, n), group)
@@ -194,6 +196,34 @@ def test_dense_onehot_mfma_128_row_blocks(vqdev, oracle, m, k, n, group):
     x[130] *= 1e20
     x[m - 1] *= 1e-30
     y = _check(vqdev, oracle, x, w, False, False, "onehot-mfma")
+    _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
+
+
+# (m, k, n, group): grids of at least 256 blocks of 256 rows (x's bf16 planes
+# read by 256-row blocks, each wave 64 rows): benchmark config 4's forward with
+# dense activations at full size, group 8, and a ragged last block (rows
+# 1024 .. 1099: one wave full, one partly past m, two wholly past it)
+DENSE_256_SHAPES = [(2048, 4096, 14336, 32), (1024, 1024, 7168, 8), (1100, 512, 16384, 16)]
+
+
+@pytest.mark.parametrize("m,k,n,group", DENSE_256_SHAPES)
+def test_dense_onehot_mfma_256_row_blocks(vqdev, m, k, n, group):
+    """Dense activations on 256-row blocks at full size: every row within
+    1e-5 of the float64 product against its own largest output, with rows of
+    very different magnitude in several blocks and waves."""
+    assert (n // (8 * group)) * ((m + 255) // 256) >= 256
+    rng = np.random.default_rng(m + k + n + group)
+    w = _weight(rng, (k, n), group)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[1] *= 1e-6
+    x[200] *= 1e20
+    x[700] *= 1e-20
+    x[m - 1] *= 1e-30
+    words = (2, m, n, k, group, 16, 0, 0)
+    assert vqdev.dense_path_name(words) == "onehot-mfma"
+    say("dense matmul 256-row blocks", m, n, k, group)
+    y, status = _run_status(vqdev, x, w, words)
+    assert status == 0
     _rows_within(y, x.astype(np.float64) @ w.decode().astype(np.float64))
 
 
