@@ -154,6 +154,158 @@ __device__ __forceinline__ uint32_t argmin_screen(const float (&x)[G], const Scr
   return proven ? i1 : kNoScreen;
 }
 
+// The same screen with the dot products on the matrix core, for a wave whose
+// 64 vectors are whole: v_mfma_f32_16x16x4f32 takes A = -2 c (16 codes x 4
+// components), B = x (4 components x 16 vectors) and C = |c|^2, so one chain of
+// G / 4 instructions gives A_c for 16 codes of 16 vectors. Lane l feeds
+// A[l % 16][l / 16] and B[l / 16][l % 16] and holds D[4 (l / 16) + r][l % 16];
+// it loads components P (l / 16) .. P (l / 16) + P - 1 (P = G / 4) of vector
+// l % 16 of each of the wave's four 16-vector sets, and instruction t of a
+// chain takes component P k + t at row k of the product. A 4 x 4 transpose of
+// 4-code blocks across the lane rows (v_permlane32_swap, then
+// v_permlane16_swap) leaves lane l with all 16 A_c of vector l, which it ranks
+// as argmin_screen does. Error: the matrix core's sum of 4 products and the
+// accumulator is taken as within 8 u of the sum of their magnitudes (measured
+// worst 3.4 u over 16,384 random tiles with spread exponents and cancellation;
+// rounding each operation to nearest gives 5 u at most; subnormal operands and
+// results measured exact). Over the chain that is 2 G u (X + 2 |c|^2), with G u
+// |c|^2 more from |c|^2 itself, so |A_c + X - d_c| <= (7 G + 4) u (X + |c|^2),
+// within the E of argmin_screen (8 (G + 2) u (xn + cmax)) at G = 8, 16 and 32.
+typedef float F4 __attribute__((ext_vector_type(4)));  // 16-byte vector
+
+template <int G>
+struct MfmaScreen {
+  float a[G / 4];  // -2 c[l % 16][(G / 4) (l / 16) + t]
+  float cn[4];     // |c|^2 of codes 4 (l / 16) + r
+};
+
+template <int G>
+__device__ __forceinline__ MfmaScreen<G> mfma_screen_load(const Screen& s) {
+  constexpr int P = G / 4;
+  const uint32_t lane = threadIdx.x % 64;
+  MfmaScreen<G> ms;
+#pragma unroll
+  for (int t = 0; t < P; ++t) ms.a[t] = s.m2[(lane % 16) * G + P * (lane / 16) + t];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) ms.cn[r] = s.cn[4 * (lane / 16) + r];
+  return ms;
+}
+
+// Swaps lanes 32..63 of a with lanes 0..31 of b (W = 32), or rows 1 and 3 of a
+// with rows 0 and 2 of b (W = 16).
+template <int W>
+__device__ __forceinline__ void lane_swap(float& a, float& b) {
+  const auto r = W == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b),
+                                                            false, false)
+                         : __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b),
+                                                            false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
+typedef float F2 __attribute__((ext_vector_type(2)));
+
+// Loads of x for the matrix-core screen: non-temporal at groups 8 and 16
+// (every value is read once; measured 46.5 against 49.0 us at g16 on 2^26
+// values, no change at g8) and the default policy at group 32 (56 against
+// 62 us).
+template <int G, typename V>
+__device__ __forceinline__ V x_load(const float* p) {
+  if (G == 32) return *reinterpret_cast<const V*>(p);
+  return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+}
+
+// A wave's 64 whole vectors as the lane feeds them to the matrix core:
+// components P (l / 16) .. + P - 1 of vector 16 g + l % 16, g = 0..3 (x: the
+// wave's first vector, 16-byte aligned at G >= 16, 8-byte at G = 8).
+template <int G>
+struct MfmaTile {
+  float v[4][G / 4];
+};
+
+template <int G>
+__device__ __forceinline__ MfmaTile<G> mfma_tile_load(const float* x) {
+  constexpr int P = G / 4;
+  const uint32_t lane = threadIdx.x % 64;
+  MfmaTile<G> t;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float* p = x + (16 * g + lane % 16) * G + P * (lane / 16);
+    if (P == 2) {
+      const F2 v = x_load<G, F2>(p);
+      t.v[g][0] = v.x;
+      t.v[g][P - 1] = v.y;
+    } else {
+#pragma unroll
+      for (int q = 0; q < P; q += 4) {
+        const F4 v = x_load<G, F4>(p + q);
+        t.v[g][q] = v.x;
+        t.v[g][q + 1] = v.y;
+        t.v[g][q + 2] = v.z;
+        t.v[g][q + 3] = v.w;
+      }
+    }
+  }
+  return t;
+}
+
+// The screened code of the lane's vector of a loaded tile, or kNoScreen.
+template <int G>
+__device__ __forceinline__ uint32_t argmin_screen_mfma(const MfmaTile<G>& tile,
+                                                       const MfmaScreen<G>& ms, const Screen& s) {
+  constexpr int P = G / 4;
+  constexpr float k2 = float(16 * (G + 2)) * 0x1p-24f;
+  const auto& xv = tile.v;
+  F4 acc[4];
+  float xp[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    acc[g] = F4{ms.cn[0], ms.cn[1], ms.cn[2], ms.cn[3]};
+    float n = 0.0f;
+#pragma unroll
+    for (int t = 0; t < P; ++t) {
+      acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(ms.a[t], xv[g][t], acc[g], 0, 0, 0);
+      n = fmaf(xv[g][t], xv[g][t], n);
+    }
+    xp[g] = n;
+  }
+  // lane row k holds codes 4 k .. 4 k + 3 of set g in ac[g]; afterwards lane
+  // row g holds codes 4 b .. 4 b + 3 of set g in ac[b] (and xp[b]: the
+  // squares of component block b)
+  float ac[4][4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ac[g][r] = acc[g][r];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    lane_swap<32>(ac[0][r], ac[2][r]);
+    lane_swap<32>(ac[1][r], ac[3][r]);
+  }
+  lane_swap<32>(xp[0], xp[2]);
+  lane_swap<32>(xp[1], xp[3]);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    lane_swap<16>(ac[0][r], ac[1][r]);
+    lane_swap<16>(ac[2][r], ac[3][r]);
+  }
+  lane_swap<16>(xp[0], xp[1]);
+  lane_swap<16>(xp[2], xp[3]);
+  const float xn = ((xp[0] + xp[1]) + xp[2]) + xp[3];
+  float b1 = ac[0][0], b2 = __int_as_float(0x7f800000);
+  uint32_t i1 = 0;
+#pragma unroll
+  for (uint32_t code = 1; code < 16; ++code) {
+    const float r = ac[code / 4][code % 4];
+    const bool lt = r < b1;
+    b2 = __builtin_amdgcn_fmed3f(b1, b2, r);
+    b1 = lt ? r : b1;
+    i1 = lt ? code : i1;
+  }
+  const bool proven = s.on && xn < 0x1p120f && (b2 - b1) > fmaf(k2, xn, s.base);
+  return proven ? i1 : kNoScreen;
+}
+
 // OR the nibbles of 8 consecutive lanes into lane (v % 8 == 0)'s word.
 __device__ __forceinline__ uint32_t gather_word(uint32_t part) {
   part |= __shfl_xor(part, 1);
@@ -162,13 +314,17 @@ __device__ __forceinline__ uint32_t gather_word(uint32_t part) {
   return part;
 }
 
-// 16-byte vector for streaming (non-temporal) stores. They speed up op 3's
-// three output streams (~7 % on config 5) and slow down decode's one.
-typedef float F4 __attribute__((ext_vector_type(4)));
+// F4 (above) also carries streaming (non-temporal) stores. They speed up op
+// 3's three output streams (~7 % on config 5) and slow down decode's one.
 
 // ---- op 0: encode -------------------------------------------------------
+// Waves per SIMD (blocks of 4 waves per compute unit) that each group's
+// encode keeps resident: the most whose registers, two tiles of x among them,
+// fit without spilling.
 template <int G>
-__global__ __launch_bounds__(kThreads) void k_encode(Operands o, uint32_t m) {
+constexpr uint32_t kEncodeWaves = G == 8 ? 8 : G == 16 ? 5 : 4;
+template <int G>
+__global__ __launch_bounds__(kThreads, kEncodeWaves<G>) void k_encode(Operands o, uint32_t m) {
   const uint32_t item = blockIdx.y;
   const float* x = item_ptr<float>(o.in[0], o.stride[0], item);
   const float* book = item_ptr<float>(o.in[1], o.stride[1], item);
@@ -182,15 +338,39 @@ __global__ __launch_bounds__(kThreads) void k_encode(Operands o, uint32_t m) {
   screen_prepare<G>(sbook, sm2, scn, 1);
   __syncthreads();
   const Screen screen = screen_load<G>(sm2, scn);
+  const MfmaScreen<G> ms = mfma_screen_load<G>(screen);
 
   const uint32_t vectors = m / G + (m % G != 0);
   const uint32_t words = vectors / 8 + (vectors % 8 != 0);
   const bool aligned = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0);
   bool bad = false;
-  for (uint32_t base = blockIdx.x * kThreads; base < words * 8; base += gridDim.x * kThreads) {
+  // A wave whose 64 vectors are whole takes the matrix-core screen, with the
+  // next step's tile loaded before this step's is ranked.
+  const uint32_t stride = gridDim.x * kThreads, wlane0 = threadIdx.x & ~63u;
+  auto mfma_step = [&](uint32_t base) { return aligned && base + wlane0 + 64 <= m / G; };
+  MfmaTile<G> next{};
+  if (mfma_step(blockIdx.x * kThreads))
+    next = mfma_tile_load<G>(x + uint64_t(blockIdx.x * kThreads + wlane0) * G);
+  for (uint32_t base = blockIdx.x * kThreads; base < words * 8; base += stride) {
     const uint32_t v = base + threadIdx.x;
     uint32_t code = 0;
-    if (v < vectors) {
+    if (mfma_step(base)) {
+      const MfmaTile<G> tile = next;
+      if (mfma_step(base + stride))
+        next = mfma_tile_load<G>(x + uint64_t(base + stride + wlane0) * G);
+      code = argmin_screen_mfma<G>(tile, ms, screen);
+      if (code == kNoScreen) {
+        float xv[G];
+#pragma unroll
+        for (int j = 0; j < G; j += 4) {
+          const float4 q = *reinterpret_cast<const float4*>(x + uint64_t(v) * G + j);
+          xv[j] = q.x; xv[j + 1] = q.y; xv[j + 2] = q.z; xv[j + 3] = q.w;
+        }
+#pragma unroll
+        for (int j = 0; j < G; ++j) bad |= !finite_f32(xv[j]);
+        code = argmin32<G, true>(xv, G, sbook, bad);
+      }
+    } else if (v < vectors) {
       const uint32_t start = v * G;
       const uint32_t valid = (m - start) < G ? (m - start) : G;
       float xv[G];
@@ -661,10 +841,19 @@ uint32_t grid_for(uint64_t items, uint32_t per_block) {
     else { KERNEL<32><<<__VA_ARGS__>>>; }                               \
   } while (0)
 
+// Encode's blocks stay resident and stream: one round of them on MI355X (256
+// compute units, kEncodeWaves blocks of 4 waves each), so every wave loads its
+// next tile while it ranks the current one.
+constexpr uint32_t kComputeUnits = 256;
+
 hipError_t launch_encode(hipStream_t s, const Operands& o, uint32_t m, uint32_t group) {
   const uint32_t vectors = m / group + (m % group != 0);
   const uint32_t words = vectors / 8 + (vectors % 8 != 0);
-  dim3 grid(grid_for(uint64_t(words) * 8, kThreads), o.count);
+  const uint32_t cap = kComputeUnits * (group == 8    ? kEncodeWaves<8>
+                                        : group == 16 ? kEncodeWaves<16>
+                                                      : kEncodeWaves<32>);
+  const uint32_t blocks = grid_for(uint64_t(words) * 8, kThreads);
+  dim3 grid(blocks < cap ? blocks : cap, o.count);
   if (group == 8) k_encode<8><<<grid, kThreads, 0, s>>>(o, m);
   else if (group == 16) k_encode<16><<<grid, kThreads, 0, s>>>(o, m);
   else k_encode<32><<<grid, kThreads, 0, s>>>(o, m);

@@ -137,6 +137,27 @@ def test_encode_status_bits(vqdev, oracle):
         np.testing.assert_array_equal(out, ref)
 
 
+@pytest.mark.parametrize("group", GROUPS)
+def test_encode_nonfinite_inside_whole_waves(vqdev, oracle, group):
+    """NaN, +-Inf and a value whose squared distance overflows, placed inside
+    runs of 64 whole vectors (the matrix-core screen's waves): the same codes
+    and status bit as the shader, and the vectors around them unaffected."""
+    rng = np.random.default_rng(400 + group)
+    x = rng.standard_normal(4096 * group).astype(np.float32)
+    book = rng.standard_normal((16, group)).astype(np.float32)
+    x[5] = np.nan
+    x[1000 * group + 3] = np.inf
+    x[2000 * group + group - 1] = -np.inf
+    x[3000 * group] = np.float32(3e19)
+    say("encode nonfinite", group)
+    words = -(-(x.size // group) // 8)
+    out, status = run_plan(vqdev, (0, x.size, 1, 1, group, 16, 0, 0), (x, book), 4 * words,
+                           np.uint32)
+    ref, ref_status = oracle.encode(x, book, group)
+    np.testing.assert_array_equal(out, ref)
+    assert status == ref_status == 1
+
+
 def test_encode_through_vqdevice_matches_cpu_image(vqdev):
     """benchmark config 1: the GPU encode of the fitted 256x256 weight gives
     the reference's 3,128-byte image."""
