@@ -462,6 +462,30 @@ struct AdamwOut {
   bool write;      // the shader writes the element (vq4.comp:92-115)
 };
 
+// The terms of vq4.comp:94-104 that depend on fewer than all four states, one
+// expression each, so that adamw_value and the fused encode's per-block tables
+// form the same bits (every operation rounded: -ffp-contract=off, IEEE
+// division and square root).
+__device__ __forceinline__ float adamw_next_m(float moment, float gradient, const Coeffs& c) {
+  return c.beta1 * moment + (1.0f - c.beta1) * gradient;
+}
+__device__ __forceinline__ float adamw_next_v(float variance, float gradient, const Coeffs& c) {
+  return c.beta2 * variance + (1.0f - c.beta2) * (gradient * gradient);
+}
+// lr * M'/c1 (M'/c1 returned through `corrected`)
+__device__ __forceinline__ float adamw_scaled(float next_m, const Coeffs& c, float& corrected) {
+  corrected = next_m / c.c1;
+  return c.lr * corrected;
+}
+// sqrt(V'/c2) + eps (V'/c2 returned through `corrected`)
+__device__ __forceinline__ float adamw_denominator(float next_v, const Coeffs& c, float& corrected) {
+  corrected = next_v / c.c2;
+  return sqrtf(corrected) + c.eps;
+}
+__device__ __forceinline__ float adamw_decayed(float weight, const Coeffs& c) {
+  return weight * (1.0f - c.lr * c.decay);
+}
+
 // adamw_value (vq4.comp:80-116) for one element given its four decoded state
 // values. Branch-free: the arithmetic always runs (a GPU raises no traps) and
 // the shader's early returns become the flags and the write decision.
@@ -470,13 +494,13 @@ __device__ __forceinline__ AdamwOut adamw_value(float weight, float moment, floa
   // bitwise, not short-circuit: the checks compile to flag arithmetic, not branches
   const bool inputs_finite =
       finite_f32(weight) & finite_f32(moment) & finite_f32(variance) & finite_f32(gradient);
-  const float next_m = c.beta1 * moment + (1.0f - c.beta1) * gradient;
-  const float next_v = c.beta2 * variance + (1.0f - c.beta2) * (gradient * gradient);
-  const float corrected_m = next_m / c.c1;
-  const float corrected_v = next_v / c.c2;
-  const float denominator = sqrtf(corrected_v) + c.eps;
-  const float decayed = weight * (1.0f - c.lr * c.decay);
-  const float next_w = decayed - c.lr * corrected_m / denominator;
+  const float next_m = adamw_next_m(moment, gradient, c);
+  const float next_v = adamw_next_v(variance, gradient, c);
+  float corrected_m, corrected_v;
+  const float scaled = adamw_scaled(next_m, c, corrected_m);
+  const float denominator = adamw_denominator(next_v, c, corrected_v);
+  const float decayed = adamw_decayed(weight, c);
+  const float next_w = decayed - scaled / denominator;
   const bool results_finite = finite_f32(next_m) & finite_f32(next_v) &
                               finite_f32(corrected_m) & finite_f32(corrected_v) &
                               finite_f32(denominator) & finite_f32(decayed) & finite_f32(next_w);
@@ -496,8 +520,8 @@ __device__ __forceinline__ void adamw_moments(float weight, float moment, float 
                                               float gradient, const Coeffs& c, float& m, float& v) {
   const bool inputs_finite =
       finite_f32(weight) & finite_f32(moment) & finite_f32(variance) & finite_f32(gradient);
-  const float next_m = c.beta1 * moment + (1.0f - c.beta1) * gradient;
-  const float next_v = c.beta2 * variance + (1.0f - c.beta2) * (gradient * gradient);
+  const float next_m = adamw_next_m(moment, gradient, c);
+  const float next_v = adamw_next_v(variance, gradient, c);
   const bool write = inputs_finite & !(variance < 0.0f);
   m = write ? next_m : 0.0f;
   v = write ? next_v : 0.0f;
@@ -736,14 +760,33 @@ __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs
 
 // Recompute W', M', V' per vector and encode each against its new book with
 // op 0's FP32 rule; count W values whose decoded value moved.
+//
+// Pair tables (G <= 16): a vector's M' depends only on its M and G codes and
+// its V' only on its V and G codes, so when the shader writes every element
+// (all four input books finite, no negative variance entry) each block first
+// forms, for all 256 (M, G) and (V, G) code pairs, M' and its code, V' and its
+// code, lr M'/c1 and sqrt(V'/c2) + eps, and W (1 - lr decay) for the 16 W
+// codes. A whole vector then costs G divisions, G subtractions and the W'
+// screen. The status bits are those of the element loop: a pair's nonfinite
+// term or nonfinite encode distance is raised by every vector that uses it.
+template <int G>
+constexpr bool kPairTables = G <= 16;
+
 template <int G>
 __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const float* books3,
                                                            uint32_t* out_codes, uint32_t* changed,
                                                            uint32_t* status) {
+  constexpr bool TAB = kPairTables<G>;
+  constexpr uint32_t TG = TAB ? G : 1;
   __shared__ float sbook[3 * 16 * G];
   __shared__ float sold[4 * 16 * G];  // the op-3 input books; W's is the old weight book
   __shared__ float sm2[3 * 16 * G];
   __shared__ float scn[3 * 16];
+  __shared__ float sscaled[256 * TG];         // lr M'/c1 at [16 c_M + c_G]
+  __shared__ float sden[256 * TG];            // sqrt(V'/c2) + eps at [16 c_V + c_G]
+  __shared__ float sdec[16 * TG];             // W (1 - lr decay) at [c_W]
+  __shared__ uint32_t spair[TAB ? 512 : 1];   // M' code | nonfinite << 4; V' at 256 +
+  __shared__ uint32_t sdecbad[TAB ? 16 : 1];
   __shared__ uint32_t bflags, bmoved;
   for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) sbook[i] = books3[i];
   for (uint32_t i = threadIdx.x; i < 4 * 16 * G; i += kThreads) sold[i] = in.books4[i];
@@ -760,6 +803,51 @@ __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const
     if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(status, c.fail);
     return;
   }
+  bool tab = false;
+  if constexpr (TAB) {
+    bool ok = true;
+    for (uint32_t i = threadIdx.x; i < 4 * 16 * G; i += kThreads)
+      ok &= finite_f32(sold[i]) & !(i >= 32 * G && i < 48 * G && sold[i] < 0.0f);
+    tab = __syncthreads_and(ok);
+    if (tab) {
+      // entry e < 256: (c_M, c_G) = (e / 16, e % 16); e >= 256: (c_V, c_G)
+      for (uint32_t e = threadIdx.x; e < 512; e += kThreads) {
+        const bool vm = e < 256;
+        const uint32_t p = e % 256, a = p / 16, cg = p % 16;
+        float xv[G];
+        bool nf = false;
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          const float gradient = sold[(48 + cg) * G + j];
+          float corrected;
+          if (vm) {
+            const float next_m = adamw_next_m(sold[(16 + a) * G + j], gradient, c);
+            sscaled[p * G + j] = adamw_scaled(next_m, c, corrected);
+            nf |= !finite_f32(next_m) | !finite_f32(corrected);
+            xv[j] = next_m;
+          } else {
+            const float next_v = adamw_next_v(sold[(32 + a) * G + j], gradient, c);
+            const float den = adamw_denominator(next_v, c, corrected);
+            sden[p * G + j] = den;
+            nf |= !finite_f32(next_v) | !finite_f32(corrected) | !finite_f32(den);
+            xv[j] = next_v;
+          }
+        }
+        uint32_t code = argmin_screen<G>(xv, vm ? screen[1] : screen[2]);
+        if (code == kNoScreen) code = argmin32<G, true>(xv, G, sbook + (vm ? 16 : 32) * G, nf);
+        spair[e] = code | (uint32_t(nf) << 4);
+      }
+      for (uint32_t i = threadIdx.x; i < 16 * G; i += kThreads) sdec[i] = adamw_decayed(sold[i], c);
+      __syncthreads();
+      if (threadIdx.x < 16) {
+        bool nf = false;
+#pragma unroll
+        for (int j = 0; j < G; ++j) nf |= !finite_f32(sdec[threadIdx.x * G + j]);
+        sdecbad[threadIdx.x] = nf;
+      }
+      __syncthreads();
+    }
+  }
   const uint32_t m = in.m;
   const uint32_t words = words_for(m, G);
   const uint32_t vectors = m / G + (m % G != 0);
@@ -769,7 +857,33 @@ __global__ __launch_bounds__(kThreads) void k_adamw_encode(AdamwInputs in, const
   for (uint32_t base = blockIdx.x * kThreads; base < words * 8; base += gridDim.x * kThreads) {
     const uint32_t v = base + threadIdx.x;
     uint32_t code[3] = {0, 0, 0};
-    if (v < vectors) {
+    bool tabled = false;
+    if constexpr (TAB) {
+      if (tab && v < m / G) {  // a whole vector from the pair tables
+        tabled = true;
+        uint32_t in_code[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) in_code[st] = nibble(in.codes4 + st * words, v);
+        const uint32_t em = 16 * in_code[1] + in_code[3], ev = 16 * in_code[2] + in_code[3];
+        const uint32_t pm = spair[em], pv = spair[256 + ev];
+        code[1] = pm & 15u;
+        code[2] = pv & 15u;
+        bool nf = ((pm | pv) >> 4) != 0 || sdecbad[in_code[0]] != 0;
+        float xw[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          const float nw = sdec[in_code[0] * G + j] - sscaled[em * G + j] / sden[ev * G + j];
+          xw[j] = nw;
+          nf |= !finite_f32(nw);
+        }
+        flags |= nf ? 1u : 0u;
+        code[0] = argmin_screen<G>(xw, screen[0]);
+        if (code[0] == kNoScreen) code[0] = argmin32<G, true>(xw, G, sbook, bad);
+#pragma unroll
+        for (int j = 0; j < G; ++j) moved += sbook[code[0] * G + j] != sold[in_code[0] * G + j];
+      }
+    }
+    if (!tabled && v < vectors) {
       const uint32_t start = v * G;
       const uint32_t valid = (m - start) < G ? (m - start) : G;
       uint32_t in_code[4];
@@ -959,11 +1073,18 @@ hipError_t launch_sum_squares(hipStream_t s, const float* x, uint64_t count, dou
   return hipGetLastError();
 }
 
+// The fused encode pass builds its pair tables once per block, so its grid is
+// one resident round (blocks of 4 waves per compute unit: 3 at group 8, 2 at
+// 16, 1 at 32, as its registers allow) and every block walks many vectors.
+constexpr uint32_t kAdamwEncodeBlocks[3] = {kComputeUnits * 3, kComputeUnits * 2, kComputeUnits};
+
 hipError_t launch_adamw_encode(hipStream_t s, const AdamwInputs& in, const float* books3,
                                uint32_t* out_codes, uint32_t* changed, uint32_t* status) {
   const uint32_t vectors = in.m / in.group + (in.m % in.group != 0);
   const uint32_t words = vectors / 8 + (vectors % 8 != 0);
-  dim3 grid(grid_for(uint64_t(words) * 8, kThreads));
+  const uint32_t cap = kAdamwEncodeBlocks[in.group == 8 ? 0 : in.group == 16 ? 1 : 2];
+  const uint32_t blocks = grid_for(uint64_t(words) * 8, kThreads);
+  dim3 grid(blocks < cap ? blocks : cap);
   if (in.group == 8) k_adamw_encode<8><<<grid, kThreads, 0, s>>>(in, books3, out_codes, changed, status);
   else if (in.group == 16) k_adamw_encode<16><<<grid, kThreads, 0, s>>>(in, books3, out_codes, changed, status);
   else k_adamw_encode<32><<<grid, kThreads, 0, s>>>(in, books3, out_codes, changed, status);

@@ -77,6 +77,45 @@ def test_fused_step_equals_the_unfused_sequence(vqdev, shape, group):
             np.testing.assert_array_equal(a.codes, b.codes)
 
 
+@pytest.mark.parametrize("group", [8, 16, 32])
+def test_fused_step_overflowing_gradient_entry_used_or_not(vqdev, group):
+    """A gradient book entry whose square overflows FP32 (V' = inf for every
+    element that reads it). No vector uses it: the fused step (whose encode
+    pass forms V' per (V, G) code pair, that entry included) completes and
+    equals the unfused sequence. One vector uses it: both refuse the step, as
+    op 3 reports a nonfinite result."""
+    from alelyon_compute_kit import ack, vq
+    rng = np.random.default_rng(70 + group)
+    shape = (256, 8 * group)
+    weight = _weight(rng, shape, group)
+    vectors = shape[0] * shape[1] // group
+    book = (rng.standard_normal((16, group)) * 1e-2).astype(np.float32)
+    book[15] = np.float32(3e19)
+    idx = rng.integers(0, 15, vectors)
+    unused = vq.VQArray(shape, group, o_pack(idx), book)
+    fused = vq.VQAdamW(vqdev, weight, lr=1e-3, betas=(0.9, 0.999))
+    plain = vq.VQAdamW(Unfused(vqdev), weight, lr=1e-3, betas=(0.9, 0.999))
+    say("adamw overflow entry unused", group)
+    r1, r2 = fused.step(unused), plain.step(unused)
+    _check_report(r1, r2, fused, unused, 1)
+    for a, b in ((fused.weight, plain.weight), (fused.momentum, plain.momentum),
+                 (fused.variance, plain.variance)):
+        np.testing.assert_array_equal(a.codebook, b.codebook)
+        np.testing.assert_array_equal(a.codes, b.codes)
+    idx[vectors // 3] = 15
+    used = vq.VQArray(shape, group, o_pack(idx), book)
+    say("adamw overflow entry used", group)
+    for opt in (vq.VQAdamW(vqdev, weight, lr=1e-3, betas=(0.9, 0.999)),
+                vq.VQAdamW(Unfused(vqdev), weight, lr=1e-3, betas=(0.9, 0.999))):
+        with pytest.raises(ack.AckError):
+            opt.step(used)
+
+
+def o_pack(idx):
+    from oracle import vq4_numpy as o
+    return o.pack_indices(idx.astype(np.int64))
+
+
 @pytest.mark.parametrize("group,rare_at", [(8, -1), (16, -1), (32, -1), (8, 1)])
 def test_zero_gradient_moves_no_weight_on_the_gpu(vqdev, group, rare_at):
     from alelyon_compute_kit import vq
