@@ -640,13 +640,64 @@ __global__ __launch_bounds__(kThreads) void k_adamw_gather(AdamwInputs in, uint3
   if (flags && (threadIdx.x % warpSize) == 0) atomicOr(status, flags);
 }
 
+// The keep decision for vector x of state st whose current code is `code`:
+// the bit of its first float64 minimum under the new book when that minimum
+// may be a candidate entry, else 0. Only the candidate entries' bits are
+// read. The vector's current code e0 certifies most vectors at once: a
+// candidate c with d_c > d_e0 is not the first minimum. ||c - e0|| >
+// 2 ||x - e0|| proves it without d_c (triangle inequality; the 2e-6 margin
+// dwarfs the float64 rounding of every distance involved); otherwise d_c is
+// computed. Any other outcome (a tie, a closer candidate, a non-finite
+// distance) takes the full argmin. sbook: the three books in rows of G + 1
+// doubles; sgap: ||c - e|| within each book; bk: state st's book, global.
+template <int G>
+__device__ __forceinline__ uint32_t keep_bit(const double (&x)[G], uint32_t st, uint32_t code,
+                                             uint32_t cand, const double* sbook,
+                                             const double* sgap, const double* __restrict__ bk) {
+  constexpr uint32_t RS = G + 1;
+  // the current code, or, when it is a candidate itself (as for a state whose
+  // codes were all zero), the nearest entry by the first two components: any
+  // entry closer than c certifies it
+  uint32_t e0 = code;
+  if (cand & (1u << e0)) {
+    float best = __int_as_float(0x7f800000);
+    for (uint32_t e = 0; e < 16; ++e) {
+      if (cand & (1u << e)) continue;  // wave-uniform
+      const float t0 = float(x[0]) - float(sbook[(st * 16 + e) * RS]);
+      const float t1 = float(x[1]) - float(sbook[(st * 16 + e) * RS + 1]);
+      const float dd = t0 * t0 + t1 * t1;
+      if (dd < best) { best = dd; e0 = e; }
+    }
+  }
+  const double d0 = fitdev::dist64<G>(x, sbook + (st * 16 + e0) * RS);
+  bool full = !(d0 <= 1.7976931348623157e308);  // NaN or infinite
+  const double reach = 2.000002 * sqrt(d0);
+  const double* gap_e0 = sgap + (st * 16) * 16 + e0;
+  for (uint32_t bits = cand; bits != 0; bits &= bits - 1) {
+    const uint32_t cidx = __builtin_ctz(bits);
+    if (gap_e0[cidx * 16] > reach) continue;
+    const double dc = fitdev::dist64<G>(x, bk + cidx * G);
+    full |= !(dc > d0);
+  }
+  return full ? 1u << fitdev::nearest64_uniform<G>(x, bk) : 0u;
+}
+
 // The fit's keep pass over the recomputed states: for each state whose fit
 // set its keep-pass switch, which of its candidate entries (empty in the
 // sample, not duplicates; the only bits the update reads) its complete
 // vectors select under the float64 rule. AdamW is evaluated once per element
 // for all three.
+//
+// Pair tables (G <= 16), as in k_adamw_encode: when the shader writes every
+// element, M' and with it the keep decision of a vector's M state depend only
+// on its (M, G) code pair, and V' on its (V, G) pair, so each block decides
+// the 256 pairs of each once and a vector ORs two table words; W', when its
+// keep pass is on, costs G divisions from the pairs' lr M'/c1 and
+// sqrt(V'/c2) + eps.
 template <int G>
 __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs a) {
+  constexpr bool TAB = G <= 16;
+  constexpr uint32_t TG = TAB ? G : 1;
   const uint32_t active = (a.flags[2] ? 1u : 0u) | (a.flags[6] ? 2u : 0u) |
                           (a.flags[10] ? 4u : 0u);
   if (active == 0) return;
@@ -657,6 +708,10 @@ __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs
   __shared__ double sbook[3 * 16 * RS];
   __shared__ double sgap[3 * 16 * 16];  // ||c - e|| between the entries of each state's book
   __shared__ float sold[4 * 16 * G];
+  __shared__ float sscaled[256 * TG];        // lr M'/c1 at [16 c_M + c_G]
+  __shared__ float sden[256 * TG];           // sqrt(V'/c2) + eps at [16 c_V + c_G]
+  __shared__ float sdec[16 * TG];            // W (1 - lr decay) at [c_W]
+  __shared__ uint32_t spbits[TAB ? 512 : 1];  // keep bits of (M, G) pairs; (V, G) at 256 +
   __shared__ uint32_t bused[3];
   for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) sbook[(i / G) * RS + i % G] = book64[i];
   for (uint32_t i = threadIdx.x; i < 4 * 16 * G; i += kThreads) sold[i] = in.books4[i];
@@ -674,6 +729,40 @@ __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs
   __syncthreads();
   const Coeffs c = load_coeffs(in.coeffs);
   if (c.fail) return;  // the gather and encode passes report coefficient failures
+  bool tab = false;
+  if constexpr (TAB) {
+    bool ok = true;
+    for (uint32_t i = threadIdx.x; i < 4 * 16 * G; i += kThreads)
+      ok &= finite_f32(sold[i]) & !(i >= 32 * G && i < 48 * G && sold[i] < 0.0f);
+    tab = __syncthreads_and(ok);
+    if (tab) {
+      // entry e < 256: (c_M, c_G) = (e / 16, e % 16); e >= 256: (c_V, c_G)
+      for (uint32_t e = threadIdx.x; e < 512; e += kThreads) {
+        const bool vm = e < 256;
+        const uint32_t p = e % 256, a0 = p / 16, cg = p % 16, st = vm ? 1 : 2;
+        double x[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          const float gradient = sold[(48 + cg) * G + j];
+          float corrected;
+          if (vm) {
+            const float next_m = adamw_next_m(sold[(16 + a0) * G + j], gradient, c);
+            sscaled[p * G + j] = adamw_scaled(next_m, c, corrected);
+            x[j] = double(next_m);
+          } else {
+            const float next_v = adamw_next_v(sold[(32 + a0) * G + j], gradient, c);
+            sden[p * G + j] = adamw_denominator(next_v, c, corrected);
+            x[j] = double(next_v);
+          }
+        }
+        spbits[e] = (active & (1u << st))
+                        ? keep_bit<G>(x, st, a0, cand[st], sbook, sgap, book64 + st * 16 * G)
+                        : 0u;
+      }
+      for (uint32_t i = threadIdx.x; i < 16 * G; i += kThreads) sdec[i] = adamw_decayed(sold[i], c);
+      __syncthreads();
+    }
+  }
   const uint32_t words = words_for(in.m, G);
   const uint32_t complete = in.m / G;
   uint32_t used[3] = {0, 0, 0};
@@ -681,6 +770,21 @@ __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs
     uint32_t code[4];
 #pragma unroll
     for (int st = 0; st < 4; ++st) code[st] = nibble(in.codes4 + st * words, v);
+    if constexpr (TAB) {
+      if (tab) {
+        const uint32_t em = 16 * code[1] + code[3], ev = 16 * code[2] + code[3];
+        used[1] |= spbits[em];
+        used[2] |= spbits[256 + ev];
+        if (active & 1u) {
+          double x0[G];
+#pragma unroll
+          for (int j = 0; j < G; ++j)
+            x0[j] = double(sdec[code[0] * G + j] - sscaled[em * G + j] / sden[ev * G + j]);
+          used[0] |= keep_bit<G>(x0, 0, code[0], cand[0], sbook, sgap, book64);
+        }
+        continue;
+      }
+    }
     double x[3][G];
     if (active & 1u) {
 #pragma unroll
@@ -703,43 +807,10 @@ __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs
         x[2][j] = double(v);
       }
     }
-    // Only the candidate entries' bits are read. The vector's current code
-    // e0 certifies most vectors at once: a candidate c with d_c > d_e0 is not
-    // the first minimum. ||c - e0|| > 2 ||x - e0|| proves it without d_c
-    // (triangle inequality; the 2e-6 margin dwarfs the float64 rounding of
-    // every distance involved); otherwise d_c is computed. Any other outcome
-    // (a tie, a closer candidate, a non-finite distance) takes the full
-    // argmin.
 #pragma unroll
-    for (int st = 0; st < 3; ++st) {
-      if (!(active & (1u << st))) continue;
-      const double* bk = book64 + st * 16 * G;
-      // the current code, or, when it is a candidate itself (as for a state
-      // whose codes were all zero), the nearest entry by the first two
-      // components: any entry closer than c certifies it
-      uint32_t e0 = code[st];
-      if (cand[st] & (1u << e0)) {
-        float best = __int_as_float(0x7f800000);
-        for (uint32_t e = 0; e < 16; ++e) {
-          if (cand[st] & (1u << e)) continue;  // wave-uniform
-          const float t0 = float(x[st][0]) - float(sbook[(st * 16 + e) * RS]);
-          const float t1 = float(x[st][1]) - float(sbook[(st * 16 + e) * RS + 1]);
-          const float dd = t0 * t0 + t1 * t1;
-          if (dd < best) { best = dd; e0 = e; }
-        }
-      }
-      const double d0 = fitdev::dist64<G>(x[st], sbook + (st * 16 + e0) * RS);
-      bool full = !(d0 <= 1.7976931348623157e308);  // NaN or infinite
-      const double reach = 2.000002 * sqrt(d0);
-      const double* gap_e0 = sgap + (st * 16) * 16 + e0;
-      for (uint32_t bits = cand[st]; bits != 0; bits &= bits - 1) {
-        const uint32_t cidx = __builtin_ctz(bits);
-        if (gap_e0[cidx * 16] > reach) continue;
-        const double dc = fitdev::dist64<G>(x[st], bk + cidx * G);
-        full |= !(dc > d0);
-      }
-      if (full) used[st] |= 1u << fitdev::nearest64_uniform<G>(x[st], bk);
-    }
+    for (int st = 0; st < 3; ++st)
+      if (active & (1u << st))
+        used[st] |= keep_bit<G>(x[st], st, code[st], cand[st], sbook, sgap, book64 + st * 16 * G);
   }
   // One global atomic per block and state, and none when the bits are
   // already set: every block reports, so atomics on the three words would
@@ -1000,11 +1071,12 @@ hipError_t launch_adamw_gather(hipStream_t s, const AdamwInputs& in, uint32_t co
 }
 
 hipError_t launch_adamw_keep(hipStream_t s, const AdamwInputs& in, const FitArgs& a) {
-  // eight blocks per compute unit, each walking many vectors: the per-block
-  // set-up (books, the entry-gap table) is paid 2,048 times, not once per
-  // 512 vectors
+  // one resident round (2 blocks per compute unit, 1 at group 32, as the
+  // registers allow), each walking many vectors: the per-block set-up (books,
+  // the entry-gap table, the pair tables) is paid once per block
+  const uint32_t cap = kComputeUnits * (in.group == 32 ? 1 : 2);
   const uint32_t blocks = grid_for(in.m / in.group, kThreads);
-  dim3 grid(blocks < 2048u ? blocks : 2048u);
+  dim3 grid(blocks < cap ? blocks : cap);
   if (in.group == 8) k_adamw_keep<8><<<grid, kThreads, 0, s>>>(in, a);
   else if (in.group == 16) k_adamw_keep<16><<<grid, kThreads, 0, s>>>(in, a);
   else k_adamw_keep<32><<<grid, kThreads, 0, s>>>(in, a);
