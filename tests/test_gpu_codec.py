@@ -221,6 +221,37 @@ def test_adamw_bit_exact(vqdev, oracle, group):
         assert status == ref_status == 0
 
 
+@pytest.mark.parametrize("group", [8, 16])
+def test_adamw_quads_tail_and_overflowing_entry(vqdev, oracle, group):
+    """Op 3 on 16-byte quads with a partial last vector (m = 1000 g + 4): a
+    gradient entry whose last component squares past FLT_MAX, so V' of that
+    component alone is infinite. Read only by the last vector, whose element
+    stops four components in, it raises nothing; read by a whole vector it
+    raises bit 1. Outputs and status as the shader's."""
+    from oracle import vq4_numpy as o
+    rng = np.random.default_rng(500 + group)
+    count = 1000 * group + 4
+    vectors = -(-count // group)
+    words = -(-vectors // 8)
+    coeff = o.adamw_coefficients(1e-3, 0.9, 0.999, 1e-8, 0.01, 3)
+    codes4, books4 = _adamw_case(rng, count, group)
+    books4 = books4.copy()
+    books4[(48 + 15) * group + group - 1] = np.float32(3e19)
+    grad_idx = o.unpack_indices(codes4[3 * words:], vectors) % 15
+    for name, where, expect in (("unused but by the tail", vectors - 1, 0),
+                                ("used by a whole vector", vectors // 2, 1)):
+        idx = grad_idx.copy()
+        idx[where] = 15
+        c4 = codes4.copy()
+        c4[3 * words:] = o.pack_indices(idx.astype(np.int64))
+        say("adamw quads", group, name)
+        out, status = run_plan(vqdev, (3, count, 1, 1, group, 16, 0, 0), (c4, books4, coeff),
+                               12 * count, np.uint32)
+        ref, ref_status = oracle.adamw(c4, books4, coeff, count, group)
+        np.testing.assert_array_equal(out, ref.view(np.uint32))
+        assert status == ref_status == expect
+
+
 def test_adamw_status_bits(vqdev, oracle):
     from oracle import vq4_numpy as o
     rng = np.random.default_rng(9)
