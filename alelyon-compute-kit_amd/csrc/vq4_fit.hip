@@ -327,6 +327,66 @@ __device__ uint32_t reseed_row_regs(const float* sample, uint32_t count, const f
   return block_farthest(best, scratch);
 }
 
+// The lowest set bit of a nonzero float's value, as a power of two.
+__device__ __forceinline__ int low_bit_exponent(float v) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t e = (b >> 23) & 255u, m = b & 0x7fffffu;
+  const uint32_t mant = e ? (m | 0x800000u) : m;
+  return (e ? int(e) - 150 : -149) + __builtin_ctz(mant);
+}
+
+// An entry's member sum per component, in any order, when that order cannot
+// matter: the values are float32, all multiples of 2^L (L the lowest set bit
+// among them), so every partial sum of any subset is a multiple of 2^L no
+// larger than the sum of magnitudes A; when 2 A < 2^(L + 53) each is a double
+// exactly, no addition rounds, and the result is the sequential sum's bits
+// (numpy's axis-0 order) in every order. (A is itself a rounded sum; its
+// relative error, below 2^-40, is covered by taking 2 A.) The wave's 64
+// lanes split the members (lane = component j + G s, member k = s mod 64 / G)
+// with four accumulators each, then combine the lanes of a component. False
+// (and the caller sums in order) when any component fails the test or meets
+// a value that is not finite. Every lane of the wave takes part; component
+// j's total ends on lanes j, j + G, ...
+template <int G>
+__device__ __forceinline__ bool exact_entry_sum(const float* xs, const uint16_t* order,
+                                                uint32_t ecount, double& total) {
+  constexpr uint32_t S = 64 / G;  // member subsets per component
+  const uint32_t lane = threadIdx.x % 64, j = lane % G, sub = lane / G;
+  double acc[4] = {0.0, 0.0, 0.0, 0.0}, mag = 0.0;
+  int low = 1 << 20;
+  bool finite = true;
+  uint32_t k = sub;
+  for (; k + 3 * S < ecount; k += 4 * S) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float v = xs[uint32_t(order[k + u * S]) * G + j];
+      acc[u] += double(v);
+      mag += fabs(double(v));
+      low = v != 0.0f ? min(low, low_bit_exponent(v)) : low;
+      finite &= fabsf(v) <= FLT_MAX;
+    }
+  }
+  for (; k < ecount; k += S) {
+    const float v = xs[uint32_t(order[k]) * G + j];
+    acc[0] += double(v);
+    mag += fabs(double(v));
+    low = v != 0.0f ? min(low, low_bit_exponent(v)) : low;
+    finite &= fabsf(v) <= FLT_MAX;
+  }
+  double part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+  for (uint32_t off = G; off < 64; off <<= 1) {
+    part += __shfl_xor(part, int(off));
+    mag += __shfl_xor(mag, int(off));
+    low = min(low, __shfl_xor(low, int(off)));
+    finite &= __shfl_xor(int(finite), int(off)) != 0;
+  }
+  // 2 mag < 2^(low + 53); mag = 0 (all members zero) always passes
+  const bool ok = finite && (mag == 0.0 || ilogb(mag) + 2 <= low + 53);
+  total = part;
+  return !__any(!ok);
+}
+
 // Means and reseeds of one iteration (vq.py:223-229). One block per problem.
 template <int G>
 __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
@@ -440,6 +500,15 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
     __syncthreads();
     n += ecount;
     const uint32_t j = lane < G ? lane : 0;
+    // One staging round: try the sum in any order first (exact_entry_sum);
+    // it stands when no partial sum can round, else the sequential loop below.
+    if (count <= kRows) {
+      double total;
+      if (exact_entry_sum<G>(xs, order + estart, ecount, total)) {
+        sum = total;
+        continue;
+      }
+    }
     // whole batches of 16: the next batch's rows are read before this batch's
     // additions, which then run unconditionally
     const uint32_t whole = ecount / 16 * 16;

@@ -48,6 +48,27 @@ def test_cold_fit_equals_the_host_fit(vqdev, group, vectors, sample, iterations)
 
 
 @pytest.mark.parametrize("group", [8, 16, 32])
+@pytest.mark.parametrize("spread", [0, 20])
+def test_fit_means_exact_in_any_order_or_in_sample_order(vqdev, group, spread):
+    """An entry's mean sums its members in sample order (numpy's axis 0). With
+    one staging round the device first sums in any order and keeps that only
+    when no partial sum can round (values within 53 bits of each other, as
+    codebook-built states are); magnitudes spread over 10^spread exceed that
+    and take the in-order sum. Both must give the host fit's books; a zero
+    book sends the whole sample to one entry (the longest sum)."""
+    rng = np.random.default_rng(300 + group + spread)
+    vectors = 4096
+    scale = 10.0 ** rng.uniform(-spread, 0, vectors * group)
+    values = (rng.standard_normal(vectors * group) * scale).astype(np.float32)
+    say("fit means", group, spread)
+    host, dev = _both(vqdev, values, group=group)
+    np.testing.assert_array_equal(dev, host)
+    zero = np.zeros((16, group), np.float32)
+    host, dev = _both(vqdev, values, group=group, init=zero)
+    np.testing.assert_array_equal(dev, host)
+
+
+@pytest.mark.parametrize("group", [8, 16, 32])
 def test_warm_fit_with_the_keep_pass_equals_the_host_fit(vqdev, group):
     """Rare vectors the strided sample misses still select entry 15 of the warm
     book, so the whole-tensor pass keeps it instead of reseeding it."""
