@@ -197,6 +197,27 @@ def test_batched_codec(vqdev, oracle, op):
     assert status == 0
 
 
+@pytest.mark.parametrize("group", GROUPS)
+@pytest.mark.parametrize("extra", [8, 9])
+def test_batched_encode_whole_waves(vqdev, oracle, group, extra):
+    """Batched encode over instances of three whole 64-vector waves and a
+    tail: the matrix-core screen per instance. With an odd length the
+    instances after the first start off a 16-byte boundary and take the
+    per-lane screen; the codes are the shader's either way."""
+    rng = np.random.default_rng(600 + group + extra)
+    m, count = 64 * group * 3 + extra, 4
+    words = -(-(-(-m // group)) // 8)
+    xs = rng.standard_normal((count, m)).astype(np.float32)
+    books = rng.standard_normal((count, 16, group)).astype(np.float32)
+    say("batch encode waves", group, m)
+    out, status = run_plan(vqdev, (0, m, 1, 1, group, 16, 0, 0), (xs, books),
+                           4 * words * count, np.uint32, count=count)
+    assert status == 0
+    for i in range(count):
+        ref, _ = oracle.encode(xs[i], books[i], group)
+        np.testing.assert_array_equal(out[i * words:(i + 1) * words], ref)
+
+
 def _adamw_case(rng, count, group, variance_sign=1.0):
     states = [image(rng, count, group, scale) for scale in (0.05, 1e-2, 1e-4, 1e-2)]
     books = [b for _, b in states]
