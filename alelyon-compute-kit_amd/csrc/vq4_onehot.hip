@@ -600,7 +600,13 @@ __global__ __launch_bounds__(256) void k_split_planes(const float* __restrict__ 
   for (int t = 0; t < kOHTerms; ++t) *reinterpret_cast<bf16x8*>(planes + t * plane + at) = d[t];
 }
 
-// grid: (n / (8 G) word columns of B, mp / (128 X)). The block's 4 waves
+// grid: n / (8 G) word columns of B x mp / (128 X) row blocks, one
+// dimension. Blocks go to the 8 XCDs in turn (block b to XCD b mod 8), so when
+// the row blocks are a multiple of 8, block b takes row block b mod 8 + 8 j and
+// word column i mod C (i = b / 8, j = i / C): every block of an XCD reads its
+// eighth of the planes, which that XCD's L2 then serves to all the columns
+// (config 4: 8 row blocks of 256 rows, 56 columns). Otherwise columns vary
+// fastest. The block's 4 waves
 // stack along rows: wave w takes rows 32 X w .. 32 X w + 32 X - 1 of the
 // block's 128 X and all 8 groups of word column q (128 S columns, four 32 x 32
 // blocks y), so each A fragment read from the planes feeds four MFMAs per
@@ -621,15 +627,24 @@ __global__ __launch_bounds__(kOHThreads, 2) void k_onehot_planes(
   __shared__ float sbook[16 * G];
   const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const uint32_t i32 = lane % 32, h = lane / 32;
-  const uint32_t q = blockIdx.x;
-  const uint32_t row0 = blockIdx.y * (128 * X) + 32 * X * wave;
+  const uint32_t cols = n / (8 * G), rblocks = mp / (128 * X), bid = blockIdx.x;
+  uint32_t q, rb;
+  if (rblocks % 8 == 0) {
+    const uint32_t i = bid / 8;
+    rb = bid % 8 + 8 * (i / cols);
+    q = i % cols;
+  } else {
+    rb = bid / cols;
+    q = bid % cols;
+  }
+  const uint32_t row0 = rb * (128 * X) + 32 * X * wave;
   const float* b_book = static_cast<const float*>(o.in[3]);
   float* out = static_cast<float*>(o.out);
   bool bad = false;
   for (uint32_t i = tid; i < 16 * G; i += kOHThreads) {
     const float b = b_book[i];
     sbook[i] = b;
-    if (blockIdx.x == 0 && blockIdx.y == 0) bad |= !finite_f32(b);
+    if (bid == 0) bad |= !finite_f32(b);
   }
   // the lane's S columns: code i32 % 16 of groups 8 q + 2 y + i32 / 16
   const uint32_t ee = (i32 % 16) * 0x11111111u;
@@ -890,7 +905,7 @@ void launch_planes(hipStream_t s, const Operands& o, uint32_t m, uint32_t n, uin
   const uint64_t lanes = uint64_t(mp) * (k / 16) * 2;  // 64 lanes per (32 rows, 16-step)
   k_split_planes<<<dim3(uint32_t((lanes + 255) / 256)), 256, 0, s>>>(
       static_cast<const float*>(o.in[0]), planes, m, mp, k);
-  dim3 grid(n / (8 * G), mp / (128 * px));
+  dim3 grid((n / (8 * G)) * (mp / (128 * px)));
   if (px == 2) k_onehot_planes<G, 2><<<grid, kOHThreads, 0, s>>>(o, m, n, k, mp, nc, planes);
   else k_onehot_planes<G, 1><<<grid, kOHThreads, 0, s>>>(o, m, n, k, mp, nc, planes);
 }
