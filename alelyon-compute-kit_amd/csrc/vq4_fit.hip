@@ -342,8 +342,9 @@ __device__ __forceinline__ int low_bit_exponent(float v) {
 // exactly, no addition rounds, and the result is the sequential sum's bits
 // (numpy's axis-0 order) in every order. (A is itself a rounded sum; its
 // relative error, below 2^-40, is covered by taking 2 A.) The wave's 64
-// lanes split the members (lane = component j + G s, member k = s mod 64 / G)
-// with four accumulators each, then combine the lanes of a component. False
+// lanes split the members (lane j + G s takes component j of the members k
+// with k mod (64 / G) = s) with four accumulators each, then combine the lanes
+// of a component. False
 // (and the caller sums in order) when any component fails the test or meets
 // a value that is not finite. Every lane of the wave takes part; component
 // j's total ends on lanes j, j + G, ...
