@@ -11,8 +11,10 @@
 //           the sample never selected is not a copy of an earlier entry;
 //   keep    (only when a warm start fits a sample smaller than the tensor)
 //           the whole tensor's float64 nearest entries, when decide said so;
-//   update  one 1024-lane block: each wave owns one entry and sums its
-//           members in sample order, in float64 (numpy's axis-0 mean);
+//   update  one 1024-lane block: the members are grouped by entry and summed
+//           in float64 (numpy's axis-0 mean), by all waves in any order
+//           when no partial sum can round, else by the entry's own wave in
+//           sample order;
 //           then entries in ascending order take their mean, or, when empty
 //           and not kept, the sample vector farthest from the book as it
 //           stands at that moment (vq.py:232-257).
@@ -23,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
+#include <climits>
 #include <cstdint>
 
 #include "fit_device.hpp"
@@ -335,57 +338,83 @@ __device__ __forceinline__ int low_bit_exponent(float v) {
   return (e ? int(e) - 150 : -149) + __builtin_ctz(mant);
 }
 
-// An entry's member sum per component, in any order, when that order cannot
-// matter: the values are float32, all multiples of 2^L (L the lowest set bit
-// among them), so every partial sum of any subset is a multiple of 2^L no
-// larger than the sum of magnitudes A; when 2 A < 2^(L + 53) each is a double
-// exactly, no addition rounds, and the result is the sequential sum's bits
-// (numpy's axis-0 order) in every order. (A is itself a rounded sum; its
-// relative error, below 2^-40, is covered by taking 2 A.) The wave's 64
-// lanes split the members (lane j + G s takes component j of the members k
-// with k mod (64 / G) = s) with four accumulators each, then combine the lanes
-// of a component. False
-// (and the caller sums in order) when any component fails the test or meets
-// a value that is not finite. Every lane of the wave takes part; component
-// j's total ends on lanes j, j + G, ...
+// Entry sums per component in any order, when that order cannot matter: the
+// values are float32, all multiples of 2^L (L the lowest set bit among an
+// entry's members in that component), so every partial sum of any subset is
+// a multiple of 2^L no larger than the sum of magnitudes A; when
+// 2 A < 2^(L + 53) each is a double exactly, no addition rounds, and the
+// result is the sequential sum's bits (numpy's axis-0 order) in every order.
+// (A is itself a rounded sum; its relative error, below 2^-40, is covered by
+// taking 2 A.)
+//
+// The members, grouped by entry in `order`, are cut into one equal share per
+// wave whatever entries they belong to, so an entry holding the whole sample
+// is summed by all 16 waves. Within a share, lane j + G s takes component j
+// of the members k with k mod (64 / G) = s, with four accumulators; the
+// lanes of a component combine, and the wave adds its partial sum, its
+// magnitude sum and its lowest bit into the (entry, component) slots with
+// LDS atomics (exact sums again). A value that is not finite sets the slot's
+// lowest bit to kNotFinite, which fails the test.
+constexpr int kNotFinite = INT_MIN;
+constexpr int kNoBit = 1 << 20;  // lowest bit of a slot no nonzero value reached
+
 template <int G>
-__device__ __forceinline__ bool exact_entry_sum(const float* xs, const uint16_t* order,
-                                                uint32_t ecount, double& total) {
+__device__ __forceinline__ void exact_share(const float* xs, const uint16_t* order,
+                                            uint32_t rows, const uint32_t* etotal,
+                                            double* epart, double* emag, int* elow) {
   constexpr uint32_t S = 64 / G;  // member subsets per component
+  constexpr uint32_t kWaves = kUpdateThreads / 64;
   const uint32_t lane = threadIdx.x % 64, j = lane % G, sub = lane / G;
-  double acc[4] = {0.0, 0.0, 0.0, 0.0}, mag = 0.0;
-  int low = 1 << 20;
-  bool finite = true;
-  uint32_t k = sub;
-  for (; k + 3 * S < ecount; k += 4 * S) {
+  const uint32_t wave = threadIdx.x / 64;
+  const uint32_t share = (rows + kWaves - 1) / kWaves;
+  const uint32_t lo = min(rows, wave * share), hi = min(rows, lo + share);
+  uint32_t start = 0;
+  for (uint32_t e = 0; e < 16; ++e) {
+    const uint32_t end = start + uint32_t(__builtin_amdgcn_readfirstlane(int(etotal[e])));
+    const uint32_t first = max(start, lo), last = min(end, hi);
+    start = end;
+    if (first >= last) continue;
+    double acc[4] = {0.0, 0.0, 0.0, 0.0}, mag = 0.0;
+    int low = kNoBit;
+    bool finite = true;
+    uint32_t k = first + sub;
+    for (; k + 3 * S < last; k += 4 * S) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float v = xs[uint32_t(order[k + u * S]) * G + j];
-      acc[u] += double(v);
+      for (int u = 0; u < 4; ++u) {
+        const float v = xs[uint32_t(order[k + u * S]) * G + j];
+        acc[u] += double(v);
+        mag += fabs(double(v));
+        low = v != 0.0f ? min(low, low_bit_exponent(v)) : low;
+        finite &= fabsf(v) <= FLT_MAX;
+      }
+    }
+    for (; k < last; k += S) {
+      const float v = xs[uint32_t(order[k]) * G + j];
+      acc[0] += double(v);
       mag += fabs(double(v));
       low = v != 0.0f ? min(low, low_bit_exponent(v)) : low;
       finite &= fabsf(v) <= FLT_MAX;
     }
-  }
-  for (; k < ecount; k += S) {
-    const float v = xs[uint32_t(order[k]) * G + j];
-    acc[0] += double(v);
-    mag += fabs(double(v));
-    low = v != 0.0f ? min(low, low_bit_exponent(v)) : low;
-    finite &= fabsf(v) <= FLT_MAX;
-  }
-  double part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    double part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    low = finite ? low : kNotFinite;
 #pragma unroll
-  for (uint32_t off = G; off < 64; off <<= 1) {
-    part += __shfl_xor(part, int(off));
-    mag += __shfl_xor(mag, int(off));
-    low = min(low, __shfl_xor(low, int(off)));
-    finite &= __shfl_xor(int(finite), int(off)) != 0;
+    for (uint32_t off = G; off < 64; off <<= 1) {
+      part += __shfl_xor(part, int(off));
+      mag += __shfl_xor(mag, int(off));
+      low = min(low, __shfl_xor(low, int(off)));
+    }
+    if (lane < G) {
+      atomicAdd(&epart[e * G + j], part);
+      atomicAdd(&emag[e * G + j], mag);
+      atomicMin(&elow[e * G + j], low);
+    }
   }
-  // 2 mag < 2^(low + 53); mag = 0 (all members zero) always passes
-  const bool ok = finite && (mag == 0.0 || ilogb(mag) + 2 <= low + 53);
-  total = part;
-  return !__any(!ok);
+}
+
+// The test of exact_share's slots for one (entry, component): every value
+// finite and 2 A < 2^(L + 53); A = 0 (every member zero) always passes.
+__device__ __forceinline__ bool exact_slot(double mag, int low) {
+  return low != kNotFinite && (mag == 0.0 || ilogb(mag) + 2 <= low + 53);
 }
 
 // Means and reseeds of one iteration (vq.py:223-229). One block per problem.
@@ -404,6 +433,9 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
   __shared__ float mean[16 * G];
   __shared__ uint32_t members[16];
   __shared__ FarKey scratch[kUpdateThreads / 64];
+  __shared__ double epart[16 * G];                    // exact_share's slots
+  __shared__ double emag[16 * G];
+  __shared__ int elow[16 * G];
 
   const uint32_t p = blockIdx.x;
   const uint32_t t = threadIdx.x;
@@ -414,7 +446,12 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
   const uint8_t* idx = a.idx + uint64_t(p) * count;
   float* book = a.book + p * 16 * G;
   uint32_t* flags = a.flags + p * 4;
-  for (uint32_t i = t; i < 16 * G; i += kUpdateThreads) cur[i] = book[i];
+  for (uint32_t i = t; i < 16 * G; i += kUpdateThreads) {
+    cur[i] = book[i];
+    epart[i] = 0.0;
+    emag[i] = 0.0;
+    elow[i] = kNoBit;
+  }
 
   // Per-entry sums in sample order. Adding +0.0 for a skipped slot is exact:
   // a sum that starts at +0 is never -0, and NaN and infinities pass through.
@@ -501,12 +538,15 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
     __syncthreads();
     n += ecount;
     const uint32_t j = lane < G ? lane : 0;
-    // One staging round: try the sum in any order first (exact_entry_sum);
-    // it stands when no partial sum can round, else the sequential loop below.
+    // One staging round: every entry's sum in any order first (exact_share,
+    // spread over all waves); an entry keeps it when no partial sum can
+    // round, else its wave takes the sequential loop below.
     if (count <= kRows) {
-      double total;
-      if (exact_entry_sum<G>(xs, order + estart, ecount, total)) {
-        sum = total;
+      exact_share<G>(xs, order, rows, etotal, epart, emag, elow);
+      __syncthreads();
+      const bool ok = lane >= G || exact_slot(emag[wave * G + j], elow[wave * G + j]);
+      if (!__any(!ok)) {
+        sum = epart[wave * G + j];
         continue;
       }
     }
