@@ -175,25 +175,81 @@ __global__ __launch_bounds__(256) void k_fit_keep_dense(FitArgs a, const float* 
 }
 
 // numpy's pairwise sum of the G >= 8 squared differences (G a multiple of
-// 8) between x and an entry: eight interleaved partial sums r[j % 8] taken in
-// j order, combined ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)).
+// 8) between x and an entry, both held as float64: eight interleaved partial
+// sums r[j % 8] taken in j order, combined ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)).
 template <int G>
-__device__ __forceinline__ double pairwise_gap(const float (&x)[G], const float* entry) {
+__device__ __forceinline__ double pairwise_gap(const double (&x)[G], const double* entry) {
   double r[8];
 #pragma unroll
   for (int j = 0; j < G; ++j) {
-    const double d = double(x[j]) - double(entry[j]);
+    const double d = x[j] - entry[j];
     const double sq = d * d;
     r[j % 8] = j < 8 ? sq : r[j % 8] + sq;
   }
   return ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
 }
 
-// The gap rule of vq.py:254-256 as a combination: a NaN distance wins, else
-// the smaller one. Gaps are sums of squares, never -0, so the result does not
-// depend on the order entries are combined in.
-__device__ __forceinline__ double nanmin(double a, double b) {
-  return a != a ? a : (b != b ? b : (b < a ? b : a));
+// The gap rule of vq.py:254-256 over several entries: a NaN distance wins,
+// else the smallest. Held as the smallest gap that is not NaN and a flag for
+// NaN; gaps are sums of squares, never -0, so neither depends on the order
+// gaps arrive in (and fmin's choice when one operand is NaN never shows).
+struct Nearest {
+  double lo;
+  uint32_t nan;  // nonzero once a NaN gap arrived: a lane value, kept off the scalar unit
+  __device__ __forceinline__ void add(double gap) {
+    lo = fmin(lo, gap);
+    nan |= uint32_t(gap != gap);
+  }
+  __device__ __forceinline__ double value() const {
+    return nan ? __longlong_as_double(0x7ff8000000000000ll) : lo;
+  }
+};
+__device__ __forceinline__ Nearest nearest_of(double gap) {
+  return Nearest{gap, uint32_t(gap != gap)};
+}
+__device__ __forceinline__ Nearest nearest_none() {
+  return Nearest{__longlong_as_double(0x7ff0000000000000ll), 0u};
+}
+
+// The first reseed's hi for one row: the gaps of the untouched entries
+// [e, 16) but the twins, storing hi over [e', 16) for each e' in `store`.
+// Visits only the entries that need a gap or a store, highest first.
+template <int G>
+__device__ __forceinline__ double untouched_gap(const double (&x)[G], const double* cur64,
+                                                uint32_t e, uint32_t twin, uint32_t store,
+                                                double* suffix, uint32_t count, uint32_t i) {
+  Nearest hi = nearest_none();
+  uint32_t todo = (~twin | store) & (0xffffu << e) & 0xffffu;
+  while (todo) {
+    const uint32_t ee = 31u - uint32_t(__builtin_clz(todo));
+    todo &= ~(1u << ee);
+    if (!((twin >> ee) & 1u)) hi.add(pairwise_gap<G>(x, cur64 + ee * G));
+    if ((store >> ee) & 1u) suffix[uint64_t(ee) * count + i] = hi.value();
+  }
+  return hi.value();
+}
+
+// A row's gap to the whole book, every entry measured (a reseed that no later
+// reseed follows keeps nothing for later).
+template <int G>
+__device__ __forceinline__ double book_gap(const double (&x)[G], const double* cur64) {
+  Nearest g = nearest_none();
+  // two entries a step for group 8, one for wider rows: unrolled further,
+  // the compiler holds every entry's float64 row in registers at once
+  constexpr int kStep = G == 8 ? 2 : 1;
+#pragma unroll kStep
+  for (uint32_t ee = 0; ee < 16; ++ee) g.add(pairwise_gap<G>(x, cur64 + ee * G));
+  return g.value();
+}
+
+template <int G>
+__device__ __forceinline__ void row_as_double(const float* sample, uint32_t i, double (&x)[G]) {
+  const float4* row = reinterpret_cast<const float4*>(sample + uint64_t(i) * G);
+#pragma unroll
+  for (int q = 0; q < G / 4; ++q) {
+    const float4 v = row[q];
+    x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+  }
 }
 
 // The argmax rule of vq.py:257 (the first NaN if any, else the largest gap,
@@ -232,110 +288,86 @@ __device__ __forceinline__ uint32_t block_farthest(FarKey best, FarKey* scratch)
 }
 
 // _reseed (vq.py:232-257) of entry e for the whole block: the sample row whose
-// nearest entry of `cur` (entries below e already updated this iteration,
-// the others as they were) is farthest. Every thread returns the same row.
+// nearest entry of the book as it stands (`cur64`: entries below e already
+// updated this iteration, the others as they were) is farthest. Every thread
+// returns the same row.
 //
-// The first reseed of an iteration (`first`) measures every row against all
-// 16 entries and keeps, per row, near[i] = the gap over the updated entries
-// [0, e) and suffix[e'][i] = the gap over the untouched entries [e', 16) for
-// e' > e. A later reseed at e only measures the entries updated since the
-// previous one ([done, e)) and combines near with suffix[e]: the same gap
-// the full scan would find.
+// A row's gap is the nearer of near, over the updated entries [0, e), and hi,
+// over the untouched entries [e, 16). The first reseed of an iteration
+// (`first`) measures both. A later reseed at e measures only the entries
+// updated since the previous one ([done, e)) and takes hi over [e, 16) from
+// suffix[head], which the first reseed stored. An untouched entry with a
+// bitwise copy at a higher index (bit set in `twin`) has that copy's gap, so
+// a minimum over a range that runs to 16 need not measure it, and two
+// reseeds with only such entries between them share one hi. `store` names
+// the entries e' whose hi over [e', 16) the first reseed stores. A first
+// reseed that no later one follows (`single`) measures the whole book in one
+// unrolled pass and keeps nothing.
 template <int G>
-__device__ uint32_t reseed_row(const float* sample, uint32_t count, const float* cur,
-                               uint32_t e, uint32_t done, bool first, double* near,
+__device__ uint32_t reseed_row(const float* sample, uint32_t count, const double* cur64,
+                               uint32_t e, uint32_t done, bool first, bool single,
+                               uint32_t twin, uint32_t store, uint32_t head, double* near,
                                double* suffix, FarKey* scratch) {
   FarKey best{0, 0xffffffffu};
-  const double inf = __longlong_as_double(0x7ff0000000000000ll);
   for (uint32_t i = threadIdx.x; i < count; i += kUpdateThreads) {
-    float x[G];
-    const float4* row = reinterpret_cast<const float4*>(sample + uint64_t(i) * G);
-#pragma unroll
-    for (int q = 0; q < G / 4; ++q) {
-      const float4 v = row[q];
-      x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+    double x[G];
+    row_as_double<G>(sample, i, x);
+    if (single) {
+      best = farther_key(best, FarKey{far_key(book_gap<G>(x, cur64)), i});
+      continue;
     }
-    double lo = first ? inf : near[i];
+    Nearest lo = first ? nearest_none() : nearest_of(near[i]);
 #pragma unroll 1
-    for (uint32_t ee = first ? 0 : done; ee < e; ++ee)
-      lo = nanmin(lo, pairwise_gap<G>(x, cur + ee * G));
-    near[i] = lo;
-    double hi;
-    if (first) {
-      hi = inf;
-#pragma unroll 1
-      for (uint32_t ee = 16; ee-- > e;) {
-        hi = nanmin(pairwise_gap<G>(x, cur + ee * G), hi);
-        if (ee > e) suffix[uint64_t(ee) * count + i] = hi;
-      }
-    } else {
-      hi = suffix[uint64_t(e) * count + i];
-    }
-    const double gap = nanmin(lo, hi);
-    best = farther_key(best, FarKey{far_key(gap), i});
+    for (uint32_t ee = first ? 0 : done; ee < e; ++ee) lo.add(pairwise_gap<G>(x, cur64 + ee * G));
+    near[i] = lo.value();
+    lo.add(first ? untouched_gap<G>(x, cur64, e, twin, store, suffix, count, i)
+                 : suffix[uint64_t(head) * count + i]);
+    best = farther_key(best, FarKey{far_key(lo.value()), i});
   }
   return block_farthest(best, scratch);
 }
 
 // reseed_row for samples of at most kRegRows rows per thread: each thread
-// keeps near[] of its rows (t, t + kUpdateThreads, ...) in registers across
-// the iteration's reseeds, and a later reseed issues its suffix reads before
-// any gap arithmetic. Same rows, same values, same choice as reseed_row.
+// keeps near and hi of its rows (t, t + kUpdateThreads, ...) in registers
+// across the iteration's reseeds; a later reseed reads a stored hi only when
+// `reload` (an entry between it and the previous reseed counts), and issues
+// those reads before any gap arithmetic. Same rows, same values, same choice
+// as reseed_row.
 constexpr uint32_t kRegRows = 4;
 template <int G>
-__device__ uint32_t reseed_row_regs(const float* sample, uint32_t count, const float* cur,
-                                    uint32_t e, uint32_t done, bool first,
-                                    double (&near_r)[kRegRows], double* suffix, FarKey* scratch) {
+__device__ uint32_t reseed_row_regs(const float* sample, uint32_t count, const double* cur64,
+                                    uint32_t e, uint32_t done, bool first, bool single,
+                                    bool reload, uint32_t twin, uint32_t store,
+                                    double (&near_r)[kRegRows], double (&hi_r)[kRegRows],
+                                    double* suffix, FarKey* scratch) {
   static_assert(G == 8, "four rows of a wider group do not fit in registers");
   FarKey best{0, 0xffffffffu};
-  const double inf = __longlong_as_double(0x7ff0000000000000ll);
-  double hi_r[kRegRows];
-  if (!first) {
+  if (reload) {
 #pragma unroll
     for (uint32_t r = 0; r < kRegRows; ++r) {
       const uint32_t i = threadIdx.x + r * kUpdateThreads;
-      hi_r[r] = i < count ? suffix[uint64_t(e) * count + i] : inf;
+      hi_r[r] = i < count ? suffix[uint64_t(e) * count + i] : 0.0;
     }
   }
 #pragma unroll
   for (uint32_t r = 0; r < kRegRows; ++r) {
     const uint32_t i = threadIdx.x + r * kUpdateThreads;
     if (i >= count) break;
-    float x[G];
-    const float4* row = reinterpret_cast<const float4*>(sample + uint64_t(i) * G);
-#pragma unroll
-    for (int q = 0; q < G / 4; ++q) {
-      const float4 v = row[q];
-      x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+    double x[G];
+    row_as_double<G>(sample, i, x);
+    if (single) {
+      best = farther_key(best, FarKey{far_key(book_gap<G>(x, cur64)), i});
+      continue;
     }
-    double lo = first ? inf : near_r[r];
+    Nearest lo = first ? nearest_none() : nearest_of(near_r[r]);
 #pragma unroll 1
-    for (uint32_t ee = first ? 0 : done; ee < e; ++ee)
-      lo = nanmin(lo, pairwise_gap<G>(x, cur + ee * G));
-    near_r[r] = lo;
-    double hi;
-    if (first) {
-      hi = inf;
-#pragma unroll 1
-      for (uint32_t ee = 16; ee-- > e;) {
-        hi = nanmin(pairwise_gap<G>(x, cur + ee * G), hi);
-        if (ee > e) suffix[uint64_t(ee) * count + i] = hi;
-      }
-    } else {
-      hi = hi_r[r];
-    }
-    const double gap = nanmin(lo, hi);
-    best = farther_key(best, FarKey{far_key(gap), i});
+    for (uint32_t ee = first ? 0 : done; ee < e; ++ee) lo.add(pairwise_gap<G>(x, cur64 + ee * G));
+    near_r[r] = lo.value();
+    if (first) hi_r[r] = untouched_gap<G>(x, cur64, e, twin, store, suffix, count, i);
+    lo.add(hi_r[r]);
+    best = farther_key(best, FarKey{far_key(lo.value()), i});
   }
   return block_farthest(best, scratch);
-}
-
-// The lowest set bit of a nonzero float's value, as a power of two.
-__device__ __forceinline__ int low_bit_exponent(float v) {
-  const uint32_t b = __float_as_uint(v);
-  const uint32_t e = (b >> 23) & 255u, m = b & 0x7fffffu;
-  const uint32_t mant = e ? (m | 0x800000u) : m;
-  return (e ? int(e) - 150 : -149) + __builtin_ctz(mant);
 }
 
 // Entry sums per component in any order, when that order cannot matter: the
@@ -358,6 +390,17 @@ __device__ __forceinline__ int low_bit_exponent(float v) {
 constexpr int kNotFinite = INT_MIN;
 constexpr int kNoBit = 1 << 20;  // lowest bit of a slot no nonzero value reached
 
+// The lowest set bit of a float's value, as a power of two; kNoBit for a
+// zero. Branch-free: the mantissa's bit 31 (never set in a float's field)
+// keeps the count of trailing zeros defined when the field is zero.
+__device__ __forceinline__ int low_bit_exponent(float v) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t e = (b >> 23) & 255u, m = b & 0x7fffffu;
+  const uint32_t mant = (e ? (m | 0x800000u) : m) | 0x80000000u;
+  const int low = (e ? int(e) - 150 : -149) + int(__builtin_ctz(mant));
+  return (b << 1) != 0u ? low : kNoBit;
+}
+
 template <int G>
 __device__ __forceinline__ void exact_share(const float* xs, const uint16_t* order,
                                             uint32_t rows, const uint32_t* etotal,
@@ -378,22 +421,27 @@ __device__ __forceinline__ void exact_share(const float* xs, const uint16_t* ord
     int low = kNoBit;
     bool finite = true;
     uint32_t k = first + sub;
-    for (; k + 3 * S < last; k += 4 * S) {
+    for (; k + 3 * S < last; k += 4 * S) {  // every load of a step, then the arithmetic
+      uint32_t ix[4];
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) ix[u] = order[k + u * S];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = xs[ix[u] * G + j];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const float v = xs[uint32_t(order[k + u * S]) * G + j];
-        acc[u] += double(v);
-        mag += fabs(double(v));
-        low = v != 0.0f ? min(low, low_bit_exponent(v)) : low;
-        finite &= fabsf(v) <= FLT_MAX;
+        acc[u] += double(v[u]);
+        mag += fabs(double(v[u]));
+        low = min(low, low_bit_exponent(v[u]));
+        finite = finite && fabsf(v[u]) <= FLT_MAX;
       }
     }
     for (; k < last; k += S) {
       const float v = xs[uint32_t(order[k]) * G + j];
       acc[0] += double(v);
       mag += fabs(double(v));
-      low = v != 0.0f ? min(low, low_bit_exponent(v)) : low;
-      finite &= fabsf(v) <= FLT_MAX;
+      low = min(low, low_bit_exponent(v));
+      finite = finite && fabsf(v) <= FLT_MAX;
     }
     double part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     low = finite ? low : kNotFinite;
@@ -429,7 +477,9 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
   __shared__ uint16_t bcount[kBlocks * 16];           // members of entry e in block b
   __shared__ uint16_t bstart[kBlocks * 16];           // where they go in `order`
   __shared__ uint32_t etotal[16];
-  __shared__ float cur[16 * G];
+  __shared__ __align__(16) float cur[16 * G];
+  __shared__ double cur64[16 * G];                    // cur as float64, for the reseed gaps
+  __shared__ uint32_t twins;                          // entries with a bitwise copy above them
   __shared__ float mean[16 * G];
   __shared__ uint32_t members[16];
   __shared__ FarKey scratch[kUpdateThreads / 64];
@@ -446,8 +496,11 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
   const uint8_t* idx = a.idx + uint64_t(p) * count;
   float* book = a.book + p * 16 * G;
   uint32_t* flags = a.flags + p * 4;
+  const uint32_t kept = flags[1];  // the keep pass's entries (read early: used at the end)
+  if (t == 0) twins = 0;
   for (uint32_t i = t; i < 16 * G; i += kUpdateThreads) {
     cur[i] = book[i];
+    cur64[i] = double(book[i]);
     epart[i] = 0.0;
     emag[i] = 0.0;
     elow[i] = kNoBit;
@@ -576,30 +629,74 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
   __syncthreads();
 
   // Entries in ascending order; a reseed sees the book as updated so far.
-  const uint32_t kept = flags[1];
+  const uint32_t filled = uint32_t(__ballot(lane < 16 && members[lane % 16] > 0));
+  const uint32_t reseeds = ~filled & ~kept & 0xffffu;  // the entries this iteration reseeds
+  const bool regs = G == 8 && count <= kRegRows * kUpdateThreads;
+  uint32_t twin = 0, heads = 0, store = 0;
   double* near = a.gaps + uint64_t(p) * count * 17;
   double* suffix = near + count;
   double near_r[G == 8 ? kRegRows : 1];
+  double hi_r[G == 8 ? kRegRows : 1];
   bool first = true;
-  uint32_t done = 0;
+  uint32_t done = 0, head = 0;
   for (uint32_t e = 0; e < 16; ++e) {
-    if (members[e] > 0) {
-      if (t < G) cur[e * G + t] = mean[e * G + t];
+    if ((filled >> e) & 1u) {
+      if (t < G) {
+        cur[e * G + t] = mean[e * G + t];
+        cur64[e * G + t] = double(mean[e * G + t]);
+      }
       continue;
     }
-    if (kept & (1u << e)) continue;
+    if ((kept >> e) & 1u) continue;
+    if (first && t < 256) {  // twins among the untouched entries: a bitwise equal to some b > a
+      const uint32_t ea = t / 16, eb = t % 16;
+      if (ea >= e && eb > ea) {
+        const uint4* ra = reinterpret_cast<const uint4*>(cur + ea * G);
+        const uint4* rb = reinterpret_cast<const uint4*>(cur + eb * G);
+        uint32_t diff = 0;
+#pragma unroll 2
+        for (int q = 0; q < G / 4; ++q) {
+          const uint4 u = ra[q], v = rb[q];
+          diff |= (u.x ^ v.x) | (u.y ^ v.y) | (u.z ^ v.z) | (u.w ^ v.w);
+        }
+        if (diff == 0) atomicOr(&twins, 1u << ea);
+      }
+    }
     __syncthreads();
+    if (first) {
+      twin = twins;
+      // heads: the later reseeds whose hi differs from the previous reseed's
+      // (an untouched entry that is no twin lies between them)
+      for (uint32_t r = e + 1, prev = e; r < 16; ++r) {
+        if (!((reseeds >> r) & 1u)) continue;
+        if (~twin & ((1u << r) - (1u << prev))) heads |= 1u << r;
+        prev = r;
+      }
+      // reseed_row reads a later non-head reseed's hi from this entry's
+      store = heads | (!regs && (reseeds & ~heads & ~(1u << e)) ? 1u << e : 0u);
+    }
+    // no later reseed this iteration (group 32 keeps the general path: its
+    // float64 rows leave no registers for the whole-book pass)
+    const bool single = G <= 16 && first && (reseeds >> (e + 1)) == 0u;
+    const bool reload = !first && ((heads >> e) & 1u);
+    head = first || reload ? e : head;
     // the staged rows when they are the whole sample (one staging round)
     const float* rows_src = count <= kRows ? xs : sample;
     uint32_t row;
     if constexpr (G == 8) {  // wider rows do not fit four per thread in registers
-      row = count <= kRegRows * kUpdateThreads
-                ? reseed_row_regs<G>(rows_src, count, cur, e, done, first, near_r, suffix, scratch)
-                : reseed_row<G>(rows_src, count, cur, e, done, first, near, suffix, scratch);
+      row = regs ? reseed_row_regs<G>(rows_src, count, cur64, e, done, first, single, reload,
+                                      twin, store, near_r, hi_r, suffix, scratch)
+                 : reseed_row<G>(rows_src, count, cur64, e, done, first, single, twin, store, head,
+                                 near, suffix, scratch);
     } else {
-      row = reseed_row<G>(rows_src, count, cur, e, done, first, near, suffix, scratch);
+      row = reseed_row<G>(rows_src, count, cur64, e, done, first, single, twin, store, head, near,
+                          suffix, scratch);
     }
-    if (t < G) cur[e * G + t] = rows_src[uint64_t(row) * G + t];
+    if (t < G) {
+      const float v = rows_src[uint64_t(row) * G + t];
+      cur[e * G + t] = v;
+      cur64[e * G + t] = double(v);
+    }
     first = false;
     done = e;
   }

@@ -101,6 +101,29 @@ def test_identical_rows_reseed_every_empty_entry(vqdev, group, sample):
     assert len(np.unique(dev, axis=0)) == 16
 
 
+@pytest.mark.parametrize("group", [8, 16, 32])
+@pytest.mark.parametrize("sample", [4096, 30000])
+def test_books_with_copies_reseed_like_the_host_fit(vqdev, group, sample):
+    """A warm book whose rows repeat (0 = 2 = 11, 1 = 6, 3 = 4 = 14, 7 = 8 = 9)
+    and two distinct rows far from the data: the later copies and the far
+    rows take no sample vector and are reseeded in turn. A reseed measures
+    the book's untouched rows; a row with a copy at a higher index gives that
+    copy's gap, so runs of reseeds separated only by copies share their
+    distances, and the others measure afresh. The books must equal the host
+    fit's, from a 4,096-row sample and from a 30,000-row one."""
+    rng = np.random.default_rng(400 + group)
+    atoms = rng.standard_normal((10, group)).astype(np.float32)
+    rows = [0, 1, 0, 2, 2, 3, 1, 4, 4, 4, 5, 0, 6, 7, 2, 8]
+    init = atoms[[r % 10 for r in rows]].copy()
+    init[5] = 40.0                                 # far from every vector
+    init[12] = -40.0
+    pick = rng.integers(0, 10, 30000)
+    values = (atoms[pick] + 0.3 * rng.standard_normal((30000, group))).astype(np.float32)
+    say("fit with copied rows", group, sample)
+    host, dev = _both(vqdev, values.reshape(-1), group=group, init=init, sample_vectors=sample)
+    np.testing.assert_array_equal(dev, host)
+
+
 @pytest.mark.parametrize("group", [8, 16])
 def test_ties_and_collapses_equal_the_host_fit(vqdev, group):
     rng = np.random.default_rng(7)
