@@ -175,14 +175,15 @@ __global__ __launch_bounds__(256) void k_fit_keep_dense(FitArgs a, const float* 
 }
 
 // numpy's pairwise sum of the G >= 8 squared differences (G a multiple of
-// 8) between x and an entry, both held as float64: eight interleaved partial
-// sums r[j % 8] taken in j order, combined ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)).
-template <int G>
-__device__ __forceinline__ double pairwise_gap(const double (&x)[G], const double* entry) {
+// 8) between x (float64) and an entry (float64, or float32 converted
+// exactly): eight interleaved partial sums r[j % 8] taken in j order,
+// combined ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)).
+template <int G, typename T>
+__device__ __forceinline__ double pairwise_gap(const double (&x)[G], const T* entry) {
   double r[8];
 #pragma unroll
   for (int j = 0; j < G; ++j) {
-    const double d = x[j] - entry[j];
+    const double d = x[j] - double(entry[j]);
     const double sq = d * d;
     r[j % 8] = j < 8 ? sq : r[j % 8] + sq;
   }
@@ -274,7 +275,10 @@ __device__ __forceinline__ FarKey shfl_xor_key(FarKey v, int off) {
   return o;
 }
 // The block's farthest row: a butterfly within each wave, then one over the
-// 16 wave results; every thread returns the same row.
+// 16 wave results; every thread returns the same row. Consecutive calls
+// alternate between two scratch halves: a wave reaches the call after next
+// only past the next call's barrier, which every wave reaches after reading
+// this one's half, so no barrier guards the reuse.
 __device__ __forceinline__ uint32_t block_farthest(FarKey best, FarKey* scratch) {
   for (int off = 1; off < warpSize; off <<= 1) best = farther_key(best, shfl_xor_key(best, off));
   const uint32_t lane = threadIdx.x % warpSize;
@@ -283,7 +287,6 @@ __device__ __forceinline__ uint32_t block_farthest(FarKey best, FarKey* scratch)
   constexpr uint32_t kWaves = kUpdateThreads / 64;
   FarKey all = lane < kWaves ? scratch[lane] : FarKey{0, 0xffffffffu};
   for (int off = 1; off < int(kWaves); off <<= 1) all = farther_key(all, shfl_xor_key(all, off));
-  __syncthreads();  // scratch is reused by the next reseed
   return uint32_t(__shfl(int(all.row), 0));
 }
 
@@ -295,7 +298,8 @@ __device__ __forceinline__ uint32_t block_farthest(FarKey best, FarKey* scratch)
 // A row's gap is the nearer of near, over the updated entries [0, e), and hi,
 // over the untouched entries [e, 16). The first reseed of an iteration
 // (`first`) measures both. A later reseed at e measures only the entries
-// updated since the previous one ([done, e)) and takes hi over [e, 16) from
+// updated since the previous one ([done, e); entry `done`, the previous
+// reseed's row, read from the sample at `done_row`) and takes hi over [e, 16) from
 // suffix[head], which the first reseed stored. An untouched entry with a
 // bitwise copy at a higher index (bit set in `twin`) has that copy's gap, so
 // a minimum over a range that runs to 16 need not measure it, and two
@@ -305,9 +309,9 @@ __device__ __forceinline__ uint32_t block_farthest(FarKey best, FarKey* scratch)
 // unrolled pass and keeps nothing.
 template <int G>
 __device__ uint32_t reseed_row(const float* sample, uint32_t count, const double* cur64,
-                               uint32_t e, uint32_t done, bool first, bool single,
-                               uint32_t twin, uint32_t store, uint32_t head, double* near,
-                               double* suffix, FarKey* scratch) {
+                               uint32_t e, uint32_t done, const float* done_row, bool first,
+                               bool single, uint32_t twin, uint32_t store, uint32_t head,
+                               double* near, double* suffix, FarKey* scratch) {
   FarKey best{0, 0xffffffffu};
   for (uint32_t i = threadIdx.x; i < count; i += kUpdateThreads) {
     double x[G];
@@ -317,8 +321,10 @@ __device__ uint32_t reseed_row(const float* sample, uint32_t count, const double
       continue;
     }
     Nearest lo = first ? nearest_none() : nearest_of(near[i]);
+    if (!first) lo.add(pairwise_gap<G>(x, done_row));
 #pragma unroll 1
-    for (uint32_t ee = first ? 0 : done; ee < e; ++ee) lo.add(pairwise_gap<G>(x, cur64 + ee * G));
+    for (uint32_t ee = first ? 0 : done + 1; ee < e; ++ee)
+      lo.add(pairwise_gap<G>(x, cur64 + ee * G));
     near[i] = lo.value();
     lo.add(first ? untouched_gap<G>(x, cur64, e, twin, store, suffix, count, i)
                  : suffix[uint64_t(head) * count + i]);
@@ -336,8 +342,9 @@ __device__ uint32_t reseed_row(const float* sample, uint32_t count, const double
 constexpr uint32_t kRegRows = 4;
 template <int G>
 __device__ uint32_t reseed_row_regs(const float* sample, uint32_t count, const double* cur64,
-                                    uint32_t e, uint32_t done, bool first, bool single,
-                                    bool reload, uint32_t twin, uint32_t store,
+                                    uint32_t e, uint32_t done, const float* done_row,
+                                    bool first, bool single, bool reload, uint32_t twin,
+                                    uint32_t store,
                                     double (&near_r)[kRegRows], double (&hi_r)[kRegRows],
                                     double* suffix, FarKey* scratch) {
   static_assert(G == 8, "four rows of a wider group do not fit in registers");
@@ -360,8 +367,10 @@ __device__ uint32_t reseed_row_regs(const float* sample, uint32_t count, const d
       continue;
     }
     Nearest lo = first ? nearest_none() : nearest_of(near_r[r]);
+    if (!first) lo.add(pairwise_gap<G>(x, done_row));
 #pragma unroll 1
-    for (uint32_t ee = first ? 0 : done; ee < e; ++ee) lo.add(pairwise_gap<G>(x, cur64 + ee * G));
+    for (uint32_t ee = first ? 0 : done + 1; ee < e; ++ee)
+      lo.add(pairwise_gap<G>(x, cur64 + ee * G));
     near_r[r] = lo.value();
     if (first) hi_r[r] = untouched_gap<G>(x, cur64, e, twin, store, suffix, count, i);
     lo.add(hi_r[r]);
@@ -482,7 +491,7 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
   __shared__ uint32_t twins;                          // entries with a bitwise copy above them
   __shared__ float mean[16 * G];
   __shared__ uint32_t members[16];
-  __shared__ FarKey scratch[kUpdateThreads / 64];
+  __shared__ FarKey scratch[2 * (kUpdateThreads / 64)];  // block_farthest's two halves
   __shared__ double epart[16 * G];                    // exact_share's slots
   __shared__ double emag[16 * G];
   __shared__ int elow[16 * G];
@@ -638,7 +647,7 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
   double near_r[G == 8 ? kRegRows : 1];
   double hi_r[G == 8 ? kRegRows : 1];
   bool first = true;
-  uint32_t done = 0, head = 0;
+  uint32_t done = 0, head = 0, row = 0, parity = 0;
   for (uint32_t e = 0; e < 16; ++e) {
     if ((filled >> e) & 1u) {
       if (t < G) {
@@ -662,7 +671,9 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
         if (diff == 0) atomicOr(&twins, 1u << ea);
       }
     }
-    __syncthreads();
+    // cur64 as this reseed reads it: the means placed since the previous
+    // reseed (whose own row comes from the sample) and, for the first, the twins
+    if (first || (filled & ((1u << e) - (2u << done))) != 0u) __syncthreads();
     if (first) {
       twin = twins;
       // heads: the later reseeds whose hi differs from the previous reseed's
@@ -682,15 +693,17 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
     head = first || reload ? e : head;
     // the staged rows when they are the whole sample (one staging round)
     const float* rows_src = count <= kRows ? xs : sample;
-    uint32_t row;
+    const float* done_row = rows_src + uint64_t(row) * G;  // the previous reseed's row
+    FarKey* half = scratch + (kUpdateThreads / 64) * parity;
+    parity ^= 1u;
     if constexpr (G == 8) {  // wider rows do not fit four per thread in registers
-      row = regs ? reseed_row_regs<G>(rows_src, count, cur64, e, done, first, single, reload,
-                                      twin, store, near_r, hi_r, suffix, scratch)
-                 : reseed_row<G>(rows_src, count, cur64, e, done, first, single, twin, store, head,
-                                 near, suffix, scratch);
+      row = regs ? reseed_row_regs<G>(rows_src, count, cur64, e, done, done_row, first, single,
+                                      reload, twin, store, near_r, hi_r, suffix, half)
+                 : reseed_row<G>(rows_src, count, cur64, e, done, done_row, first, single, twin,
+                                 store, head, near, suffix, half);
     } else {
-      row = reseed_row<G>(rows_src, count, cur64, e, done, first, single, twin, store, head, near,
-                          suffix, scratch);
+      row = reseed_row<G>(rows_src, count, cur64, e, done, done_row, first, single, twin, store,
+                          head, near, suffix, half);
     }
     if (t < G) {
       const float v = rows_src[uint64_t(row) * G + t];
