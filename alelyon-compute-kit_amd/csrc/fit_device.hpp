@@ -88,5 +88,37 @@ __device__ __forceinline__ uint32_t nearest64_uniform(const double (&x)[G],
   return sel;
 }
 
+// vq.py:216-222's condition for the keep pass, for `problems` (at most 4)
+// fits at once: the entries each problem's sample left unused (bit clear in
+// flags[4 p], the assign pass's mask) that are not copies of an earlier entry
+// of its book (float compare: -0 equals 0, NaN equals nothing). Called by
+// every thread of the block; scand[p] receives problem p's entries. `sbook`
+// is block scratch of problems x 16 x G floats.
+template <int G>
+__device__ __forceinline__ void keep_candidates(const float* book, const uint32_t* flags,
+                                                uint32_t problems, float* sbook,
+                                                uint32_t* scand) {
+  for (uint32_t i = threadIdx.x; i < problems * 16 * G; i += blockDim.x) sbook[i] = book[i];
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const uint32_t p = threadIdx.x / 16, e = threadIdx.x % 16;
+    bool candidate = false;
+    if (p < problems && !((flags[4 * p] >> e) & 1u)) {
+      const float* row = sbook + (p * 16 + e) * G;
+      bool duplicate = false;
+      for (uint32_t j = 0; j < e && !duplicate; ++j) {
+        const float* other = sbook + (p * 16 + j) * G;
+        bool equal = true;
+        for (int q = 0; q < G; ++q) equal &= row[q] == other[q];
+        duplicate = equal;
+      }
+      candidate = !duplicate;
+    }
+    const uint64_t bits = __ballot(candidate);
+    if (threadIdx.x < problems) scand[threadIdx.x] = uint32_t(bits >> (16 * threadIdx.x)) & 0xffffu;
+  }
+  __syncthreads();
+}
+
 }  // namespace fitdev
 }  // namespace ackvq

@@ -698,11 +698,13 @@ template <int G>
 __global__ __launch_bounds__(kThreads) void k_adamw_keep(AdamwInputs in, FitArgs a) {
   constexpr bool TAB = G <= 16;
   constexpr uint32_t TG = TAB ? G : 1;
-  const uint32_t active = (a.flags[2] ? 1u : 0u) | (a.flags[6] ? 2u : 0u) |
-                          (a.flags[10] ? 4u : 0u);
+  __shared__ float sfit[3 * 16 * G];
+  __shared__ uint32_t scand[3];
+  fitdev::keep_candidates<G>(a.book, a.flags, 3, sfit, scand);
+  const uint32_t cand[3] = {scand[0], scand[1], scand[2]};
+  const uint32_t active = (cand[0] ? 1u : 0u) | (cand[1] ? 2u : 0u) | (cand[2] ? 4u : 0u);
   if (active == 0) return;
-  const double* __restrict__ book64 = a.book64;  // written by the decide kernel
-  const uint32_t cand[3] = {a.flags[3], a.flags[7], a.flags[11]};
+  const double* __restrict__ book64 = a.book64;  // written by the assign pass
   // rows padded to G + 1 doubles, so per-lane row gathers spread over the banks
   constexpr uint32_t RS = G + 1;
   __shared__ double sbook[3 * 16 * RS];

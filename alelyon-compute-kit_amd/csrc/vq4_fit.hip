@@ -7,10 +7,11 @@
 // single-block kernels); the fused VQAdamW step runs its three state fits as
 // three problems of the same launches. Per iteration:
 //   assign  one lane per sample vector: float64 nearest entry, the used mask;
-//   decide  the warm-start keep rule's condition (vq.py:216-222): some entry
-//           the sample never selected is not a copy of an earlier entry;
 //   keep    (only when a warm start fits a sample smaller than the tensor)
-//           the whole tensor's float64 nearest entries, when decide said so;
+//           each block first decides the warm-start keep rule's condition
+//           (vq.py:216-222: some entry the sample never selected is not a
+//           copy of an earlier entry); when it holds, the whole tensor's
+//           float64 nearest entries;
 //   update  one 1024-lane block: the members are grouped by entry and summed
 //           in float64 (numpy's axis-0 mean), by all waves in any order
 //           when no partial sum can round, else by the entry's own wave in
@@ -98,6 +99,8 @@ __global__ __launch_bounds__(kAssignThreads) void k_fit_assign(FitArgs a) {
   __shared__ double sbook[16 * G];
   load_book64<G>(a.book + p * 16 * G, sbook);
   __syncthreads();
+  if (blockIdx.x == 0)  // the keep pass reads the book as float64 from here
+    for (uint32_t i = threadIdx.x; i < 16 * G; i += kAssignThreads) a.book64[p * 16 * G + i] = sbook[i];
   const float* sample = sample_of<G>(a, p);
   uint8_t* idx = a.idx + uint64_t(p) * a.count;
   uint32_t used = 0;
@@ -118,40 +121,14 @@ __global__ __launch_bounds__(kAssignThreads) void k_fit_assign(FitArgs a) {
   if (used && (threadIdx.x % warpSize) == 0) atomicOr(&a.flags[p * 4], used);
 }
 
-// vq.py:216-222's condition: an entry the sample left unused that is not a
-// copy of an earlier entry (float compare: -0 equals 0, NaN equals nothing).
-// One wave per problem; lane e tests entry e.
-template <int G>
-__global__ __launch_bounds__(64) void k_fit_decide(FitArgs a) {
-  const uint32_t p = blockIdx.x;
-  const float* book = a.book + p * 16 * G;
-  const uint32_t used = a.flags[p * 4];
-  const uint32_t e = threadIdx.x;
-  bool candidate = false;
-  if (e < 16 && !(used & (1u << e))) {
-    bool duplicate = false;
-    for (uint32_t j = 0; j < e && !duplicate; ++j) {
-      bool equal = true;
-      for (int t = 0; t < G; ++t) equal &= book[e * G + t] == book[j * G + t];
-      duplicate = equal;
-    }
-    candidate = !duplicate;
-  }
-  // lanes 0-15 are the entries; the keep pass needs only the candidates
-  const uint32_t candidates = uint32_t(__ballot(candidate) & 0xffffu);
-  if (threadIdx.x == 0) {
-    a.flags[p * 4 + 2] = candidates != 0 ? 1u : 0u;
-    a.flags[p * 4 + 3] = candidates;
-  }
-  // the keep pass reads the book as float64 from here
-  for (uint32_t i = threadIdx.x; i < 16 * G; i += blockDim.x) a.book64[p * 16 * G + i] = double(book[i]);
-}
-
 // The keep pass over a dense tensor (one problem): entries its complete
 // vectors select under the current book.
 template <int G>
 __global__ __launch_bounds__(256) void k_fit_keep_dense(FitArgs a, const float* values) {
-  if (a.flags[2] == 0) return;
+  __shared__ float sbk[16 * G];
+  __shared__ uint32_t scand[1];
+  fitdev::keep_candidates<G>(a.book, a.flags, 1, sbk, scand);
+  if (scand[0] == 0) return;
   const double* __restrict__ book64 = a.book64;
   __shared__ uint32_t bused;
   if (threadIdx.x == 0) bused = 0;
@@ -735,7 +712,6 @@ hipError_t fit_group(hipStream_t s, const FitArgs& a, uint32_t problems, uint32_
   for (uint32_t it = 0; it < iterations; ++it) {
     k_fit_assign<G><<<assign_grid, kAssignThreads, 0, s>>>(a);
     if (keep) {
-      k_fit_decide<G><<<problems, 64, 0, s>>>(a);
       if (whole.adamw != nullptr) {
         hipError_t e = launch_adamw_keep(s, *whole.adamw, a);
         if (e != hipSuccess) return e;
