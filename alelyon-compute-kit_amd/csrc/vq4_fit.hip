@@ -356,6 +356,82 @@ __device__ uint32_t reseed_row_regs(const float* sample, uint32_t count, const d
   return block_farthest(best, scratch);
 }
 
+// A reseed that no later one follows, over a staged sample (`rows` in LDS,
+// `ids` each row's entry from the assign pass). A row's gap to its own
+// entry, U, bounds its nearest gap g from above (the same float64 steps, over
+// one of the 16 entries). Each wave's row of largest U is measured exactly
+// (256 lanes: 16 rows x 16 entries), and T is the largest of those 16 g.
+// Every row that can win or tie has g >= T, so U >= T: only those rows,
+// listed in `list`, are measured against the whole book. A NaN U, or a NaN
+// T, keeps a row on the list. Same row as measuring every row. `wrow` holds
+// 16 row numbers, `sgap` 256 gaps and T.
+template <int G>
+__device__ __noinline__ uint32_t lone_reseed(const float* rows, const uint8_t* ids,
+                                             uint32_t count, const double* cur64,
+                                             uint16_t* list, uint32_t* nlist, double* sgap,
+                                             uint32_t* wrow, FarKey* scratch) {
+  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  FarKey best{0, 0xffffffffu};
+  for (uint32_t i = threadIdx.x; i < count; i += kUpdateThreads) {
+    double x[G];
+    row_as_double<G>(rows, i, x);
+    best = farther_key(best, FarKey{far_key(pairwise_gap<G>(x, cur64 + uint32_t(ids[i]) * G)), i});
+  }
+  for (int off = 1; off < warpSize; off <<= 1) best = farther_key(best, shfl_xor_key(best, off));
+  if (lane == 0) wrow[wave] = best.row < count ? best.row : 0u;  // a wave with no row: row 0
+  if (threadIdx.x == 0) *nlist = 0;
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    double x[G];
+    row_as_double<G>(rows, wrow[threadIdx.x / 16], x);
+    sgap[threadIdx.x] = pairwise_gap<G>(x, cur64 + (threadIdx.x % 16) * G);
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {  // T: the largest exact g of the 16 rows, NaN if any is NaN
+    double v = 0.0;
+    uint32_t vnan = 0;
+    if (lane < 16) {
+      Nearest g = nearest_none();
+      for (uint32_t q = 0; q < 16; ++q) g.add(sgap[lane * 16 + q]);
+      v = g.lo;
+      vnan = g.nan;
+    }
+    for (int off = 1; off < 16; off <<= 1) {
+      v = fmax(v, __shfl_xor(v, off));
+      vnan |= uint32_t(__shfl_xor(int(vnan), off));
+    }
+    if (lane == 0) sgap[256] = vnan ? __longlong_as_double(0x7ff8000000000000ll) : v;
+  }
+  __syncthreads();
+  const double T = sgap[256];
+  for (uint32_t i0 = 0; i0 < count; i0 += kUpdateThreads) {  // whole waves: the list by ballot
+    const uint32_t i = i0 + threadIdx.x;
+    bool keep = false;
+    if (i < count) {
+      double x[G];
+      row_as_double<G>(rows, i, x);
+      keep = !(pairwise_gap<G>(x, cur64 + uint32_t(ids[i]) * G) < T);
+    }
+    const uint64_t bal = __ballot(keep);
+    uint32_t base = 0;
+    if (lane == 0 && bal != 0) base = atomicAdd(nlist, uint32_t(__popcll(bal)));
+    base = uint32_t(__shfl(int(base), 0));
+    const uint32_t rank =
+        __builtin_amdgcn_mbcnt_hi(uint32_t(bal >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u));
+    if (keep) list[base + rank] = uint16_t(i);
+  }
+  __syncthreads();
+  const uint32_t n = *nlist;
+  FarKey win{0, 0xffffffffu};
+  for (uint32_t k = threadIdx.x; k < n; k += kUpdateThreads) {
+    const uint32_t i = list[k];
+    double x[G];
+    row_as_double<G>(rows, i, x);
+    win = farther_key(win, FarKey{far_key(book_gap<G>(x, cur64)), i});
+  }
+  return block_farthest(win, scratch);
+}
+
 // Entry sums per component in any order, when that order cannot matter: the
 // values are float32, all multiples of 2^L (L the lowest set bit among an
 // entry's members in that component), so every partial sum of any subset is
@@ -466,6 +542,9 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
   __shared__ __align__(16) float cur[16 * G];
   __shared__ double cur64[16 * G];                    // cur as float64, for the reseed gaps
   __shared__ uint32_t twins;                          // entries with a bitwise copy above them
+  __shared__ uint32_t nlist;                          // lone_reseed's list length
+  __shared__ double sgap[257];                        // lone_reseed's 16 rows x 16 entries, T
+  __shared__ uint32_t wrow[16];
   __shared__ float mean[16 * G];
   __shared__ uint32_t members[16];
   __shared__ FarKey scratch[2 * (kUpdateThreads / 64)];  // block_farthest's two halves
@@ -673,7 +752,9 @@ __global__ __launch_bounds__(kUpdateThreads) void k_fit_update(FitArgs a) {
     const float* done_row = rows_src + uint64_t(row) * G;  // the previous reseed's row
     FarKey* half = scratch + (kUpdateThreads / 64) * parity;
     parity ^= 1u;
-    if constexpr (G == 8) {  // wider rows do not fit four per thread in registers
+    if (single && count <= kRows) {  // order and ids are free after the sums
+      row = lone_reseed<G>(xs, ids, count, cur64, order, &nlist, sgap, wrow, scratch);
+    } else if constexpr (G == 8) {  // wider rows do not fit four per thread in registers
       row = regs ? reseed_row_regs<G>(rows_src, count, cur64, e, done, done_row, first, single,
                                       reload, twin, store, near_r, hi_r, suffix, half)
                  : reseed_row<G>(rows_src, count, cur64, e, done, done_row, first, single, twin,
