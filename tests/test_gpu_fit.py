@@ -124,6 +124,25 @@ def test_books_with_copies_reseed_like_the_host_fit(vqdev, group, sample):
     np.testing.assert_array_equal(dev, host)
 
 
+@pytest.mark.parametrize("group,vectors", [(8, 3000), (8, 4096), (16, 2000)])
+def test_lone_reseed_equals_the_host_fit(vqdev, group, vectors):
+    """One entry of a warm book lies far from every vector, so the first
+    iteration reseeds it alone, over a sample staged whole in LDS: the search
+    that measures only the rows whose gap to their own entry reaches the best
+    exact gap of 16 probe rows. Outlier rows (three identical, tying for the
+    farthest gap) and a spread of distances must give the host fit's books."""
+    rng = np.random.default_rng(500 + group + vectors)
+    atoms = rng.standard_normal((15, group)).astype(np.float32)
+    pick = rng.integers(0, 15, vectors)
+    spread = rng.uniform(0.05, 0.6, (vectors, 1)).astype(np.float32)
+    values = (atoms[pick] + spread * rng.standard_normal((vectors, group))).astype(np.float32)
+    values[[700, 1500, 1900]] = 9.0
+    init = np.concatenate([atoms, np.full((1, group), -30.0, np.float32)])
+    say("lone reseed", group, vectors)
+    host, dev = _both(vqdev, values.reshape(-1), group=group, init=init, sample_vectors=vectors)
+    np.testing.assert_array_equal(dev, host)
+
+
 @pytest.mark.parametrize("group", [8, 16])
 def test_ties_and_collapses_equal_the_host_fit(vqdev, group):
     rng = np.random.default_rng(7)
