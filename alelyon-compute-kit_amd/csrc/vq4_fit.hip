@@ -473,9 +473,10 @@ __device__ __forceinline__ void exact_share(const float* xs, const uint16_t* ord
   const uint32_t wave = threadIdx.x / 64;
   const uint32_t share = (rows + kWaves - 1) / kWaves;
   const uint32_t lo = min(rows, wave * share), hi = min(rows, lo + share);
+  const int totals = lane < 16 ? int(etotal[lane]) : 0;  // one LDS read; lane e holds entry e's
   uint32_t start = 0;
   for (uint32_t e = 0; e < 16; ++e) {
-    const uint32_t end = start + uint32_t(__builtin_amdgcn_readfirstlane(int(etotal[e])));
+    const uint32_t end = start + uint32_t(__builtin_amdgcn_readlane(totals, int(e)));
     const uint32_t first = max(start, lo), last = min(end, hi);
     start = end;
     if (first >= last) continue;
