@@ -1006,10 +1006,10 @@ int32_t ack_vq_fit_codebook(const AckDevice* handle, const AckBuffer* values,
   fit.status = static_cast<uint32_t*>(bufs[3]->ptr);
   ackvq::FitWhole whole;
   whole.values = static_cast<const float*>(bufs[0]->ptr);
-  hipError_t e = ackvq::launch_fit_sample_dense(dev->stream, whole.values, group, fit);
+  const float* init_book = bufs[1] ? static_cast<const float*>(bufs[1]->ptr) : nullptr;
+  hipError_t e = ackvq::launch_fit_sample_dense(dev->stream, whole.values, group, fit, init_book);
   if (e == hipSuccess)
-    e = ackvq::launch_fit(dev->stream, fit, group, 1, iterations,
-                          bufs[1] ? static_cast<const float*>(bufs[1]->ptr) : nullptr, whole);
+    e = ackvq::launch_fit(dev->stream, fit, group, 1, iterations, init_book, whole, true);
   if (e != hipSuccess) return hip_failure(*dev, "vq fit: launch", e, true);
   return ACK_OK;
 }

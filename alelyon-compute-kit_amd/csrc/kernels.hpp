@@ -153,15 +153,19 @@ struct FitWhole {
 };
 
 // Samples rows linspace(0, complete-1, count) of a dense tensor into
-// a.sample; a nonfinite sampled value sets status bit 1.
+// a.sample, and sets up a one-problem fit: book = init or the sample's rows
+// linspace(0, count-1, 16), flags cleared. A nonfinite sampled or init value
+// sets status bit 1.
 hipError_t launch_fit_sample_dense(hipStream_t s, const float* values, uint32_t group,
-                                   const FitArgs& a);
+                                   const FitArgs& a, const float* init);
 // The Lloyd iterations: book = init (problem p at init + p * 16 * group) or
-// sample rows linspace(0, count-1, 16), then `iterations` rounds of assign,
+// sample rows linspace(0, count-1, 16) (unless `book_ready`: set up already,
+// as launch_fit_sample_dense does), then `iterations` rounds of assign,
 // optional keep pass over `whole`, and update. Enqueue only; allocates
 // nothing.
 hipError_t launch_fit(hipStream_t s, const FitArgs& a, uint32_t group, uint32_t problems,
-                      uint32_t iterations, const float* init, const FitWhole& whole);
+                      uint32_t iterations, const float* init, const FitWhole& whole,
+                      bool book_ready = false);
 
 // AdamW at fit_codebook's strided sample of whole vectors (rows
 // linspace(0, m/group - 1, count)): out = [3][count][group]. Also clears

@@ -51,8 +51,12 @@ __device__ __forceinline__ const float* sample_of(const FitArgs& a, uint32_t p) 
 }
 
 // Rows linspace(0, complete-1, count) of a dense tensor; one lane per value.
+// Block 0 also sets up the (one-problem) fit as k_fit_init does: the starting
+// book (init, or sample rows linspace(0, count-1, 16), read straight from the
+// tensor) and cleared flags, saving that launch.
 template <int G>
-__global__ __launch_bounds__(256) void k_fit_sample_dense(const float* values, FitArgs a) {
+__global__ __launch_bounds__(256) void k_fit_sample_dense(const float* values, FitArgs a,
+                                                          const float* init) {
   float* out = const_cast<float*>(a.sample);
   const uint32_t total = a.count * G;
   bool bad = false;
@@ -61,6 +65,20 @@ __global__ __launch_bounds__(256) void k_fit_sample_dense(const float* values, F
     const float v = values[uint64_t(row) * G + e % G];
     bad |= !finite_f32(v);
     out[e] = v;
+  }
+  if (blockIdx.x == 0) {
+    for (uint32_t i = threadIdx.x; i < 16 * G; i += 256) {
+      float v;
+      if (init != nullptr) {
+        v = init[i];
+        bad |= !finite_f32(v);
+      } else {
+        const uint32_t row = linspace_at(a.complete, a.count, linspace_at(a.count, 16, i / G));
+        v = values[uint64_t(row) * G + i % G];
+      }
+      a.book[i] = v;
+    }
+    if (threadIdx.x < 4) a.flags[threadIdx.x] = 0;
   }
   if (__any(bad) && (threadIdx.x % warpSize) == 0) atomicOr(a.status, 1u);
 }
@@ -785,8 +803,8 @@ uint32_t blocks_for(uint64_t items, uint32_t per_block, uint32_t cap) {
 
 template <int G>
 hipError_t fit_group(hipStream_t s, const FitArgs& a, uint32_t problems, uint32_t iterations,
-                     const float* init, const FitWhole& whole) {
-  k_fit_init<G><<<problems, 256, 0, s>>>(a, init);
+                     const float* init, const FitWhole& whole, bool book_ready) {
+  if (!book_ready) k_fit_init<G><<<problems, 256, 0, s>>>(a, init);
   // The keep pass can only be due for a warm start on a sample smaller than
   // the tensor (vq.py:219).
   const bool keep = init != nullptr && a.count < a.complete;
@@ -809,19 +827,20 @@ hipError_t fit_group(hipStream_t s, const FitArgs& a, uint32_t problems, uint32_
 }  // namespace
 
 hipError_t launch_fit_sample_dense(hipStream_t s, const float* values, uint32_t group,
-                                   const FitArgs& a) {
+                                   const FitArgs& a, const float* init) {
   const dim3 grid(blocks_for(uint64_t(a.count) * group, 256, 4096));
-  if (group == 8) k_fit_sample_dense<8><<<grid, 256, 0, s>>>(values, a);
-  else if (group == 16) k_fit_sample_dense<16><<<grid, 256, 0, s>>>(values, a);
-  else k_fit_sample_dense<32><<<grid, 256, 0, s>>>(values, a);
+  if (group == 8) k_fit_sample_dense<8><<<grid, 256, 0, s>>>(values, a, init);
+  else if (group == 16) k_fit_sample_dense<16><<<grid, 256, 0, s>>>(values, a, init);
+  else k_fit_sample_dense<32><<<grid, 256, 0, s>>>(values, a, init);
   return hipGetLastError();
 }
 
 hipError_t launch_fit(hipStream_t s, const FitArgs& a, uint32_t group, uint32_t problems,
-                      uint32_t iterations, const float* init, const FitWhole& whole) {
-  if (group == 8) return fit_group<8>(s, a, problems, iterations, init, whole);
-  if (group == 16) return fit_group<16>(s, a, problems, iterations, init, whole);
-  return fit_group<32>(s, a, problems, iterations, init, whole);
+                      uint32_t iterations, const float* init, const FitWhole& whole,
+                      bool book_ready) {
+  if (group == 8) return fit_group<8>(s, a, problems, iterations, init, whole, book_ready);
+  if (group == 16) return fit_group<16>(s, a, problems, iterations, init, whole, book_ready);
+  return fit_group<32>(s, a, problems, iterations, init, whole, book_ready);
 }
 
 }  // namespace ackvq
