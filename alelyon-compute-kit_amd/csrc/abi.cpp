@@ -1092,8 +1092,9 @@ int32_t ack_vq_adamw_step(const AckDevice* handle, const AckBuffer* b0, const Ac
   whole.adamw = &in;
 
   hipError_t e = ackvq::launch_adamw_gather(s, in, count, const_cast<float*>(fit.sample),
-                                               static_cast<uint32_t*>(bufs[5]->ptr), st);
-  if (e == hipSuccess) e = ackvq::launch_fit(s, fit, g, 3, iterations, in.books4, whole);
+                                               static_cast<uint32_t*>(bufs[5]->ptr), st, fit.book,
+                                               fit.flags);
+  if (e == hipSuccess) e = ackvq::launch_fit(s, fit, g, 3, iterations, in.books4, whole, true);
   if (e == hipSuccess)
     e = ackvq::launch_adamw_encode(s, in, fit.book, static_cast<uint32_t*>(bufs[3]->ptr),
                                    static_cast<uint32_t*>(bufs[5]->ptr), st);

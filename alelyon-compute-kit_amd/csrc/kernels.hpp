@@ -169,9 +169,12 @@ hipError_t launch_fit(hipStream_t s, const FitArgs& a, uint32_t group, uint32_t 
 
 // AdamW at fit_codebook's strided sample of whole vectors (rows
 // linspace(0, m/group - 1, count)): out = [3][count][group]. Also clears
-// *changed, which the encode pass counts into.
+// *changed, which the encode pass counts into, and sets up the three state
+// fits as launch_fit would: fit_book = the W, M, V books (a nonfinite entry
+// sets status bit 1), the fits' 12 flag words cleared.
 hipError_t launch_adamw_gather(hipStream_t s, const AdamwInputs& in, uint32_t count, float* out,
-                               uint32_t* changed, uint32_t* status);
+                               uint32_t* changed, uint32_t* status, float* fit_book,
+                               uint32_t* fit_flags);
 // Keep pass of the fit over the three recomputed states (FitArgs problems
 // 0..2): entries selected by complete vectors under the float64 rule, OR-ed
 // into each problem's kept mask when its keep-pass switch is set.

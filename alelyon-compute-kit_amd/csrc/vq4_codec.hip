@@ -617,8 +617,19 @@ __global__ __launch_bounds__(kThreads) void k_adamw(Operands o, uint32_t m) {
 template <int G>
 __global__ __launch_bounds__(kThreads) void k_adamw_gather(AdamwInputs in, uint32_t count,
                                                            float* out, uint32_t* changed,
-                                                           uint32_t* status) {
+                                                           uint32_t* status, float* fit_book,
+                                                           uint32_t* fit_flags) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *changed = 0;  // the encode pass counts into it
+  if (blockIdx.x == 0) {  // the three fits' set-up: each starts from its state's book
+    bool bad = false;
+    for (uint32_t i = threadIdx.x; i < 3 * 16 * G; i += kThreads) {
+      const float v = in.books4[i];
+      bad = bad || !finite_f32(v);
+      fit_book[i] = v;
+    }
+    if (threadIdx.x < 12) fit_flags[threadIdx.x] = 0;
+    if (__any(bad) && (threadIdx.x % warpSize) == 0) atomicOr(status, 1u);
+  }
   const Coeffs c = load_coeffs(in.coeffs);
   if (c.fail) {
     if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(status, c.fail);
@@ -1064,11 +1075,15 @@ hipError_t launch_adamw(hipStream_t s, const Operands& o, uint32_t m, uint32_t g
 }
 
 hipError_t launch_adamw_gather(hipStream_t s, const AdamwInputs& in, uint32_t count, float* out,
-                               uint32_t* changed, uint32_t* status) {
+                               uint32_t* changed, uint32_t* status, float* fit_book,
+                               uint32_t* fit_flags) {
   dim3 grid(grid_for(uint64_t(count) * in.group, kThreads));
-  if (in.group == 8) k_adamw_gather<8><<<grid, kThreads, 0, s>>>(in, count, out, changed, status);
-  else if (in.group == 16) k_adamw_gather<16><<<grid, kThreads, 0, s>>>(in, count, out, changed, status);
-  else k_adamw_gather<32><<<grid, kThreads, 0, s>>>(in, count, out, changed, status);
+  if (in.group == 8)
+    k_adamw_gather<8><<<grid, kThreads, 0, s>>>(in, count, out, changed, status, fit_book, fit_flags);
+  else if (in.group == 16)
+    k_adamw_gather<16><<<grid, kThreads, 0, s>>>(in, count, out, changed, status, fit_book, fit_flags);
+  else
+    k_adamw_gather<32><<<grid, kThreads, 0, s>>>(in, count, out, changed, status, fit_book, fit_flags);
   return hipGetLastError();
 }
 
