@@ -470,14 +470,17 @@ __device__ __noinline__ uint32_t lone_reseed(const float* rows, const uint8_t* i
 constexpr int kNotFinite = INT_MIN;
 constexpr int kNoBit = 1 << 20;  // lowest bit of a slot no nonzero value reached
 
-// The lowest set bit of a float's value, as a power of two; kNoBit for a
-// zero. Branch-free: the mantissa's bit 31 (never set in a float's field)
-// keeps the count of trailing zeros defined when the field is zero.
+// The lowest set bit of a finite float's value, as a power of two; kNoBit for
+// a zero. Branch-free: bit 23 set in the word stands for the implicit bit of a
+// normal (ctz = the mantissa field's trailing zeros, 23 when it is zero) and
+// caps a denormal's count; max(e, 1) - 150 is the exponent of the field's
+// bit 0 for both. Equal, for every finite bit pattern, to the field-by-field
+// form (exponent e - 150 or -149, plus the trailing zeros of the mantissa
+// with its implicit bit).
 __device__ __forceinline__ int low_bit_exponent(float v) {
   const uint32_t b = __float_as_uint(v);
-  const uint32_t e = (b >> 23) & 255u, m = b & 0x7fffffu;
-  const uint32_t mant = (e ? (m | 0x800000u) : m) | 0x80000000u;
-  const int low = (e ? int(e) - 150 : -149) + int(__builtin_ctz(mant));
+  const uint32_t e = (b >> 23) & 255u;
+  const int low = int(e > 1u ? e : 1u) - 150 + int(__builtin_ctz(b | 0x800000u));
   return (b << 1) != 0u ? low : kNoBit;
 }
 
