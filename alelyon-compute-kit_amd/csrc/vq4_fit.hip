@@ -503,7 +503,7 @@ __device__ __forceinline__ void exact_share(const float* xs, const uint16_t* ord
     if (first >= last) continue;
     double acc[4] = {0.0, 0.0, 0.0, 0.0}, mag = 0.0;
     int low = kNoBit;
-    bool finite = true;
+    uint32_t top = 0;  // largest magnitude's bits shifted left: 0xff000000 and up is not finite
     uint32_t k = first + sub;
     for (; k + 3 * S < last; k += 4 * S) {  // every load of a step, then the arithmetic
       uint32_t ix[4];
@@ -517,7 +517,7 @@ __device__ __forceinline__ void exact_share(const float* xs, const uint16_t* ord
         acc[u] += double(v[u]);
         mag += fabs(double(v[u]));
         low = min(low, low_bit_exponent(v[u]));
-        finite = finite && fabsf(v[u]) <= FLT_MAX;
+        top = max(top, __float_as_uint(v[u]) << 1);
       }
     }
     for (; k < last; k += S) {
@@ -525,10 +525,10 @@ __device__ __forceinline__ void exact_share(const float* xs, const uint16_t* ord
       acc[0] += double(v);
       mag += fabs(double(v));
       low = min(low, low_bit_exponent(v));
-      finite = finite && fabsf(v) <= FLT_MAX;
+      top = max(top, __float_as_uint(v) << 1);
     }
     double part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    low = finite ? low : kNotFinite;
+    low = top < 0xff000000u ? low : kNotFinite;
 #pragma unroll
     for (uint32_t off = G; off < 64; off <<= 1) {
       part += __shfl_xor(part, int(off));
